@@ -1,0 +1,90 @@
+"""Seeded synthetic MoE layers for the parity tests (test helper).
+
+Every tensor is drawn from the oracle's counter-based generator, keyed by (seed, stream, index),
+so the host (for the oracle) and the GPU generator (for the bench) produce the same bytes.
+Stream ids: (layer << 32) | tensor id, with the tensor ids below.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+T_ROUTER, T_SHEXP_GATE, T_X, T_RMS_W, T_BIAS = 1, 2, 3, 4, 5
+T_SH_GATE, T_SH_UP, T_SH_DOWN = 8, 9, 10
+
+
+def t_gate(e):
+    return 16 + 3 * e
+
+
+def t_up(e):
+    return 17 + 3 * e
+
+
+def t_down(e):
+    return 18 + 3 * e
+
+
+def stream(layer, tid):
+    return (layer << 32) | tid
+
+
+def zipf_bias(seed, E, s=1.1, layer=0):
+    """b_e = log p_{pi(e)}, p_j ~ 1/j^s over a seeded permutation pi."""
+    keys = np.array([O.rng_u64(seed, stream(layer, T_BIAS), e) for e in range(E)], np.uint64)
+    perm = np.argsort(keys, kind="stable")  # perm[j] = expert with rank j
+    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
+    p /= p.sum()
+    b = np.zeros(E, np.float32)
+    b[perm] = np.log(p).astype(np.float32)
+    return b
+
+
+class Layer:
+    """Raw GGUF bytes for one MoE layer: experts [E][rows*row_bytes] for gate/up/down."""
+
+    def __init__(self, seed=1, H=2048, E=512, F=512, layer=0, down_fmt=O.FMT_Q4_K, gate_fmt=O.FMT_Q4_K,
+                 bias=None, lazy=False):
+        self.seed, self.H, self.E, self.F, self.layer = seed, H, E, F, layer
+        self.gate_fmt, self.down_fmt = gate_fmt, down_fmt
+        self.router = O.gen_normal(seed, stream(layer, T_ROUTER), E * H, 0.02).reshape(E, H)
+        self.shexp_gate = O.gen_normal(seed, stream(layer, T_SHEXP_GATE), H, 0.02)
+        self.bias = bias
+        self.sh_gate = O.gen_gguf(gate_fmt, seed, stream(layer, T_SH_GATE), F, H)
+        self.sh_up = O.gen_gguf(gate_fmt, seed, stream(layer, T_SH_UP), F, H)
+        self.sh_down = O.gen_gguf(down_fmt, seed, stream(layer, T_SH_DOWN), H, F)
+        self._cache = {}
+        if not lazy:
+            for e in range(E):
+                self.expert(e)
+
+    def expert(self, e):
+        if e not in self._cache:
+            s = self.seed
+            self._cache[e] = (O.gen_gguf(self.gate_fmt, s, stream(self.layer, t_gate(e)), self.F, self.H),
+                              O.gen_gguf(self.gate_fmt, s, stream(self.layer, t_up(e)), self.F, self.H),
+                              O.gen_gguf(self.down_fmt, s, stream(self.layer, t_down(e)), self.H, self.F))
+        return self._cache[e]
+
+    def gate(self, e):
+        return self.expert(e)[0]
+
+    def up(self, e):
+        return self.expert(e)[1]
+
+    def down(self, e):
+        return self.expert(e)[2]
+
+    def oracle(self):
+        return O.OracleLayer(self.H, self.E, self.F, self.router, self.shexp_gate, self.gate, self.up, self.down,
+                             self.sh_gate, self.sh_up, self.sh_down, gate_fmt=self.gate_fmt,
+                             down_fmt=self.down_fmt, router_bias=self.bias)
+
+    def x(self, M, tid=T_X, sigma=1.0):
+        return O.gen_normal(self.seed, stream(self.layer, tid), M * self.H, sigma).reshape(M, self.H)
+
+    def stacked(self, which):
+        """[E][bytes] contiguous expert stack (what the GPU library takes)."""
+        idx = {"gate": 0, "up": 1, "down": 2}[which]
+        return np.stack([self.expert(e)[idx] for e in range(self.E)])
