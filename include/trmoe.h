@@ -1,0 +1,201 @@
+/*
+ * trmoe — MI355X (gfx950) HIP implementation of tr-infer's MoE block behind a C ABI.
+ *
+ * Drop-in for the CPU MoE path of tokenring-ai/tr-infer: the router, top-k / cumulative-mass
+ * routing, the token-to-expert dispatch, the Q4_K/Q6_K SwiGLU experts against int8-quantised
+ * activations, the shared expert with its sigmoid gate, and the combine.  Results follow the
+ * reference's CPU arithmetic (per-block f32 epilogue, FMA chains, accumulation order).
+ *
+ * Conventions (mirroring the kernel contracts of crates/tr-kernels/src in the reference):
+ *   - every pointer argument is a DEVICE pointer unless stated otherwise; the caller owns all
+ *     buffers (the reference preallocates workspaces at load, exec.rs:733-779);
+ *   - `stream` is a hipStream_t (0 = the null stream); all work is stream-ordered and
+ *     asynchronous unless a function says it synchronises;
+ *   - functions return a trk_status; the reference's asserts/panics (gemv.rs:35, quant.rs:68-71,
+ *     router.rs:75) become TRK_E_INVALID and MoePolicy::validate errors (router.rs:32-44) become
+ *     TRK_E_POLICY, with the message in trk_last_error();
+ *   - nothing here allocates device memory except trk_create.
+ */
+#ifndef TRMOE_H
+#define TRMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRK_ABI_VERSION 1
+#define TRK_MOE_K_MAX 32 /* router.rs:6 MOE_K_MAX */
+
+typedef enum {
+    TRK_OK = 0,
+    TRK_E_INVALID = -1,  /* bad shape / pointer / codec: the reference asserts */
+    TRK_E_POLICY = -2,   /* MoePolicy::validate (router.rs:32-44) */
+    TRK_E_CAPACITY = -3, /* more rows than the context was created for */
+    TRK_E_HIP = -4,      /* a HIP runtime call failed */
+    TRK_E_NOMEM = -5
+} trk_status;
+
+enum { TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
+enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
+
+/* A stack of `count` weight matrices [rows][k] in GGUF superblocks, row-major, `stride` bytes
+ * apart.  Replaces tr_model::weights::TqMat {ptr, rows, k, codec, count, stride}
+ * (crates/tr-model/src/weights.rs:14-35): `fmt` names the GGUF block format read directly on
+ * the GPU where the CPU path reads its TQ re-layout. */
+typedef struct {
+    const void *ptr;
+    uint32_t rows, k;
+    uint32_t fmt;
+    uint32_t count;
+    uint64_t stride;
+} trk_mat;
+
+/* One layer's MoE weights. Replaces tr_model::exec::MoeW (crates/tr-model/src/exec.rs:86-96). */
+typedef struct {
+    const float *router;      /* [E][H] f32 (ffn_gate_inp) */
+    const float *router_bias; /* [E] f32 or NULL: additive logit bias for synthetic load skew;
+                                 the reference has no bias (pass NULL for its semantics) */
+    const float *shexp_gate;  /* [H] f32 (ffn_gate_inp_shexp) */
+    trk_mat gate, up, down;   /* routed experts: gate/up [F][H] (Q4_K), down [H][F] (Q4_K|Q6_K) */
+    trk_mat sh_gate, sh_up, sh_down; /* shared expert, count 1 */
+} trk_moe_w;
+
+/* Cumulative-mass routing. Replaces tr_kernels::router::MoePolicy (router.rs:18-30). */
+typedef struct {
+    uint32_t min, max;
+    float mass;
+    uint32_t basis;
+} trk_moe_policy;
+
+/* Layer shape and workspace sizing (ModelConfig, crates/tr-model/src/config.rs:5-99). */
+typedef struct {
+    uint32_t hidden;           /* H (multiple of 256) */
+    uint32_t n_expert;         /* E (<= 1024) */
+    uint32_t n_ff;             /* F, per routed and shared expert (multiple of 256) */
+    uint32_t n_expert_used;    /* k of the fixed top-k routing (<= 32) */
+    uint32_t m_max;            /* most rows one call may carry (the reference's batch_max) */
+    uint32_t k_cap;            /* most experts one token may select, sizes the entry buffers
+                                  (0 = n_expert_used; a policy's max must not exceed it) */
+    uint32_t router_dot_max_m; /* batch logits use the per-row dot order when M < this, else the
+                                  gemm_f32_nt order (exec_batch.rs:989-1019: the reference
+                                  switches at its tile's core count); 0 = 16 */
+    int32_t hiprec;            /* M == 1: two-level activations (TR_HIPREC, exec.rs:782) */
+} trk_cfg;
+
+/* Replaces tr_model::exec::MoeStats counters rows/experts (exec.rs:558-605). */
+typedef struct {
+    uint64_t rows, experts;
+} trk_moe_stats;
+
+typedef struct trk_ctx trk_ctx;
+
+/* ---- layer-level entry points ---------------------------------------------------------- */
+
+/* Allocate the device workspaces for cfg (Model::load_with sizing, exec.rs:733-779) on the
+ * current HIP device. */
+int trk_create(const trk_cfg *cfg, trk_ctx **out);
+int trk_destroy(trk_ctx *ctx);
+
+/* Switch the routing policy; NULL = the fixed top-n_expert_used.
+ * Replaces Model::set_moe (exec.rs:619-625). */
+int trk_set_moe(trk_ctx *ctx, const trk_moe_policy *policy);
+
+/* out[M][H] = MoE(x[M][H]).  M == 1 follows Model::moe_block (exec.rs:1540-1623, with the S5
+ * router dot of exec.rs:1003-1011); M >= 2 follows Model::moe_batch (exec_batch.rs:1404-1580,
+ * with the router of exec_batch.rs:989-1019).  rlog: [M][E] precomputed logits or NULL to
+ * compute them from w->router.  Replaces both call sites' worker-side bodies (one call per layer
+ * from one host thread instead of an SPMD pool run). */
+int trk_moe_forward(trk_ctx *ctx, const trk_moe_w *w, const float *x, const float *rlog, uint32_t m,
+                    float *out, void *stream);
+
+/* Config-5 layer: h[M][H] += MoE(rmsnorm(h; rms_w, eps)).  Composes elem::rmsnorm
+ * (elem.rs:255-262), the MoE block and elem::add_inplace (elem.rs:104-118). */
+int trk_moe_residual(trk_ctx *ctx, const trk_moe_w *w, const float *rms_w, float eps, float *h,
+                     uint32_t m, void *stream);
+
+/* Read (and optionally reset) the routing counters; synchronises the device. */
+int trk_get_stats(trk_ctx *ctx, trk_moe_stats *out, int reset);
+
+/* Message of the last error on this thread (static storage). */
+const char *trk_last_error(void);
+
+/* ---- kernel-level entry points (mirrors of tr-kernels, on caller buffers) --------------- */
+
+/* Router logits rlog[m][E] = router . x[m] (+ bias): gemm_order 0 = attn::dot per row
+ * (attn.rs:329-357), 1 = smallgemm::gemm_f32_nt (smallgemm.rs:8-59).  Also the shared-gate
+ * logit sh[m] = dot(shexp_gate, x[m]) when shexp_gate is not NULL. */
+int trk_router_logits(const float *router, const float *bias, const float *shexp_gate, const float *x,
+                      uint32_t m, uint32_t n_expert, uint32_t hidden, int gemm_order, float *rlog,
+                      float *sh, void *stream);
+
+/* Per-row routing: route_topk (router.rs:106-113) or, with a policy, route_mass
+ * (router.rs:118-148).  ids/w: [m][32], n_sel: [m]. */
+int trk_route(const float *logits, uint32_t m, uint32_t n_expert, uint32_t k, const trk_moe_policy *policy,
+              uint32_t *ids, float *w, uint32_t *n_sel, void *stream);
+
+/* int8 activation quantisation per kb-block (kb 16 or 32): QActRef::quantize_into
+ * (quant.rs:36-48); pair != 0 quantises ONE row into (coarse, residual) rows, quantize_pair_into
+ * (quant.rs:50-53).  q [m or 2][k], scale/sum [m or 2][k/kb]. */
+int trk_quantize(const float *x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t *q, float *scale,
+                 int32_t *sum, void *stream);
+
+/* y[rows[i]][r] (+)= W_item[r] . x_i for int8 activation rows x (gemv_tq_rows / gemm_tq_rows,
+ * gemv.rs:25-78) on a GGUF matrix.  The activation block is 32 for k = W.k rows read as gate/up
+ * and 16 for down-style use: kb must be 32 (Q4_K only) or 16 (Q4_K, Q6_K).  pair: rows come in
+ * (coarse, residual) pairs, m counts physical rows.  rows: NULL = identity. */
+int trk_gemv(const trk_mat *w, uint32_t item, uint32_t kb, const int8_t *q, const float *scale,
+             const int32_t *sum, uint32_t m, int pair, float *y, uint32_t ldy, const uint32_t *rows,
+             int accumulate, void *stream);
+
+/* y = silu(g) * u (elem::swiglu_vec, elem.rs:173-175) over n floats. */
+int trk_swiglu(const float *g, const float *u, float *y, size_t n, void *stream);
+
+/* y[m][n] = rmsnorm(x[m][n]; w, eps) (elem.rs:255-262). */
+int trk_rmsnorm(const float *x, const float *w, float eps, uint32_t m, uint32_t n, float *y, void *stream);
+
+/* y[i] += a[i] (elem.rs:104-118). */
+int trk_add_inplace(float *y, const float *a, size_t n, void *stream);
+
+/* ---- synthetic data (bit-identical to the test oracle's generator) ---------------------- */
+/* GGUF superblocks of a [rows][k] matrix: d (and dmin) ~ U(dlo, dhi) as f16, all other bytes
+ * uniform; fmt Q4_K or Q6_K. */
+int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
+                 float dhi, void *out, void *stream);
+/* n normals N(0, sigma) (Box-Muller in double, rounded to f32). */
+int trk_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float *out, void *stream);
+
+/* ---- measurement and introspection ------------------------------------------------------ */
+/* Per-kernel timing (the HIP counterpart of the reference's TR_PROFILE laps, exec.rs:344-430):
+ * when on, every kernel a forward launches is bracketed by HIP events on the call's stream. */
+int trk_set_timing(trk_ctx *ctx, int on);
+/* Sum of the recorded durations per kernel since the last call, then forget them (synchronises).
+ * Fills up to cap entries (kernel name, total ms, launches); returns the number of kernels. */
+int trk_get_timing(trk_ctx *ctx, const char **names, double *ms, uint64_t *launches, int cap);
+
+/* Copy an internal workspace buffer of the last forward to host memory (synchronises). */
+enum {
+    TRK_WS_RLOG = 1,     /* [M][E] f32 */
+    TRK_WS_IDS = 2,      /* [M][32] u32 */
+    TRK_WS_W = 3,        /* [M][32] f32 */
+    TRK_WS_NSEL = 4,     /* [M] u32 */
+    TRK_WS_ENT_TOK = 5,  /* [n_ent] u32 */
+    TRK_WS_ENT_W = 6,    /* [n_ent] f32 */
+    TRK_WS_ENT_EXP = 7,  /* [n_ent] u32 */
+    TRK_WS_GRP_START = 8,/* [n_groups+1] u32 */
+    TRK_WS_GRP_EXP = 9,  /* [n_groups] u32 */
+    TRK_WS_NGROUPS = 10, /* [2] u32: n_groups, n_ent */
+    TRK_WS_XQ = 11,      /* [rows][H] i8 (pair: 2 rows) */
+    TRK_WS_XS = 12,      /* [rows][H/32] f32 */
+    TRK_WS_ACTQ = 13,    /* activation rows of the down input, i8 */
+    TRK_WS_ACTS = 14,    /* their folded scales, f32 */
+    TRK_WS_SHLOGIT = 15  /* [M] f32: dot(shexp_gate, x) */
+};
+int trk_debug_read(trk_ctx *ctx, int which, void *host_dst, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

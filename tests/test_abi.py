@@ -1,0 +1,53 @@
+"""CPU-side checks of the C ABI: the library builds for gfx950, loads, and exports every entry
+point include/trmoe.h declares; argument validation returns the documented status codes without
+touching a GPU."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import pytest
+
+import trmoe
+
+
+def test_library_exports_every_declared_symbol():
+    L = trmoe.lib()
+    names = trmoe.header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_header_declares_the_boundary():
+    names = set(trmoe.header_functions())
+    for n in ("trk_create", "trk_destroy", "trk_set_moe", "trk_moe_forward", "trk_moe_residual", "trk_route",
+              "trk_quantize", "trk_gemv", "trk_router_logits", "trk_last_error"):
+        assert n in names
+
+
+def test_invalid_arguments_are_rejected_on_the_host():
+    L = trmoe.lib()
+    # QAct::zeros asserts kb in {16, 32} (quant.rs:68-71): status, not a crash
+    rc = L.trk_quantize(C.c_void_p(16), 1, 48, 24, 0, C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None)
+    assert rc == -1 and b"kb" in L.trk_last_error()
+    # MoePolicy::validate (router.rs:32-44)
+    for pol in [(0, 10, 0.9, 1), (1, 33, 0.9, 1), (1, 10, 0.0, 1), (3, 2, 0.5, 0)]:
+        p = trmoe.Policy(*pol)
+        rc = L.trk_route(C.c_void_p(16), 1, 512, 10, C.byref(p), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None)
+        assert rc == -2, pol
+    p = trmoe.Policy(1, 20, 0.9, 1)
+    assert L.trk_route(C.c_void_p(16), 1, 16, 10, C.byref(p), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None) == -2
+    # bad shapes for trk_create
+    h = C.c_void_p()
+    bad = trmoe.Cfg(2000, 512, 512, 10, 1, 0, 16, 1)
+    assert L.trk_create(C.byref(bad), C.byref(h)) == -1
+    bad = trmoe.Cfg(2048, 512, 512, 33, 1, 0, 16, 1)
+    assert L.trk_create(C.byref(bad), C.byref(h)) == -1
+
+
+def test_build_flags_keep_numerics_contract():
+    mk = open(os.path.join(trmoe.PKG_ROOT, "Makefile")).read()
+    for flag in ("-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt", "-packed-fp32-ops",
+                 "--offload-arch=$(ARCH)"):
+        assert flag in mk

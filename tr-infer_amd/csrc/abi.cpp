@@ -1,0 +1,482 @@
+// C ABI of the MoE library: argument checks, workspace ownership and the launch sequence of the
+// decode (M = 1) and batch (M >= 2) paths.  Kernels live in k_*.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "trmoe_internal.h"
+
+using namespace trk;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                             \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess) return fail(TRK_E_HIP, "%s: %s", #expr, hipGetErrorString(e_));    \
+    } while (0)
+
+uint32_t row_bytes(uint32_t fmt, uint32_t k) {
+    if (fmt == TRK_FMT_Q4_K) return k / 256 * 144;
+    if (fmt == TRK_FMT_Q6_K) return k / 256 * 210;
+    return 0;
+}
+
+}  // namespace
+
+// Kernel ids for trk_get_timing.
+enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
+                K_RMSNORM, K_COUNT };
+static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
+                                                  "decode_down", "dispatch", "batch_gateup", "batch_down",
+                                                  "batch_combine", "rmsnorm"};
+
+struct TimedLaunch {
+    int kid;
+    hipEvent_t start, stop;
+};
+
+struct trk_ctx {
+    trk_cfg cfg;
+    Workspace ws;
+    Policy pol;
+    int device;
+    void* block;  // one device allocation holding every workspace buffer
+    int timing;
+    std::vector<TimedLaunch> timed;
+    std::vector<hipEvent_t> spare;
+};
+
+extern "C" const char* trk_last_error(void) { return g_err; }
+
+static int check_policy(const trk_ctx* c, const trk_moe_policy* p) {
+    // MoePolicy::validate (router.rs:32-44), plus the workspace capacity
+    if (p->min < 1 || p->min > p->max)
+        return fail(TRK_E_POLICY, "moe policy: need 1 <= min (%u) <= max (%u)", p->min, p->max);
+    uint32_t lim = std::min<uint32_t>(TRK_MOE_K_MAX, c->cfg.n_expert);
+    if (p->max > TRK_MOE_K_MAX || p->max > c->cfg.n_expert)
+        return fail(TRK_E_POLICY, "moe policy: max (%u) above the limit (%u)", p->max, lim);
+    if (!(p->mass > 0.0f) || p->mass != p->mass)
+        return fail(TRK_E_POLICY, "moe policy: target mass (%g) must be positive", (double)p->mass);
+    if (p->max > c->ws.k_cap)
+        return fail(TRK_E_POLICY, "moe policy: max (%u) above the context's k_cap (%u)", p->max, c->ws.k_cap);
+    return TRK_OK;
+}
+
+extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
+    if (!cfg || !out) return fail(TRK_E_INVALID, "trk_create: null argument");
+    const uint32_t H = cfg->hidden, E = cfg->n_expert, F = cfg->n_ff, k = cfg->n_expert_used;
+    if (H == 0 || H % 256 || F == 0 || F % 256)
+        return fail(TRK_E_INVALID, "hidden (%u) and n_ff (%u) must be positive multiples of 256", H, F);
+    if (E == 0 || E > 1024) return fail(TRK_E_INVALID, "n_expert (%u) must be in 1..1024", E);
+    if (k < 1 || k > TRK_MOE_K_MAX || k > E) return fail(TRK_E_INVALID, "n_expert_used (%u) must be in 1..min(32, E)", k);
+    if (cfg->m_max == 0) return fail(TRK_E_INVALID, "m_max must be positive");
+    uint32_t k_cap = cfg->k_cap ? cfg->k_cap : k;
+    if (k_cap < k || k_cap > TRK_MOE_K_MAX) return fail(TRK_E_INVALID, "k_cap (%u) must be in n_expert_used..32", k_cap);
+
+    trk_ctx* c = new (std::nothrow) trk_ctx();
+    if (!c) return fail(TRK_E_NOMEM, "host allocation failed");
+    c->cfg = *cfg;
+    if (!c->cfg.router_dot_max_m) c->cfg.router_dot_max_m = 16;
+    c->pol = Policy{0, 0, 0, 0, 0.0f};
+    HIP_TRY(hipGetDevice(&c->device));
+
+    Workspace& ws = c->ws;
+    const size_t M = cfg->m_max, rows_x = std::max<size_t>(2, M);
+    ws.H = H;
+    ws.E = E;
+    ws.F = F;
+    ws.m_max = cfg->m_max;
+    ws.k_cap = k_cap;
+    ws.ent_cap = (uint32_t)(M * k_cap);
+    ws.item_cap = E + (ws.ent_cap + 7) / 8 + (uint32_t)((M + 7) / 8) + 1;
+    ws.act_rows = std::max<size_t>((size_t)(TRK_MOE_K_MAX + 1) * 2, (size_t)ws.ent_cap + M);
+
+    // carve one allocation (256-byte aligned pieces)
+    struct Piece {
+        void** p;
+        size_t bytes;
+    };
+    const size_t yrows = (size_t)ws.ent_cap + M;
+    Piece pieces[] = {
+        {(void**)&ws.xq, rows_x * H},
+        {(void**)&ws.xs, rows_x * (H / 32) * 4},
+        {(void**)&ws.xsum, rows_x * (H / 32) * 4},
+        {(void**)&ws.xn, M * H * 4},
+        {(void**)&ws.rlog, M * E * 4},
+        {(void**)&ws.shl, M * 4},
+        {(void**)&ws.ids, M * TRK_MOE_K_MAX * 4},
+        {(void**)&ws.w, M * TRK_MOE_K_MAX * 4},
+        {(void**)&ws.n_sel, M * 4},
+        {(void**)&ws.ent_tok, (size_t)ws.ent_cap * 4},
+        {(void**)&ws.ent_w, (size_t)ws.ent_cap * 4},
+        {(void**)&ws.ent_exp, (size_t)ws.ent_cap * 4},
+        {(void**)&ws.ent_of, M * TRK_MOE_K_MAX * 4},
+        {(void**)&ws.grp_start, (E + 2) * 4},
+        {(void**)&ws.grp_exp, (E + 1) * 4},
+        {(void**)&ws.n_groups, 16},
+        {(void**)&ws.chunk_cnt, 16},
+        {(void**)&ws.items, (size_t)ws.item_cap * sizeof(Item)},
+        {(void**)&ws.actq, ws.act_rows * F},
+        {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
+        {(void**)&ws.actsum, ws.act_rows * (F / 16) * 4},
+        {(void**)&ws.yent, yrows * H * 4},
+        {(void**)&ws.out_tmp, M * H * 4},
+        {(void**)&ws.stats, 16},
+    };
+    size_t total = 0;
+    for (auto& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
+    hipError_t e = hipMalloc(&c->block, total);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(TRK_E_NOMEM, "hipMalloc(%zu): %s", total, hipGetErrorString(e));
+    }
+    e = hipMemset(c->block, 0, total);
+    if (e != hipSuccess) {
+        (void)hipFree(c->block);
+        delete c;
+        return fail(TRK_E_HIP, "workspace clear: %s", hipGetErrorString(e));
+    }
+    size_t off = 0;
+    for (auto& pc : pieces) {
+        *pc.p = (char*)c->block + off;
+        off += (pc.bytes + 255) / 256 * 256;
+    }
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(c->block);
+        delete c;
+        return fail(TRK_E_HIP, "workspace init: %s", hipGetErrorString(e));
+    }
+    *out = c;
+    return TRK_OK;
+}
+
+extern "C" int trk_destroy(trk_ctx* c) {
+    if (!c) return TRK_OK;
+    for (auto& t : c->timed) {
+        (void)hipEventDestroy(t.start);
+        (void)hipEventDestroy(t.stop);
+    }
+    for (auto ev : c->spare) (void)hipEventDestroy(ev);
+    (void)hipFree(c->block);
+    delete c;
+    return TRK_OK;
+}
+
+extern "C" int trk_set_moe(trk_ctx* c, const trk_moe_policy* p) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    if (!p) {
+        c->pol = Policy{0, 0, 0, 0, 0.0f};
+        return TRK_OK;
+    }
+    int rc = check_policy(c, p);
+    if (rc) return rc;
+    c->pol = Policy{1, p->min, p->max, p->basis, p->mass};
+    return TRK_OK;
+}
+
+static int make_mat(const trk_mat& m, uint32_t rows, uint32_t k, bool down_ok_q6, uint32_t min_count, const char* name,
+                    Mat& out) {
+    if (!m.ptr) return fail(TRK_E_INVALID, "%s: null weight pointer", name);
+    if (m.rows != rows || m.k != k)
+        return fail(TRK_E_INVALID, "%s: shape [%u][%u], expected [%u][%u]", name, m.rows, m.k, rows, k);
+    if (!(m.fmt == TRK_FMT_Q4_K || (down_ok_q6 && m.fmt == TRK_FMT_Q6_K)))
+        return fail(TRK_E_INVALID, "%s: unsupported format %u", name, m.fmt);
+    if (m.count < min_count) return fail(TRK_E_INVALID, "%s: %u matrices, need %u", name, m.count, min_count);
+    uint32_t rb = row_bytes(m.fmt, k);
+    uint64_t mb = (uint64_t)rb * rows;
+    if (m.count > 1 && m.stride < mb) return fail(TRK_E_INVALID, "%s: stride %llu below matrix bytes %llu", name,
+                                                  (unsigned long long)m.stride, (unsigned long long)mb);
+    uint64_t align = m.fmt == TRK_FMT_Q4_K ? 16 : 2;
+    if ((uintptr_t)m.ptr % align || (m.count > 1 && m.stride % align))
+        return fail(TRK_E_INVALID, "%s: pointer/stride must be %llu-byte aligned", name, (unsigned long long)align);
+    out = Mat{(const uint8_t*)m.ptr, m.count > 1 ? m.stride : mb, rows, k, m.fmt, rb};
+    return TRK_OK;
+}
+
+struct Mats {
+    Mat gate, up, down, shg, shu, shd;
+};
+
+static int check_weights(trk_ctx* c, const trk_moe_w* w, Mats& M) {
+    const uint32_t H = c->cfg.hidden, F = c->cfg.n_ff, E = c->cfg.n_expert;
+    if (!w || !w->shexp_gate) return fail(TRK_E_INVALID, "weights: null pointer");
+    int rc;
+    if ((rc = make_mat(w->gate, F, H, false, E, "gate", M.gate))) return rc;
+    if ((rc = make_mat(w->up, F, H, false, E, "up", M.up))) return rc;
+    if ((rc = make_mat(w->down, H, F, true, E, "down", M.down))) return rc;
+    if ((rc = make_mat(w->sh_gate, F, H, false, 1, "sh_gate", M.shg))) return rc;
+    if ((rc = make_mat(w->sh_up, F, H, false, 1, "sh_up", M.shu))) return rc;
+    if ((rc = make_mat(w->sh_down, H, F, true, 1, "sh_down", M.shd))) return rc;
+    return TRK_OK;
+}
+
+static hipError_t take_event(trk_ctx* c, hipEvent_t* ev) {
+    if (!c->spare.empty()) {
+        *ev = c->spare.back();
+        c->spare.pop_back();
+        return hipSuccess;
+    }
+    return hipEventCreate(ev);
+}
+
+// Run one launch; with timing on, bracket it with events on the launch's stream.
+template <typename F>
+static hipError_t timed(trk_ctx* c, int kid, hipStream_t st, F&& launch) {
+    if (!c->timing) return launch();
+    TimedLaunch t{kid, nullptr, nullptr};
+    hipError_t e;
+    if ((e = take_event(c, &t.start)) != hipSuccess || (e = take_event(c, &t.stop)) != hipSuccess) return e;
+    if ((e = hipEventRecord(t.start, st)) != hipSuccess) return e;
+    e = launch();
+    if (e != hipSuccess) return e;
+    if ((e = hipEventRecord(t.stop, st)) != hipSuccess) return e;
+    c->timed.push_back(t);
+    return hipSuccess;
+}
+#define TIMED(kid, expr) HIP_TRY(timed(c, kid, st, [&]() { return (expr); }))
+
+// The MoE block on x (already normed).  residual: out += moe instead of out = moe.
+static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m, float* out,
+                   int residual, hipStream_t st) {
+    Mats M;
+    int rc = check_weights(c, w, M);
+    if (rc) return rc;
+    if (!x || !out) return fail(TRK_E_INVALID, "null x/out");
+    if (m == 0) return TRK_OK;
+    if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
+    if (!rlog && !w->router) return fail(TRK_E_INVALID, "need router weights or precomputed logits");
+    Workspace& ws = c->ws;
+    const uint32_t H = ws.H, E = ws.E, k = c->cfg.n_expert_used;
+    const uint32_t kcap = c->pol.enabled ? c->pol.max : k;
+    const float* lg = rlog ? rlog : ws.rlog;
+    const int gemm_order = m >= c->cfg.router_dot_max_m ? 1 : 0;
+    if (rlog)
+        TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st));
+    else
+        TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H,
+                                             m == 1 ? 0 : gemm_order, ws.rlog, ws.shl, st));
+    TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+    if (m == 1) {
+        const int pair = c->cfg.hiprec ? 1 : 0;
+        TIMED(K_QUANT, launch_quantize(x, 1, H, 32, pair, ws.xq, ws.xs, ws.xsum, st));
+        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, ws, pair, kcap, st));
+        TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
+    } else {
+        TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, st));
+        TIMED(K_DISPATCH, launch_dispatch(ws, m, st));
+        TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));
+        TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, st));
+        TIMED(K_B_COMBINE, launch_batch_combine(ws, m, out, residual, st));
+    }
+    return TRK_OK;
+}
+
+extern "C" int trk_moe_forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m,
+                               float* out, void* stream) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    return forward(c, w, x, rlog, m, out, 0, (hipStream_t)stream);
+}
+
+extern "C" int trk_moe_residual(trk_ctx* c, const trk_moe_w* w, const float* rms_w, float eps, float* h, uint32_t m,
+                                void* stream) {
+    if (!c || !h) return fail(TRK_E_INVALID, "null argument");
+    if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
+    hipStream_t st = (hipStream_t)stream;
+    TIMED(K_RMSNORM, launch_rmsnorm(h, rms_w, eps, m, c->cfg.hidden, c->ws.xn, st));
+    return forward(c, w, c->ws.xn, nullptr, m, h, 1, st);
+}
+
+extern "C" int trk_get_stats(trk_ctx* c, trk_moe_stats* out, int reset) {
+    if (!c || !out) return fail(TRK_E_INVALID, "null argument");
+    unsigned long long v[2];
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(v, c->ws.stats, sizeof v, hipMemcpyDeviceToHost));
+    out->rows = v[0];
+    out->experts = v[1];
+    if (reset) {
+        HIP_TRY(hipMemset(c->ws.stats, 0, sizeof v));
+        HIP_TRY(hipDeviceSynchronize());
+    }
+    return TRK_OK;
+}
+
+extern "C" int trk_set_timing(trk_ctx* c, int on) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    c->timing = on ? 1 : 0;
+    return TRK_OK;
+}
+
+extern "C" int trk_get_timing(trk_ctx* c, const char** names, double* ms, uint64_t* launches, int cap) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    double tot[K_COUNT] = {0};
+    uint64_t cnt[K_COUNT] = {0};
+    for (auto& t : c->timed) {
+        HIP_TRY(hipEventSynchronize(t.stop));
+        float v = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&v, t.start, t.stop));
+        tot[t.kid] += v;
+        cnt[t.kid]++;
+        c->spare.push_back(t.start);
+        c->spare.push_back(t.stop);
+    }
+    c->timed.clear();
+    int n = 0;
+    for (int k = 0; k < K_COUNT; k++) {
+        if (!cnt[k]) continue;
+        if (n < cap) {
+            if (names) names[n] = kKernelNames[k];
+            if (ms) ms[n] = tot[k];
+            if (launches) launches[n] = cnt[k];
+        }
+        n++;
+    }
+    return n;
+}
+
+extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes) {
+    if (!c || !host) return fail(TRK_E_INVALID, "null argument");
+    const Workspace& ws = c->ws;
+    const void* src = nullptr;
+    size_t cap = 0;
+    const size_t M = ws.m_max, rows_x = std::max<size_t>(2, M);
+    switch (which) {
+    case TRK_WS_RLOG: src = ws.rlog; cap = M * ws.E * 4; break;
+    case TRK_WS_IDS: src = ws.ids; cap = M * TRK_MOE_K_MAX * 4; break;
+    case TRK_WS_W: src = ws.w; cap = M * TRK_MOE_K_MAX * 4; break;
+    case TRK_WS_NSEL: src = ws.n_sel; cap = M * 4; break;
+    case TRK_WS_ENT_TOK: src = ws.ent_tok; cap = (size_t)ws.ent_cap * 4; break;
+    case TRK_WS_ENT_W: src = ws.ent_w; cap = (size_t)ws.ent_cap * 4; break;
+    case TRK_WS_ENT_EXP: src = ws.ent_exp; cap = (size_t)ws.ent_cap * 4; break;
+    case TRK_WS_GRP_START: src = ws.grp_start; cap = (ws.E + 2) * 4; break;
+    case TRK_WS_GRP_EXP: src = ws.grp_exp; cap = (ws.E + 1) * 4; break;
+    case TRK_WS_NGROUPS: src = ws.n_groups; cap = 16; break;
+    case TRK_WS_XQ: src = ws.xq; cap = rows_x * ws.H; break;
+    case TRK_WS_XS: src = ws.xs; cap = rows_x * (ws.H / 32) * 4; break;
+    case TRK_WS_ACTQ: src = ws.actq; cap = ws.act_rows * ws.F; break;
+    case TRK_WS_ACTS: src = ws.acts; cap = ws.act_rows * (ws.F / 16) * 4; break;
+    case TRK_WS_SHLOGIT: src = ws.shl; cap = M * 4; break;
+    default: return fail(TRK_E_INVALID, "unknown workspace buffer %d", which);
+    }
+    if (bytes > cap) return fail(TRK_E_INVALID, "read of %zu bytes above the buffer's %zu", bytes, cap);
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
+    return TRK_OK;
+}
+
+// ---- kernel-level entry points --------------------------------------------------------------
+
+extern "C" int trk_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
+                                 uint32_t m, uint32_t n_expert, uint32_t hidden, int gemm_order, float* rlog, float* sh,
+                                 void* stream) {
+    if (!x || (n_expert && (!router || !rlog)) || (shexp_gate && !sh)) return fail(TRK_E_INVALID, "null argument");
+    if (hidden == 0 || hidden % 16) return fail(TRK_E_INVALID, "hidden (%u) must be a positive multiple of 16", hidden);
+    if (m == 0) return TRK_OK;
+    HIP_TRY(launch_router_logits(router, bias, shexp_gate, x, m, n_expert, hidden, gemm_order, rlog, sh,
+                                 (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_route(const float* logits, uint32_t m, uint32_t n_expert, uint32_t k, const trk_moe_policy* p,
+                         uint32_t* ids, float* w, uint32_t* n_sel, void* stream) {
+    if (!logits || !ids || !w || !n_sel) return fail(TRK_E_INVALID, "null argument");
+    if (n_expert == 0 || n_expert > 1024) return fail(TRK_E_INVALID, "n_expert (%u) must be in 1..1024", n_expert);
+    Policy pol{0, 0, 0, 0, 0.0f};
+    if (p) {
+        if (p->min < 1 || p->min > p->max)
+            return fail(TRK_E_POLICY, "moe policy: need 1 <= min (%u) <= max (%u)", p->min, p->max);
+        if (p->max > TRK_MOE_K_MAX || p->max > n_expert)
+            return fail(TRK_E_POLICY, "moe policy: max (%u) above the limit (%u)", p->max,
+                        std::min<uint32_t>(TRK_MOE_K_MAX, n_expert));
+        if (!(p->mass > 0.0f) || p->mass != p->mass)
+            return fail(TRK_E_POLICY, "moe policy: target mass (%g) must be positive", (double)p->mass);
+        pol = Policy{1, p->min, p->max, p->basis, p->mass};
+    } else if (k < 1 || k > TRK_MOE_K_MAX || k > n_expert) {
+        return fail(TRK_E_INVALID, "k (%u) must be in 1..min(32, n_expert)", k);
+    }
+    if (m == 0) return TRK_OK;
+    HIP_TRY(launch_route(logits, m, n_expert, k, pol, ids, w, n_sel, nullptr, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* scale,
+                            int32_t* sum, void* stream) {
+    // QAct::zeros asserts kb in {16, 32} and k % kb == 0 (quant.rs:68-71)
+    if (!x || !q || !scale || !sum) return fail(TRK_E_INVALID, "null argument");
+    if (!(kb == 16 || kb == 32) || k == 0 || k % kb) return fail(TRK_E_INVALID, "need kb in {16,32} and k %% kb == 0");
+    if ((uintptr_t)x % 16 || k % 4) return fail(TRK_E_INVALID, "x must be 16-byte aligned");
+    if (pair && m != 1) return fail(TRK_E_INVALID, "pair quantisation takes one row");
+    if (m == 0) return TRK_OK;
+    HIP_TRY(launch_quantize(x, m, k, kb, pair, q, scale, sum, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_gemv(const trk_mat* w, uint32_t item, uint32_t kb, const int8_t* q, const float* scale,
+                        const int32_t* sum, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
+                        int accumulate, void* stream) {
+    if (!w || !q || !scale || !sum || !y) return fail(TRK_E_INVALID, "null argument");
+    if (!w->ptr || w->k == 0 || w->k % 256 || w->rows == 0) return fail(TRK_E_INVALID, "bad matrix");
+    if (!((w->fmt == TRK_FMT_Q4_K && (kb == 32 || kb == 16)) || (w->fmt == TRK_FMT_Q6_K && kb == 16)))
+        return fail(TRK_E_INVALID, "unsupported (fmt %u, kb %u)", w->fmt, kb);
+    if (item >= (w->count ? w->count : 1)) return fail(TRK_E_INVALID, "item %u out of range", item);
+    if (pair && m % 2) return fail(TRK_E_INVALID, "pair rows come in twos");
+    if (ldy < w->rows && !(m == (pair ? 2u : 1u) && !rows)) return fail(TRK_E_INVALID, "ldy below rows");
+    uint32_t rb = row_bytes(w->fmt, w->k);
+    Mat M{(const uint8_t*)w->ptr, w->count > 1 ? w->stride : (uint64_t)rb * w->rows, w->rows, w->k, w->fmt, rb};
+    if (m == 0) return TRK_OK;
+    HIP_TRY(launch_gemv(M, item, kb, q, scale, sum, m, pair, y, ldy, rows, accumulate, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_swiglu(const float* g, const float* u, float* y, size_t n, void* stream) {
+    if (!g || !u || !y) return fail(TRK_E_INVALID, "null argument");
+    if (n == 0) return TRK_OK;
+    HIP_TRY(launch_swiglu(g, u, y, n, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y, void* stream) {
+    if (!x || !y) return fail(TRK_E_INVALID, "null argument");
+    if (m == 0 || n == 0) return TRK_OK;
+    HIP_TRY(launch_rmsnorm(x, w, eps, m, n, y, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_add_inplace(float* y, const float* a, size_t n, void* stream) {
+    if (!y || !a) return fail(TRK_E_INVALID, "null argument");
+    if (n == 0) return TRK_OK;
+    HIP_TRY(launch_add(y, a, n, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
+                            float dhi, void* out, void* stream) {
+    if (!out) return fail(TRK_E_INVALID, "null argument");
+    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K) || k % 256) return fail(TRK_E_INVALID, "bad format/k");
+    if (rows == 0) return TRK_OK;
+    HIP_TRY(launch_gen_gguf(fmt, seed, stream_id, rows, k, dlo, dhi, out, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float* out, void* stream) {
+    if (!out) return fail(TRK_E_INVALID, "null argument");
+    if (n == 0) return TRK_OK;
+    HIP_TRY(launch_gen_normal(seed, stream_id, n, sigma, out, (hipStream_t)stream));
+    return TRK_OK;
+}

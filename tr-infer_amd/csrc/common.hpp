@@ -1,0 +1,127 @@
+// Device-side building blocks shared by the MoE kernels (gfx950, wave64).
+//
+// Arithmetic follows the reference's CPU path bit for bit: products and sums round on their own
+// (the library is built with -ffp-contract=off), and every FMA of the reference is an explicit
+// __builtin_fmaf here.  Citations are to tokenring-ai/tr-infer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "trmoe_internal.h"
+
+namespace trk {
+
+constexpr int WAVE = 64;
+
+// ---- half precision ------------------------------------------------------------------------
+// f16 bits -> f32 (exact) and f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, h);
+    return (float)v;
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ float f16_round(float f) { return (float)(_Float16)f; }
+
+__device__ __forceinline__ uint16_t ld16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// ---- x86 min/max semantics (maxps(a, b) = a > b ? a : b) --------------------------------------
+__device__ __forceinline__ float mx_ps(float a, float b) { return a > b ? a : b; }
+__device__ __forceinline__ float mn_ps(float a, float b) { return a < b ? a : b; }
+
+// ---- exp / sigmoid / SiLU ------------------------------------------------------------------
+// elem.rs:7-25: clamped degree-6 polynomial exp with a two-part ln2 (tr-infer's own constants).
+__device__ __forceinline__ float exp512(float x) {
+    x = mn_ps(mx_ps(x, -87.3f), 88.3f);
+    float fx = __builtin_rintf(x * 1.442695041f);
+    float r = __builtin_fmaf(-fx, 0.693145752f, x);
+    r = __builtin_fmaf(-fx, 1.42860677e-6f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    float r2 = r * r;
+    p = __builtin_fmaf(p, r2, r);
+    p = p + 1.0f;
+    return __builtin_ldexpf(p, (int)fx);
+}
+// elem.rs:27-38
+__device__ __forceinline__ float sigmoid512(float x) { return 1.0f / (1.0f + exp512(0.0f - x)); }
+__device__ __forceinline__ float silu512(float x) { return x * sigmoid512(x); }
+
+// Rust f32::exp (libm expf): evaluated in double and rounded once to f32.  This is the correctly
+// rounded value except in rare near-tie cases, where libm's expf may land one ulp away.
+__device__ __forceinline__ float expf_libm(float x) { return (float)::exp((double)x); }
+// elem.rs:57-59
+__device__ __forceinline__ float sigmoid_libm(float x) { return 1.0f / (1.0f + expf_libm(-x)); }
+
+// ---- activation quantisation (quant.rs:112-166) --------------------------------------------
+__device__ __forceinline__ int32_t cvt_rne(float v) { return (int32_t)__builtin_rintf(v); }
+__device__ __forceinline__ int8_t sat_i8(int32_t v) { return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v)); }
+
+// Quantise n (16 or 32) values in registers; optionally produce the fnmadd residual.
+template <int N>
+__device__ __forceinline__ void quant_block_regs(const float* x, int8_t* q, float& scale, int32_t& sum,
+                                                 float* resid) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; i++) amax = mx_ps(amax, __builtin_fabsf(x[i]));
+    float s = amax / 127.0f;
+    float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    int32_t su = 0;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        int32_t qi = cvt_rne(x[i] * inv);
+        su += qi;
+        q[i] = sat_i8(qi);
+        if (resid) resid[i] = __builtin_fmaf(-(float)qi, s, x[i]);
+    }
+    scale = s;
+    sum = su;
+}
+
+// ---- _mm512_reduce_add_ps halving tree over 16 lanes ------------------------------------------
+__device__ __forceinline__ float reduce16(const float* v) {
+    float a[8], b[4], c[2];
+#pragma unroll
+    for (int i = 0; i < 8; i++) a[i] = v[i] + v[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) b[i] = a[i] + a[i + 4];
+#pragma unroll
+    for (int i = 0; i < 2; i++) c[i] = b[i] + b[i + 2];
+    return c[0] + c[1];
+}
+
+// Cross-lane version for a value held by lanes j of a 16-lane group (lane j holds element j):
+// returns the tree sum in every lane of the group.
+__device__ __forceinline__ float reduce16_lanes(float v) {
+    v = v + __shfl_xor(v, 8, 16);
+    v = v + __shfl_xor(v, 4, 16);
+    v = v + __shfl_xor(v, 2, 16);
+    v = v + __shfl_xor(v, 1, 16);
+    return v;
+}
+
+// ---- Q4_K / Q6_K superblock decoding ------------------------------------------------------------
+// blocks.py:16-22 (_scale_min_k)
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& sc, int& mn) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[4 + j] & 63;
+    } else {
+        sc = (s[8 + j - 4] & 15) | ((s[j - 4] >> 6) << 4);
+        mn = (s[8 + j - 4] >> 4) | ((s[4 + j - 4] >> 6) << 4);
+    }
+}
+
+// blocks.py:35-36: dd = f16(d*sc), mm = f16(-(dmin*mn)), then widened back to f32 (gemv.rs:104-105)
+__device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, float& dd, float& mm) {
+    dd = f16_round(d * (float)sc);
+    mm = f16_round(-(dmin * (float)mn));
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+}  // namespace trk

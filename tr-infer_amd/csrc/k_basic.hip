@@ -1,0 +1,550 @@
+// Router logits, routing, activation quantisation, the kernel-level GEMV mirror, elementwise
+// kernels and the synthetic-data generators.
+#include "common.hpp"
+
+namespace trk {
+
+// ============================================================================================
+// activation quantisation (quant.rs:36-53, 96-166)
+// ============================================================================================
+
+template <int KB>
+__global__ void quantize_rows_kernel(const float* __restrict__ x, uint32_t m, uint32_t k, int8_t* __restrict__ q,
+                                     float* __restrict__ s, int32_t* __restrict__ su) {
+    uint32_t nb = k / KB;
+    uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= m * nb) return;
+    uint32_t r = idx / nb, b = idx % nb;
+    const float* src = x + (size_t)r * k + (size_t)b * KB;
+    float v[KB];
+#pragma unroll
+    for (int i = 0; i < KB; i += 4) {
+        float4 t = *reinterpret_cast<const float4*>(src + i);
+        v[i] = t.x; v[i + 1] = t.y; v[i + 2] = t.z; v[i + 3] = t.w;
+    }
+    int8_t qq[KB];
+    float sc;
+    int32_t sm;
+    quant_block_regs<KB>(v, qq, sc, sm, nullptr);
+    int8_t* dst = q + (size_t)r * k + (size_t)b * KB;
+#pragma unroll
+    for (int i = 0; i < KB; i++) dst[i] = qq[i];
+    s[idx] = sc;
+    su[idx] = sm;
+}
+
+// quantize_pair_blocks (quant.rs:96-108): row 0 = coarse, row 1 = quantised fnmadd residual
+template <int KB>
+__global__ void quantize_pair_kernel(const float* __restrict__ x, uint32_t k, int8_t* __restrict__ q,
+                                     float* __restrict__ s, int32_t* __restrict__ su) {
+    uint32_t nb = k / KB;
+    uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const float* src = x + (size_t)b * KB;
+    float v[KB], r[KB];
+#pragma unroll
+    for (int i = 0; i < KB; i += 4) {
+        float4 t = *reinterpret_cast<const float4*>(src + i);
+        v[i] = t.x; v[i + 1] = t.y; v[i + 2] = t.z; v[i + 3] = t.w;
+    }
+    int8_t q0[KB], q1[KB];
+    float s0, s1;
+    int32_t m0, m1;
+    quant_block_regs<KB>(v, q0, s0, m0, r);
+    quant_block_regs<KB>(r, q1, s1, m1, nullptr);
+#pragma unroll
+    for (int i = 0; i < KB; i++) {
+        q[(size_t)b * KB + i] = q0[i];
+        q[(size_t)k + (size_t)b * KB + i] = q1[i];
+    }
+    s[b] = s0;
+    su[b] = m0;
+    s[nb + b] = s1;
+    su[nb + b] = m1;
+}
+
+hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* s,
+                           int32_t* su, hipStream_t st) {
+    uint32_t nb = k / kb;
+    if (pair) {
+        dim3 g((nb + 63) / 64);
+        if (kb == 32)
+            quantize_pair_kernel<32><<<g, 64, 0, st>>>(x, k, q, s, su);
+        else
+            quantize_pair_kernel<16><<<g, 64, 0, st>>>(x, k, q, s, su);
+    } else {
+        dim3 g((m * nb + 255) / 256);
+        if (kb == 32)
+            quantize_rows_kernel<32><<<g, 256, 0, st>>>(x, m, k, q, s, su);
+        else
+            quantize_rows_kernel<16><<<g, 256, 0, st>>>(x, m, k, q, s, su);
+    }
+    return hipGetLastError();
+}
+
+// ============================================================================================
+// router logits
+// ============================================================================================
+
+// attn::dot (attn.rs:329-357) with one wave per weight row: lane L = 16c + j is lane j of
+// accumulator chain c, so the wave holds exactly the reference's four 16-lane FMA chains; the
+// 16-wide tail goes into chain 0, then (c0 + c1) + (c2 + c3) lanewise and the halving tree.
+// Rows [0, E) are router rows (+ bias), row E (if shexp_gate) the shared-expert gate.
+constexpr int DOT_MR = 8;
+__global__ void router_dot_kernel(const float* __restrict__ router, const float* __restrict__ bias,
+                                  const float* __restrict__ shg, const float* __restrict__ x, uint32_t m,
+                                  uint32_t E, uint32_t H, float* __restrict__ rlog, float* __restrict__ sh) {
+    uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    uint32_t lane = threadIdx.x % WAVE;
+    uint32_t nrow = E + (shg ? 1u : 0u);
+    if (wave >= nrow) return;
+    const float* wr = wave < E ? router + (size_t)wave * H : shg;
+    for (uint32_t m0 = 0; m0 < m; m0 += DOT_MR) {
+        uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
+        float acc[DOT_MR];
+#pragma unroll
+        for (int r = 0; r < DOT_MR; r++) acc[r] = 0.0f;
+        uint32_t i = 0;
+        for (; i + 64 <= H; i += 64) {
+            float a = wr[i + lane];
+#pragma unroll
+            for (int r = 0; r < DOT_MR; r++)
+                if ((uint32_t)r < mr) acc[r] = __builtin_fmaf(a, x[(size_t)(m0 + r) * H + i + lane], acc[r]);
+        }
+        for (; i + 16 <= H; i += 16) {
+            if (lane < 16) {
+                float a = wr[i + lane];
+#pragma unroll
+                for (int r = 0; r < DOT_MR; r++)
+                    if ((uint32_t)r < mr) acc[r] = __builtin_fmaf(a, x[(size_t)(m0 + r) * H + i + lane], acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < DOT_MR; r++) {
+            if ((uint32_t)r >= mr) break;
+            float c1 = __shfl(acc[r], (lane + 16) & 63);
+            float c2 = __shfl(acc[r], (lane + 32) & 63);
+            float c3 = __shfl(acc[r], (lane + 48) & 63);
+            float v = (acc[r] + c1) + (c2 + c3);
+            float s = reduce16_lanes(v);  // lanes 0..15 hold the tree sum
+            if (lane == 0) {
+                // scalar tail of attn.rs:351-354 (H % 16 != 0 is rejected by the host)
+                if (wave < E) {
+                    if (bias) s = s + bias[wave];
+                    rlog[(size_t)(m0 + r) * E + wave] = s;
+                } else {
+                    sh[m0 + r] = s;
+                }
+            }
+        }
+    }
+}
+
+// smallgemm::gemm_f32_nt (smallgemm.rs:8-59): each output is the halving-tree sum of 16 lane
+// chains, lane l accumulating x[kk + l] * w[kk + l] over kk in steps of 16.  A 16-lane group of
+// the wave plays the 16 lanes of one AVX-512 register; each thread carries 4 rows x 4 experts.
+__global__ void router_gemm_kernel(const float* __restrict__ router, const float* __restrict__ bias,
+                                   const float* __restrict__ x, uint32_t m, uint32_t E, uint32_t H,
+                                   float* __restrict__ rlog) {
+    uint32_t l = threadIdx.x & 15, g = threadIdx.x >> 4;  // 16 groups
+    uint32_t rg = g >> 2, eg = g & 3;
+    uint32_t row0 = blockIdx.y * 16 + rg * 4, e0 = blockIdx.x * 16 + eg * 4;
+    const float* xr[4];
+    const float* wr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        uint32_t rr = row0 + r < m ? row0 + r : m - 1;
+        xr[r] = x + (size_t)rr * H + l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        uint32_t ee = e0 + e < E ? e0 + e : E - 1;
+        wr[e] = router + (size_t)ee * H + l;
+    }
+    float acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[r][e] = 0.0f;
+    for (uint32_t kk = 0; kk < H; kk += 16) {
+        float xv[4], wv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) xv[r] = xr[r][kk];
+#pragma unroll
+        for (int e = 0; e < 4; e++) wv[e] = wr[e][kk];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[r][e] = __builtin_fmaf(xv[r], wv[e], acc[r][e]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float s = reduce16_lanes(acc[r][e]);
+            if (l == (uint32_t)(r * 4 + e) && row0 + r < m && e0 + e < E) {
+                if (bias) s = s + bias[e0 + e];
+                rlog[(size_t)(row0 + r) * E + e0 + e] = s;
+            }
+        }
+}
+
+hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
+                                uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
+                                hipStream_t st) {
+    if (!gemm_order) {
+        uint32_t nrow = E + (shexp_gate ? 1 : 0);
+        router_dot_kernel<<<(nrow + 3) / 4, 256, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh);
+    } else {
+        dim3 g((E + 15) / 16, (m + 15) / 16);
+        router_gemm_kernel<<<g, 256, 0, st>>>(router, bias, x, m, E, H, rlog);
+        if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
+            router_dot_kernel<<<1, 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh);
+    }
+    return hipGetLastError();
+}
+
+// ============================================================================================
+// routing (router.rs:70-148): one wave per token
+// ============================================================================================
+
+constexpr int ROUTE_MAXJ = 16;  // E <= 1024
+__global__ void route_kernel(const float* __restrict__ logits, uint32_t m, uint32_t E, uint32_t k, Policy pol,
+                             uint32_t* __restrict__ ids, float* __restrict__ wout, uint32_t* __restrict__ n_sel,
+                             unsigned long long* __restrict__ stats) {
+    extern __shared__ float ex_all[];  // [waves][E] for MassBasis::All
+    uint32_t wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    uint32_t row = blockIdx.x * (blockDim.x / WAVE) + wv;
+    if (row >= m) return;
+    const float* lg = logits + (size_t)row * E;
+    float v[ROUTE_MAXJ];
+    uint32_t nj = (E + 63) / 64;
+#pragma unroll
+    for (int j = 0; j < ROUTE_MAXJ; j++) {
+        uint32_t i = lane + 64u * j;
+        v[j] = ((uint32_t)j < nj && i < E) ? lg[i] : -__builtin_inff();
+    }
+    uint32_t kk = pol.enabled ? pol.max : k;
+    // topk_sorted: the k largest under (value desc, index asc); values that are not > -inf
+    // (nan, -inf) never enter, and unfilled slots keep (-inf, u32::MAX).
+    float my_tv = -__builtin_inff();
+    uint32_t my_ti = 0xffffffffu;
+    uint32_t taken = 0;
+    for (uint32_t rd = 0; rd < kk; rd++) {
+        float bv = -__builtin_inff();
+        uint32_t bi = 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < ROUTE_MAXJ; j++) {
+            uint32_t i = lane + 64u * j;
+            if (!((taken >> j) & 1u) && v[j] > -__builtin_inff() && (v[j] > bv || (v[j] == bv && i < bi))) {
+                bv = v[j];
+                bi = i;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            float ov = __shfl_xor(bv, off);
+            uint32_t oi = __shfl_xor(bi, off);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi != 0xffffffffu && bi % 64u == lane) taken |= 1u << (bi / 64u);
+        if (lane == rd) {
+            my_tv = bv;
+            my_ti = bi;
+        }
+    }
+    float mx = __shfl(my_tv, 0);
+    float e = lane < kk ? expf_libm(my_tv - mx) : 0.0f;
+    uint32_t count = kk;
+    if (pol.enabled) {
+        float denom = 0.0f;
+        if (pol.basis == TRK_BASIS_ALL) {
+            float* ea = ex_all + (size_t)wv * E;
+#pragma unroll
+            for (int j = 0; j < ROUTE_MAXJ; j++) {
+                uint32_t i = lane + 64u * j;
+                if ((uint32_t)j < nj && i < E) ea[i] = expf_libm(lg[i] - mx);
+            }
+            // make the wave's LDS writes visible to all its lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (uint32_t i = 0; i < E; i++) denom += ea[i];
+        } else {
+            for (uint32_t j = 0; j < kk; j++) denom += __shfl(e, j);
+        }
+        float mass = 0.0f;
+        count = 0;
+        while (count < kk) {
+            mass += __shfl(e, count) / denom;
+            count++;
+            if (count >= pol.min && mass >= pol.mass) break;
+        }
+    }
+    // Fewer than `count` selectable logits (nan / -inf rows): the reference would index expert
+    // u32::MAX; here the selection stops at the valid ids (they are a prefix of the rounds).
+    const uint32_t nvalid = (uint32_t)__popcll(__ballot(lane < kk && my_ti != 0xffffffffu));
+    if (count > nvalid) count = nvalid;
+    // renorm (router.rs:93-104)
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < count; j++) sum += __shfl(e, j);
+    if (lane < count) {
+        ids[(size_t)row * K_MAX + lane] = my_ti;
+        wout[(size_t)row * K_MAX + lane] = e / sum;
+    }
+    if (lane == 0) {
+        n_sel[row] = count;
+        if (stats) {
+            atomicAdd(&stats[0], 1ull);
+            atomicAdd(&stats[1], (unsigned long long)count);
+        }
+    }
+}
+
+hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
+                        float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st) {
+    const uint32_t waves = 4;
+    size_t lds = (pol.enabled && pol.basis == TRK_BASIS_ALL) ? (size_t)waves * E * sizeof(float) : 0;
+    route_kernel<<<(m + waves - 1) / waves, waves * WAVE, lds, st>>>(logits, m, E, k, pol, ids, w, n_sel, stats);
+    return hipGetLastError();
+}
+
+// ============================================================================================
+// kernel-level GEMV mirror (gemv.rs:25-78) on GGUF rows: one thread per (output row, logical
+// activation row), blocks in ascending order with the per-block epilogue of gemv.rs:141-148.
+// Reference semantics, not a fast path.
+// ============================================================================================
+
+__device__ __forceinline__ void block_dm(const uint8_t* wrow, uint32_t fmt, int kb, int b, float& dd, float& mm) {
+    if (fmt == TRK_FMT_Q4_K) {
+        int j32 = kb == 32 ? b : b / 2;
+        const uint8_t* hdr = wrow + (size_t)(j32 / 8) * 144;
+        int sc, mn;
+        q4k_scale_min(hdr + 4, j32 % 8, sc, mn);
+        q4k_dm(h2f(ld16(hdr)), h2f(ld16(hdr + 2)), sc, mn, dd, mm);
+    } else {  // Q6_K, kb = 16
+        const uint8_t* sbp = wrow + (size_t)(b / 16) * 210;
+        float d = h2f(ld16(sbp + 208));
+        int8_t sc = (int8_t)sbp[192 + b % 16];
+        dd = f16_round(d * (float)sc);
+        mm = f16_round(-32.0f * dd);
+    }
+}
+
+__device__ __forceinline__ int block_q(const uint8_t* wrow, uint32_t fmt, int kb, int b, int i) {
+    if (fmt == TRK_FMT_Q4_K) {
+        int e = b * kb + i;  // element index in the row
+        int sb = e / 256, j = (e % 256) / 32, ii = e % 32;
+        const uint8_t* qs = wrow + (size_t)sb * 144 + 16;
+        uint8_t byte = qs[(j / 2) * 32 + ii];
+        return (j & 1) ? (byte >> 4) : (byte & 15);
+    }
+    int e = b * kb + i;
+    int sb = e / 256, r = e % 256;
+    int n = r / 128, g = (r % 128) / 32, l = r % 32;
+    const uint8_t* p = wrow + (size_t)sb * 210;
+    uint8_t lo = p[64 * n + l + ((g & 1) ? 32 : 0)];
+    int nib = (g >> 1) ? (lo >> 4) : (lo & 15);
+    int hi = (p[128 + 32 * n + l] >> (2 * g)) & 3;
+    return nib | (hi << 4);
+}
+
+__global__ void gemv_mirror_kernel(Mat w, uint32_t item, uint32_t kb, const int8_t* __restrict__ q,
+                                   const float* __restrict__ s, const int32_t* __restrict__ su, uint32_t m,
+                                   int pair, float* __restrict__ y, uint32_t ldy, const uint32_t* __restrict__ rows,
+                                   int accumulate) {
+    uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t logical = blockIdx.y;
+    if (r >= w.rows) return;
+    const uint8_t* wrow = w.ptr + (size_t)item * w.stride + (size_t)r * w.row_bytes;
+    uint32_t K = w.k, nb = K / kb, per = pair ? 2 : 1;
+    float acc[2] = {0.0f, 0.0f};
+    for (uint32_t b = 0; b < nb; b++) {
+        float dd, mm;
+        block_dm(wrow, w.fmt, kb, b, dd, mm);
+        for (uint32_t p = 0; p < per; p++) {
+            uint32_t mi = logical * per + p;
+            const int8_t* xp = q + (size_t)mi * K + (size_t)b * kb;
+            int dot = 0;
+            for (uint32_t i = 0; i < kb; i++) dot += block_q(wrow, w.fmt, kb, b, i) * (int)xp[i];
+            float sx = s[(size_t)mi * nb + b];
+            float u = sx * (float)su[(size_t)mi * nb + b];
+            float t = dd * sx;
+            acc[p] = __builtin_fmaf(mm, u, acc[p]);
+            acc[p] = __builtin_fmaf((float)dot, t, acc[p]);
+        }
+    }
+    float v = pair ? acc[0] + acc[1] : acc[0];
+    size_t yr = rows ? rows[logical] : logical;
+    float* yp = y + yr * ldy + r;
+    *yp = accumulate ? *yp + v : v;
+}
+
+hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t kb, const int8_t* q, const float* s,
+                       const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
+                       int accumulate, hipStream_t st) {
+    uint32_t logical = pair ? m / 2 : m;
+    // rows of one call go in sequence so that a row map with repeats accumulates in order
+    for (uint32_t i = 0; i < logical; i++) {
+        dim3 g((w.rows + 127) / 128, 1);
+        const int8_t* qi = q + (size_t)i * (pair ? 2 : 1) * w.k;
+        const float* si = s + (size_t)i * (pair ? 2 : 1) * (w.k / kb);
+        const int32_t* sui = su + (size_t)i * (pair ? 2 : 1) * (w.k / kb);
+        const uint32_t* ri = rows ? rows + i : nullptr;
+        float* yi = rows ? y : y + (size_t)i * ldy;
+        gemv_mirror_kernel<<<g, 128, 0, st>>>(w, item, kb, qi, si, sui, pair ? 2 : 1, pair, yi, ldy, ri, accumulate);
+    }
+    return hipGetLastError();
+}
+
+// ============================================================================================
+// elementwise (elem.rs)
+// ============================================================================================
+
+// swiglu_vec via zip16 (elem.rs:173-175, 209-221): silu512 on full 16-blocks, scalar silu on the
+// tail.
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                              size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    size_t body = n / 16 * 16;
+    float gv = g[i];
+    y[i] = (i < body ? silu512(gv) : gv * sigmoid_libm(gv)) * u[i];
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st) {
+    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g, u, y, n);
+    return hipGetLastError();
+}
+
+// rmsnorm (elem.rs:255-262) with sumsq (elem.rs:224-252) in the dot order: one wave per row.
+__global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps, uint32_t m,
+                               uint32_t n, float* __restrict__ y) {
+    uint32_t row = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    uint32_t lane = threadIdx.x % WAVE;
+    if (row >= m) return;
+    const float* xr = x + (size_t)row * n;
+    float acc = 0.0f;
+    uint32_t i = 0;
+    for (; i + 64 <= n; i += 64) {
+        float a = xr[i + lane];
+        acc = __builtin_fmaf(a, a, acc);
+    }
+    for (; i + 16 <= n; i += 16)
+        if (lane < 16) {
+            float a = xr[i + lane];
+            acc = __builtin_fmaf(a, a, acc);
+        }
+    float c1 = __shfl(acc, (lane + 16) & 63), c2 = __shfl(acc, (lane + 32) & 63), c3 = __shfl(acc, (lane + 48) & 63);
+    float s = reduce16_lanes((acc + c1) + (c2 + c3));
+    s = __shfl(s, 0);
+    for (; i < n; i++) s += xr[i] * xr[i];
+    float r = 1.0f / __builtin_sqrtf(s / (float)n + eps);
+    for (uint32_t j = lane; j < n; j += WAVE) y[(size_t)row * n + j] = w ? (xr[j] * r) * w[j] : xr[j] * r;
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
+                          hipStream_t st) {
+    rmsnorm_kernel<<<(m + 3) / 4, 256, 0, st>>>(x, w, eps, m, n, y);
+    return hipGetLastError();
+}
+
+__global__ void add_kernel(float* __restrict__ y, const float* __restrict__ a, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = y[i] + a[i];
+}
+
+hipError_t launch_add(float* y, const float* a, size_t n, hipStream_t st) {
+    add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(y, a, n);
+    return hipGetLastError();
+}
+
+// ============================================================================================
+// synthetic data: the test oracle's counter-based generator, bit for bit
+// ============================================================================================
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t rng_u64(uint64_t key, uint64_t idx) { return mix64(key + idx * 0xd1b54a32d192ed03ull); }
+__device__ __forceinline__ float unif24(uint64_t r, float lo, float hi) {
+    float u = (float)(uint32_t)(r & 0xffffffu) * (1.0f / 16777216.0f);
+    float span = hi - lo;
+    float p = u * span;
+    return lo + p;
+}
+
+// one thread per 8-byte word of a superblock (18 words for Q4_K, 27 for Q6_K)
+__global__ void gen_gguf_kernel(uint32_t fmt, uint64_t key, size_t nsb, float dlo, float dhi, uint8_t* out) {
+    size_t sbb = fmt == TRK_FMT_Q6_K ? 210 : 144;
+    size_t nw = (sbb + 7) / 8;
+    size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nsb * nw) return;
+    size_t sb = t / nw, wi = t % nw;
+    uint8_t* b = out + sb * sbb;
+    uint64_t r = rng_u64(key, sb * 32 + wi);
+    uint64_t rd = rng_u64(key, sb * 32 + 31);
+    for (int j = 0; j < 8; j++) {
+        size_t o = wi * 8 + j;
+        if (o >= sbb) break;
+        uint8_t v = (uint8_t)(r >> (8 * j));
+        if (fmt == TRK_FMT_Q6_K) {
+            if (o == 208 || o == 209) {
+                uint16_t d = f2h(unif24(rd, dlo, dhi));
+                v = o == 208 ? (uint8_t)(d & 0xff) : (uint8_t)(d >> 8);
+            }
+        } else if (o < 4) {
+            uint16_t d = f2h(unif24(o < 2 ? rd : rd >> 24, dlo, dhi));
+            v = (o & 1) ? (uint8_t)(d >> 8) : (uint8_t)(d & 0xff);
+        }
+        b[o] = v;
+    }
+}
+
+hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
+                           float dhi, void* out, hipStream_t st) {
+    // key = mix64(seed ^ mix64(stream)), as orc_rng_u64
+    auto hmix = [](uint64_t z) {
+        z += 0x9e3779b97f4a7c15ull;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    };
+    uint64_t key = hmix(seed ^ hmix(stream_id));
+    size_t nsb = (size_t)rows * (k / 256);
+    size_t nw = fmt == TRK_FMT_Q6_K ? 27 : 18;
+    size_t n = nsb * nw;
+    gen_gguf_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(fmt, key, nsb, dlo, dhi, (uint8_t*)out);
+    return hipGetLastError();
+}
+
+__global__ void gen_normal_kernel(uint64_t key, size_t n, double sigma, float* out) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint64_t a = rng_u64(key, 2 * i), b = rng_u64(key, 2 * i + 1);
+    double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+    double z = ::sqrt(-2.0 * ::log(u1)) * ::cos(6.283185307179586 * u2);
+    out[i] = (float)(z * sigma);
+}
+
+hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float* out,
+                             hipStream_t st) {
+    auto hmix = [](uint64_t z) {
+        z += 0x9e3779b97f4a7c15ull;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    };
+    uint64_t key = hmix(seed ^ hmix(stream_id));
+    gen_normal_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(key, n, sigma, out);
+    return hipGetLastError();
+}
+
+}  // namespace trk

@@ -1,0 +1,95 @@
+// Internal interfaces between the C ABI (abi.cpp) and the kernel translation units (*.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/trmoe.h"
+
+namespace trk {
+
+constexpr int K_MAX = TRK_MOE_K_MAX;
+constexpr int SH_SLOT = K_MAX;  // decode: the shared expert's activation slot (after 32 routed)
+
+// Routing policy as the kernels take it (enabled == 0: fixed top-k).
+struct Policy {
+    uint32_t enabled, min, max, basis;
+    float mass;
+};
+
+// A weight stack as the kernels take it.
+struct Mat {
+    const uint8_t* ptr;
+    uint64_t stride;  // bytes between experts
+    uint32_t rows, k, fmt;
+    uint32_t row_bytes;
+};
+
+// Grouped-GEMM work item: `nrows` entry rows starting at `row0` of the sorted entries, all of
+// expert `expert` (expert == 0xffffffff: the shared expert, rows are tokens).
+struct Item {
+    uint32_t expert, row0, nrows, pad;
+};
+
+// Device workspace (sized at trk_create).
+struct Workspace {
+    uint32_t H, E, F, m_max, k_cap, ent_cap, item_cap;
+    int8_t* xq;           // [max(2, m_max)][H]
+    float* xs;            // [max(2, m_max)][H/32]
+    int32_t* xsum;
+    float* xn;            // [m_max][H]: normed input (config-5 layers)
+    float* rlog;          // [m_max][E]
+    float* shl;           // [m_max]: shared-gate logits
+    uint32_t* ids;        // [m_max][32]
+    float* w;             // [m_max][32]
+    uint32_t* n_sel;      // [m_max]
+    uint32_t* ent_tok;    // [ent_cap]
+    float* ent_w;
+    uint32_t* ent_exp;
+    uint32_t* ent_of;     // [m_max][32]: entry index of (token, slot)
+    uint32_t* grp_start;  // [E + 2]
+    uint32_t* grp_exp;    // [E + 1]
+    uint32_t* n_groups;   // [4]: n_groups, n_ent, n_items, pad
+    uint32_t* chunk_cnt;  // dispatch scratch: [chunks][E]
+    Item* items;          // [item_cap]
+    int8_t* actq;         // [act_rows][F] (decode: [33][2][F])
+    float* acts;          // [act_rows][F/16]
+    int32_t* actsum;
+    float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
+    float* out_tmp;       // [m_max][H]
+    unsigned long long* stats;  // [2] rows, experts
+    size_t act_rows;
+};
+
+// ---- launchers (return hipError_t of the launch) ----
+hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* s,
+                           int32_t* su, hipStream_t st);
+hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
+                                uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
+                                hipStream_t st);
+hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
+                        float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
+hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
+                                const Workspace& ws, int pair, uint32_t kcap, hipStream_t st);
+hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
+                              uint32_t kcap, float* out, int residual, hipStream_t st);
+hipError_t launch_dispatch(const Workspace& ws, uint32_t m, hipStream_t st);
+hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
+                               const Workspace& ws, uint32_t m, hipStream_t st);
+hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m,
+                             hipStream_t st);
+hipError_t launch_batch_combine(const Workspace& ws, uint32_t m, float* out, int residual, hipStream_t st);
+hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t kb, const int8_t* q, const float* s,
+                       const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
+                       int accumulate, hipStream_t st);
+hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st);
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
+                          hipStream_t st);
+hipError_t launch_add(float* y, const float* a, size_t n, hipStream_t st);
+hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k,
+                           float dlo, float dhi, void* out, hipStream_t st);
+hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float* out,
+                             hipStream_t st);
+
+}  // namespace trk

@@ -1,0 +1,314 @@
+"""Python host side of the trmoe C ABI (include/trmoe.h) — ctypes bindings plus a small layer
+object that keeps one MoE layer's weights in HBM.
+
+This mirrors the reference's Rust call sites (tr_model::exec::Model::moe_block /
+exec_batch::moe_batch) for tests and the benchmark; device memory and streams come from torch.
+There is no CPU fallback: without the built HIP library every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG_ROOT, "libtrmoe.so")
+HEADER = os.path.join(os.path.dirname(PKG_ROOT), "include", "trmoe.h")
+
+FMT_Q4_K, FMT_Q6_K = 12, 14
+BASIS_ALL, BASIS_TOP = 0, 1
+K_MAX = 32
+(WS_RLOG, WS_IDS, WS_W, WS_NSEL, WS_ENT_TOK, WS_ENT_W, WS_ENT_EXP, WS_GRP_START, WS_GRP_EXP, WS_NGROUPS, WS_XQ,
+ WS_XS, WS_ACTQ, WS_ACTS, WS_SHLOGIT) = range(1, 16)
+
+
+class TrkError(RuntimeError):
+    pass
+
+
+class Mat(C.Structure):
+    _fields_ = [("ptr", C.c_void_p), ("rows", C.c_uint32), ("k", C.c_uint32), ("fmt", C.c_uint32),
+                ("count", C.c_uint32), ("stride", C.c_uint64)]
+
+
+class MoeW(C.Structure):
+    _fields_ = [("router", C.c_void_p), ("router_bias", C.c_void_p), ("shexp_gate", C.c_void_p),
+                ("gate", Mat), ("up", Mat), ("down", Mat), ("sh_gate", Mat), ("sh_up", Mat), ("sh_down", Mat)]
+
+
+class Policy(C.Structure):
+    _fields_ = [("min", C.c_uint32), ("max", C.c_uint32), ("mass", C.c_float), ("basis", C.c_uint32)]
+
+
+class Cfg(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("n_expert", C.c_uint32), ("n_ff", C.c_uint32),
+                ("n_expert_used", C.c_uint32), ("m_max", C.c_uint32), ("k_cap", C.c_uint32),
+                ("router_dot_max_m", C.c_uint32), ("hiprec", C.c_int32)]
+
+
+class Stats(C.Structure):
+    _fields_ = [("rows", C.c_uint64), ("experts", C.c_uint64)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libtrmoe.so (built by `make -C tr-infer_amd` / __graft_entry__.build())."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TrkError(f"{LIB_PATH} is not built: run __graft_entry__.build() (make -C tr-infer_amd)")
+        L = C.CDLL(LIB_PATH)
+        vp, u32, u64, i, f, sz = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_size_t
+        L.trk_last_error.restype = C.c_char_p
+        L.trk_create.argtypes = [C.POINTER(Cfg), C.POINTER(vp)]
+        L.trk_destroy.argtypes = [vp]
+        L.trk_set_moe.argtypes = [vp, C.POINTER(Policy)]
+        L.trk_moe_forward.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, vp]
+        L.trk_moe_residual.argtypes = [vp, C.POINTER(MoeW), vp, f, vp, u32, vp]
+        L.trk_get_stats.argtypes = [vp, C.POINTER(Stats), i]
+        L.trk_router_logits.argtypes = [vp, vp, vp, vp, u32, u32, u32, i, vp, vp, vp]
+        L.trk_route.argtypes = [vp, u32, u32, u32, C.POINTER(Policy), vp, vp, vp, vp]
+        L.trk_quantize.argtypes = [vp, u32, u32, u32, i, vp, vp, vp, vp]
+        L.trk_gemv.argtypes = [C.POINTER(Mat), u32, u32, vp, vp, vp, u32, i, vp, u32, vp, i, vp]
+        L.trk_swiglu.argtypes = [vp, vp, vp, sz, vp]
+        L.trk_rmsnorm.argtypes = [vp, vp, f, u32, u32, vp, vp]
+        L.trk_add_inplace.argtypes = [vp, vp, sz, vp]
+        L.trk_gen_gguf.argtypes = [u32, u64, u64, u32, u32, f, f, vp, vp]
+        L.trk_gen_normal.argtypes = [u64, u64, sz, C.c_double, vp, vp]
+        L.trk_debug_read.argtypes = [vp, i, vp, sz]
+        L.trk_set_timing.argtypes = [vp, i]
+        L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise TrkError(f"trmoe error {rc}: {lib().trk_last_error().decode()}")
+
+
+def header_functions() -> list[str]:
+    """Names of the functions include/trmoe.h declares."""
+    import re
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(trk_\w+)\s*\(", txt, re.M)))
+
+
+def row_bytes(fmt: int, k: int) -> int:
+    return k // 256 * (144 if fmt == FMT_Q4_K else 210)
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class Context:
+    """trk_create/trk_destroy around one layer shape (Model::load_with's workspace sizing)."""
+
+    def __init__(self, hidden, n_expert, n_ff, k, m_max, k_cap=0, router_dot_max_m=16, hiprec=True):
+        self.cfg = Cfg(hidden, n_expert, n_ff, k, m_max, k_cap, router_dot_max_m, int(hiprec))
+        h = C.c_void_p()
+        check(lib().trk_create(C.byref(self.cfg), C.byref(h)))
+        self.h = h
+        self.k = k
+
+    def close(self):
+        if self.h:
+            lib().trk_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_moe(self, policy):
+        """policy: None or (min, max, mass, basis) (Model::set_moe)."""
+        if policy is None:
+            check(lib().trk_set_moe(self.h, None))
+        else:
+            p = Policy(*policy)
+            check(lib().trk_set_moe(self.h, C.byref(p)))
+
+    def forward(self, w: "LayerWeights", x, out, rlog=None, stream=None):
+        check(lib().trk_moe_forward(self.h, C.byref(w.moew), _ptr(x), _ptr(rlog), x.shape[0], _ptr(out),
+                                    _stream(stream)))
+
+    def residual(self, w: "LayerWeights", rms_w, eps, h, stream=None):
+        check(lib().trk_moe_residual(self.h, C.byref(w.moew), _ptr(rms_w), eps, _ptr(h), h.shape[0], _stream(stream)))
+
+    def stats(self, reset=False):
+        s = Stats()
+        check(lib().trk_get_stats(self.h, C.byref(s), int(reset)))
+        return s.rows, s.experts
+
+    def set_timing(self, on: bool):
+        check(lib().trk_set_timing(self.h, int(on)))
+
+    def timing(self):
+        """{kernel: (total ms, launches)} since the last call (synchronises)."""
+        cap = 16
+        names = (C.c_char_p * cap)()
+        ms = (C.c_double * cap)()
+        cnt = (C.c_uint64 * cap)()
+        n = lib().trk_get_timing(self.h, names, ms, cnt, cap)
+        if n < 0:
+            check(n)
+        return {names[i].decode(): (ms[i], int(cnt[i])) for i in range(min(n, cap))}
+
+    def read(self, which, nbytes, dtype):
+        import numpy as np
+        buf = np.zeros(nbytes, np.uint8)
+        check(lib().trk_debug_read(self.h, which, buf.ctypes.data_as(C.c_void_p), nbytes))
+        return buf.view(dtype)
+
+
+class LayerWeights:
+    """One layer's weights resident on the GPU: expert stacks [E][rows*row_bytes] as uint8 tensors."""
+
+    def __init__(self, H, E, F, router, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, gate_fmt=FMT_Q4_K,
+                 down_fmt=FMT_Q4_K, router_bias=None):
+        self.H, self.E, self.F = H, E, F
+        self.tensors = dict(router=router, shexp_gate=shexp_gate, gate=gate, up=up, down=down, sh_gate=sh_gate,
+                            sh_up=sh_up, sh_down=sh_down, router_bias=router_bias)
+        gb, db = row_bytes(gate_fmt, H), row_bytes(down_fmt, F)
+
+        def mat(t, rows, k, fmt, count, rb):
+            return Mat(t.data_ptr(), rows, k, fmt, count, rows * rb)
+
+        self.moew = MoeW(router.data_ptr() if router is not None else None,
+                         router_bias.data_ptr() if router_bias is not None else None, shexp_gate.data_ptr(),
+                         mat(gate, F, H, gate_fmt, E, gb), mat(up, F, H, gate_fmt, E, gb), mat(down, H, F, down_fmt, E, db),
+                         mat(sh_gate, F, H, gate_fmt, 1, gb), mat(sh_up, F, H, gate_fmt, 1, gb),
+                         mat(sh_down, H, F, down_fmt, 1, db))
+        self.bytes_per_expert = 2 * F * gb + H * db
+
+    @classmethod
+    def from_host(cls, layer, device="cuda"):
+        """Upload a host-side layer (raw GGUF bytes; see tests/layerdata.py)."""
+        import numpy as np
+        import torch
+
+        def dev(a, dtype=None):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        return cls(layer.H, layer.E, layer.F, dev(layer.router), dev(layer.shexp_gate), dev(layer.stacked("gate")),
+                   dev(layer.stacked("up")), dev(layer.stacked("down")), dev(layer.sh_gate), dev(layer.sh_up),
+                   dev(layer.sh_down), layer.gate_fmt, layer.down_fmt,
+                   None if layer.bias is None else dev(layer.bias))
+
+    @classmethod
+    def generate(cls, seed, layer, H, E, F, down_fmt=FMT_Q4_K, router_bias=None, device="cuda", stream=None):
+        """Synthesise a layer on the GPU with the same generator the test oracle uses."""
+        import torch
+        gb, db = row_bytes(FMT_Q4_K, H), row_bytes(down_fmt, F)
+        L = lib()
+        st = _stream(stream)
+
+        def sid(t):
+            return (layer << 32) | t
+
+        router = torch.empty(E * H, dtype=torch.float32, device=device)
+        check(L.trk_gen_normal(seed, sid(1), E * H, 0.02, _ptr(router), st))
+        shg = torch.empty(H, dtype=torch.float32, device=device)
+        check(L.trk_gen_normal(seed, sid(2), H, 0.02, _ptr(shg), st))
+        gate = torch.empty((E, F * gb), dtype=torch.uint8, device=device)
+        up = torch.empty((E, F * gb), dtype=torch.uint8, device=device)
+        down = torch.empty((E, H * db), dtype=torch.uint8, device=device)
+        for e in range(E):
+            check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(16 + 3 * e), F, H, 1e-4, 2e-3, C.c_void_p(gate[e].data_ptr()), st))
+            check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(17 + 3 * e), F, H, 1e-4, 2e-3, C.c_void_p(up[e].data_ptr()), st))
+            check(L.trk_gen_gguf(down_fmt, seed, sid(18 + 3 * e), H, F, 1e-4, 2e-3, C.c_void_p(down[e].data_ptr()), st))
+        sh_gate = torch.empty(F * gb, dtype=torch.uint8, device=device)
+        sh_up = torch.empty(F * gb, dtype=torch.uint8, device=device)
+        sh_down = torch.empty(H * db, dtype=torch.uint8, device=device)
+        check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(8), F, H, 1e-4, 2e-3, _ptr(sh_gate), st))
+        check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(9), F, H, 1e-4, 2e-3, _ptr(sh_up), st))
+        check(L.trk_gen_gguf(down_fmt, seed, sid(10), H, F, 1e-4, 2e-3, _ptr(sh_down), st))
+        return cls(H, E, F, router, shg, gate, up, down, sh_gate, sh_up, sh_down, FMT_Q4_K, down_fmt, router_bias)
+
+
+# ---- kernel-level wrappers (torch tensors on the GPU) ----------------------------------------
+
+def quantize(x, kb, pair=False, stream=None):
+    import torch
+    m, k = (1, x.numel()) if pair else x.shape
+    rows = 2 if pair else m
+    q = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((rows, k // kb), dtype=torch.float32, device=x.device)
+    su = torch.empty((rows, k // kb), dtype=torch.int32, device=x.device)
+    check(lib().trk_quantize(_ptr(x), m, k, kb, int(pair), _ptr(q), _ptr(s), _ptr(su), _stream(stream)))
+    return q, s, su
+
+
+def router_logits(router, x, bias=None, shexp_gate=None, gemm_order=False, stream=None):
+    import torch
+    m, H = x.shape
+    E = router.shape[0] if router is not None else 0
+    rlog = torch.empty((m, max(E, 1)), dtype=torch.float32, device=x.device)
+    sh = torch.empty(m, dtype=torch.float32, device=x.device)
+    check(lib().trk_router_logits(_ptr(router), _ptr(bias), _ptr(shexp_gate), _ptr(x), m, E, H, int(gemm_order),
+                                  _ptr(rlog), _ptr(sh), _stream(stream)))
+    return rlog[:, :E], sh
+
+
+def route(logits, k, policy=None, stream=None):
+    import torch
+    m, E = logits.shape
+    ids = torch.zeros((m, K_MAX), dtype=torch.int32, device=logits.device)
+    w = torch.zeros((m, K_MAX), dtype=torch.float32, device=logits.device)
+    n = torch.zeros(m, dtype=torch.int32, device=logits.device)
+    p = C.byref(Policy(*policy)) if policy is not None else None
+    check(lib().trk_route(_ptr(logits), m, E, k, p, _ptr(ids), _ptr(w), _ptr(n), _stream(stream)))
+    return ids, w, n
+
+
+def gemv(wt, rows, k, fmt, item, count, kb, q, s, su, pair=False, y=None, ldy=None, rowmap=None, accumulate=False,
+         stream=None):
+    import torch
+    m = q.shape[0]
+    logical = m // 2 if pair else m
+    if y is None:
+        y = torch.zeros((logical, rows), dtype=torch.float32, device=q.device)
+    mat = Mat(wt.data_ptr(), rows, k, fmt, count, rows * row_bytes(fmt, k))
+    check(lib().trk_gemv(C.byref(mat), item, kb, _ptr(q), _ptr(s), _ptr(su), m, int(pair), _ptr(y),
+                         ldy if ldy is not None else rows, _ptr(rowmap), int(accumulate), _stream(stream)))
+    return y
+
+
+def swiglu(g, u, stream=None):
+    import torch
+    y = torch.empty_like(g)
+    check(lib().trk_swiglu(_ptr(g), _ptr(u), _ptr(y), g.numel(), _stream(stream)))
+    return y
+
+
+def rmsnorm(x, w, eps, stream=None):
+    import torch
+    y = torch.empty_like(x)
+    m, n = x.shape
+    check(lib().trk_rmsnorm(_ptr(x), _ptr(w), eps, m, n, _ptr(y), _stream(stream)))
+    return y
+
+
+def gen_gguf(fmt, seed, stream_id, rows, k, dlo=1e-4, dhi=2e-3, device="cuda", stream=None):
+    import torch
+    out = torch.empty(rows * row_bytes(fmt, k), dtype=torch.uint8, device=device)
+    check(lib().trk_gen_gguf(fmt, seed, stream_id, rows, k, dlo, dhi, _ptr(out), _stream(stream)))
+    return out
+
+
+def gen_normal(seed, stream_id, n, sigma=1.0, device="cuda", stream=None):
+    import torch
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    check(lib().trk_gen_normal(seed, stream_id, n, sigma, _ptr(out), _stream(stream)))
+    return out
