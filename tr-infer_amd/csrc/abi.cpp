@@ -40,9 +40,9 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 }  // namespace
 
 // Kernel ids for trk_get_timing.
-enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
+enum KernelId { K_LOGITS, K_ROUTE, K_ROUTER_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
                 K_RMSNORM, K_COUNT };
-static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
+static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "router_route", "quantize", "decode_gateup",
                                                   "decode_down", "dispatch", "batch_gateup", "batch_down",
                                                   "batch_combine", "rmsnorm"};
 
@@ -104,7 +104,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
     ws.m_max = cfg->m_max;
     ws.k_cap = k_cap;
     ws.ent_cap = (uint32_t)(M * k_cap);
-    ws.item_cap = E + (ws.ent_cap + 7) / 8 + (uint32_t)((M + 7) / 8) + 1;
+    ws.item_cap = E + (ws.ent_cap + 63) / 64 + (uint32_t)((M + 63) / 64) + 1;  // items of <= 64 rows
     ws.act_rows = std::max<size_t>((size_t)(TRK_MOE_K_MAX + 1) * 2, (size_t)ws.ent_cap + M);
 
     // carve one allocation (256-byte aligned pieces)
@@ -117,6 +117,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.xq, rows_x * H},
         {(void**)&ws.xs, rows_x * (H / 32) * 4},
         {(void**)&ws.xsum, rows_x * (H / 32) * 4},
+        {(void**)&ws.xu, rows_x * (H / 32) * 4},
         {(void**)&ws.xn, M * H * 4},
         {(void**)&ws.rlog, M * E * 4},
         {(void**)&ws.shl, M * 4},
@@ -135,9 +136,11 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.actq, ws.act_rows * F},
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.actsum, ws.act_rows * (F / 16) * 4},
+        {(void**)&ws.actu, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.yent, yrows * H * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
+        {(void**)&ws.counters, 64},
     };
     size_t total = 0;
     for (auto& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
@@ -267,19 +270,26 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     const uint32_t kcap = c->pol.enabled ? c->pol.max : k;
     const float* lg = rlog ? rlog : ws.rlog;
     const int gemm_order = m >= c->cfg.router_dot_max_m ? 1 : 0;
-    if (rlog)
-        TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st));
-    else
-        TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H,
-                                             m == 1 ? 0 : gemm_order, ws.rlog, ws.shl, st));
-    TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
     if (m == 1) {
         const int pair = c->cfg.hiprec ? 1 : 0;
-        TIMED(K_QUANT, launch_quantize(x, 1, H, 32, pair, ws.xq, ws.xs, ws.xsum, st));
-        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, ws, pair, kcap, st));
+        if (rlog) {
+            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st));
+            TIMED(K_ROUTE, launch_route(rlog, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+        } else {
+            TIMED(K_ROUTER_ROUTE, launch_router_route(w->router, w->router_bias, w->shexp_gate, x, 1, E, H, ws.rlog,
+                                                      ws.shl, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats,
+                                                      ws.counters, st));
+        }
+        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, ws, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
     } else {
-        TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, st));
+        if (rlog)
+            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st));
+        else
+            TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
+                                                 ws.rlog, ws.shl, st));
+        TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+        TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, ws.xu, st));
         TIMED(K_DISPATCH, launch_dispatch(ws, m, st));
         TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));
         TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, st));
@@ -423,7 +433,7 @@ extern "C" int trk_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb,
     if ((uintptr_t)x % 16 || k % 4) return fail(TRK_E_INVALID, "x must be 16-byte aligned");
     if (pair && m != 1) return fail(TRK_E_INVALID, "pair quantisation takes one row");
     if (m == 0) return TRK_OK;
-    HIP_TRY(launch_quantize(x, m, k, kb, pair, q, scale, sum, (hipStream_t)stream));
+    HIP_TRY(launch_quantize(x, m, k, kb, pair, q, scale, sum, nullptr, (hipStream_t)stream));
     return TRK_OK;
 }
 

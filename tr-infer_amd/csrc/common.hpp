@@ -61,22 +61,29 @@ __device__ __forceinline__ float sigmoid_libm(float x) { return 1.0f / (1.0f + e
 __device__ __forceinline__ int32_t cvt_rne(float v) { return (int32_t)__builtin_rintf(v); }
 __device__ __forceinline__ int8_t sat_i8(int32_t v) { return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v)); }
 
-// Quantise n (16 or 32) values in registers; optionally produce the fnmadd residual.
-template <int N>
-__device__ __forceinline__ void quant_block_regs(const float* x, int8_t* q, float& scale, int32_t& sum,
-                                                 float* resid) {
+// Quantise N (16 or 32) values in registers; q comes back packed 4 per word (little-endian bytes);
+// optionally produce the fnmadd residual.
+template <int N, bool RESID = false>
+__device__ __forceinline__ void quant_block_regs(const float* x, uint32_t* qw, float& scale, int32_t& sum,
+                                                 float* resid = nullptr) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < N; i++) amax = mx_ps(amax, __builtin_fabsf(x[i]));
-    float s = amax / 127.0f;
-    float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float s = amax / 127.0f;
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
     int32_t su = 0;
 #pragma unroll
-    for (int i = 0; i < N; i++) {
-        int32_t qi = cvt_rne(x[i] * inv);
-        su += qi;
-        q[i] = sat_i8(qi);
-        if (resid) resid[i] = __builtin_fmaf(-(float)qi, s, x[i]);
+    for (int w = 0; w < N / 4; w++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int i = 4 * w + b;
+            const int32_t qi = cvt_rne(x[i] * inv);
+            su += qi;
+            packed |= (uint32_t)(uint8_t)sat_i8(qi) << (8 * b);
+            if (RESID) resid[i] = __builtin_fmaf(-(float)qi, s, x[i]);
+        }
+        qw[w] = packed;
     }
     scale = s;
     sum = su;
@@ -116,6 +123,22 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& sc, 
     }
 }
 
+// The same from the header words of a superblock held in registers: bytes 4..15 of the header
+// are words w1, w2, w3 (little-endian); j must be a compile-time constant after unrolling.
+__device__ __forceinline__ void q4k_scale_min_w(uint32_t w1, uint32_t w2, uint32_t w3, int j, int& sc, int& mn) {
+    auto byte = [&](int i) -> int {
+        const uint32_t w = i < 4 ? w1 : (i < 8 ? w2 : w3);
+        return (int)((w >> (8 * (i & 3))) & 0xffu);
+    };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        mn = byte(4 + j) & 63;
+    } else {
+        sc = (byte(8 + j - 4) & 15) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(8 + j - 4) >> 4) | ((byte(4 + j - 4) >> 6) << 4);
+    }
+}
+
 // blocks.py:35-36: dd = f16(d*sc), mm = f16(-(dmin*mn)), then widened back to f32 (gemv.rs:104-105)
 __device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, float& dd, float& mm) {
     dd = f16_round(d * (float)sc);
@@ -123,5 +146,23 @@ __device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, floa
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// ---- wave-wide reductions with DPP (row shifts, then row broadcasts 15 / 31) ----------------------
+// The result of the running scan sits in lane 63; it is returned in every lane (readlane).
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    // lanes without a source keep their own value (old = v), the identity of max / min
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x113, 0xf, 0xf, false));  // row_shr:3
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xf, 0xe, false));  // row_shr:4
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x118, 0xf, 0xc, false));  // row_shr:8
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_reduce_u32<true>(v); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_reduce_u32<false>(v); }
 
 }  // namespace trk

@@ -1,5 +1,5 @@
-// Router logits, routing, activation quantisation, the kernel-level GEMV mirror, elementwise
-// kernels and the synthetic-data generators.
+// Activation quantisation, the kernel-level GEMV mirror, elementwise kernels and the
+// synthetic-data generators.
 #include "common.hpp"
 
 namespace trk {
@@ -10,7 +10,7 @@ namespace trk {
 
 template <int KB>
 __global__ void quantize_rows_kernel(const float* __restrict__ x, uint32_t m, uint32_t k, int8_t* __restrict__ q,
-                                     float* __restrict__ s, int32_t* __restrict__ su) {
+                                     float* __restrict__ s, int32_t* __restrict__ su, float* __restrict__ u) {
     uint32_t nb = k / KB;
     uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= m * nb) return;
@@ -22,15 +22,16 @@ __global__ void quantize_rows_kernel(const float* __restrict__ x, uint32_t m, ui
         float4 t = *reinterpret_cast<const float4*>(src + i);
         v[i] = t.x; v[i + 1] = t.y; v[i + 2] = t.z; v[i + 3] = t.w;
     }
-    int8_t qq[KB];
+    uint32_t qq[KB / 4];
     float sc;
     int32_t sm;
-    quant_block_regs<KB>(v, qq, sc, sm, nullptr);
-    int8_t* dst = q + (size_t)r * k + (size_t)b * KB;
+    quant_block_regs<KB>(v, qq, sc, sm);
+    uint4* dst = reinterpret_cast<uint4*>(q + (size_t)r * k + (size_t)b * KB);
 #pragma unroll
-    for (int i = 0; i < KB; i++) dst[i] = qq[i];
+    for (int i = 0; i < KB / 16; i++) dst[i] = make_uint4(qq[4 * i], qq[4 * i + 1], qq[4 * i + 2], qq[4 * i + 3]);
     s[idx] = sc;
     su[idx] = sm;
+    if (u) u[idx] = sc * (float)sm;  // gemv.rs:144
 }
 
 // quantize_pair_blocks (quant.rs:96-108): row 0 = coarse, row 1 = quantised fnmadd residual
@@ -47,15 +48,17 @@ __global__ void quantize_pair_kernel(const float* __restrict__ x, uint32_t k, in
         float4 t = *reinterpret_cast<const float4*>(src + i);
         v[i] = t.x; v[i + 1] = t.y; v[i + 2] = t.z; v[i + 3] = t.w;
     }
-    int8_t q0[KB], q1[KB];
+    uint32_t q0[KB / 4], q1[KB / 4];
     float s0, s1;
     int32_t m0, m1;
-    quant_block_regs<KB>(v, q0, s0, m0, r);
-    quant_block_regs<KB>(r, q1, s1, m1, nullptr);
+    quant_block_regs<KB, true>(v, q0, s0, m0, r);
+    quant_block_regs<KB>(r, q1, s1, m1);
+    uint4* d0 = reinterpret_cast<uint4*>(q + (size_t)b * KB);
+    uint4* d1 = reinterpret_cast<uint4*>(q + (size_t)k + (size_t)b * KB);
 #pragma unroll
-    for (int i = 0; i < KB; i++) {
-        q[(size_t)b * KB + i] = q0[i];
-        q[(size_t)k + (size_t)b * KB + i] = q1[i];
+    for (int i = 0; i < KB / 16; i++) {
+        d0[i] = make_uint4(q0[4 * i], q0[4 * i + 1], q0[4 * i + 2], q0[4 * i + 3]);
+        d1[i] = make_uint4(q1[4 * i], q1[4 * i + 1], q1[4 * i + 2], q1[4 * i + 3]);
     }
     s[b] = s0;
     su[b] = m0;
@@ -64,7 +67,7 @@ __global__ void quantize_pair_kernel(const float* __restrict__ x, uint32_t k, in
 }
 
 hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* s,
-                           int32_t* su, hipStream_t st) {
+                           int32_t* su, float* u, hipStream_t st) {
     uint32_t nb = k / kb;
     if (pair) {
         dim3 g((nb + 63) / 64);
@@ -75,240 +78,10 @@ hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, 
     } else {
         dim3 g((m * nb + 255) / 256);
         if (kb == 32)
-            quantize_rows_kernel<32><<<g, 256, 0, st>>>(x, m, k, q, s, su);
+            quantize_rows_kernel<32><<<g, 256, 0, st>>>(x, m, k, q, s, su, u);
         else
-            quantize_rows_kernel<16><<<g, 256, 0, st>>>(x, m, k, q, s, su);
+            quantize_rows_kernel<16><<<g, 256, 0, st>>>(x, m, k, q, s, su, u);
     }
-    return hipGetLastError();
-}
-
-// ============================================================================================
-// router logits
-// ============================================================================================
-
-// attn::dot (attn.rs:329-357) with one wave per weight row: lane L = 16c + j is lane j of
-// accumulator chain c, so the wave holds exactly the reference's four 16-lane FMA chains; the
-// 16-wide tail goes into chain 0, then (c0 + c1) + (c2 + c3) lanewise and the halving tree.
-// Rows [0, E) are router rows (+ bias), row E (if shexp_gate) the shared-expert gate.
-constexpr int DOT_MR = 8;
-__global__ void router_dot_kernel(const float* __restrict__ router, const float* __restrict__ bias,
-                                  const float* __restrict__ shg, const float* __restrict__ x, uint32_t m,
-                                  uint32_t E, uint32_t H, float* __restrict__ rlog, float* __restrict__ sh) {
-    uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
-    uint32_t lane = threadIdx.x % WAVE;
-    uint32_t nrow = E + (shg ? 1u : 0u);
-    if (wave >= nrow) return;
-    const float* wr = wave < E ? router + (size_t)wave * H : shg;
-    for (uint32_t m0 = 0; m0 < m; m0 += DOT_MR) {
-        uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
-        float acc[DOT_MR];
-#pragma unroll
-        for (int r = 0; r < DOT_MR; r++) acc[r] = 0.0f;
-        uint32_t i = 0;
-        for (; i + 64 <= H; i += 64) {
-            float a = wr[i + lane];
-#pragma unroll
-            for (int r = 0; r < DOT_MR; r++)
-                if ((uint32_t)r < mr) acc[r] = __builtin_fmaf(a, x[(size_t)(m0 + r) * H + i + lane], acc[r]);
-        }
-        for (; i + 16 <= H; i += 16) {
-            if (lane < 16) {
-                float a = wr[i + lane];
-#pragma unroll
-                for (int r = 0; r < DOT_MR; r++)
-                    if ((uint32_t)r < mr) acc[r] = __builtin_fmaf(a, x[(size_t)(m0 + r) * H + i + lane], acc[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < DOT_MR; r++) {
-            if ((uint32_t)r >= mr) break;
-            float c1 = __shfl(acc[r], (lane + 16) & 63);
-            float c2 = __shfl(acc[r], (lane + 32) & 63);
-            float c3 = __shfl(acc[r], (lane + 48) & 63);
-            float v = (acc[r] + c1) + (c2 + c3);
-            float s = reduce16_lanes(v);  // lanes 0..15 hold the tree sum
-            if (lane == 0) {
-                // scalar tail of attn.rs:351-354 (H % 16 != 0 is rejected by the host)
-                if (wave < E) {
-                    if (bias) s = s + bias[wave];
-                    rlog[(size_t)(m0 + r) * E + wave] = s;
-                } else {
-                    sh[m0 + r] = s;
-                }
-            }
-        }
-    }
-}
-
-// smallgemm::gemm_f32_nt (smallgemm.rs:8-59): each output is the halving-tree sum of 16 lane
-// chains, lane l accumulating x[kk + l] * w[kk + l] over kk in steps of 16.  A 16-lane group of
-// the wave plays the 16 lanes of one AVX-512 register; each thread carries 4 rows x 4 experts.
-__global__ void router_gemm_kernel(const float* __restrict__ router, const float* __restrict__ bias,
-                                   const float* __restrict__ x, uint32_t m, uint32_t E, uint32_t H,
-                                   float* __restrict__ rlog) {
-    uint32_t l = threadIdx.x & 15, g = threadIdx.x >> 4;  // 16 groups
-    uint32_t rg = g >> 2, eg = g & 3;
-    uint32_t row0 = blockIdx.y * 16 + rg * 4, e0 = blockIdx.x * 16 + eg * 4;
-    const float* xr[4];
-    const float* wr[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        uint32_t rr = row0 + r < m ? row0 + r : m - 1;
-        xr[r] = x + (size_t)rr * H + l;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        uint32_t ee = e0 + e < E ? e0 + e : E - 1;
-        wr[e] = router + (size_t)ee * H + l;
-    }
-    float acc[4][4];
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[r][e] = 0.0f;
-    for (uint32_t kk = 0; kk < H; kk += 16) {
-        float xv[4], wv[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) xv[r] = xr[r][kk];
-#pragma unroll
-        for (int e = 0; e < 4; e++) wv[e] = wr[e][kk];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[r][e] = __builtin_fmaf(xv[r], wv[e], acc[r][e]);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            float s = reduce16_lanes(acc[r][e]);
-            if (l == (uint32_t)(r * 4 + e) && row0 + r < m && e0 + e < E) {
-                if (bias) s = s + bias[e0 + e];
-                rlog[(size_t)(row0 + r) * E + e0 + e] = s;
-            }
-        }
-}
-
-hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
-                                uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
-                                hipStream_t st) {
-    if (!gemm_order) {
-        uint32_t nrow = E + (shexp_gate ? 1 : 0);
-        router_dot_kernel<<<(nrow + 3) / 4, 256, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh);
-    } else {
-        dim3 g((E + 15) / 16, (m + 15) / 16);
-        router_gemm_kernel<<<g, 256, 0, st>>>(router, bias, x, m, E, H, rlog);
-        if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
-            router_dot_kernel<<<1, 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh);
-    }
-    return hipGetLastError();
-}
-
-// ============================================================================================
-// routing (router.rs:70-148): one wave per token
-// ============================================================================================
-
-constexpr int ROUTE_MAXJ = 16;  // E <= 1024
-__global__ void route_kernel(const float* __restrict__ logits, uint32_t m, uint32_t E, uint32_t k, Policy pol,
-                             uint32_t* __restrict__ ids, float* __restrict__ wout, uint32_t* __restrict__ n_sel,
-                             unsigned long long* __restrict__ stats) {
-    extern __shared__ float ex_all[];  // [waves][E] for MassBasis::All
-    uint32_t wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    uint32_t row = blockIdx.x * (blockDim.x / WAVE) + wv;
-    if (row >= m) return;
-    const float* lg = logits + (size_t)row * E;
-    float v[ROUTE_MAXJ];
-    uint32_t nj = (E + 63) / 64;
-#pragma unroll
-    for (int j = 0; j < ROUTE_MAXJ; j++) {
-        uint32_t i = lane + 64u * j;
-        v[j] = ((uint32_t)j < nj && i < E) ? lg[i] : -__builtin_inff();
-    }
-    uint32_t kk = pol.enabled ? pol.max : k;
-    // topk_sorted: the k largest under (value desc, index asc); values that are not > -inf
-    // (nan, -inf) never enter, and unfilled slots keep (-inf, u32::MAX).
-    float my_tv = -__builtin_inff();
-    uint32_t my_ti = 0xffffffffu;
-    uint32_t taken = 0;
-    for (uint32_t rd = 0; rd < kk; rd++) {
-        float bv = -__builtin_inff();
-        uint32_t bi = 0xffffffffu;
-#pragma unroll
-        for (int j = 0; j < ROUTE_MAXJ; j++) {
-            uint32_t i = lane + 64u * j;
-            if (!((taken >> j) & 1u) && v[j] > -__builtin_inff() && (v[j] > bv || (v[j] == bv && i < bi))) {
-                bv = v[j];
-                bi = i;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            float ov = __shfl_xor(bv, off);
-            uint32_t oi = __shfl_xor(bi, off);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (bi != 0xffffffffu && bi % 64u == lane) taken |= 1u << (bi / 64u);
-        if (lane == rd) {
-            my_tv = bv;
-            my_ti = bi;
-        }
-    }
-    float mx = __shfl(my_tv, 0);
-    float e = lane < kk ? expf_libm(my_tv - mx) : 0.0f;
-    uint32_t count = kk;
-    if (pol.enabled) {
-        float denom = 0.0f;
-        if (pol.basis == TRK_BASIS_ALL) {
-            float* ea = ex_all + (size_t)wv * E;
-#pragma unroll
-            for (int j = 0; j < ROUTE_MAXJ; j++) {
-                uint32_t i = lane + 64u * j;
-                if ((uint32_t)j < nj && i < E) ea[i] = expf_libm(lg[i] - mx);
-            }
-            // make the wave's LDS writes visible to all its lanes
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            for (uint32_t i = 0; i < E; i++) denom += ea[i];
-        } else {
-            for (uint32_t j = 0; j < kk; j++) denom += __shfl(e, j);
-        }
-        float mass = 0.0f;
-        count = 0;
-        while (count < kk) {
-            mass += __shfl(e, count) / denom;
-            count++;
-            if (count >= pol.min && mass >= pol.mass) break;
-        }
-    }
-    // Fewer than `count` selectable logits (nan / -inf rows): the reference would index expert
-    // u32::MAX; here the selection stops at the valid ids (they are a prefix of the rounds).
-    const uint32_t nvalid = (uint32_t)__popcll(__ballot(lane < kk && my_ti != 0xffffffffu));
-    if (count > nvalid) count = nvalid;
-    // renorm (router.rs:93-104)
-    float sum = 0.0f;
-    for (uint32_t j = 0; j < count; j++) sum += __shfl(e, j);
-    if (lane < count) {
-        ids[(size_t)row * K_MAX + lane] = my_ti;
-        wout[(size_t)row * K_MAX + lane] = e / sum;
-    }
-    if (lane == 0) {
-        n_sel[row] = count;
-        if (stats) {
-            atomicAdd(&stats[0], 1ull);
-            atomicAdd(&stats[1], (unsigned long long)count);
-        }
-    }
-}
-
-hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
-                        float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st) {
-    const uint32_t waves = 4;
-    size_t lds = (pol.enabled && pol.basis == TRK_BASIS_ALL) ? (size_t)waves * E * sizeof(float) : 0;
-    route_kernel<<<(m + waves - 1) / waves, waves * WAVE, lds, st>>>(logits, m, E, k, pol, ids, w, n_sel, stats);
     return hipGetLastError();
 }
 

@@ -38,6 +38,7 @@ struct Workspace {
     int8_t* xq;           // [max(2, m_max)][H]
     float* xs;            // [max(2, m_max)][H/32]
     int32_t* xsum;
+    float* xu;            // [max(2, m_max)][H/32]: scale * (float)sum, the epilogue's u term
     float* xn;            // [m_max][H]: normed input (config-5 layers)
     float* rlog;          // [m_max][E]
     float* shl;           // [m_max]: shared-gate logits
@@ -56,21 +57,27 @@ struct Workspace {
     int8_t* actq;         // [act_rows][F] (decode: [33][2][F])
     float* acts;          // [act_rows][F/16]
     int32_t* actsum;
+    float* actu;          // [act_rows][F/16]: folded scale * (float)sum
     float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
+    uint32_t* counters;   // [16] device-scope arrival counters (kept at zero between launches)
     size_t act_rows;
 };
 
 // ---- launchers (return hipError_t of the launch) ----
 hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* s,
-                           int32_t* su, hipStream_t st);
+                           int32_t* su, float* u, hipStream_t st);
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
                                 hipStream_t st);
 hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
-hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
+hipError_t launch_router_route(const float* router, const float* bias, const float* shexp_gate, const float* x,
+                               uint32_t m, uint32_t E, uint32_t H, float* rlog, float* sh, uint32_t k, Policy pol,
+                               uint32_t* ids, float* w, uint32_t* n_sel, unsigned long long* stats, uint32_t* counter,
+                               hipStream_t st);
+hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
                                 const Workspace& ws, int pair, uint32_t kcap, hipStream_t st);
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
