@@ -65,6 +65,7 @@ def main():
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -114,13 +115,29 @@ def main():
             ctx.forward(weights(i % args.layers, M), x, out[:M])
         torch.cuda.synchronize()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # eager launches (host-side launch cost included)
         ev0.record(stream)
         for i in range(args.steps):
             ctx.forward(weights(i % args.layers, M), x, out[:M])
         ev1.record(stream)
         torch.cuda.synchronize()
-        ms = ev0.elapsed_time(ev1)
-        per = ms / args.steps
+        per_eager = ev0.elapsed_time(ev1) / args.steps
+        per = per_eager
+        if not args.eager:
+            # the same K steps captured once into a HIP graph (as a decode loop would run them),
+            # replayed once untimed and once timed
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(args.steps):
+                    ctx.forward(weights(i % args.layers, M), x, out[:M])
+            g.replay()
+            torch.cuda.synchronize()
+            ev0.record(stream)
+            g.replay()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            per = ev0.elapsed_time(ev1) / args.steps
+            del g
         nbytes = sum(layer_bytes(touched[i % args.layers], M) for i in range(args.steps)) / args.steps
         nops = sum(layer_ops(ents[i % args.layers], M) for i in range(args.steps)) / args.steps
         # per-kernel durations over the same rotation (events around each launch, same stream)
@@ -130,13 +147,14 @@ def main():
         kern = ctx.timing()
         ctx.set_timing(False)
         results[M] = dict(
-            tokens_per_s=M / (per * 1e-3), us_per_layer=per * 1e3, layer_GBps=nbytes / (per * 1e-3) / 1e9,
+            tokens_per_s=M / (per * 1e-3), us_per_layer=per * 1e3, us_per_layer_eager=per_eager * 1e3,
+            layer_GBps=nbytes / (per * 1e-3) / 1e9,
             hbm_frac=nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, int8_TOPS=nops / (per * 1e-3) / 1e12,
             mfma_frac=nops / (per * 1e-3) / 1e12 / INT8_PEAK_TOPS, experts_touched=float(np.mean(touched)),
             layer_MB=nbytes / 1e6,
             kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in kern.items()},
             _kern=kern, _touched=touched, _ents=ents)
-        log(f"M={M}: {per * 1e3:.1f} us/layer, {M / (per * 1e-3):.0f} tok/s, "
+        log(f"M={M}: {per * 1e3:.1f} us/layer (eager {per_eager * 1e3:.1f}), {M / (per * 1e-3):.0f} tok/s, "
             f"{nbytes / (per * 1e-3) / 1e9:.0f} GB/s, kernels {results[M]['kernels_us']}")
 
     prim = 1 if 1 in results else ms_list[0]

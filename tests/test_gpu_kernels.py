@@ -99,9 +99,8 @@ def test_router_logits_bit_exact(m):
     assert np.array_equal(host(lg2).view(np.uint32), want2.view(np.uint32))
 
 
-def routing_cases():
+def routing_cases(E=512):
     rng = np.random.default_rng(5)
-    E = 512
     lg = [rng.standard_normal((8, E)).astype(np.float32),
           (rng.integers(0, 40, (8, E)) * 0.25).astype(np.float32),   # many exact ties (router.rs:277-312)
           np.tile(np.array([((i * 37) % 101) * 0.1 for i in range(E)], np.float32), (2, 1))]
@@ -113,14 +112,24 @@ def routing_cases():
     nanrow[0, ::3] = np.nan
     nanrow[0, 1::7] = -np.inf
     lg.append(nanrow)
+    # more than 64 keys at or above the selection threshold: every logit equal, and 100 copies
+    # of the maximum (with -0.0 / +0.0 mixed, which compare equal)
+    lg.append(np.zeros((1, E), np.float32))
+    signed_zero = np.zeros((1, E), np.float32)
+    signed_zero[0, 1::2] = -0.0
+    lg.append(signed_zero)
+    hundred = np.clip(rng.standard_normal((1, E)), -4, 2.9).astype(np.float32)
+    hundred[0, rng.permutation(E)[:100]] = 3.0
+    lg.append(hundred)
     return np.concatenate(lg)
 
 
+@pytest.mark.parametrize("E", [512, 1000])
 @pytest.mark.parametrize("policy", [None, (1, 10, 0.9, O.BASIS_TOP), (1, 10, 0.95, O.BASIS_ALL), (4, 4, 0.5, O.BASIS_TOP),
                                     (1, 32, 1.0, O.BASIS_ALL), (8, 10, 0.5, O.BASIS_ALL)])
-def test_route_matches_oracle(policy):
-    say(f"route policy={policy}")
-    lg = routing_cases()
+def test_route_matches_oracle(policy, E):
+    say(f"route policy={policy} E={E}")
+    lg = routing_cases(E)
     ids, w, n = trmoe.route(to_dev(lg), 10, policy)
     ids, w, n = host(ids).view(np.uint32), host(w), host(n)
     worst = 0

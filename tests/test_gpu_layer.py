@@ -56,12 +56,15 @@ def layer(key, **kw):
 
 SMALL = dict(seed=11, H=512, E=32, F=256)
 FULL = dict(seed=1, H=2048, E=512, F=512, lazy=False)
+WIDE = dict(seed=12, H=512, E=600, F=256)   # E > 512: 16 logits per routing lane
+SHAPES = {"small": SMALL, "full": FULL, "wide": WIDE}
 
 
-@pytest.mark.parametrize("shape,k,hiprec", [("small", 4, True), ("small", 4, False), ("full", 10, True)])
+@pytest.mark.parametrize("shape,k,hiprec", [("small", 4, True), ("small", 4, False), ("full", 10, True),
+                                            ("wide", 8, True)])
 def test_decode_layer(shape, k, hiprec):
     say(f"decode layer {shape} k={k} hiprec={hiprec}")
-    L, orc, W = layer(shape, **(SMALL if shape == "small" else FULL))
+    L, orc, W = layer(shape, **SHAPES[shape])
     ctx = trmoe.Context(L.H, L.E, L.F, k, 4, hiprec=hiprec)
     import torch
     for t in range(3):

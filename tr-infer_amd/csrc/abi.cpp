@@ -40,9 +40,9 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 }  // namespace
 
 // Kernel ids for trk_get_timing.
-enum KernelId { K_LOGITS, K_ROUTE, K_ROUTER_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
+enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
                 K_RMSNORM, K_COUNT };
-static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "router_route", "quantize", "decode_gateup",
+static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
                                                   "decode_down", "dispatch", "batch_gateup", "batch_down",
                                                   "batch_combine", "rmsnorm"};
 
@@ -271,16 +271,14 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     const float* lg = rlog ? rlog : ws.rlog;
     const int gemm_order = m >= c->cfg.router_dot_max_m ? 1 : 0;
     if (m == 1) {
+        // logits (and the shared gate's logit), then routing + gate/up in one launch, then down
         const int pair = c->cfg.hiprec ? 1 : 0;
-        if (rlog) {
+        if (rlog)
             TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st));
-            TIMED(K_ROUTE, launch_route(rlog, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
-        } else {
-            TIMED(K_ROUTER_ROUTE, launch_router_route(w->router, w->router_bias, w->shexp_gate, x, 1, E, H, ws.rlog,
-                                                      ws.shl, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats,
-                                                      ws.counters, st));
-        }
-        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, ws, pair, kcap, st));
+        else
+            TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, 1, E, H, 0, ws.rlog,
+                                                 ws.shl, st));
+        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
     } else {
         if (rlog)

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "trmoe_internal.h"
 
 namespace trk {
@@ -101,14 +103,32 @@ __device__ __forceinline__ float reduce16(const float* v) {
     return c[0] + c[1];
 }
 
-// Cross-lane version for a value held by lanes j of a 16-lane group (lane j holds element j):
-// returns the tree sum in every lane of the group.
+// Cross-lane version for a value held by lanes j of a 16-lane row (lane j holds element j):
+// returns the tree sum in every lane of the row.  The partners come from DPP row rotations by 8,
+// 4, 2, 1: after the step with distance d every lane's value equals that of lane j ^ d', d' >= d,
+// so the rotation partner holds the same value as the xor partner and lane 0 computes exactly
+// a[0] = v0 + v8, b[0] = a0 + a4, c[0] = b0 + b2, c0 + c1 (other lanes: the same sums commuted).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float reduce16_lanes(float v) {
-    v = v + __shfl_xor(v, 8, 16);
-    v = v + __shfl_xor(v, 4, 16);
-    v = v + __shfl_xor(v, 2, 16);
-    v = v + __shfl_xor(v, 1, 16);
+    v = v + dpp_f<0x128>(v);  // row_ror:8
+    v = v + dpp_f<0x124>(v);  // row_ror:4
+    v = v + dpp_f<0x122>(v);  // row_ror:2
+    v = v + dpp_f<0x121>(v);  // row_ror:1
     return v;
+}
+
+// (row0 + row1) + (row2 + row3) of a wave, lanewise (lane j of every row gets the sum over
+// lanes j, j+16, j+32, j+48 in that bracketing): permlane16_swap pairs rows 0/1 and 2/3,
+// permlane32_swap the two halves.  Both swaps are symmetric, so the sum of their two results
+// does not depend on which of the pair carries which half.
+__device__ __forceinline__ float rows4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // ---- Q4_K / Q6_K superblock decoding ------------------------------------------------------------
@@ -163,6 +183,23 @@ __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_reduce_u32<true>(v); }
+
+// All-reduce within each 16-lane row with DPP: quad_perm [1,0,3,2], quad_perm [2,3,0,1], half-row
+// mirror, row mirror.  The pairing differs from an xor butterfly, so it is only for operations
+// whose result does not depend on the order (max of non-NaN values, integer sums).
+template <typename T, typename Op>
+__device__ __forceinline__ T row16_allreduce(T v, Op op) {
+    static_assert(sizeof(T) == 4, "32-bit values");
+    auto mv = [](T x, auto ctrl) -> T {
+        return __builtin_bit_cast(T, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), decltype(ctrl)::value, 0xf,
+                                                              0xf, false));
+    };
+    v = op(v, mv(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+    v = op(v, mv(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+    v = op(v, mv(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+    v = op(v, mv(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+    return v;
+}
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_reduce_u32<false>(v); }
 
 }  // namespace trk

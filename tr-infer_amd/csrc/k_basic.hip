@@ -211,9 +211,7 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
             float a = xr[i + lane];
             acc = __builtin_fmaf(a, a, acc);
         }
-    float c1 = __shfl(acc, (lane + 16) & 63), c2 = __shfl(acc, (lane + 32) & 63), c3 = __shfl(acc, (lane + 48) & 63);
-    float s = reduce16_lanes((acc + c1) + (c2 + c3));
-    s = __shfl(s, 0);
+    float s = reduce16_lanes(rows4_sum(acc));  // the same value in every lane
     for (; i < n; i++) s += xr[i] * xr[i];
     float r = 1.0f / __builtin_sqrtf(s / (float)n + eps);
     for (uint32_t j = lane; j < n; j += WAVE) y[(size_t)row * n + j] = w ? (xr[j] * r) * w[j] : xr[j] * r;

@@ -317,19 +317,12 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     for (int i = 0; i < 4; i++) {
         const uint32_t row = t0 + 4 * g + i;
         const float v = silu512(accg[i]) * accu[i];
-        float amax = __builtin_fabsf(v);
-        amax = mx_ps(amax, __shfl_xor(amax, 1, 16));
-        amax = mx_ps(amax, __shfl_xor(amax, 2, 16));
-        amax = mx_ps(amax, __shfl_xor(amax, 4, 16));
-        amax = mx_ps(amax, __shfl_xor(amax, 8, 16));
+        // the 16 lanes of an entry's strip are one DPP row (lanes 16g .. 16g+15)
+        const float amax = row16_allreduce(__builtin_fabsf(v), [](float a, float b) { return mx_ps(a, b); });
         const float s = amax / 127.0f;
         const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
         const int32_t qi = cvt_rne(v * inv);
-        int32_t sum = qi;
-        sum += __shfl_xor(sum, 1, 16);
-        sum += __shfl_xor(sum, 2, 16);
-        sum += __shfl_xor(sum, 4, 16);
-        sum += __shfl_xor(sum, 8, 16);
+        const int32_t sum = row16_allreduce(qi, [](int32_t a, int32_t b) { return a + b; });
         if (row < item.nrows) {
             const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
             ws.actq[(size_t)arow * F + strip * 16 + f] = sat_i8(qi);

@@ -13,12 +13,13 @@
 //            row's superblocks, forms the per-16 block dots against the staged activations and
 //            runs the chain in registers; slot 0 is stored and later slots (routing order,
 //            shared last) are added — tasks C with the combine fused.
-#include "common.hpp"
+#include "route.hpp"
 
 namespace trk {
 
-constexpr int GU_ROWS = 32;  // 16 gate + 16 up rows per workgroup
-constexpr int DN_R = 8;      // output rows per down workgroup
+// gate/up threads: a lane per (row, superblock) of the 32 rows, at least two waves (routing, x)
+#define GU_THREADS(nsb) (32 * (nsb) < 128 ? 128 : 32 * (nsb))
+constexpr int DN_R = 4;      // output rows per down workgroup
 
 __device__ __forceinline__ uint32_t nib(uint32_t w, int h) { return (w >> (4 * h)) & 0x0f0f0f0fu; }
 
@@ -33,37 +34,36 @@ __device__ __forceinline__ float lane_up(float v) {
         return __shfl_up(v, 1);
 }
 
-template <int P, int NSB>
-__global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_kernel(
-        Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, Workspace ws, uint32_t kcap) {
-    constexpr uint32_t H = NSB * 256, nb = NSB * 8;
-    const uint32_t F = gate.rows;
+template <int P, int NSB, int NJ>
+__global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
+        Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
+        uint32_t k, Policy pol, uint32_t kcap) {
+    constexpr uint32_t H = NSB * 256, nb = NSB * 8, XSB = 256 + 16, XP = NSB * XSB;
+    const uint32_t F = gate.rows, E = ws.E;
     const uint32_t slot = blockIdx.y, strip = blockIdx.x, tid = threadIdx.x;
     const bool shared = slot == kcap;
     extern __shared__ __align__(16) uint8_t smem[];
-    int8_t* xq = (int8_t*)smem;              // [P][H]
-    float* xs = (float*)(smem + P * H);      // [P][nb]  activation scales
+    int8_t* xq = (int8_t*)smem;              // [P][NSB][XSB]: superblocks padded against bank conflicts
+    float* xs = (float*)(smem + P * XP);     // [P][nb]  activation scales
     float* xu = xs + P * nb;                 // [P][nb]  sx * sum
     float* hres = xu + P * nb;               // [32][P]
-    float* act = hres + 32 * P;              // [16]
+    uint32_t* r_ids = (uint32_t*)(hres + 32 * P);  // [32] this token's routing
+    float* r_w = (float*)(r_ids + K_MAX);          // [32]
+    uint32_t* r_n = (uint32_t*)(r_w + K_MAX);      // [4]
+    uint2* cand = (uint2*)(r_n + 4);               // [ROUTE_CAND] routing scratch
+    float* ex = (float*)(cand + ROUTE_CAND);       // [E] (MassBasis::All only)
 
     // x first: its loads must not queue behind the (id-dependent) weight loads
     float4 xv[8];
-    const bool qthread = tid < nb;
+    const bool qthread = tid >= 64 && tid < 64 + nb;
     if (qthread) {
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)tid * 32);
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)(tid - 64) * 32);
 #pragma unroll
         for (int i = 0; i < 8; i++) xv[i] = src[i];
     }
-    const uint32_t n = ws.n_sel[0];
-    if (!shared && slot >= n) return;
-    const uint32_t e = shared ? 0u : ws.ids[slot];
-    const Mat& G = shared ? shg : gate;
-    const Mat& U = shared ? shu : up;
     const uint32_t r = tid / NSB, sb = tid % NSB;
     const bool wthread = r < 32;
-    uint4 wq[9];
-    {
+    auto load_rows = [&](const Mat& G, const Mat& U, uint32_t e, uint4* wq) {
         const uint32_t rr = wthread ? r : 0u;
         const uint8_t* rowp = (rr < 16 ? G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + rr) * G.row_bytes
                                        : U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + rr - 16) * U.row_bytes) +
@@ -71,10 +71,35 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         const uint4* s4 = reinterpret_cast<const uint4*>(rowp);
 #pragma unroll
         for (int i = 0; i < 9; i++) wq[i] = s4[i];
+    };
+    uint4 wq[9];
+    float shl = 0.0f;
+    if (shared) {
+        load_rows(shg, shu, 0u, wq);  // the shared expert does not wait for the routing
+        shl = ws.shl[0];
+    } else if (tid < 64) {
+        // route this token (wave 0): every routed workgroup repeats it, so no separate launch and
+        // no round trip through memory sits between the logits and the expert weights
+        const uint32_t n = route_row<NJ>(lg, E, k, pol, tid, cand, ex, r_ids, r_w);
+        if (tid == 0) r_n[0] = n;
+        if (slot == 0 && strip == 0) {  // one workgroup publishes it (down kernel, introspection)
+            wave_sync();
+            if (tid < n) {
+                ws.ids[tid] = r_ids[tid];
+                ws.w[tid] = r_w[tid];
+            }
+            if (tid == 0) {
+                ws.n_sel[0] = n;
+                if (ws.stats) {
+                    atomicAdd(&ws.stats[0], 1ull);
+                    atomicAdd(&ws.stats[1], (unsigned long long)n);
+                }
+            }
+        }
     }
     // quantise x per 32 (quantize_pair_blocks, quant.rs:96-108, or QAct::quantize) into LDS
     if (qthread) {
-        const uint32_t b = tid;
+        const uint32_t b = tid - 64;
         float v[32], rs[32];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -84,8 +109,9 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         float s;
         int32_t su;
         quant_block_regs<32, P == 2>(v, q, s, su, rs);
-        *reinterpret_cast<uint4*>(xq + b * 32) = make_uint4(q[0], q[1], q[2], q[3]);
-        *reinterpret_cast<uint4*>(xq + b * 32 + 16) = make_uint4(q[4], q[5], q[6], q[7]);
+        const uint32_t xo = (b / 8) * XSB + (b % 8) * 32;  // LDS offset of block b
+        *reinterpret_cast<uint4*>(xq + xo) = make_uint4(q[0], q[1], q[2], q[3]);
+        *reinterpret_cast<uint4*>(xq + xo + 16) = make_uint4(q[4], q[5], q[6], q[7]);
         xs[b] = s;
         xu[b] = s * (float)su;  // gemv.rs:144
         if (shared && strip == 0) {  // one workgroup publishes the quantised input (introspection)
@@ -96,8 +122,8 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         }
         if (P == 2) {
             quant_block_regs<32>(rs, q, s, su);
-            *reinterpret_cast<uint4*>(xq + H + b * 32) = make_uint4(q[0], q[1], q[2], q[3]);
-            *reinterpret_cast<uint4*>(xq + H + b * 32 + 16) = make_uint4(q[4], q[5], q[6], q[7]);
+            *reinterpret_cast<uint4*>(xq + XP + xo) = make_uint4(q[0], q[1], q[2], q[3]);
+            *reinterpret_cast<uint4*>(xq + XP + xo + 16) = make_uint4(q[4], q[5], q[6], q[7]);
             xs[nb + b] = s;
             xu[nb + b] = s * (float)su;
             if (shared && strip == 0) {
@@ -109,6 +135,12 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         }
     }
     __syncthreads();
+    float wgt = 0.0f;
+    if (!shared) {
+        if (slot >= r_n[0]) return;  // workgroup-uniform
+        load_rows(gate, up, r_ids[slot], wq);
+        wgt = r_w[slot];
+    }
 
     // this lane's 8 blocks: exact dots, (dd, mm), t = dd * sx and u from LDS
     const uint32_t* w32 = reinterpret_cast<const uint32_t*>(wq);  // [0..3] header, [4..35] qs
@@ -140,7 +172,7 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
     for (int p = 0; p < P; p++) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int4* xa = reinterpret_cast<const int4*>(xq + p * H + sb * 256 + 64 * c);  // sub-blocks 2c, 2c+1
+            const int4* xa = reinterpret_cast<const int4*>(xq + p * XP + sb * XSB + 64 * c);  // sub-blocks 2c, 2c+1
             const int4 x0 = xa[0], x1 = xa[1], x2 = xa[2], x3 = xa[3];
             const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
@@ -188,7 +220,7 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         const float g = P == 2 ? hres[tid * P] + hres[tid * P + 1] : hres[tid * P];
         const float u = P == 2 ? hres[(16 + tid) * P] + hres[(16 + tid) * P + 1] : hres[(16 + tid) * P];
         const float av = silu512(g) * u;
-        const float wgt = shared ? sigmoid_libm(ws.shl[0]) : ws.w[slot];
+        if (shared) wgt = sigmoid_libm(shl);  // exec.rs:1606
         const uint32_t aslot = shared ? (uint32_t)SH_SLOT : slot;
         const uint32_t nbf = F / 16;
         int8_t* dq = ws.actq + (size_t)aslot * P * F + strip * 16;
@@ -197,19 +229,11 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
         float v = av;
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            float amax = __builtin_fabsf(v);
-            amax = mx_ps(amax, __shfl_xor(amax, 1, 16));
-            amax = mx_ps(amax, __shfl_xor(amax, 2, 16));
-            amax = mx_ps(amax, __shfl_xor(amax, 4, 16));
-            amax = mx_ps(amax, __shfl_xor(amax, 8, 16));
+            const float amax = row16_allreduce(__builtin_fabsf(v), [](float a, float b) { return mx_ps(a, b); });
             const float sc = amax / 127.0f;
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             const int32_t qi = cvt_rne(v * inv);
-            int32_t sum = qi;
-            sum += __shfl_xor(sum, 1, 16);
-            sum += __shfl_xor(sum, 2, 16);
-            sum += __shfl_xor(sum, 4, 16);
-            sum += __shfl_xor(sum, 8, 16);
+            const int32_t sum = row16_allreduce(qi, [](int32_t a, int32_t b) { return a + b; });
             dq[p * F + tid] = sat_i8(qi);
             if (tid == 0) {
                 ds[p * nbf] = sc * wgt;
@@ -221,18 +245,24 @@ __global__ __launch_bounds__(32 * NSB < 64 ? 64 : 32 * NSB) void decode_gateup_k
 }
 
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
-                                const Workspace& ws, int pair, uint32_t kcap, hipStream_t st) {
+                                const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
+                                hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32, nsb = H / 256;
     const int P = pair ? 2 : 1;
-    const size_t lds = (size_t)P * H + (size_t)P * nb * 8 + 32 * P * 4 + 64;
+    size_t lds = (size_t)P * nsb * 272 + (size_t)P * nb * 8 + 32 * P * 4 + K_MAX * 8 + 16 + ROUTE_CAND * 8;
+    if (pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;
     const dim3 g(F / 16, kcap + 1);
-    const uint32_t threads = 32 * nsb < 64 ? 64 : 32 * nsb;
-    switch (nsb * 2 + (pair ? 1 : 0)) {
-#define GU_CASE(ns) \
-    case ns * 2: decode_gateup_kernel<1, ns><<<g, threads, lds, st>>>(gate, up, sh_gate, sh_up, x, ws, kcap); break; \
-    case ns * 2 + 1: decode_gateup_kernel<2, ns><<<g, threads, lds, st>>>(gate, up, sh_gate, sh_up, x, ws, kcap); break;
+    const uint32_t threads = GU_THREADS(nsb);
+    const bool nj16 = route_nj(ws.E) == 16;
+    switch ((nsb * 2 + (pair ? 1 : 0)) * 2 + (nj16 ? 1 : 0)) {
+#define GU_CASE2(ns, p, nj)                                                                                      \
+    case (ns * 2 + p - 1) * 2 + (nj == 16 ? 1 : 0):                                                              \
+        decode_gateup_kernel<p, ns, nj><<<g, threads, lds, st>>>(gate, up, sh_gate, sh_up, x, lg, ws, k, pol, kcap); \
+        break;
+#define GU_CASE(ns) GU_CASE2(ns, 1, 8) GU_CASE2(ns, 1, 16) GU_CASE2(ns, 2, 8) GU_CASE2(ns, 2, 16)
         GU_CASE(1) GU_CASE(2) GU_CASE(3) GU_CASE(4) GU_CASE(5) GU_CASE(6) GU_CASE(7) GU_CASE(8)
 #undef GU_CASE
+#undef GU_CASE2
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -240,146 +270,241 @@ hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_ga
 
 // ---- down ------------------------------------------------------------------------------------
 
-// One (slot, row) of the down projection: the row's superblocks in order, 16 blocks of 16 each,
-// per-block epilogue chain for P activation rows kept in registers.  All NSB superblocks of the
-// row are loaded before any is used.
-template <int P, int NSB>
-__device__ __forceinline__ void down_row_chain_q4k(const uint8_t* __restrict__ rowp,
-                                                  const int8_t* __restrict__ aq /*[P][F]*/, uint32_t F,
-                                                  const float* __restrict__ as, const float* __restrict__ au,
-                                                  uint32_t nbf, float* acc) {
-    uint4 wq[NSB][9];
-#pragma unroll
-    for (int sb = 0; sb < NSB; sb++)
-#pragma unroll
-        for (int i = 0; i < 9; i++) wq[sb][i] = reinterpret_cast<const uint4*>(rowp + sb * 144)[i];
-#pragma unroll
-    for (int sb = 0; sb < NSB; sb++) {
-        const uint32_t* w32 = reinterpret_cast<const uint32_t*>(wq[sb]);
-        const float d = h2f((uint16_t)(wq[sb][0].x & 0xffff)), dmin = h2f((uint16_t)(wq[sb][0].x >> 16));
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            q4k_scale_min_w(wq[sb][0].y, wq[sb][0].z, wq[sb][0].w, j, sc, mn);
-            float ddv, mmv;
-            q4k_dm(d, dmin, sc, mn, ddv, mmv);
-            const int c = j / 2, h = j % 2;
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-                const uint32_t b = sb * 16 + 2 * j + half;
-#pragma unroll
-                for (int p = 0; p < P; p++) {
-                    const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + b * 16);
-                    int dot = sdot4((int)nib(w32[4 + 8 * c + 4 * half + 0], h), xv.x, 0);
-                    dot = sdot4((int)nib(w32[4 + 8 * c + 4 * half + 1], h), xv.y, dot);
-                    dot = sdot4((int)nib(w32[4 + 8 * c + 4 * half + 2], h), xv.z, dot);
-                    dot = sdot4((int)nib(w32[4 + 8 * c + 4 * half + 3], h), xv.w, dot);
-                    const float sx = as[p * nbf + b];
-                    const float t = ddv * sx;
-                    acc[p] = __builtin_fmaf(mmv, au[p * nbf + b], acc[p]);
-                    acc[p] = __builtin_fmaf((float)dot, t, acc[p]);
-                }
-            }
-        }
-    }
+// A unit is one (slot, output row) of a down workgroup; its 16-blocks are split over DN_L = 2*NSB
+// lanes, half a superblock (8 blocks) each, in chain order.  The lanes of a unit sit side by side
+// in one wave and never straddle a wave.
+template <int NSB>
+struct DownLanes {
+    static constexpr int L = 2 * NSB;        // lanes per unit
+    static constexpr int UPW = 64 / L;       // units per wave
+    static constexpr int UPP = 4 * UPW;      // units per pass of the 256-thread workgroup
+};
+
+// the running accumulator one lane up (towards the next half-superblock of the unit)
+template <int L>
+__device__ __forceinline__ float unit_up(float v) {
+    if constexpr (16 % L == 0)
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
+    else
+        return __shfl_up(v, 1);
 }
 
-// Q6_K rows (210-byte superblocks, 2-byte aligned): the extension mapping — unsigned 6-bit q,
-// dd = f16(d*sc), mm = f16(-32*dd), one block per scale (16 values).
+// Q4_K half superblock h2 of superblock sb: the 16-byte header and the 64 qs bytes of its four
+// sub-blocks (sub-block j = 4*h2 + jj lives in nibble j%2 of qs[32*(j/2) + i]).
+__device__ __forceinline__ void load_half_q4k(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2, uint4& hdr,
+                                              uint4 (&qs)[4]) {
+    const uint4* p = reinterpret_cast<const uint4*>(rowp + sb * 144);
+    hdr = p[0];
+    const uint4* q = reinterpret_cast<const uint4*>(rowp + sb * 144 + 16 + 64 * h2);
+#pragma unroll
+    for (int i = 0; i < 4; i++) qs[i] = q[i];
+}
+
+// per-block terms of a lane's 8 blocks (blocks 16*sb + 8*h2 + 0..7): exact int dot, t = dd*sx,
+// mm and the activation's u = sx*sum, for P activation rows
 template <int P>
-__device__ __forceinline__ void down_row_chain_q6k(const uint8_t* __restrict__ rowp, uint32_t nsb,
-                                                  const int8_t* __restrict__ aq, uint32_t F,
-                                                  const float* __restrict__ as, const float* __restrict__ au,
-                                                  uint32_t nbf, float* acc) {
-    for (uint32_t sb = 0; sb < nsb; sb++) {
-        const uint16_t* s2 = reinterpret_cast<const uint16_t*>(rowp + sb * 210);
-        uint16_t w16[105];
+__device__ __forceinline__ void half_terms_q4k(const uint4& hdr, const uint4 (&qs)[4], uint32_t h2,
+                                               const int8_t* __restrict__ aq /*[P] rows, stride F, at block 0*/,
+                                               uint32_t F, const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+    const uint32_t* w32 = reinterpret_cast<const uint32_t*>(qs);
+    const float d = h2f((uint16_t)(hdr.x & 0xffff)), dmin = h2f((uint16_t)(hdr.x >> 16));
 #pragma unroll
-        for (int i = 0; i < 105; i++) w16[i] = s2[i];
-        auto dw = [&](int o) -> uint32_t { return (uint32_t)w16[o >> 1] | ((uint32_t)w16[(o >> 1) + 1] << 16); };
-        const float d = h2f(w16[104]);
+    for (int p = 0; p < P; p++) {
+        const float4* s4 = reinterpret_cast<const float4*>(as + p * nbf);
+        const float4* u4 = reinterpret_cast<const float4*>(au + p * nbf);
+        const float4 s0 = s4[0], s1 = s4[1], u0 = u4[0], u1 = u4[1];
+        const float sa[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const float ua[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int8_t sc = (int8_t)((w16[(192 + j) >> 1] >> (((192 + j) & 1) * 8)) & 0xff);
-            const float ddv = f16_round(d * (float)sc);
-            const float mmv = f16_round(-32.0f * ddv);
-            const int nn = j / 8, g = (j % 8) / 2, l0 = 16 * (j % 2);
-            const uint32_t b = sb * 16 + j;
+        for (int i = 0; i < 8; i++) {
+            tv[p][i] = sa[i];
+            uv[p][i] = ua[i];
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        int sc, mn;
+        // h2 is 0 or 1: select the sub-block's scale/min without indexing by a runtime value
+        int sc0, mn0, sc1, mn1;
+        q4k_scale_min_w(hdr.y, hdr.z, hdr.w, jj, sc0, mn0);
+        q4k_scale_min_w(hdr.y, hdr.z, hdr.w, 4 + jj, sc1, mn1);
+        sc = h2 ? sc1 : sc0;
+        mn = h2 ? mn1 : mn0;
+        float ddv, mm;
+        q4k_dm(d, dmin, sc, mn, ddv, mm);
+        const int c = jj / 2, h = jj % 2;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int i = 2 * jj + hh;
+            mmv[i] = mm;
 #pragma unroll
             for (int p = 0; p < P; p++) {
-                const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + b * 16);
-                const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
-                int dot = 0;
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    uint32_t lo = dw(64 * nn + 32 * (g & 1) + l0 + 4 * t);
-                    lo = (g >> 1) ? ((lo >> 4) & 0x0f0f0f0fu) : (lo & 0x0f0f0f0fu);
-                    const uint32_t hi = (dw(128 + 32 * nn + l0 + 4 * t) >> (2 * g)) & 0x03030303u;
-                    dot = sdot4((int)(lo | (hi << 4)), xa[t], dot);
-                }
-                const float sx = as[p * nbf + b];
-                const float t = ddv * sx;
-                acc[p] = __builtin_fmaf(mmv, au[p * nbf + b], acc[p]);
-                acc[p] = __builtin_fmaf((float)dot, t, acc[p]);
+                const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
+                int dot = sdot4((int)nib(w32[8 * c + 4 * hh + 0], h), xv.x, 0);
+                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 1], h), xv.y, dot);
+                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 2], h), xv.z, dot);
+                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 3], h), xv.w, dot);
+                dotv[p][i] = (float)dot;
+                tv[p][i] = ddv * tv[p][i];  // t = d * sx (gemv.rs:145)
             }
         }
     }
 }
 
+// Q6_K (210-byte superblocks, 2-byte aligned) half superblock h2: blocks j = 8*h2 + 0..7 use
+// ql[64*h2 + ...], qh[32*h2 + ...], scales[8*h2 + ...] and d — the extension mapping: unsigned
+// 6-bit q, dd = f16(d*sc), mm = f16(-32*dd), one block per scale.
+template <int P>
+__device__ __forceinline__ void half_terms_q6k(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2,
+                                               const int8_t* __restrict__ aq, uint32_t F,
+                                               const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(rowp + sb * 210);
+    uint16_t ql[32], qh[16], sc2[4];
+#pragma unroll
+    for (int i = 0; i < 32; i++) ql[i] = s2[32 * h2 + i];
+#pragma unroll
+    for (int i = 0; i < 16; i++) qh[i] = s2[64 + 16 * h2 + i];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sc2[i] = s2[96 + 4 * h2 + i];
+    const float d = h2f(s2[104]);
+    auto dl = [&](int o) -> uint32_t { return (uint32_t)ql[o >> 1] | ((uint32_t)ql[(o >> 1) + 1] << 16); };
+    auto dh = [&](int o) -> uint32_t { return (uint32_t)qh[o >> 1] | ((uint32_t)qh[(o >> 1) + 1] << 16); };
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int8_t sc = (int8_t)((sc2[i >> 1] >> ((i & 1) * 8)) & 0xff);
+        const float ddv = f16_round(d * (float)sc);
+        mmv[i] = f16_round(-32.0f * ddv);
+        const int g = i / 2, l0 = 16 * (i % 2);
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
+            const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
+            int dot = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                uint32_t lo = dl(32 * (g & 1) + l0 + 4 * t);
+                lo = (g >> 1) ? ((lo >> 4) & 0x0f0f0f0fu) : (lo & 0x0f0f0f0fu);
+                const uint32_t hi = (dh(l0 + 4 * t) >> (2 * g)) & 0x03030303u;
+                dot = sdot4((int)(lo | (hi << 4)), xa[t], dot);
+            }
+            dotv[p][i] = (float)dot;
+            tv[p][i] = ddv * as[p * nbf + i];
+            uv[p][i] = au[p * nbf + i];
+        }
+    }
+}
+
+// Work unit u = slot * DN_R + row of a workgroup; slots 0..kcap-1 are the routed slots (those at
+// or past n_sel idle), slot kcap is the shared expert.  Activation rows are staged in LDS with
+// slot stride P*F + 16 bytes (fewer bank conflicts between slots).
 template <int P, int NSB>
-__global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, float* __restrict__ out,
-                                                         int residual) {
-    constexpr uint32_t F = NSB * 256, nsb = NSB, nbf = NSB * 16;
+__global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t kcap,
+                                                         float* __restrict__ out, int residual) {
+    using DL = DownLanes<NSB>;
+    constexpr uint32_t F = NSB * 256, nbf = NSB * 16, SQ = P * F + 16;
     const uint32_t tid = threadIdx.x, row0 = blockIdx.x * DN_R;
-    const uint32_t n = ws.n_sel[0], slots = n + 1;
+    const uint32_t slots = kcap + 1, units = slots * DN_R;
+    const uint32_t n = ws.n_sel[0];
+    const uint32_t wv = tid / 64, ln = tid % 64, q = ln % DL::L;
+    const bool lane_ok = ln < (uint32_t)(DL::UPW * DL::L);
+    const uint32_t sb = q / 2, h2 = q % 2;
+    const bool q4 = down.fmt == TRK_FMT_Q4_K;
 
     extern __shared__ __align__(16) uint8_t smem[];
-    int8_t* aq = (int8_t*)smem;                               // [slots][P][F]
-    float* as = (float*)(smem + (size_t)slots * P * F);       // [slots][P][nbf] folded scale
-    float* au = as + slots * P * nbf;                         // [slots][P][nbf] scale * sum
-    float* vres = au + slots * P * nbf;                       // [slots][R]
+    int8_t* aq = (int8_t*)smem;                                // [slots][SQ]
+    float* as = (float*)(smem + (size_t)slots * SQ);           // [slots][P][nbf] folded scale
+    float* au = as + slots * P * nbf;                          // [slots][P][nbf] scale * sum
+    float* vres = au + slots * P * nbf;                        // [slots][DN_R]
 
-    // stage the slots' activation rows: flat index over (slot, 16-byte piece) with the loads of
-    // four pieces in flight per thread
+    auto unit_row = [&](uint32_t u, bool& live) -> const uint8_t* {
+        const uint32_t s = u / DN_R, r = u % DN_R;
+        const bool sh = s == kcap;
+        live = lane_ok && u < units && (sh || s < n);
+        const Mat& D = sh ? shd : down;
+        const uint32_t e = (sh || !live) ? 0u : ws.ids[s];
+        return D.ptr + (size_t)e * D.stride + (size_t)(row0 + r) * D.row_bytes;
+    };
+    // this lane's first unit: its weights are requested before the activations are staged
+    const uint32_t u0 = wv * DL::UPW + ln / DL::L;
+    bool live0;
+    const uint8_t* row_first = unit_row(u0, live0);
+    uint4 hdr = make_uint4(0, 0, 0, 0), qs[4] = {hdr, hdr, hdr, hdr};
+    if (live0 && q4) load_half_q4k(row_first, sb, h2, hdr, qs);
+
     {
         constexpr uint32_t QP = P * F / 16, SP = P * nbf;  // int4 pieces and scales per slot
         const uint32_t nq = slots * QP, ns = slots * SP;
 #pragma unroll 4
         for (uint32_t i = tid; i < nq; i += 256) {
             const uint32_t s = i / QP, o = i % QP;
-            const uint32_t a = s < n ? s : (uint32_t)SH_SLOT;
-            reinterpret_cast<int4*>(aq)[i] = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F)[o];
+            const uint32_t a = s < kcap ? s : (uint32_t)SH_SLOT;
+            *reinterpret_cast<int4*>(aq + (size_t)s * SQ + o * 16) =
+                    reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F)[o];
         }
 #pragma unroll 4
         for (uint32_t i = tid; i < ns; i += 256) {
             const uint32_t s = i / SP, o = i % SP;
-            const uint32_t a = s < n ? s : (uint32_t)SH_SLOT;
+            const uint32_t a = s < kcap ? s : (uint32_t)SH_SLOT;
             const float sc = ws.acts[(size_t)a * SP + o];
             as[i] = sc;
             au[i] = sc * (float)ws.actsum[(size_t)a * SP + o];
         }
     }
     __syncthreads();
-    for (uint32_t it = tid; it < slots * DN_R; it += blockDim.x) {
-        const uint32_t s = it / DN_R, r = it % DN_R;
-        const Mat& D = s < n ? down : shd;
-        const uint32_t e = s < n ? ws.ids[s] : 0u;
-        const uint8_t* rowp = D.ptr + (size_t)e * D.stride + (size_t)(row0 + r) * D.row_bytes;
+    for (uint32_t pass = 0; pass * DL::UPP < units; pass++) {
+        const uint32_t u = pass * DL::UPP + u0;
+        bool live = live0;
+        const uint8_t* rowp = row_first;
+        if (pass > 0) {
+            rowp = unit_row(u, live);
+            if (live && q4) load_half_q4k(rowp, sb, h2, hdr, qs);
+        }
+        const uint32_t s = live ? u / DN_R : 0u;
+        float dotv[P][8], tv[P][8], mmv[8], uv[P][8];
+        const uint32_t b0 = 8 * q;  // first block of this lane within the row
+        const int8_t* a = aq + (size_t)s * SQ + b0 * 16;
+        const float* sa = as + s * P * nbf + b0;
+        const float* ua = au + s * P * nbf + b0;
+        if (q4)
+            half_terms_q4k<P>(hdr, qs, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
+        else
+            half_terms_q6k<P>(rowp, sb, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
+        // the chain (gemv.rs:141-148) over the unit's lanes in block order
         float acc[P];
 #pragma unroll
         for (int p = 0; p < P; p++) acc[p] = 0.0f;
-        const int8_t* a = aq + (size_t)s * P * F;
-        if (D.fmt == TRK_FMT_Q4_K)
-            down_row_chain_q4k<P, NSB>(rowp, a, F, as + s * P * nbf, au + s * P * nbf, nbf, acc);
-        else
-            down_row_chain_q6k<P>(rowp, nsb, a, F, as + s * P * nbf, au + s * P * nbf, nbf, acc);
-        vres[s * DN_R + r] = P == 2 ? acc[0] + acc[1] : acc[0];  // gemv.rs:154
+#pragma unroll
+        for (int st = 0; st < DL::L; st++) {
+            float in[P];
+#pragma unroll
+            for (int p = 0; p < P; p++) in[p] = st > 0 ? unit_up<DL::L>(acc[p]) : 0.0f;
+            if (q == (uint32_t)st) {
+#pragma unroll
+                for (int p = 0; p < P; p++) {
+                    float v = in[p];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v = __builtin_fmaf(mmv[i], uv[p][i], v);
+                        v = __builtin_fmaf(dotv[p][i], tv[p][i], v);
+                    }
+                    acc[p] = v;
+                }
+            }
+        }
+        if (live && q == (uint32_t)DL::L - 1)
+            vres[s * DN_R + u % DN_R] = P == 2 ? acc[0] + acc[1] : acc[0];  // gemv.rs:154
     }
     __syncthreads();
     if (tid < DN_R) {
-        // slot 0 stores, later slots accumulate (gemv.rs:150-160 with accumulate = slot > 0)
-        float y = vres[tid];
-        for (uint32_t s = 1; s < slots; s++) y = y + vres[s * DN_R + tid];
+        // slot 0 stores, later slots accumulate, the shared expert last (gemv.rs:150-160 with
+        // accumulate = slot > 0; exec.rs:1607-1620)
+        float y = n > 0 ? vres[tid] : vres[kcap * DN_R + tid];
+        for (uint32_t s = 1; s < n; s++) y = y + vres[s * DN_R + tid];
+        if (n > 0) y = y + vres[kcap * DN_R + tid];
         float* o = out + row0 + tid;
         *o = residual ? *o + y : y;
     }
@@ -390,11 +515,11 @@ hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspa
     const uint32_t H = down.rows, F = down.k, nbf = F / 16;
     const int P = pair ? 2 : 1;
     const size_t slots = kcap + 1;
-    const size_t lds = slots * P * F + slots * P * nbf * 8 + slots * DN_R * 4 + 64;
+    const size_t lds = slots * ((size_t)P * F + 16) + slots * P * nbf * 8 + slots * DN_R * 4 + 64;
     switch (F / 256 * 2 + (pair ? 1 : 0)) {
 #define DN_CASE(ns) \
-    case ns * 2: decode_down_kernel<1, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, out, residual); break; \
-    case ns * 2 + 1: decode_down_kernel<2, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, out, residual); break;
+    case ns * 2: decode_down_kernel<1, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break; \
+    case ns * 2 + 1: decode_down_kernel<2, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break;
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
         default: return hipErrorInvalidValue;

@@ -6,11 +6,9 @@
 //                 (c0 + c1) + (c2 + c3) lanewise and the halving tree of _mm512_reduce_add_ps.
 //   router_gemm:  smallgemm::gemm_f32_nt order (smallgemm.rs:8-59): per output, 16 lane chains
 //                 over 16-wide steps, then the halving tree.
-//   route_row:    route_topk / route_mass (router.rs:70-148) for one token on one wave: lanes
-//                 sort their logits, then k rounds of a DPP wave arg-max over the lane heads.
-//   router_route: the decode path's logits and routing in one launch — the last workgroup to
-//                 finish its logits (device-scope counter) routes.
-#include "common.hpp"
+//   route:        one wave per token runs route_row (route.hpp).  The decode path (M = 1) routes
+//                 inside its gate/up kernel instead (k_decode.hip).
+#include "route.hpp"
 
 namespace trk {
 
@@ -55,10 +53,8 @@ __device__ __forceinline__ void dot_rows(const float* __restrict__ wr, const flo
         }
 #pragma unroll
     for (int r = 0; r < DOT_MR; r++) {
-        const float c1 = __shfl(acc[r], (lane + 16) & 63);
-        const float c2 = __shfl(acc[r], (lane + 32) & 63);
-        const float c3 = __shfl(acc[r], (lane + 48) & 63);
-        res[r] = reduce16_lanes((acc[r] + c1) + (c2 + c3));  // H % 16 == 0: no scalar tail
+        if ((uint32_t)r >= mr) break;
+        res[r] = reduce16_lanes(rows4_sum(acc[r]));  // H % 16 == 0: no scalar tail
     }
 }
 
@@ -143,118 +139,16 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
 
 // ---- routing -----------------------------------------------------------------------------------
 
-constexpr int ROUTE_NJ = 16;  // E <= 1024: 16 logits per lane
-
-// order-preserving key of a logit (-0 and +0 share one key, as they compare equal); 0 for values
-// that never enter the top-k (nan, -inf: router.rs:75-76)
-__device__ __forceinline__ uint32_t fkey(float v) {
-    if (!(v > -__builtin_inff())) return 0u;
-    const uint32_t u = __float_as_uint(v + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float fkey_inv(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-__device__ __forceinline__ float rdl(float v, uint32_t l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
-}
-
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// One token on one (whole) wave.  Writes the first `count` ids / weights and returns count.
-// Each lane sorts its NJ logits (value desc, index asc); then k rounds of a wave-wide arg-max over
-// the lanes' heads — exactly the order of the reference's insertion sort (router.rs:70-89).
-// `ex` (E floats of LDS) is used only for MassBasis::All.
-template <int NJ>
-__device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
-                              float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
-    uint32_t key[NJ], jj[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const uint32_t i = lane + 64u * j;
-        key[j] = i < E ? fkey(lg[i]) : 0u;
-        jj[j] = (uint32_t)j;
-    }
-    // odd-even transposition sort, descending key; equal keys keep ascending j (stable)
-#pragma unroll
-    for (int pass = 0; pass < NJ; pass++)
-#pragma unroll
-        for (int j = pass & 1; j + 1 < NJ; j += 2)
-            if (key[j + 1] > key[j]) {
-                const uint32_t tk = key[j], tj = jj[j];
-                key[j] = key[j + 1];
-                jj[j] = jj[j + 1];
-                key[j + 1] = tk;
-                jj[j + 1] = tj;
-            }
-    const uint32_t kk = pol.enabled ? pol.max : k;
-    uint32_t my_key = 0, my_idx = 0xffffffffu, ksel = 0;
-    for (uint32_t rd = 0; rd < kk; rd++) {
-        const uint32_t wmax = wave_max_u32(key[0]);
-        if (wmax == 0u) break;  // no selectable logit left
-        const uint32_t widx = wave_min_u32(key[0] == wmax ? lane + 64u * jj[0] : 0xffffffffu);
-        if (lane == widx % 64u) {  // pop this lane's head
-#pragma unroll
-            for (int j = 0; j + 1 < NJ; j++) {
-                key[j] = key[j + 1];
-                jj[j] = jj[j + 1];
-            }
-            key[NJ - 1] = 0u;
-        }
-        if (lane == rd) {
-            my_key = wmax;
-            my_idx = widx;
-        }
-        ksel = rd + 1;
-    }
-    if (ksel == 0) return 0;  // nothing selectable (the reference would index u32::MAX)
-    const float my_tv = lane < ksel ? fkey_inv(my_key) : -__builtin_inff();
-    const float mx = rdl(my_tv, 0);
-    const float e = lane < kk ? expf_libm(my_tv - mx) : 0.0f;  // slots past ksel: exp(-inf) = 0
-    uint32_t count = kk;
-    if (pol.enabled) {  // route_mass (router.rs:118-148)
-        float denom = 0.0f;
-        if (pol.basis == TRK_BASIS_ALL) {
-            for (uint32_t i = lane; i < E; i += 64u) ex[i] = expf_libm(lg[i] - mx);
-            wave_sync();
-            if (lane == 0)
-                for (uint32_t i = 0; i < E; i++) denom += ex[i];
-            denom = rdl(denom, 0);
-        } else {
-            for (uint32_t j = 0; j < kk; j++) denom += rdl(e, j);
-        }
-        float mass = 0.0f;
-        count = 0;
-        while (count < kk) {
-            mass += rdl(e, count) / denom;
-            count++;
-            if (count >= pol.min && mass >= pol.mass) break;
-        }
-    }
-    if (count > ksel) count = ksel;
-    float sum = 0.0f;  // renorm (router.rs:93-104)
-    for (uint32_t j = 0; j < count; j++) sum += rdl(e, j);
-    if (lane < count) {
-        ids_out[lane] = my_idx;
-        w_out[lane] = e / sum;
-    }
-    return count;
-}
-
 template <int NJ>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, uint32_t m, uint32_t E, uint32_t k,
                                                    Policy pol, uint32_t* __restrict__ ids, float* __restrict__ wout,
                                                    uint32_t* __restrict__ n_sel, unsigned long long* __restrict__ stats) {
+    __shared__ uint2 cand[4][ROUTE_CAND];
     extern __shared__ float ex_all[];  // [4][E] for MassBasis::All
     const uint32_t wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const uint32_t row = blockIdx.x * 4 + wv;
     if (row >= m) return;
-    const uint32_t n = route_row<NJ>(logits + (size_t)row * E, E, k, pol, lane, ex_all + (size_t)wv * E,
+    const uint32_t n = route_row<NJ>(logits + (size_t)row * E, E, k, pol, lane, cand[wv], ex_all + (size_t)wv * E,
                                      ids + (size_t)row * K_MAX, wout + (size_t)row * K_MAX);
     if (lane == 0) {
         n_sel[row] = n;
@@ -271,75 +165,7 @@ hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k,
     if (E <= 512)
         route_kernel<8><<<(m + 3) / 4, 256, lds, st>>>(logits, m, E, k, pol, ids, w, n_sel, stats);
     else
-        route_kernel<ROUTE_NJ><<<(m + 3) / 4, 256, lds, st>>>(logits, m, E, k, pol, ids, w, n_sel, stats);
-    return hipGetLastError();
-}
-
-// ---- decode: logits + routing in one launch ------------------------------------------------------
-
-// Two waves per workgroup compute router rows (dot order) for all m <= ROUTER_ROUTE_MAX_M rows;
-// the workgroup that finishes last (device-scope counter; its fence makes every workgroup's
-// logits visible) routes every row and re-arms the counter for the next launch.
-template <int NJ>
-__global__ __launch_bounds__(128) void router_route_kernel(const float* __restrict__ router,
-                                                          const float* __restrict__ bias,
-                                                          const float* __restrict__ shg,
-                                                          const float* __restrict__ x, uint32_t m, uint32_t E,
-                                                          uint32_t H, float* __restrict__ rlog, float* __restrict__ sh,
-                                                          uint32_t k, Policy pol, uint32_t* __restrict__ ids,
-                                                          float* __restrict__ wout, uint32_t* __restrict__ n_sel,
-                                                          unsigned long long* __restrict__ stats,
-                                                          uint32_t* __restrict__ counter) {
-    __shared__ uint32_t last;
-    extern __shared__ float ex_all[];  // [2][E] for MassBasis::All
-    const uint32_t wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const uint32_t wave = blockIdx.x * 2 + wv;
-    if (wave < E + 1) {
-        const float* wr = wave < E ? router + (size_t)wave * H : shg;
-        for (uint32_t m0 = 0; m0 < m; m0 += DOT_MR) {
-            const uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
-            float res[DOT_MR];
-            dot_rows(wr, x, m0, mr, H, lane, res);
-            if (lane == 0)
-                for (uint32_t r = 0; r < mr; r++) {
-                    if (wave < E)
-                        rlog[(size_t)(m0 + r) * E + wave] = bias ? res[r] + bias[wave] : res[r];
-                    else
-                        sh[m0 + r] = res[r];
-                }
-        }
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(counter, 1u) == gridDim.x - 1 ? 1u : 0u;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (uint32_t row = wv; row < m; row += 2) {
-        const uint32_t n = route_row<NJ>(rlog + (size_t)row * E, E, k, pol, lane, ex_all + (size_t)wv * E,
-                                         ids + (size_t)row * K_MAX, wout + (size_t)row * K_MAX);
-        if (lane == 0) {
-            n_sel[row] = n;
-            if (stats) {
-                atomicAdd(&stats[0], 1ull);
-                atomicAdd(&stats[1], (unsigned long long)n);
-            }
-        }
-    }
-    if (threadIdx.x == 0) *counter = 0u;
-}
-
-hipError_t launch_router_route(const float* router, const float* bias, const float* shexp_gate, const float* x,
-                               uint32_t m, uint32_t E, uint32_t H, float* rlog, float* sh, uint32_t k, Policy pol,
-                               uint32_t* ids, float* w, uint32_t* n_sel, unsigned long long* stats, uint32_t* counter,
-                               hipStream_t st) {
-    const size_t lds = (pol.enabled && pol.basis == TRK_BASIS_ALL) ? (size_t)2 * E * sizeof(float) : 0;
-    if (E <= 512)
-        router_route_kernel<8><<<(E + 2) / 2, 128, lds, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh, k, pol,
-                                                              ids, w, n_sel, stats, counter);
-    else
-        router_route_kernel<ROUTE_NJ><<<(E + 2) / 2, 128, lds, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh, k,
-                                                                     pol, ids, w, n_sel, stats, counter);
+        route_kernel<16><<<(m + 3) / 4, 256, lds, st>>>(logits, m, E, k, pol, ids, w, n_sel, stats);
     return hipGetLastError();
 }
 

@@ -1,0 +1,186 @@
+// Routing of one token on one wave: route_topk / route_mass (crates/tr-kernels/src/router.rs:70-148).
+//
+// Selection.  Each lane holds NJ logits (index lane + 64 j) as order-preserving u32 keys.  The
+// winners come out in exactly the order of the reference's insertion sort: value descending, the
+// lower index first among equal values (a later index only displaces strictly smaller values).
+// NaN and -inf map to key 0 and are never selected, as `v > top_v[k-1]` never holds for them.
+//
+// Weights.  exp of (v - max) in f32 through a double exp (Rust's f32::exp, see expf_libm), the
+// mass loop of route_mass, then the renormalisation of renorm() with its sequential f32 sum.
+#pragma once
+
+#include "common.hpp"
+
+namespace trk {
+
+// order-preserving key of a logit (-0 and +0 share one key, as they compare equal); 0 for values
+// that never enter the top-k (nan, -inf: router.rs:75-76)
+__device__ __forceinline__ uint32_t fkey(float v) {
+    if (!(v > -__builtin_inff())) return 0u;
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ float rdl(float v, uint32_t l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Fallback selection (more than 64 candidates, i.e. many equal logits): each lane sorts its keys
+// (key desc, j asc), then kk rounds of a wave arg-max over the lane heads.  Lane rd < ksel gets
+// the key and index of the rd-th winner; returns ksel.
+template <int NJ>
+__device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict__ lg, uint32_t E, uint32_t kk,
+                                                        uint32_t lane, uint32_t& my_key, uint32_t& my_idx) {
+    uint32_t key[NJ], jj[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const uint32_t i = lane + 64u * j;
+        key[j] = i < E ? fkey(lg[i]) : 0u;
+        jj[j] = (uint32_t)j;
+    }
+    // odd-even transposition sort, descending key; equal keys keep ascending j (stable)
+#pragma unroll
+    for (int pass = 0; pass < NJ; pass++)
+#pragma unroll
+        for (int j = pass & 1; j + 1 < NJ; j += 2)
+            if (key[j + 1] > key[j]) {
+                const uint32_t tk = key[j], tj = jj[j];
+                key[j] = key[j + 1];
+                jj[j] = jj[j + 1];
+                key[j + 1] = tk;
+                jj[j + 1] = tj;
+            }
+    uint32_t ksel = 0;
+    for (uint32_t rd = 0; rd < kk; rd++) {
+        const uint32_t wmax = wave_max_u32(key[0]);
+        if (wmax == 0u) break;  // no selectable logit left
+        const uint32_t widx = wave_min_u32(key[0] == wmax ? lane + 64u * jj[0] : 0xffffffffu);
+        if (lane == widx % 64u) {  // pop this lane's head
+#pragma unroll
+            for (int j = 0; j + 1 < NJ; j++) {
+                key[j] = key[j + 1];
+                jj[j] = jj[j + 1];
+            }
+            key[NJ - 1] = 0u;
+        }
+        if (lane == rd) {
+            my_key = wmax;
+            my_idx = widx;
+        }
+        ksel = rd + 1;
+    }
+    return ksel;
+}
+
+// One token on one whole wave.  Lanes < count write ids_out[lane] / w_out[lane]; returns count.
+// `cand` is 96 entries of LDS for this wave; `ex` (E floats of LDS) is used only for
+// MassBasis::All.
+//
+// Selection: T = the kk-th largest of the 64 lane maxima (a 32-step radix select over ballots) is
+// a lower bound on the kk-th largest key, since the kk lanes with the largest maxima hold kk keys
+// >= T.  The keys >= T (usually a few more than kk) are compacted into LDS in ascending index
+// order; each candidate's rank is the number of candidates with a larger key plus the earlier
+// ones with an equal key, and the candidates of rank < kk are written to their rank's slot.
+template <int NJ>
+__device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
+                              uint2* cand, float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
+    uint32_t key[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const uint32_t i = lane + 64u * j;
+        key[j] = i < E ? fkey(lg[i]) : 0u;
+    }
+    const uint32_t kk = pol.enabled ? pol.max : k;
+    uint32_t lmax = key[0];
+#pragma unroll
+    for (int j = 1; j < NJ; j++) lmax = lmax > key[j] ? lmax : key[j];
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t t = T | (1u << b);
+        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= kk) T = t;
+    }
+    const uint32_t L = T > 1u ? T : 1u;  // key 0 (nan, -inf) is never selectable
+    uint32_t C = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const bool c = key[j] >= L;
+        const uint64_t m = __ballot(c);
+        if (c) {
+            const uint32_t pos =
+                    C + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (pos < 64u) cand[pos] = make_uint2(key[j], lane + 64u * j);
+        }
+        C += (uint32_t)__popcll(m);
+    }
+    uint32_t my_key = 0, my_idx = 0xffffffffu, ksel;
+    if (C <= 64u) {
+        wave_sync();
+        if (lane < C) {
+            const uint2 me = cand[lane];
+            uint32_t rank = 0;
+            for (uint32_t t = 0; t < C; t++) {
+                const uint32_t kt = cand[t].x;
+                rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
+            }
+            if (rank < kk) cand[64 + rank] = me;
+        }
+        wave_sync();
+        ksel = C < kk ? C : kk;
+        if (lane < ksel) {
+            const uint2 w = cand[64 + lane];
+            my_key = w.x;
+            my_idx = w.y;
+        }
+    } else {
+        ksel = route_select_rounds<NJ>(lg, E, kk, lane, my_key, my_idx);
+    }
+    if (ksel == 0) return 0;  // nothing selectable (the reference would index u32::MAX)
+    const float my_tv = lane < ksel ? fkey_inv(my_key) : -__builtin_inff();
+    const float mx = rdl(my_tv, 0);
+    const float e = lane < kk ? expf_libm(my_tv - mx) : 0.0f;  // slots past ksel: exp(-inf) = 0
+    uint32_t count = kk;
+    if (pol.enabled) {  // route_mass (router.rs:118-148)
+        float denom = 0.0f;
+        if (pol.basis == TRK_BASIS_ALL) {
+            for (uint32_t i = lane; i < E; i += 64u) ex[i] = expf_libm(lg[i] - mx);
+            wave_sync();
+            if (lane == 0)
+                for (uint32_t i = 0; i < E; i++) denom += ex[i];
+            denom = rdl(denom, 0);
+        } else {
+            for (uint32_t j = 0; j < kk; j++) denom += rdl(e, j);
+        }
+        float mass = 0.0f;
+        count = 0;
+        while (count < kk) {
+            mass += rdl(e, count) / denom;
+            count++;
+            if (count >= pol.min && mass >= pol.mass) break;
+        }
+    }
+    if (count > ksel) count = ksel;
+    float sum = 0.0f;  // renorm (router.rs:93-104)
+    for (uint32_t j = 0; j < count; j++) sum += rdl(e, j);
+    if (lane < count) {
+        ids_out[lane] = my_idx;
+        w_out[lane] = e / sum;
+    }
+    return count;
+}
+
+constexpr uint32_t ROUTE_CAND = 96;  // LDS entries (uint2) of route_row's candidate lists per wave
+
+// Logits per lane for E experts: 8 up to 512 experts, 16 up to 1024.
+constexpr uint32_t route_nj(uint32_t E) { return E <= 512 ? 8u : 16u; }
+
+}  // namespace trk

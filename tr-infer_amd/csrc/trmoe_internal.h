@@ -73,12 +73,9 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
                                 hipStream_t st);
 hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
-hipError_t launch_router_route(const float* router, const float* bias, const float* shexp_gate, const float* x,
-                               uint32_t m, uint32_t E, uint32_t H, float* rlog, float* sh, uint32_t k, Policy pol,
-                               uint32_t* ids, float* w, uint32_t* n_sel, unsigned long long* stats, uint32_t* counter,
-                               hipStream_t st);
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
-                                const Workspace& ws, int pair, uint32_t kcap, hipStream_t st);
+                                const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
+                                hipStream_t st);
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, hipStream_t st);
