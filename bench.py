@@ -34,16 +34,8 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def zipf_bias(seed, E, s=1.1):
-    """Router bias b_e = log p_{pi(e)}, p_j ~ j^-s over a seeded permutation."""
-    import numpy as np
-    rng = np.random.default_rng(seed)
-    perm = rng.permutation(E)
-    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
-    p /= p.sum()
-    b = np.zeros(E, np.float32)
-    b[perm] = np.log(p).astype(np.float32)
-    return b
+DECODE_KERNELS = ("router_logits", "decode_gateup", "decode_down")
+BATCH_KERNELS = ("router_logits", "route", "quantize", "dispatch", "batch_gateup", "batch_down", "batch_combine")
 
 
 def layer_bytes(n_experts_touched, M):
@@ -66,6 +58,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
+                    help="finish with three device copies of MIB MiB (a known-size kernel for calibrating "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -85,7 +80,7 @@ def main():
     m_max = max(ms_list)
 
     t0 = time.time()
-    bias = torch.from_numpy(zipf_bias(1, E)).to(dev)
+    bias = torch.from_numpy(trmoe.zipf_bias(1, E)).to(dev)
     layers = [trmoe.LayerWeights.generate(1, l, H, E, F, device=dev) for l in range(args.layers)]
     torch.cuda.synchronize()
     log(f"generated {args.layers} layers ({args.layers * E * EXPERT_BYTES / 1e9:.1f} GB experts) in {time.time() - t0:.1f}s")
@@ -140,12 +135,19 @@ def main():
             del g
         nbytes = sum(layer_bytes(touched[i % args.layers], M) for i in range(args.steps)) / args.steps
         nops = sum(layer_ops(ents[i % args.layers], M) for i in range(args.steps)) / args.steps
-        # per-kernel durations over the same rotation (events around each launch, same stream)
-        ctx.set_timing(True)
-        for i in range(args.steps):
-            ctx.forward(weights(i % args.layers, M), x, out[:M])
-        kern = ctx.timing()
-        ctx.set_timing(False)
+        # per-kernel durations: each kernel of the sequence alone, launched K times back to back
+        # over the same layer rotation, between two events on the launch stream (the workspace
+        # holds the last forward's routing and activations, so every launch does a real call's
+        # work on cold weights)
+        kern = {}
+        for name in (DECODE_KERNELS if M == 1 else BATCH_KERNELS):
+            ctx.forward(weights(0, M), x, out[:M])
+            ev0.record(stream)
+            for i in range(args.steps):
+                ctx.launch_kernel(name, weights(i % args.layers, M), x, out[:M])
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            kern[name] = (ev0.elapsed_time(ev1), args.steps)
         results[M] = dict(
             tokens_per_s=M / (per * 1e-3), us_per_layer=per * 1e3, us_per_layer_eager=per_eager * 1e3,
             layer_GBps=nbytes / (per * 1e-3) / 1e9,
@@ -174,8 +176,8 @@ def main():
     if alg:
         ach = alg / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": int(alg),
-                "avg_launch_us": round(avg_ms * 1e3, 2)}
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, prim),
+                "alg_bytes_per_launch": int(alg), "avg_launch_us": round(avg_ms * 1e3, 2)}
 
     cpu = None
     if not args.no_cpu and prim == 1:
@@ -195,6 +197,27 @@ def main():
                                if not k.startswith("_")} for M, res in results.items()},
     }
     print(json.dumps(line), flush=True)
+    if args.copy_cal:
+        n = args.copy_cal << 18  # floats
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copies: 3 x {args.copy_cal} MiB")
+
+
+def measured_traffic(kernel, m):
+    """HBM bytes per launch of `kernel` at M = m from the committed rocprofv3 counter passes
+    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of known
+    size), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t[f"{kernel}@M={m}"]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(w, x_dev, seconds):

@@ -164,6 +164,10 @@ int trk_add_inplace(float *y, const float *a, size_t n, void *stream);
  * uniform; fmt Q4_K or Q6_K. */
 int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
                  float dhi, void *out, void *stream);
+/* The same for a stack of `count` matrices `stride` bytes apart, matrix e drawing from stream
+ * stream0 + e * stream_step (one launch; what trk_gen_gguf gives per matrix). */
+int trk_gen_gguf_stack(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t stream_step, uint32_t count,
+                       uint32_t rows, uint32_t k, float dlo, float dhi, void *out, uint64_t stride, void *stream);
 /* n normals N(0, sigma) (Box-Muller in double, rounded to f32). */
 int trk_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float *out, void *stream);
 
@@ -174,6 +178,13 @@ int trk_set_timing(trk_ctx *ctx, int on);
 /* Sum of the recorded durations per kernel since the last call, then forget them (synchronises).
  * Fills up to cap entries (kernel name, total ms, launches); returns the number of kernels. */
 int trk_get_timing(trk_ctx *ctx, const char **names, double *ms, uint64_t *launches, int cap);
+
+/* Launch only the kernel `name` (a name trk_get_timing reports) of the forward sequence for
+ * (w, x, rlog, m, out), on the workspace as the previous calls left it.  For timing one kernel in
+ * isolation (bench.py; the reference's kbench, crates/tr-kernels/benches): the results are only
+ * meaningful when the calls before it prepared the workspace for the same inputs. */
+int trk_launch_kernel(trk_ctx *ctx, const trk_moe_w *w, const float *x, const float *rlog, uint32_t m,
+                      float *out, const char *name, void *stream);
 
 /* Copy an internal workspace buffer of the last forward to host memory (synchronises). */
 enum {

@@ -14,6 +14,10 @@
  *   - the lane order of _mm512_reduce_add_ps (taken as the halving tree 16->8->4->2->1, the
  *     order Intel documents and stdarch implements) inside dot / gemm_f32_nt / sumsq;
  *   - Rust's f32::exp, taken as glibc expf (what rustc links on x86_64 Linux).
+ * One piece has no reference at all and is "parity unpinned":
+ *   - Q6_K (orc_q6k_rows and its uses): the reference has no Q6_K converter or kernel; this
+ *     restatement's mapping (unsigned 6-bit q, dd = f16(d*sc), mm = f16(-32*dd), one block per
+ *     scale) is checked only against a brute-force f64 dequantisation of the same bytes.
  */
 #ifndef TR_ORACLE_H
 #define TR_ORACLE_H

@@ -31,14 +31,9 @@ def stream(layer, tid):
 
 
 def zipf_bias(seed, E, s=1.1, layer=0):
-    """b_e = log p_{pi(e)}, p_j ~ 1/j^s over a seeded permutation pi."""
-    keys = np.array([O.rng_u64(seed, stream(layer, T_BIAS), e) for e in range(E)], np.uint64)
-    perm = np.argsort(keys, kind="stable")  # perm[j] = expert with rank j
-    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
-    p /= p.sum()
-    b = np.zeros(E, np.float32)
-    b[perm] = np.log(p).astype(np.float32)
-    return b
+    """The package's Zipf router bias on this layer's bias stream."""
+    import trmoe
+    return trmoe.zipf_bias(seed, E, s, stream_id=stream(layer, T_BIAS))
 
 
 class Layer:

@@ -253,11 +253,15 @@ static hipError_t timed(trk_ctx* c, int kid, hipStream_t st, F&& launch) {
     c->timed.push_back(t);
     return hipSuccess;
 }
-#define TIMED(kid, expr) HIP_TRY(timed(c, kid, st, [&]() { return (expr); }))
+// One launch of the forward sequence; with `only` >= 0, only the kernel of that id is launched.
+#define TIMED(kid, expr)                                                              \
+    do {                                                                              \
+        if (only < 0 || only == (kid)) HIP_TRY(timed(c, kid, st, [&]() { return (expr); })); \
+    } while (0)
 
 // The MoE block on x (already normed).  residual: out += moe instead of out = moe.
 static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m, float* out,
-                   int residual, hipStream_t st) {
+                   int residual, hipStream_t st, int only = -1) {
     Mats M;
     int rc = check_weights(c, w, M);
     if (rc) return rc;
@@ -302,11 +306,20 @@ extern "C" int trk_moe_forward(trk_ctx* c, const trk_moe_w* w, const float* x, c
     return forward(c, w, x, rlog, m, out, 0, (hipStream_t)stream);
 }
 
+extern "C" int trk_launch_kernel(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m,
+                                 float* out, const char* name, void* stream) {
+    if (!c || !name) return fail(TRK_E_INVALID, "null argument");
+    for (int kid = 0; kid < K_COUNT; kid++)
+        if (std::strcmp(name, kKernelNames[kid]) == 0) return forward(c, w, x, rlog, m, out, 0, (hipStream_t)stream, kid);
+    return fail(TRK_E_INVALID, "no kernel named '%s'", name);
+}
+
 extern "C" int trk_moe_residual(trk_ctx* c, const trk_moe_w* w, const float* rms_w, float eps, float* h, uint32_t m,
                                 void* stream) {
     if (!c || !h) return fail(TRK_E_INVALID, "null argument");
     if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
     hipStream_t st = (hipStream_t)stream;
+    const int only = -1;
     TIMED(K_RMSNORM, launch_rmsnorm(h, rms_w, eps, m, c->cfg.hidden, c->ws.xn, st));
     return forward(c, w, c->ws.xn, nullptr, m, h, 1, st);
 }
@@ -478,7 +491,22 @@ extern "C" int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uin
     if (!out) return fail(TRK_E_INVALID, "null argument");
     if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K) || k % 256) return fail(TRK_E_INVALID, "bad format/k");
     if (rows == 0) return TRK_OK;
-    HIP_TRY(launch_gen_gguf(fmt, seed, stream_id, rows, k, dlo, dhi, out, (hipStream_t)stream));
+    HIP_TRY(launch_gen_gguf(fmt, seed, stream_id, 0, 1, rows, k, dlo, dhi, out, 0, (hipStream_t)stream));
+    return TRK_OK;
+}
+
+extern "C" int trk_gen_gguf_stack(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t stream_step,
+                                  uint32_t count, uint32_t rows, uint32_t k, float dlo, float dhi, void* out,
+                                  uint64_t stride, void* stream) {
+    if (!out) return fail(TRK_E_INVALID, "null argument");
+    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K) || k % 256) return fail(TRK_E_INVALID, "bad format/k");
+    const uint64_t mb = (uint64_t)rows * (k / 256) * (fmt == TRK_FMT_Q6_K ? 210 : 144);
+    if (count > 1 && stride < mb) return fail(TRK_E_INVALID, "stride %llu below matrix bytes %llu",
+                                              (unsigned long long)stride, (unsigned long long)mb);
+    if (count > 65535) return fail(TRK_E_INVALID, "count (%u) above 65535", count);
+    if (rows == 0 || count == 0) return TRK_OK;
+    HIP_TRY(launch_gen_gguf(fmt, seed, stream0, stream_step, count, rows, k, dlo, dhi, out, stride,
+                            (hipStream_t)stream));
     return TRK_OK;
 }
 

@@ -251,47 +251,44 @@ __device__ __forceinline__ float unif24(uint64_t r, float lo, float hi) {
     return lo + p;
 }
 
-// one thread per 8-byte word of a superblock (18 words for Q4_K, 27 for Q6_K)
-__global__ void gen_gguf_kernel(uint32_t fmt, uint64_t key, size_t nsb, float dlo, float dhi, uint8_t* out) {
-    size_t sbb = fmt == TRK_FMT_Q6_K ? 210 : 144;
-    size_t nw = (sbb + 7) / 8;
-    size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+// one thread per 8-byte word of a superblock (18 words for Q4_K, 27 for Q6_K); grid.y runs over
+// the `count` matrices of a stack, matrix e drawing from stream stream0 + e * step
+__global__ void gen_gguf_kernel(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t step, size_t nsb,
+                                uint64_t stride, float dlo, float dhi, uint8_t* out) {
+    const size_t sbb = fmt == TRK_FMT_Q6_K ? 210 : 144;
+    const size_t nw = (sbb + 7) / 8;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= nsb * nw) return;
-    size_t sb = t / nw, wi = t % nw;
-    uint8_t* b = out + sb * sbb;
-    uint64_t r = rng_u64(key, sb * 32 + wi);
-    uint64_t rd = rng_u64(key, sb * 32 + 31);
+    const uint64_t key = mix64(seed ^ mix64(stream0 + (uint64_t)blockIdx.y * step));  // as orc_rng_u64
+    const size_t sb = t / nw, wi = t % nw;
+    uint8_t* b = out + (size_t)blockIdx.y * stride + sb * sbb;
+    const uint64_t r = rng_u64(key, sb * 32 + wi);
+    const uint64_t rd = rng_u64(key, sb * 32 + 31);
     for (int j = 0; j < 8; j++) {
-        size_t o = wi * 8 + j;
+        const size_t o = wi * 8 + j;
         if (o >= sbb) break;
         uint8_t v = (uint8_t)(r >> (8 * j));
         if (fmt == TRK_FMT_Q6_K) {
             if (o == 208 || o == 209) {
-                uint16_t d = f2h(unif24(rd, dlo, dhi));
+                const uint16_t d = f2h(unif24(rd, dlo, dhi));
                 v = o == 208 ? (uint8_t)(d & 0xff) : (uint8_t)(d >> 8);
             }
         } else if (o < 4) {
-            uint16_t d = f2h(unif24(o < 2 ? rd : rd >> 24, dlo, dhi));
+            const uint16_t d = f2h(unif24(o < 2 ? rd : rd >> 24, dlo, dhi));
             v = (o & 1) ? (uint8_t)(d >> 8) : (uint8_t)(d & 0xff);
         }
         b[o] = v;
     }
 }
 
-hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
-                           float dhi, void* out, hipStream_t st) {
-    // key = mix64(seed ^ mix64(stream)), as orc_rng_u64
-    auto hmix = [](uint64_t z) {
-        z += 0x9e3779b97f4a7c15ull;
-        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-        return z ^ (z >> 31);
-    };
-    uint64_t key = hmix(seed ^ hmix(stream_id));
-    size_t nsb = (size_t)rows * (k / 256);
-    size_t nw = fmt == TRK_FMT_Q6_K ? 27 : 18;
-    size_t n = nsb * nw;
-    gen_gguf_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(fmt, key, nsb, dlo, dhi, (uint8_t*)out);
+hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t step, uint32_t count,
+                           uint32_t rows, uint32_t k, float dlo, float dhi, void* out, uint64_t stride,
+                           hipStream_t st) {
+    const size_t nsb = (size_t)rows * (k / 256);
+    const size_t nw = fmt == TRK_FMT_Q6_K ? 27 : 18;
+    const size_t n = nsb * nw;
+    gen_gguf_kernel<<<dim3((unsigned)((n + 255) / 256), count), 256, 0, st>>>(fmt, seed, stream0, step, nsb, stride,
+                                                                               dlo, dhi, (uint8_t*)out);
     return hipGetLastError();
 }
 

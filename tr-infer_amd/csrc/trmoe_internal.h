@@ -91,8 +91,9 @@ hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hip
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
                           hipStream_t st);
 hipError_t launch_add(float* y, const float* a, size_t n, hipStream_t st);
-hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k,
-                           float dlo, float dhi, void* out, hipStream_t st);
+hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t step, uint32_t count,
+                           uint32_t rows, uint32_t k, float dlo, float dhi, void* out, uint64_t stride,
+                           hipStream_t st);
 hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float* out,
                              hipStream_t st);
 

@@ -76,8 +76,10 @@ def lib() -> C.CDLL:
         L.trk_rmsnorm.argtypes = [vp, vp, f, u32, u32, vp, vp]
         L.trk_add_inplace.argtypes = [vp, vp, sz, vp]
         L.trk_gen_gguf.argtypes = [u32, u64, u64, u32, u32, f, f, vp, vp]
+        L.trk_gen_gguf_stack.argtypes = [u32, u64, u64, u64, u32, u32, u32, f, f, vp, u64, vp]
         L.trk_gen_normal.argtypes = [u64, u64, sz, C.c_double, vp, vp]
         L.trk_debug_read.argtypes = [vp, i, vp, sz]
+        L.trk_launch_kernel.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, C.c_char_p, vp]
         L.trk_set_timing.argtypes = [vp, i]
         L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
         _lib = L
@@ -142,6 +144,11 @@ class Context:
     def forward(self, w: "LayerWeights", x, out, rlog=None, stream=None):
         check(lib().trk_moe_forward(self.h, C.byref(w.moew), _ptr(x), _ptr(rlog), x.shape[0], _ptr(out),
                                     _stream(stream)))
+
+    def launch_kernel(self, name: str, w: "LayerWeights", x, out, rlog=None, stream=None):
+        """Launch one kernel of the forward sequence (timing in isolation; see trk_launch_kernel)."""
+        check(lib().trk_launch_kernel(self.h, C.byref(w.moew), _ptr(x), _ptr(rlog), x.shape[0], _ptr(out),
+                                      name.encode(), _stream(stream)))
 
     def residual(self, w: "LayerWeights", rms_w, eps, h, stream=None):
         check(lib().trk_moe_residual(self.h, C.byref(w.moew), _ptr(rms_w), eps, _ptr(h), h.shape[0], _stream(stream)))
@@ -224,10 +231,9 @@ class LayerWeights:
         gate = torch.empty((E, F * gb), dtype=torch.uint8, device=device)
         up = torch.empty((E, F * gb), dtype=torch.uint8, device=device)
         down = torch.empty((E, H * db), dtype=torch.uint8, device=device)
-        for e in range(E):
-            check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(16 + 3 * e), F, H, 1e-4, 2e-3, C.c_void_p(gate[e].data_ptr()), st))
-            check(L.trk_gen_gguf(FMT_Q4_K, seed, sid(17 + 3 * e), F, H, 1e-4, 2e-3, C.c_void_p(up[e].data_ptr()), st))
-            check(L.trk_gen_gguf(down_fmt, seed, sid(18 + 3 * e), H, F, 1e-4, 2e-3, C.c_void_p(down[e].data_ptr()), st))
+        # expert e: gate / up / down from streams 16 + 3e, 17 + 3e, 18 + 3e of this layer
+        for t, fmt, rows, k, buf in ((gate, FMT_Q4_K, F, H, 16), (up, FMT_Q4_K, F, H, 17), (down, down_fmt, H, F, 18)):
+            check(L.trk_gen_gguf_stack(fmt, seed, sid(buf), 3, E, rows, k, 1e-4, 2e-3, _ptr(t), t.stride(0), st))
         sh_gate = torch.empty(F * gb, dtype=torch.uint8, device=device)
         sh_up = torch.empty(F * gb, dtype=torch.uint8, device=device)
         sh_down = torch.empty(H * db, dtype=torch.uint8, device=device)
@@ -312,3 +318,44 @@ def gen_normal(seed, stream_id, n, sigma=1.0, device="cuda", stream=None):
     out = torch.empty(n, dtype=torch.float32, device=device)
     check(lib().trk_gen_normal(seed, stream_id, n, sigma, _ptr(out), _stream(stream)))
     return out
+
+
+# ---- synthetic workloads ------------------------------------------------------------------------
+
+_M64 = (1 << 64) - 1
+
+
+def _mix64(z: int) -> int:
+    z = (z + 0x9E3779B97F4A7C15) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def rng_u64(seed: int, stream_id: int, idx: int) -> int:
+    """The counter-based draw that trk_gen_gguf / trk_gen_normal use: one u64 per (seed, stream, idx)."""
+    key = _mix64((seed ^ _mix64(stream_id)) & _M64)
+    return _mix64((key + idx * 0xD1B54A32D192ED03) & _M64)
+
+
+# Scale of the Zipf log-probabilities in the router bias.  Top-k over logits + log p (with the
+# router's N(0, 0.905^2) logits) concentrates the load far beyond Zipf: only ~99 experts are
+# touched at M = 512.  The load the Zipf(1.1) config describes is that of drawing k distinct
+# experts per token from p (Gumbel-top-k: 464 experts touched, 48 empty, median group 3 at
+# M = 512, k = 10).  Scaling log p by 0.40 reproduces the touched and empty counts (464, 48;
+# median 4, largest group ~290 instead of ~470), found by simulating top-10 over i.i.d.
+# N(0, 0.905^2) logits.
+ZIPF_BIAS_SCALE = 0.40
+
+
+def zipf_bias(seed: int, E: int, s: float = 1.1, scale: float = ZIPF_BIAS_SCALE, stream_id: int = 5):
+    """Router bias b_e = scale * log p_{pi(e)}, p_j ~ j^-s, over the permutation pi that sorts
+    rng_u64(seed, stream_id, e) (float32 numpy array of E)."""
+    import numpy as np
+    keys = np.array([rng_u64(seed, stream_id, e) for e in range(E)], np.uint64)
+    perm = np.argsort(keys, kind="stable")  # perm[j] = the expert of rank j
+    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
+    p /= p.sum()
+    b = np.zeros(E, np.float32)
+    b[perm] = (scale * np.log(p)).astype(np.float32)
+    return b
