@@ -138,16 +138,23 @@ def main():
         # per-kernel durations: each kernel of the sequence alone, launched K times back to back
         # over the same layer rotation, between two events on the launch stream (the workspace
         # holds the last forward's routing and activations, so every launch does a real call's
-        # work on cold weights)
+        # work on cold weights); the K launches are captured into a HIP graph so that host launch
+        # cost does not hide short kernels
         kern = {}
         for name in (DECODE_KERNELS if M == 1 else BATCH_KERNELS):
             ctx.forward(weights(0, M), x, out[:M])
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(args.steps):
+                    ctx.launch_kernel(name, weights(i % args.layers, M), x, out[:M])
+            g.replay()
+            torch.cuda.synchronize()
             ev0.record(stream)
-            for i in range(args.steps):
-                ctx.launch_kernel(name, weights(i % args.layers, M), x, out[:M])
+            g.replay()
             ev1.record(stream)
             torch.cuda.synchronize()
             kern[name] = (ev0.elapsed_time(ev1), args.steps)
+            del g
         results[M] = dict(
             tokens_per_s=M / (per * 1e-3), us_per_layer=per * 1e3, us_per_layer_eager=per_eager * 1e3,
             layer_GBps=nbytes / (per * 1e-3) / 1e9,

@@ -104,7 +104,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
     ws.m_max = cfg->m_max;
     ws.k_cap = k_cap;
     ws.ent_cap = (uint32_t)(M * k_cap);
-    ws.item_cap = E + (ws.ent_cap + 63) / 64 + (uint32_t)((M + 63) / 64) + 1;  // items of <= 64 rows
+    ws.item_cap = E + (ws.ent_cap + 15) / 16 + (uint32_t)((M + 15) / 16) + 1;  // items of <= 16 rows
     ws.act_rows = std::max<size_t>((size_t)(TRK_MOE_K_MAX + 1) * 2, (size_t)ws.ent_cap + M);
 
     // carve one allocation (256-byte aligned pieces)
@@ -292,7 +292,7 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
                                                  ws.rlog, ws.shl, st));
         TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
         TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, ws.xu, st));
-        TIMED(K_DISPATCH, launch_dispatch(ws, m, st));
+        TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));
         TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, st));
         TIMED(K_B_COMBINE, launch_batch_combine(ws, m, out, residual, st));

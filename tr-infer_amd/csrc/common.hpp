@@ -167,6 +167,13 @@ __device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, floa
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// LDS writes of this wave visible to its own later reads (no workgroup barrier)
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---- wave-wide reductions with DPP (row shifts, then row broadcasts 15 / 31) ----------------------
 // The result of the running scan sits in lane 63; it is returned in every lane (readlane).
 template <bool MAX>

@@ -14,16 +14,31 @@
 //             reference's overwrite-then-accumulate order, exec_batch.rs:1539-1561).
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace trk {
 
-constexpr uint32_t BR = 64;  // entry rows per work item: 4 waves x one 16-row MFMA tile
+constexpr uint32_t BR = 16;  // entry rows per work item: one 16-row MFMA tile
 constexpr uint32_t DISPATCH_WAVES = 8;
 constexpr uint32_t NO_EXPERT = 0xffffffffu;
 
 __device__ __forceinline__ uint32_t popc64(unsigned long long v) { return (uint32_t)__popcll(v); }
 
-// single workgroup (DISPATCH_WAVES waves)
-__global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m) {
+// A token's selected experts: the first ceil(kcap / 4) 16-byte pieces of its id row, all requested
+// at once; returns n_sel.
+__device__ __forceinline__ uint32_t load_ids(const Workspace& ws, uint32_t t, uint32_t kc4, uint32_t (&id)[K_MAX]) {
+    const uint32_t ns = ws.n_sel[t];
+#pragma unroll
+    for (uint32_t q = 0; q < K_MAX / 4; q++)
+        if (q < kc4) {
+            const uint4 v = reinterpret_cast<const uint4*>(ws.ids + (size_t)t * K_MAX)[q];
+            id[4 * q] = v.x; id[4 * q + 1] = v.y; id[4 * q + 2] = v.z; id[4 * q + 3] = v.w;
+        }
+    return ns;
+}
+
+// single workgroup (DISPATCH_WAVES waves); kc4 = ceil(largest selection / 4)
+__global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m, uint32_t kc4) {
     const uint32_t E = ws.E, tid = threadIdx.x, nt = blockDim.x;
     const uint32_t wv = tid / 64, lane = tid % 64;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -38,8 +53,11 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     for (uint32_t e = tid; e < E; e += nt) cnt[e] = 0;
     __syncthreads();
     for (uint32_t t = tid; t < m; t += nt) {
-        const uint32_t ns = ws.n_sel[t];
-        for (uint32_t s = 0; s < ns; s++) atomicAdd(&cnt[ws.ids[(size_t)t * K_MAX + s]], 1u);
+        uint32_t id[K_MAX];
+        const uint32_t ns = load_ids(ws, t, kc4, id);
+#pragma unroll
+        for (uint32_t s = 0; s < K_MAX; s++)
+            if (s < ns) atomicAdd(&cnt[id[s]], 1u);
     }
     __syncthreads();
     // exclusive scans over experts: entry starts, and group index of each non-empty expert
@@ -80,11 +98,11 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         __syncthreads();
         const uint32_t c = c0 + wv, t = c * 64 + lane;
         const bool live = c < nchunks && t < m;
-        const uint32_t ns = live ? ws.n_sel[t] : 0u;
-        for (uint32_t s = 0; s < ns; s++) {
-            const uint32_t e = ws.ids[(size_t)t * K_MAX + s];
-            atomicOr(&masks[(wv * E + e) * 2 + (lane >> 5)], 1u << (lane & 31));
-        }
+        uint32_t id[K_MAX];
+        const uint32_t ns = live ? load_ids(ws, t, kc4, id) : 0u;
+#pragma unroll
+        for (uint32_t s = 0; s < K_MAX; s++)
+            if (s < ns) atomicOr(&masks[(wv * E + id[s]) * 2 + (lane >> 5)], 1u << (lane & 31));
         __syncthreads();
         for (uint32_t e = tid; e < E; e += nt) {
             uint32_t r = run[e];
@@ -96,16 +114,25 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         }
         __syncthreads();
         const unsigned long long below = lane ? ((1ull << lane) - 1ull) : 0ull;
-        for (uint32_t s = 0; s < ns; s++) {
-            const uint32_t e = ws.ids[(size_t)t * K_MAX + s];
-            const unsigned long long mk = (unsigned long long)masks[(wv * E + e) * 2] |
-                                          ((unsigned long long)masks[(wv * E + e) * 2 + 1] << 32);
-            const uint32_t pos = off[wv * E + e] + popc64(mk & below);
-            ws.ent_tok[pos] = t;
-            ws.ent_w[pos] = ws.w[(size_t)t * K_MAX + s];
-            ws.ent_exp[pos] = e;
-            ws.ent_of[(size_t)t * K_MAX + s] = pos;
-        }
+        float wt[K_MAX];
+#pragma unroll
+        for (uint32_t q = 0; q < K_MAX / 4; q++)
+            if (q < kc4 && live) {
+                const float4 v = reinterpret_cast<const float4*>(ws.w + (size_t)t * K_MAX)[q];
+                wt[4 * q] = v.x; wt[4 * q + 1] = v.y; wt[4 * q + 2] = v.z; wt[4 * q + 3] = v.w;
+            }
+#pragma unroll
+        for (uint32_t s = 0; s < K_MAX; s++)
+            if (s < ns) {
+                const uint32_t e = id[s];
+                const unsigned long long mk = (unsigned long long)masks[(wv * E + e) * 2] |
+                                              ((unsigned long long)masks[(wv * E + e) * 2 + 1] << 32);
+                const uint32_t pos = off[wv * E + e] + popc64(mk & below);
+                ws.ent_tok[pos] = t;
+                ws.ent_w[pos] = wt[s];
+                ws.ent_exp[pos] = e;
+                ws.ent_of[(size_t)t * K_MAX + s] = pos;
+            }
         __syncthreads();
     }
     // group table (only non-empty experts, ascending) and work items
@@ -149,10 +176,10 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     }
 }
 
-hipError_t launch_dispatch(const Workspace& ws, uint32_t m, hipStream_t st) {
+hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st) {
     const size_t E = ws.E;
     size_t lds = (4 * E + DISPATCH_WAVES * E + 2 * E + DISPATCH_WAVES * E * 2) * 4;
-    dispatch_kernel<<<1, DISPATCH_WAVES * 64, lds, st>>>(ws, m);
+    dispatch_kernel<<<1, DISPATCH_WAVES * 64, lds, st>>>(ws, m, (kcap + 3) / 4);
     return hipGetLastError();
 }
 
@@ -185,16 +212,74 @@ __device__ __forceinline__ uint32_t item_token(const Workspace& ws, const Item& 
     return shared ? it.row0 + r : ws.ent_tok[it.row0 + r];
 }
 
+// Shared by the two grouped kernels.  A workgroup takes one item (<= 16 entry rows of one expert,
+// or <= 16 tokens of the shared expert) and a range of 16-row weight strips, one strip per wave at
+// a time.  The item's int8 activations are staged once in LDS in MFMA operand order (block b,
+// lane l -> the 8 bytes A[row l%16][k 8(l/16)..]), with their per-block scales; every wave then
+// streams its strips' weights straight from HBM into registers, one superblock ahead.  The
+// (dd, mm) pairs of a superblock are decoded cooperatively by the wave (each lane a quarter) into
+// a per-wave LDS table.
+
+// (dd, mm) of Q4_K sub-block j (runtime) from the header words: blocks.py:16-22 with the byte
+// selected by shifts
+__device__ __forceinline__ float2 q4k_dm_rt(uint4 hdr, uint32_t j) {
+    const uint32_t sh = 8 * (j & 3);
+    const uint32_t b1 = (hdr.y >> sh) & 0xffu, b2 = (hdr.z >> sh) & 0xffu, b3 = (hdr.w >> sh) & 0xffu;
+    const int sc = j < 4 ? (int)(b1 & 63u) : (int)((b3 & 15u) | ((b1 >> 6) << 4));
+    const int mn = j < 4 ? (int)(b2 & 63u) : (int)((b3 >> 4) | ((b2 >> 6) << 4));
+    float dd, mm;
+    q4k_dm(h2f((uint16_t)(hdr.x & 0xffff)), h2f((uint16_t)(hdr.x >> 16)), sc, mn, dd, mm);
+    return make_float2(dd, mm);
+}
+
+// Q4_K operands of one superblock for lane (g, r): the header and, per sub-block pair c, the
+// 8 qs bytes 32c + 8g .. 32c + 8g + 7 (k-group g of both sub-blocks 2c and 2c+1).
+struct Q4Sb {
+    uint4 hdr;
+    uint2 qs[4];
+};
+__device__ __forceinline__ void load_q4sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q4Sb& w) {
+    const uint8_t* p = rowp + sb * 144;
+    w.hdr = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int c = 0; c < 4; c++) w.qs[c] = *reinterpret_cast<const uint2*>(p + 16 + 32 * c + 8 * g);
+}
+
+// Stage an item's activation rows (int8, one block = 32 bytes per row) in MFMA operand order.
+__device__ __forceinline__ void stage_a(const int8_t* __restrict__ src_rows, const uint32_t* rowoff, uint32_t K,
+                                        long* As, uint32_t tid) {
+    // K is a multiple of 256, so 16 rows are a multiple of 256 pieces: every thread loads the same
+    // number, all requested before any is stored
+    const uint32_t pieces = K / 16;  // 16-byte pieces per row
+    for (uint32_t i0 = 0; i0 < 16 * pieces; i0 += 2048) {
+        uint4 v[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * pieces ? i : 16 * pieces - 1;
+            v[c] = *reinterpret_cast<const uint4*>(src_rows + (size_t)rowoff[ic / pieces] + (ic % pieces) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + 256 * c;
+            if (i < 16 * pieces) {
+                const uint32_t t = i / pieces, o = i % pieces;
+                const uint32_t b = o / 2, g0 = (o % 2) * 2;  // 16 bytes = k-groups g0, g0+1 of block b
+                As[b * 64 + g0 * 16 + t] = (long)(((unsigned long long)v[c].y << 32) | v[c].x);
+                As[b * 64 + (g0 + 1) * 16 + t] = (long)(((unsigned long long)v[c].w << 32) | v[c].z);
+            }
+        }
+    }
+}
+
+constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table (16 + 1 against bank conflicts)
+
 // gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
-// Workgroup: one item (<= 64 entry rows, a 16-row tile per wave) x one 16-row strip of F (16 gate
-// rows and 16 up rows staged in LDS).  NSB = H / 256 superblocks per weight row.
+// Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.
 template <int NSB>
 __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat shg, Mat shu, Workspace ws) {
-    constexpr uint32_t H = NSB * 256, nb = NSB * 8, rb = NSB * 144, rbp = rb + 16;  // padded LDS row
-    constexpr uint32_t PER = rb;  // uint4 per 16-row strip of one matrix (contiguous rows)
-    constexpr uint32_t NL = (2 * PER + 255) / 256;
+    constexpr uint32_t H = NSB * 256, nb = NSB * 8;
     const uint32_t F = gate.rows, nbf = F / 16;
-    const uint32_t strip = blockIdx.x, itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
     if (itn >= ws.n_groups[2]) return;
     const Item item = ws.items[itn];
     const bool shared = item.expert == NO_EXPERT;
@@ -204,134 +289,127 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     const uint32_t e = shared ? 0u : item.expert;
 
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t* wts = smem;                              // [32][rbp]: 16 gate rows, then 16 up rows
-    float2* dm = (float2*)(smem + 32 * rbp);          // [32][nb] (dd, mm)
+    long* As = reinterpret_cast<long*>(smem);                        // [nb][64]
+    float* Sx = reinterpret_cast<float*>(smem + nb * 64 * 8);        // [nb][16] activation scales
+    float* Su = Sx + nb * 16;                                        // [nb][16] scale * sum
+    float2* Dm = reinterpret_cast<float2*>(Su + nb * 16);            // [4 waves][2][16][DM_STRIDE]
+    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Dm + 4 * 2 * 16 * DM_STRIDE);  // [16]
+    uint32_t* tokv = rowoff + 16;                                    // [16]
 
-    {
-        const uint8_t* src0 = G.ptr + (size_t)e * G.stride + (size_t)strip * 16 * rb;
-        const uint8_t* src1 = U.ptr + (size_t)e * U.stride + (size_t)strip * 16 * rb;
-        uint4 t[NL];
-#pragma unroll
-        for (uint32_t l = 0; l < NL; l++) {
-            const uint32_t i = tid + 256 * l < 2 * PER ? tid + 256 * l : 0u;  // clamped: always a valid load
-            t[l] = *reinterpret_cast<const uint4*>((i < PER ? src0 : src1) + (i % PER) * 16);
-        }
-#pragma unroll
-        for (uint32_t l = 0; l < NL; l++) {
-            const uint32_t i = tid + 256 * l;
-            if (i < 2 * PER) {
-                const uint32_t mat = i / PER, o = (i % PER) * 16;
-                *reinterpret_cast<uint4*>(wts + (mat * 16 + o / rb) * rbp + o % rb) = t[l];
-            }
-        }
+    if (tid < 16) {
+        const uint32_t tok = item_token(ws, item, shared, tid);
+        tokv[tid] = tok;
+        rowoff[tid] = tok * H;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < 32 * NSB; i += blockDim.x) {
-        const uint32_t r = i / NSB, sb = i % NSB;
-        const uint8_t* hb = wts + r * rbp + sb * 144;
-        const float d = h2f(ld16(hb)), dmin = h2f(ld16(hb + 2));
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int sc, mn;
-            q4k_scale_min(hb + 4, j, sc, mn);
-            float a, b;
-            q4k_dm(d, dmin, sc, mn, a, b);
-            dm[r * nb + sb * 8 + j] = make_float2(a, b);
-        }
-    }
-    __syncthreads();
-
-    // Per-superblock entry scales (sx and u = sx * sum of the item's 64 entry rows) pass through a
-    // double-buffered LDS stage: every thread moves one float4 per superblock.
-    float* scl = reinterpret_cast<float*>(dm + 32 * nb);  // [2][64 entries][16]: sx[8] | u[8]
-    const uint32_t le = tid / 4, lp = tid % 4;
-    const float* lsrc = (lp < 2 ? ws.xs : ws.xu) + (size_t)item_token(ws, item, shared, le) * nb + (lp & 1) * 4;
-    auto scl_load = [&](uint32_t sb) { return *reinterpret_cast<const float4*>(lsrc + sb * 8); };
-    auto scl_store = [&](uint32_t buf, float4 v) {
-        *reinterpret_cast<float4*>(scl + buf * 1024 + le * 16 + lp * 4) = v;
-    };
-
-    const uint32_t t0 = wv * 16;
-    const bool active = t0 < item.nrows;  // waves past the item still stage scales
-    const uint32_t g = lane / 16, f = lane % 16;
-    const int8_t* xa = ws.xq + (size_t)item_token(ws, item, shared, t0 + f) * H + 8 * g;
-    float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const uint8_t* wg = wts + f * rbp + 16 + 8 * g;
-    const uint8_t* wu = wts + (16 + f) * rbp + 16 + 8 * g;
-    long a0[8], a1[8];  // A operands of a superblock (8 chunks), one superblock ahead
-    auto fetch_a = [&](uint32_t sb, long* a) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = *reinterpret_cast<const long*>(xa + sb * 256 + 32 * j);
-    };
-    auto step = [&](uint32_t sb, const long* a) {
-        const float* sc = scl + (sb & 1) * 1024 + (t0 + 4 * g) * 16;
+    stage_a(ws.xq, rowoff, H, As, tid);
+    for (uint32_t i0 = 0; i0 < 16 * nb; i0 += 1024) {
+        float a[4], c2[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint2 pg = *reinterpret_cast<const uint2*>(wg + sb * 144 + 32 * c);
-            const uint2 pu = *reinterpret_cast<const uint2*>(wu + sb * 144 + 32 * c);
-            float2 sxv[4], suv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                sxv[i] = *reinterpret_cast<const float2*>(sc + i * 16 + 2 * c);
-                suv[i] = *reinterpret_cast<const float2*>(sc + i * 16 + 8 + 2 * c);
-            }
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int j = 2 * c + h;
-                const v4i cg = mfma_i8(a[j], unpack8(pg, h));
-                const v4i cu = mfma_i8(a[j], unpack8(pu, h));
-                const float2 dg = dm[f * nb + sb * 8 + j], du = dm[(16 + f) * nb + sb * 8 + j];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float sx = h ? sxv[i].y : sxv[i].x, u = h ? suv[i].y : suv[i].x;
-                    const float tg = dg.x * sx, tu = du.x * sx;
-                    accg[i] = __builtin_fmaf(dg.y, u, accg[i]);
-                    accg[i] = __builtin_fmaf((float)cg[i], tg, accg[i]);
-                    accu[i] = __builtin_fmaf(du.y, u, accu[i]);
-                    accu[i] = __builtin_fmaf((float)cu[i], tu, accu[i]);
-                }
-            }
+            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nb ? i : 16 * nb - 1;
+            a[c] = ws.xs[(size_t)tokv[ic / nb] * nb + ic % nb];
+            c2[c] = ws.xu[(size_t)tokv[ic / nb] * nb + ic % nb];
         }
-    };
-    scl_store(0, scl_load(0));
-    if (active) fetch_a(0, a0);
-    __syncthreads();
-#pragma unroll 1
-    for (uint32_t sb = 0; sb < NSB; sb += 2) {
-        const float4 n1 = sb + 1 < NSB ? scl_load(sb + 1) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (active && sb + 1 < NSB) fetch_a(sb + 1, a1);
-        if (active) step(sb, a0);
-        if (sb + 1 < NSB) scl_store(1, n1);
-        __syncthreads();
-        if (sb + 1 < NSB) {
-            const float4 n2 = sb + 2 < NSB ? scl_load(sb + 2) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (active && sb + 2 < NSB) fetch_a(sb + 2, a0);
-            if (active) step(sb + 1, a1);
-            if (sb + 2 < NSB) scl_store(0, n2);
-            __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = i0 + tid + 256 * c;
+            if (i < 16 * nb) {
+                Sx[(i % nb) * 16 + i / nb] = a[c];
+                Su[(i % nb) * 16 + i / nb] = c2[c];
+            }
         }
     }
-    if (!active) return;
-    // SwiGLU (elem.rs:173) and per-16 quantisation across the 16 lanes holding one entry's strip
+    const uint32_t g = lane / 16, r = lane % 16;
+    // routing weight of this lane's four entry rows (exec_batch.rs:1533-1535; shared: the gate)
+    float wgt[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t row = t0 + 4 * g + i;
-        const float v = silu512(accg[i]) * accu[i];
-        // the 16 lanes of an entry's strip are one DPP row (lanes 16g .. 16g+15)
-        const float amax = row16_allreduce(__builtin_fabsf(v), [](float a, float b) { return mx_ps(a, b); });
-        const float s = amax / 127.0f;
-        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-        const int32_t qi = cvt_rne(v * inv);
-        const int32_t sum = row16_allreduce(qi, [](int32_t a, int32_t b) { return a + b; });
-        if (row < item.nrows) {
-            const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
-            ws.actq[(size_t)arow * F + strip * 16 + f] = sat_i8(qi);
-            if (f == 0) {
-                const float wgt = shared ? sigmoid_libm(ws.shl[item.row0 + row]) : ws.ent_w[item.row0 + row];
-                const float sf = s * wgt;  // exec_batch.rs:1533-1535
-                ws.acts[(size_t)arow * nbf + strip] = sf;
-                ws.actsum[(size_t)arow * nbf + strip] = sum;
-                ws.actu[(size_t)arow * nbf + strip] = sf * (float)sum;
+        const uint32_t row = 4 * g + i < item.nrows ? 4 * g + i : 0u;
+        wgt[i] = shared ? sigmoid_libm(ws.shl[item.row0 + row]) : ws.ent_w[item.row0 + row];
+    }
+    __syncthreads();
+
+    float2* dmw = Dm + wv * 2 * 16 * DM_STRIDE;
+    const uint32_t strips = F / 16 / gridDim.x;  // per workgroup
+    const uint32_t nstep = (strips / 4) * NSB;   // (strip, superblock) steps of this wave
+    auto rows_of = [&](uint32_t step, const uint8_t*& rg, const uint8_t*& ru) {
+        const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+        rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + r) * G.row_bytes;
+        ru = U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + r) * U.row_bytes;
+    };
+    Q4Sb cg, cu;
+    {
+        const uint8_t *rg, *ru;
+        rows_of(0, rg, ru);
+        load_q4sb(rg, 0, g, cg);
+        load_q4sb(ru, 0, g, cu);
+    }
+    float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t step = 0; step < nstep; step++) {
+        const uint32_t sb = step % NSB;
+        Q4Sb ng = cg, nu = cu;
+        if (step + 1 < nstep) {  // the next superblock's loads go out before this one's math
+            const uint8_t *rg, *ru;
+            rows_of(step + 1, rg, ru);
+            load_q4sb(rg, (step + 1) % NSB, g, ng);
+            load_q4sb(ru, (step + 1) % NSB, g, nu);
+        }
+        // (dd, mm) of sub-blocks 2g, 2g+1 of row r, gate then up
+        wave_sync();
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const uint32_t j = 2 * g + jj;
+            dmw[r * DM_STRIDE + j] = q4k_dm_rt(cg.hdr, j);
+            dmw[(16 + r) * DM_STRIDE + j] = q4k_dm_rt(cu.hdr, j);
+        }
+        wave_sync();
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t B = sb * 8 + j;
+            const long a = As[B * 64 + lane];
+            const v4i dg = mfma_i8(a, unpack8(cg.qs[j / 2], j % 2));
+            const v4i du = mfma_i8(a, unpack8(cu.qs[j / 2], j % 2));
+            const float2 mg = dmw[r * DM_STRIDE + j], mu = dmw[(16 + r) * DM_STRIDE + j];
+            const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + 4 * g);
+            const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + 4 * g);
+            const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
+                accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
+                accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
+                accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
+                accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
+            }
+        }
+        cg = ng;
+        cu = nu;
+        if (sb == NSB - 1) {
+            // SwiGLU (elem.rs:173) and per-16 quantisation across the 16 lanes holding one entry's
+            // strip (lanes 16g .. 16g+15, one DPP row)
+            const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t row = 4 * g + i;
+                const float v = silu512(accg[i]) * accu[i];
+                const float amax =
+                        row16_allreduce(__builtin_fabsf(v), [](float x, float y) { return mx_ps(x, y); });
+                const float s = amax / 127.0f;
+                const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+                const int32_t qi = cvt_rne(v * inv);
+                const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
+                if (row < item.nrows) {
+                    const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
+                    ws.actq[(size_t)arow * F + strip * 16 + r] = sat_i8(qi);
+                    if (r == 0) {
+                        const float sf = s * wgt[i];  // exec_batch.rs:1533-1535
+                        ws.acts[(size_t)arow * nbf + strip] = sf;
+                        ws.actsum[(size_t)arow * nbf + strip] = sum;
+                        ws.actu[(size_t)arow * nbf + strip] = sf * (float)sum;
+                    }
+                }
+                accg[i] = 0.0f;
+                accu[i] = 0.0f;
             }
         }
     }
@@ -340,8 +418,10 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
                                const Workspace& ws, uint32_t m, hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32;
-    const size_t lds = 32 * (size_t)(gate.row_bytes + 16) + 32 * (size_t)nb * 8 + 2 * 64 * 16 * 4;
-    const dim3 grid(F / 16, ws.item_cap);
+    const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_STRIDE * 8 + 32 * 4;
+    // a workgroup per (item, 16 strips) once the items fill the GPU; otherwise per (item, 4 strips)
+    // so that a wave's chain of dependent weight loads stays short
+    const dim3 grid(m >= 64 ? F / 256 : F / 64, ws.item_cap);
     switch (H / 256) {
 #define GU_CASE(n) \
     case n: batch_gateup_kernel<n><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws); break;
@@ -355,164 +435,175 @@ hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gat
 
 // ---- down ---------------------------------------------------------------------------------------
 //
-// Workgroup: one item x 64 rows of H (4 MFMA column tiles).  The down input is quantised per 16,
-// so each 32-byte activation chunk feeds two MFMAs with the other half of its k-groups zeroed,
-// giving the exact dot of each 16-block.  Q6_K superblocks are re-laid to 224 bytes in LDS so
-// that every 8-byte operand read is aligned.
+// Grid (H / 256, items): a workgroup covers 256 rows of H, each wave 4 strips of 16.  The down
+// input is quantised per 16, so each 32-byte activation chunk feeds two MFMAs with the other
+// half of its k-groups zeroed, giving the exact dot of each 16-block.
 
-constexpr uint32_t DN_COLS = 64;
-
-__device__ __forceinline__ long q6k_operand(const uint8_t* sbp, uint32_t q8, uint32_t g) {
-    // 8 consecutive values e = 32*q8 + 8g .. +7 of a superblock: ql nibble, qh 2-bit field
-    const uint32_t n = q8 / 4, g6 = q8 % 4;
-    const uint2 lo = *reinterpret_cast<const uint2*>(sbp + 64 * n + 32 * (g6 & 1) + 8 * g);
-    const uint2 hi = *reinterpret_cast<const uint2*>(sbp + 128 + 32 * n + 8 * g);
+// Q6_K operands of one superblock for lane (g, r), read with 2-byte loads (superblocks are only
+// 2-byte aligned): ql bytes 64n + 32s + 8g (n, s in {0, 1}), qh bytes 128 + 32n + 8g, the
+// scales of blocks 4g .. 4g+3 (this lane decodes them) and d.
+struct Q6Sb {
+    uint2 ql[4], qh[2];
+    uint32_t sc;  // int8 scales of blocks 4g .. 4g+3
+    uint16_t d;
+};
+__device__ __forceinline__ uint32_t ld32_a2(const uint8_t* p) {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+__device__ __forceinline__ uint2 ld64_a2(const uint8_t* p) { return make_uint2(ld32_a2(p), ld32_a2(p + 4)); }
+__device__ __forceinline__ void load_q6sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q6Sb& w) {
+    const uint8_t* p = rowp + sb * 210;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w.ql[i] = ld64_a2(p + 64 * (i / 2) + 32 * (i % 2) + 8 * g);
+#pragma unroll
+    for (int n = 0; n < 2; n++) w.qh[n] = ld64_a2(p + 128 + 32 * n + 8 * g);
+    w.sc = ld32_a2(p + 192 + 4 * g);
+    w.d = *reinterpret_cast<const uint16_t*>(p + 208);
+}
+// 8 consecutive 6-bit values e = 32*q8 + 8g .. +7 of the superblock (q8 compile-time)
+__device__ __forceinline__ long q6_operand(const Q6Sb& w, int q8) {
+    const int n = q8 / 4, g6 = q8 % 4;
+    const uint2 lo = w.ql[2 * n + (g6 & 1)], hi = w.qh[n];
     const int sh = (g6 >> 1) ? 4 : 0;
     const uint32_t l0 = (lo.x >> sh) & 0x0f0f0f0fu, l1 = (lo.y >> sh) & 0x0f0f0f0fu;
     const uint32_t h0 = (hi.x >> (2 * g6)) & 0x03030303u, h1 = (hi.y >> (2 * g6)) & 0x03030303u;
     return (long)(((unsigned long long)(l1 | (h1 << 4)) << 32) | (l0 | (h0 << 4)));
 }
 
-template <int NSB>
+template <int NSB, bool Q6>
 __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws) {
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
     const uint32_t H = down.rows;
-    const uint32_t strip = blockIdx.x, itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
     if (itn >= ws.n_groups[2]) return;
     const Item item = ws.items[itn];
     const bool shared = item.expert == NO_EXPERT;
     const uint32_t n_ent = ws.n_groups[1];
     const Mat& D = shared ? shd : down;
     const uint32_t e = shared ? 0u : item.expert;
-    const bool q6 = D.fmt == TRK_FMT_Q6_K;
-    const uint32_t sbb = q6 ? 224u : 144u;          // LDS bytes per superblock
-    const uint32_t rbp = NSB * sbb + 16;            // padded LDS row stride
     const uint32_t arow0 = shared ? n_ent + item.row0 : item.row0;
 
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t* wts = smem;                                  // [64][rbp]
-    float2* dm = (float2*)(smem + DN_COLS * rbp);         // [64][nbf] (dd, mm)
+    long* As = reinterpret_cast<long*>(smem);                        // [NQ][64]
+    float* Sx = reinterpret_cast<float*>(smem + NQ * 64 * 8);        // [nbf][16] folded scales
+    float* Su = Sx + nbf * 16;                                       // [nbf][16] scale * sum
+    float2* Dm = reinterpret_cast<float2*>(Su + nbf * 16);           // [4 waves][16][DM_STRIDE]
+    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [16]
 
-    const uint8_t* src = D.ptr + (size_t)e * D.stride + (size_t)strip * DN_COLS * D.row_bytes;
-    if (!q6) {
-        constexpr uint32_t rb = NSB * 144, PER = DN_COLS * rb / 16;
-#pragma unroll 8
-        for (uint32_t i = tid; i < PER; i += 256)
-            *reinterpret_cast<uint4*>(wts + (i * 16 / rb) * rbp + (i * 16) % rb) =
-                reinterpret_cast<const uint4*>(src)[i];
-    } else {
-        const uint32_t per = DN_COLS * NSB * 105;  // 2-byte words
-        for (uint32_t i = tid; i < per; i += blockDim.x) {
-            const uint32_t r = i / (NSB * 105), rem = i % (NSB * 105), sb = rem / 105, w = rem % 105;
-            reinterpret_cast<uint16_t*>(wts + r * rbp + sb * sbb)[w] =
-                reinterpret_cast<const uint16_t*>(src + (size_t)r * D.row_bytes + sb * 210)[w];
-        }
-    }
+    if (tid < 16) rowoff[tid] = (arow0 + (tid < item.nrows ? tid : 0u)) * F;
     __syncthreads();
-    for (uint32_t i = tid; i < DN_COLS * NSB; i += blockDim.x) {
-        const uint32_t r = i / NSB, sb = i % NSB;
-        const uint8_t* hb = wts + r * rbp + sb * sbb;
-        if (!q6) {
-            const float d = h2f(ld16(hb)), dmin = h2f(ld16(hb + 2));
+    stage_a(ws.actq, rowoff, F, As, tid);
+    for (uint32_t i0 = 0; i0 < 16 * nbf; i0 += 1024) {
+        float a[4], c2[4];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                int sc, mn;
-                q4k_scale_min(hb + 4, j, sc, mn);
-                float a, b;
-                q4k_dm(d, dmin, sc, mn, a, b);
-                dm[r * nbf + sb * 16 + 2 * j] = make_float2(a, b);
-                dm[r * nbf + sb * 16 + 2 * j + 1] = make_float2(a, b);
-            }
-        } else {
-            const float d = h2f(ld16(hb + 208));
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float a = f16_round(d * (float)(int8_t)hb[192 + j]);
-                dm[r * nbf + sb * 16 + j] = make_float2(a, f16_round(-32.0f * a));
-            }
-        }
-    }
-    __syncthreads();
-
-    // the item's activation scales (folded sx and u) for all nbf blocks, staged once
-    float2* scl = reinterpret_cast<float2*>(dm + DN_COLS * nbf);  // [64 entries][nbf] (sx, u)
-#pragma unroll 8
-    for (uint32_t i = tid; i < 64 * nbf; i += 256) {
-        const uint32_t r = i / nbf, b = i % nbf;
-        const size_t row = (size_t)arow0 + (r < item.nrows ? r : 0u);
-        scl[i] = make_float2(ws.acts[row * nbf + b], ws.actu[row * nbf + b]);
-    }
-    __syncthreads();
-
-    const uint32_t t0 = wv * 16;
-    if (t0 >= item.nrows) return;  // no barrier below
-    const uint32_t g = lane / 16, f = lane % 16;
-    const uint32_t ra = t0 + f < item.nrows ? t0 + f : 0u;  // A row (entry) of this lane
-    const int8_t* xa = ws.actq + (size_t)(arow0 + ra) * F + 8 * g;
-    const float2* sce = scl + (t0 + 4 * g) * nbf;  // this lane's 4 entries
-    float acc[4][4];
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[c][i] = 0.0f;
-    auto step = [&](uint32_t q, long af) {
-        const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
-        const uint32_t sb = q / 8, q8 = q % 8;
-        float2 s0[4], s1[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            s0[i] = sce[i * nbf + 2 * q];
-            s1[i] = sce[i * nbf + 2 * q + 1];
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nbf ? i : 16 * nbf - 1;
+            const size_t row = rowoff[ic / nbf] / F;
+            a[c] = ws.acts[row * nbf + ic % nbf];
+            c2[c] = ws.actu[row * nbf + ic % nbf];
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint8_t* sbp = wts + (c * 16 + f) * rbp + sb * sbb;
-            long b;
-            if (!q6) {
-                const uint2 p = *reinterpret_cast<const uint2*>(sbp + 16 + 32 * (q8 / 2) + 8 * g);
-                b = unpack8(p, (int)(q8 % 2));
-            } else {
-                b = q6k_operand(sbp, q8, g);
+            const uint32_t i = i0 + tid + 256 * c;
+            if (i < 16 * nbf) {
+                Sx[(i % nbf) * 16 + i / nbf] = a[c];
+                Su[(i % nbf) * 16 + i / nbf] = c2[c];
             }
-            const v4i c0 = mfma_i8(alo, b), c1 = mfma_i8(ahi, b);
-            const float2 d0 = dm[(c * 16 + f) * nbf + 2 * q], d1 = dm[(c * 16 + f) * nbf + 2 * q + 1];
+        }
+    }
+    __syncthreads();
+
+    const uint32_t g = lane / 16, r = lane % 16;
+    float2* dmw = Dm + wv * 16 * DM_STRIDE;
+    const uint32_t strips = H / 16 / gridDim.x;
+    const uint32_t nstep = (strips / 4) * NSB;
+    auto row_of = [&](uint32_t step) -> const uint8_t* {
+        const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+        return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
+    };
+    using W = typename std::conditional<Q6, Q6Sb, Q4Sb>::type;
+    auto load = [&](uint32_t step, W& w) {
+        if constexpr (Q6)
+            load_q6sb(row_of(step), step % NSB, g, w);
+        else
+            load_q4sb(row_of(step), step % NSB, g, w);
+    };
+    W cw;
+    load(0, cw);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t step = 0; step < nstep; step++) {
+        const uint32_t sb = step % NSB;
+        W nw = cw;
+        if (step + 1 < nstep) load(step + 1, nw);
+        // (dd, mm) of the superblock's 16 blocks of row r: this lane decodes blocks 4g .. 4g+3
+        wave_sync();
+        if constexpr (Q6) {
+            const float d = h2f(cw.d);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                acc[c][i] = __builtin_fmaf(d0.y, s0[i].y, acc[c][i]);
-                acc[c][i] = __builtin_fmaf((float)c0[i], d0.x * s0[i].x, acc[c][i]);
-                acc[c][i] = __builtin_fmaf(d1.y, s1[i].y, acc[c][i]);
-                acc[c][i] = __builtin_fmaf((float)c1[i], d1.x * s1[i].x, acc[c][i]);
+                const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
+                dmw[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
+            }
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) {  // sub-block 2g + jj covers blocks 4g + 2jj, +1
+                const float2 v = q4k_dm_rt(cw.hdr, 2 * g + jj);
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
             }
         }
-    };
-    long af0 = *reinterpret_cast<const long*>(xa), af1;
-#pragma unroll 1
-    for (uint32_t q = 0; q < NQ; q += 2) {  // 32-wide chunks = block pairs (2q, 2q+1); NQ is even
-        af1 = *reinterpret_cast<const long*>(xa + 32 * (q + 1));
-        step(q, af0);
-        if (q + 2 < NQ) af0 = *reinterpret_cast<const long*>(xa + 32 * (q + 2));
-        step(q + 1, af1);
-    }
+        wave_sync();
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t r = t0 + 4 * g + i;
-        if (r < item.nrows) {
-            float* y = ws.yent + (size_t)(arow0 + r) * H + strip * DN_COLS + f;
+        for (int q8 = 0; q8 < 8; q8++) {  // 32-wide chunks of the superblock = block pairs
+            const uint32_t q = sb * 8 + q8;
+            const long af = As[q * 64 + lane];
+            const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
+            long bw;
+            if constexpr (Q6)
+                bw = q6_operand(cw, q8);
+            else
+                bw = unpack8(cw.qs[q8 / 2], q8 % 2);
+            const v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+            const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
+            const float4 s0 = *reinterpret_cast<const float4*>(Sx + (2 * q) * 16 + 4 * g);
+            const float4 u0 = *reinterpret_cast<const float4*>(Su + (2 * q) * 16 + 4 * g);
+            const float4 s1 = *reinterpret_cast<const float4*>(Sx + (2 * q + 1) * 16 + 4 * g);
+            const float4 u1 = *reinterpret_cast<const float4*>(Su + (2 * q + 1) * 16 + 4 * g);
+            const float s0a[4] = {s0.x, s0.y, s0.z, s0.w}, u0a[4] = {u0.x, u0.y, u0.z, u0.w};
+            const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
-            for (int c = 0; c < 4; c++) y[c * 16] = acc[c][i];
+            for (int i = 0; i < 4; i++) {
+                acc[i] = __builtin_fmaf(d0.y, u0a[i], acc[i]);
+                acc[i] = __builtin_fmaf((float)c0[i], d0.x * s0a[i], acc[i]);
+                acc[i] = __builtin_fmaf(d1.y, u1a[i], acc[i]);
+                acc[i] = __builtin_fmaf((float)c1[i], d1.x * s1a[i], acc[i]);
+            }
+        }
+        cw = nw;
+        if (sb == NSB - 1) {
+            const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t row = 4 * g + i;
+                if (row < item.nrows) ws.yent[(size_t)(arow0 + row) * H + strip * 16 + r] = acc[i];
+                acc[i] = 0.0f;
+            }
         }
     }
+    (void)NQ;
 }
 
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, hipStream_t st) {
-    const uint32_t H = down.rows, F = down.k, nsb = F / 256, nbf = F / 16;
-    const bool q6 = down.fmt == TRK_FMT_Q6_K || sh_down.fmt == TRK_FMT_Q6_K;
-    const size_t rbp = nsb * (q6 ? 224 : 144) + 16;
-    const size_t lds = DN_COLS * rbp + (size_t)DN_COLS * nbf * 8 + (size_t)64 * nbf * 8;
-    const dim3 grid(H / DN_COLS, ws.item_cap);
-    switch (nsb) {
-#define DN_CASE(n) \
-    case n: batch_down_kernel<n><<<grid, 256, lds, st>>>(down, sh_down, ws); break;
+    const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
+    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 8 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
+    const dim3 grid(m >= 64 ? H / 256 : H / 64, ws.item_cap);
+    const bool q6 = down.fmt == TRK_FMT_Q6_K;
+    if (q6 != (sh_down.fmt == TRK_FMT_Q6_K)) return hipErrorInvalidValue;  // one format per layer
+    switch (F / 256 * 2 + (q6 ? 1 : 0)) {
+#define DN_CASE(n)                                                                          \
+    case n * 2: batch_down_kernel<n, false><<<grid, 256, lds, st>>>(down, sh_down, ws); break; \
+    case n * 2 + 1: batch_down_kernel<n, true><<<grid, 256, lds, st>>>(down, sh_down, ws); break;
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
         default: return hipErrorInvalidValue;
@@ -526,28 +617,35 @@ __global__ __launch_bounds__(256) void batch_combine_kernel(Workspace ws, uint32
                                                            int residual) {
     const uint32_t t = blockIdx.x, H = ws.H, tid = threadIdx.x;
     __shared__ uint32_t pos[K_MAX];
-    __shared__ uint32_t np;
-    if (tid == 0) {
-        const uint32_t ns = ws.n_sel[t];
-        // entries are sorted by (expert, token): ascending position = ascending expert
-        for (uint32_t s = 0; s < ns; s++) {
-            uint32_t v = ws.ent_of[(size_t)t * K_MAX + s];
-            int j = (int)s - 1;
-            while (j >= 0 && pos[j] > v) {
-                pos[j + 1] = pos[j];
-                j--;
-            }
-            pos[j + 1] = v;
-        }
-        np = ns;
+    const uint32_t ns = ws.n_sel[t];
+    const uint32_t n_ent = ws.n_groups[1];
+    if (tid < 64) {
+        // the token's entry positions (distinct), ranked: entries are sorted by (expert, token), so
+        // ascending position = ascending expert
+        const uint32_t v = tid < ns ? ws.ent_of[(size_t)t * K_MAX + tid] : 0xffffffffu;
+        uint32_t rank = 0;
+        for (uint32_t s2 = 0; s2 < ns; s2++) rank += (uint32_t)__builtin_amdgcn_readlane((int)v, (int)s2) < v ? 1u : 0u;
+        if (tid < ns) pos[rank] = v;
     }
     __syncthreads();
-    const uint32_t n_ent = ws.n_groups[1];
-    for (uint32_t c = tid; c < H; c += blockDim.x) {
-        float y = ws.yent[(size_t)(n_ent + t) * H + c];
-        for (uint32_t j = 0; j < np; j++) y = y + ws.yent[(size_t)pos[j] * H + c];
-        float* o = out + (size_t)t * H + c;
-        *o = residual ? *o + y : y;
+    const float4* y4 = reinterpret_cast<const float4*>(ws.yent);
+    const uint32_t H4 = H / 4;
+    for (uint32_t c = tid; c < H4; c += blockDim.x) {
+        float4 y = y4[(size_t)(n_ent + t) * H4 + c];
+#pragma unroll 4
+        for (uint32_t j = 0; j < ns; j++) {
+            const float4 v = y4[(size_t)pos[j] * H4 + c];
+            y.x = y.x + v.x;
+            y.y = y.y + v.y;
+            y.z = y.z + v.z;
+            y.w = y.w + v.w;
+        }
+        float4* o = reinterpret_cast<float4*>(out + (size_t)t * H) + c;
+        if (residual) {
+            const float4 h = *o;
+            y = make_float4(h.x + y.x, h.y + y.y, h.z + y.z, h.w + y.w);
+        }
+        *o = y;
     }
 }
 

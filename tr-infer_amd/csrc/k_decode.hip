@@ -34,20 +34,27 @@ __device__ __forceinline__ float lane_up(float v) {
         return __shfl_up(v, 1);
 }
 
-template <int P, int NSB, int NJ>
-__global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
-        Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
-        uint32_t k, Policy pol, uint32_t kcap) {
+// One gate/up unit (slot, strip) on a workgroup of at least GU_THREADS(NSB) threads.  Wave 0
+// routes the token into LDS when `route` is set (always for routed slots).  `hook(r_ids, n)` runs
+// on every thread once the routing is in LDS, before any weight of a routed slot is requested
+// (the fused layer kernel issues its down-projection prefetch there).  active = false: route
+// and hook only.
+template <int P, int NSB, int NJ, typename Hook>
+__device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, const Mat& shg, const Mat& shu,
+                                            const float* __restrict__ x, const float* __restrict__ lg,
+                                            const Workspace& ws, uint32_t k, const Policy& pol, uint32_t kcap,
+                                            uint32_t slot, uint32_t strip, bool active, bool route, bool publish,
+                                            uint8_t* smem, uint8_t* rsm, Hook&& hook) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8, XSB = 256 + 16, XP = NSB * XSB;
     const uint32_t F = gate.rows, E = ws.E;
-    const uint32_t slot = blockIdx.y, strip = blockIdx.x, tid = threadIdx.x;
-    const bool shared = slot == kcap;
-    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t tid = threadIdx.x;
+    const bool shared = active && slot == kcap;
+    route = route || !shared;
     int8_t* xq = (int8_t*)smem;              // [P][NSB][XSB]: superblocks padded against bank conflicts
     float* xs = (float*)(smem + P * XP);     // [P][nb]  activation scales
     float* xu = xs + P * nb;                 // [P][nb]  sx * sum
     float* hres = xu + P * nb;               // [32][P]
-    uint32_t* r_ids = (uint32_t*)(hres + 32 * P);  // [32] this token's routing
+    uint32_t* r_ids = (uint32_t*)rsm;              // [32] this token's routing
     float* r_w = (float*)(r_ids + K_MAX);          // [32]
     uint32_t* r_n = (uint32_t*)(r_w + K_MAX);      // [4]
     uint2* cand = (uint2*)(r_n + 4);               // [ROUTE_CAND] routing scratch
@@ -55,7 +62,7 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
 
     // x first: its loads must not queue behind the (id-dependent) weight loads
     float4 xv[8];
-    const bool qthread = tid >= 64 && tid < 64 + nb;
+    const bool qthread = active && tid >= 64 && tid < 64 + nb;
     if (qthread) {
         const float4* src = reinterpret_cast<const float4*>(x + (size_t)(tid - 64) * 32);
 #pragma unroll
@@ -77,12 +84,13 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
     if (shared) {
         load_rows(shg, shu, 0u, wq);  // the shared expert does not wait for the routing
         shl = ws.shl[0];
-    } else if (tid < 64) {
+    }
+    if (route && tid < 64) {
         // route this token (wave 0): every routed workgroup repeats it, so no separate launch and
         // no round trip through memory sits between the logits and the expert weights
         const uint32_t n = route_row<NJ>(lg, E, k, pol, tid, cand, ex, r_ids, r_w);
         if (tid == 0) r_n[0] = n;
-        if (slot == 0 && strip == 0) {  // one workgroup publishes it (down kernel, introspection)
+        if (publish) {  // one workgroup publishes it (down kernel, introspection)
             wave_sync();
             if (tid < n) {
                 ws.ids[tid] = r_ids[tid];
@@ -135,6 +143,8 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
         }
     }
     __syncthreads();
+    hook(r_ids, route ? r_n[0] : 0u);
+    if (!active) return;
     float wgt = 0.0f;
     if (!shared) {
         if (slot >= r_n[0]) return;  // workgroup-uniform
@@ -244,12 +254,30 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
     }
 }
 
+// LDS of a gate/up unit: x (padded superblocks), scales, row results; then the routing area
+template <int P, int NSB>
+constexpr uint32_t gu_lds_x() { return P * NSB * (256 + 16) + P * NSB * 8 * 8 + 32 * P * 4; }
+constexpr uint32_t ROUTE_LDS = K_MAX * 8 + 16 + ROUTE_CAND * 8;  // + E floats for MassBasis::All
+
+struct NoHook {
+    __device__ void operator()(const uint32_t*, uint32_t) const {}
+};
+
+template <int P, int NSB, int NJ>
+__global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
+        Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
+        uint32_t k, Policy pol, uint32_t kcap) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    gateup_unit<P, NSB, NJ>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
+                            blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoHook{});
+}
+
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
                                 const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
                                 hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32, nsb = H / 256;
     const int P = pair ? 2 : 1;
-    size_t lds = (size_t)P * nsb * 272 + (size_t)P * nb * 8 + 32 * P * 4 + K_MAX * 8 + 16 + ROUTE_CAND * 8;
+    size_t lds = (size_t)P * nsb * 272 + (size_t)P * nb * 8 + 32 * P * 4 + ROUTE_LDS;
     if (pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;
     const dim3 g(F / 16, kcap + 1);
     const uint32_t threads = GU_THREADS(nsb);
@@ -399,68 +427,111 @@ __device__ __forceinline__ void half_terms_q6k(const uint8_t* __restrict__ rowp,
 }
 
 // Work unit u = slot * DN_R + row of a workgroup; slots 0..kcap-1 are the routed slots (those at
-// or past n_sel idle), slot kcap is the shared expert.  Activation rows are staged in LDS with
-// slot stride P*F + 16 bytes (fewer bank conflicts between slots).
+// or past n idle), slot kcap is the shared expert.  Activation rows are staged in LDS with slot
+// stride P*F + 16 bytes (fewer bank conflicts between slots).  `ids` / `n` are the routing (in
+// global memory for the standalone kernel, in LDS for the fused layer kernel).
+
+// A lane's first unit, with its weights requested ahead of everything else.
+struct DownFirst {
+    bool live;
+    const uint8_t* rowp;
+    uint4 hdr, qs[4];
+};
+
+template <int NSB>
+__device__ __forceinline__ const uint8_t* down_unit_row(const Mat& down, const Mat& shd, uint32_t kcap, uint32_t n,
+                                                        const uint32_t* ids, uint32_t row0, uint32_t u, bool& live) {
+    using DL = DownLanes<NSB>;
+    const uint32_t ln = threadIdx.x % 64;
+    const uint32_t s = u / DN_R, r = u % DN_R;
+    const bool sh = s == kcap;
+    live = ln < (uint32_t)(DL::UPW * DL::L) && u < (kcap + 1) * DN_R && (sh || s < n);
+    // per-lane choice of matrix: select the fields (a per-lane reference would put both in scratch)
+    const uint8_t* base = sh ? shd.ptr : down.ptr;
+    const uint64_t stride = sh ? shd.stride : down.stride;
+    const uint32_t rb = sh ? shd.row_bytes : down.row_bytes;
+    const uint32_t e = (sh || !live) ? 0u : ids[s];
+    return base + (size_t)e * stride + (size_t)(row0 + r) * rb;
+}
+
+template <int NSB>
+__device__ __forceinline__ void down_first(const Mat& down, const Mat& shd, uint32_t kcap, uint32_t n,
+                                           const uint32_t* ids, uint32_t row0, DownFirst& f) {
+    using DL = DownLanes<NSB>;
+    const uint32_t wv = threadIdx.x / 64, ln = threadIdx.x % 64, q = ln % DL::L;
+    const uint32_t u0 = wv * DL::UPW + ln / DL::L;
+    f.rowp = down_unit_row<NSB>(down, shd, kcap, n, ids, row0, u0, f.live);
+    f.hdr = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) f.qs[i] = f.hdr;
+    if (f.live && down.fmt == TRK_FMT_Q4_K) load_half_q4k(f.rowp, q / 2, q % 2, f.hdr, f.qs);
+}
+
 template <int P, int NSB>
-__global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t kcap,
-                                                         float* __restrict__ out, int residual) {
+__device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const Workspace& ws, uint32_t kcap,
+                                          uint32_t n, const uint32_t* ids, float* __restrict__ out, int residual,
+                                          uint32_t row0, uint8_t* smem, const DownFirst& first) {
     using DL = DownLanes<NSB>;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, SQ = P * F + 16;
-    const uint32_t tid = threadIdx.x, row0 = blockIdx.x * DN_R;
+    const uint32_t tid = threadIdx.x;
     const uint32_t slots = kcap + 1, units = slots * DN_R;
-    const uint32_t n = ws.n_sel[0];
     const uint32_t wv = tid / 64, ln = tid % 64, q = ln % DL::L;
-    const bool lane_ok = ln < (uint32_t)(DL::UPW * DL::L);
     const uint32_t sb = q / 2, h2 = q % 2;
     const bool q4 = down.fmt == TRK_FMT_Q4_K;
 
-    extern __shared__ __align__(16) uint8_t smem[];
     int8_t* aq = (int8_t*)smem;                                // [slots][SQ]
     float* as = (float*)(smem + (size_t)slots * SQ);           // [slots][P][nbf] folded scale
     float* au = as + slots * P * nbf;                          // [slots][P][nbf] scale * sum
     float* vres = au + slots * P * nbf;                        // [slots][DN_R]
 
-    auto unit_row = [&](uint32_t u, bool& live) -> const uint8_t* {
-        const uint32_t s = u / DN_R, r = u % DN_R;
-        const bool sh = s == kcap;
-        live = lane_ok && u < units && (sh || s < n);
-        const Mat& D = sh ? shd : down;
-        const uint32_t e = (sh || !live) ? 0u : ws.ids[s];
-        return D.ptr + (size_t)e * D.stride + (size_t)(row0 + r) * D.row_bytes;
-    };
-    // this lane's first unit: its weights are requested before the activations are staged
-    const uint32_t u0 = wv * DL::UPW + ln / DL::L;
-    bool live0;
-    const uint8_t* row_first = unit_row(u0, live0);
-    uint4 hdr = make_uint4(0, 0, 0, 0), qs[4] = {hdr, hdr, hdr, hdr};
-    if (live0 && q4) load_half_q4k(row_first, sb, h2, hdr, qs);
-
     {
+        // loads first (clamped indices, so no per-lane branch separates them), then the stores:
+        // one memory round trip per chunk of 4 pieces per thread
         constexpr uint32_t QP = P * F / 16, SP = P * nbf;  // int4 pieces and scales per slot
         const uint32_t nq = slots * QP, ns = slots * SP;
-#pragma unroll 4
-        for (uint32_t i = tid; i < nq; i += 256) {
-            const uint32_t s = i / QP, o = i % QP;
-            const uint32_t a = s < kcap ? s : (uint32_t)SH_SLOT;
-            *reinterpret_cast<int4*>(aq + (size_t)s * SQ + o * 16) =
-                    reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F)[o];
+        for (uint32_t i0 = 0; i0 < nq; i0 += 1024) {
+            int4 t[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
+                const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
+                t[c] = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F)[ic % QP];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t i = i0 + tid + 256 * c;
+                if (i < nq) *reinterpret_cast<int4*>(aq + (size_t)(i / QP) * SQ + (i % QP) * 16) = t[c];
+            }
         }
-#pragma unroll 4
-        for (uint32_t i = tid; i < ns; i += 256) {
-            const uint32_t s = i / SP, o = i % SP;
-            const uint32_t a = s < kcap ? s : (uint32_t)SH_SLOT;
-            const float sc = ws.acts[(size_t)a * SP + o];
-            as[i] = sc;
-            au[i] = sc * (float)ws.actsum[(size_t)a * SP + o];
+        for (uint32_t i0 = 0; i0 < ns; i0 += 1024) {
+            float sc[4];
+            int32_t su[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t i = i0 + tid + 256 * c, ic = i < ns ? i : ns - 1;
+                const uint32_t s = ic / SP, a = s < kcap ? s : (uint32_t)SH_SLOT;
+                sc[c] = ws.acts[(size_t)a * SP + ic % SP];
+                su[c] = ws.actsum[(size_t)a * SP + ic % SP];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t i = i0 + tid + 256 * c;
+                if (i < ns) {
+                    as[i] = sc[c];
+                    au[i] = sc[c] * (float)su[c];
+                }
+            }
         }
     }
     __syncthreads();
+    const uint32_t u0 = wv * DL::UPW + ln / DL::L;
+    uint4 hdr = first.hdr, qs[4] = {first.qs[0], first.qs[1], first.qs[2], first.qs[3]};
     for (uint32_t pass = 0; pass * DL::UPP < units; pass++) {
         const uint32_t u = pass * DL::UPP + u0;
-        bool live = live0;
-        const uint8_t* rowp = row_first;
+        bool live = first.live;
+        const uint8_t* rowp = first.rowp;
         if (pass > 0) {
-            rowp = unit_row(u, live);
+            rowp = down_unit_row<NSB>(down, shd, kcap, n, ids, row0, u, live);
             if (live && q4) load_half_q4k(rowp, sb, h2, hdr, qs);
         }
         const uint32_t s = live ? u / DN_R : 0u;
@@ -508,6 +579,16 @@ __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Wor
         float* o = out + row0 + tid;
         *o = residual ? *o + y : y;
     }
+}
+
+template <int P, int NSB>
+__global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t kcap,
+                                                         float* __restrict__ out, int residual) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t row0 = blockIdx.x * DN_R, n = ws.n_sel[0];
+    DownFirst first;
+    down_first<NSB>(down, shd, kcap, n, ws.ids, row0, first);
+    down_unit<P, NSB>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first);
 }
 
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair, uint32_t kcap,

@@ -5,7 +5,7 @@
 //                 16-lane FMA chains (64-wide steps), the 16-wide tail goes to chain 0, then
 //                 (c0 + c1) + (c2 + c3) lanewise and the halving tree of _mm512_reduce_add_ps.
 //   router_gemm:  smallgemm::gemm_f32_nt order (smallgemm.rs:8-59): per output, 16 lane chains
-//                 over 16-wide steps, then the halving tree.
+//                 over 16-wide steps, then the halving tree; LDS-staged register tiles.
 //   route:        one wave per token runs route_row (route.hpp).  The decode path (M = 1) routes
 //                 inside its gate/up kernel instead (k_decode.hip).
 #include "route.hpp"
@@ -81,44 +81,107 @@ __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict
         }
 }
 
-// Each 16-lane group plays the 16 lanes of one AVX-512 register; each thread carries 4 rows x 4
-// experts of the 16 x 16 output tile.
+// gemm_f32_nt order: output (m, e) has 16 lane chains j, chain j = fma over the steps s of
+// x[m][16s + j] * w[e][16s + j], then the halving tree.  Thread (j, q) of a 256-thread workgroup
+// carries chain j of an RM x RE block of outputs (q = qm * QE + qe); the workgroup tile is
+// (QM*RM) rows x (QE*RE) experts.  x and router chunks of KC columns go through LDS transposed
+// ([k][row]), double-buffered, so a thread reads its RM rows / RE experts at column 16s + j with
+// vector LDS reads.
+template <int RM, int RE, int QM>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restrict__ router,
                                                          const float* __restrict__ bias,
                                                          const float* __restrict__ x, uint32_t m, uint32_t E,
                                                          uint32_t H, float* __restrict__ rlog) {
-    const uint32_t l = threadIdx.x & 15, g = threadIdx.x >> 4;
-    const uint32_t rg = g >> 2, eg = g & 3;
-    const uint32_t row0 = blockIdx.y * 16 + rg * 4, e0 = blockIdx.x * 16 + eg * 4;
-    const float* xr[4];
-    const float* wr[4];
+    constexpr int QE = 16 / QM, TM = QM * RM, TE = QE * RE, KC = 64;
+    constexpr int XP = TM + 4, WP = TE + 4;  // padded LDS rows (keep 16-byte alignment)
+    __shared__ __align__(16) float xs[2][KC][XP];
+    __shared__ __align__(16) float wsm[2][KC][WP];
+    const uint32_t tid = threadIdx.x, j = tid % 16, q = tid / 16, qm = q / QE, qe = q % QE;
+    const uint32_t m0 = blockIdx.y * TM, e0 = blockIdx.x * TE;
+
+    // staging: TM rows of x and TE rows of the router, KC columns each, as float4 along k
+    constexpr int XV = TM * KC / 4, WV = TE * KC / 4;  // float4 per chunk
+    constexpr int NV = (XV + WV + 255) / 256;
+    float4 st[NV];
+    auto fetch = [&](uint32_t k0) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) xr[r] = x + (size_t)(row0 + r < m ? row0 + r : m - 1) * H + l;
+        for (int i = 0; i < NV; i++) {
+            const uint32_t v = tid + 256 * i;
+            if (v < (uint32_t)XV) {
+                const uint32_t r = v / (KC / 4), c4 = v % (KC / 4);
+                const uint32_t row = m0 + r < m ? m0 + r : m - 1;
+                st[i] = *reinterpret_cast<const float4*>(x + (size_t)row * H + k0 + 4 * c4);
+            } else if (v < (uint32_t)(XV + WV)) {
+                const uint32_t u = v - XV, r = u / (KC / 4), c4 = u % (KC / 4);
+                const uint32_t ex = e0 + r < E ? e0 + r : E - 1;
+                st[i] = *reinterpret_cast<const float4*>(router + (size_t)ex * H + k0 + 4 * c4);
+            }
+        }
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) wr[e] = router + (size_t)(e0 + e < E ? e0 + e : E - 1) * H + l;
-    float acc[4][4];
+        for (int i = 0; i < NV; i++) {
+            const uint32_t v = tid + 256 * i;
+            if (v < (uint32_t)XV) {
+                const uint32_t r = v / (KC / 4), c4 = v % (KC / 4);
+                xs[buf][4 * c4 + 0][r] = st[i].x;
+                xs[buf][4 * c4 + 1][r] = st[i].y;
+                xs[buf][4 * c4 + 2][r] = st[i].z;
+                xs[buf][4 * c4 + 3][r] = st[i].w;
+            } else if (v < (uint32_t)(XV + WV)) {
+                const uint32_t u = v - XV, r = u / (KC / 4), c4 = u % (KC / 4);
+                wsm[buf][4 * c4 + 0][r] = st[i].x;
+                wsm[buf][4 * c4 + 1][r] = st[i].y;
+                wsm[buf][4 * c4 + 2][r] = st[i].z;
+                wsm[buf][4 * c4 + 3][r] = st[i].w;
+            }
+        }
+    };
+    float acc[RM][RE];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int a = 0; a < RM; a++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) acc[r][e] = 0.0f;
-    for (uint32_t kk = 0; kk < H; kk += 16) {
-        float xv[4], wv[4];
+        for (int b = 0; b < RE; b++) acc[a][b] = 0.0f;
+    fetch(0);
+    store(0);
+    __syncthreads();
+    const uint32_t nchunk = H / KC;
+    for (uint32_t ck = 0; ck < nchunk; ck++) {
+        const int buf = ck & 1;
+        if (ck + 1 < nchunk) fetch((ck + 1) * KC);
 #pragma unroll
-        for (int r = 0; r < 4; r++) xv[r] = xr[r][kk];
+        for (int s4 = 0; s4 < KC / 16; s4++) {
+            const uint32_t c = 16 * s4 + j;
+            float xv[RM], wv[RE];
 #pragma unroll
-        for (int e = 0; e < 4; e++) wv[e] = wr[e][kk];
+            for (int a = 0; a < RM; a += 4) {
+                const float4 t = *reinterpret_cast<const float4*>(&xs[buf][c][qm * RM + a]);
+                xv[a] = t.x; xv[a + 1] = t.y; xv[a + 2] = t.z; xv[a + 3] = t.w;
+            }
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+            for (int b = 0; b < RE; b += 2) {
+                const float2 t = *reinterpret_cast<const float2*>(&wsm[buf][c][qe * RE + b]);
+                wv[b] = t.x; wv[b + 1] = t.y;
+            }
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[r][e] = __builtin_fmaf(xv[r], wv[e], acc[r][e]);
+            for (int a = 0; a < RM; a++)
+#pragma unroll
+                for (int b = 0; b < RE; b++) acc[a][b] = __builtin_fmaf(xv[a], wv[b], acc[a][b]);
+        }
+        if (ck + 1 < nchunk) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
     }
+    // halving trees (all lanes of the 16-lane row get each sum); lane j stores every 16th output
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int a = 0; a < RM; a++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float s = reduce16_lanes(acc[r][e]);
-            if (l == (uint32_t)(r * 4 + e) && row0 + r < m && e0 + e < E)
-                rlog[(size_t)(row0 + r) * E + e0 + e] = bias ? s + bias[e0 + e] : s;
+        for (int b = 0; b < RE; b++) {
+            const float sum = reduce16_lanes(acc[a][b]);
+            const uint32_t row = m0 + qm * RM + a, ex = e0 + qe * RE + b;
+            if (((uint32_t)(a * RE + b) % 16u) == j && row < m && ex < E)
+                rlog[(size_t)row * E + ex] = bias ? sum + bias[ex] : sum;
         }
 }
 
@@ -130,7 +193,15 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         const uint32_t nrow = E + (shexp_gate ? 1 : 0);
         router_dot_kernel<<<dim3((nrow + 1) / 2, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh);
     } else {
-        router_gemm_kernel<<<dim3((E + 15) / 16, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E, H, rlog);
+        if (m >= 256)
+            router_gemm_kernel<8, 8, 4><<<dim3((E + 31) / 32, (m + 31) / 32), 256, 0, st>>>(router, bias, x, m, E,
+                                                                                         H, rlog);
+        else if (m >= 64)
+            router_gemm_kernel<4, 4, 4><<<dim3((E + 15) / 16, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E,
+                                                                                         H, rlog);
+        else
+            router_gemm_kernel<4, 2, 4><<<dim3((E + 7) / 8, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E, H,
+                                                                                       rlog);
         if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
             router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh);
     }

@@ -28,12 +28,6 @@ __device__ __forceinline__ float rdl(float v, uint32_t l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)l));
 }
 
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Fallback selection (more than 64 candidates, i.e. many equal logits): each lane sorts its keys
 // (key desc, j asc), then kk rounds of a wave arg-max over the lane heads.  Lane rd < ksel gets
 // the key and index of the rd-th winner; returns ksel.
@@ -41,10 +35,15 @@ template <int NJ>
 __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict__ lg, uint32_t E, uint32_t kk,
                                                         uint32_t lane, uint32_t& my_key, uint32_t& my_idx) {
     uint32_t key[NJ], jj[NJ];
+    float v[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const uint32_t i = lane + 64u * j;
-        key[j] = i < E ? fkey(lg[i]) : 0u;
+        v[j] = lg[i < E ? i : E - 1];
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        key[j] = lane + 64u * j < E ? fkey(v[j]) : 0u;
         jj[j] = (uint32_t)j;
     }
     // odd-even transposition sort, descending key; equal keys keep ascending j (stable)
@@ -93,21 +92,29 @@ __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict_
 template <int NJ>
 __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
                               uint2* cand, float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
-    uint32_t key[NJ];
+    // all NJ loads go out together: clamped indices, no per-load branch
+    float v[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const uint32_t i = lane + 64u * j;
-        key[j] = i < E ? fkey(lg[i]) : 0u;
+        v[j] = lg[i < E ? i : E - 1];
     }
+    uint32_t key[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) key[j] = lane + 64u * j < E ? fkey(v[j]) : 0u;
     const uint32_t kk = pol.enabled ? pol.max : k;
     uint32_t lmax = key[0];
 #pragma unroll
     for (int j = 1; j < NJ; j++) lmax = lmax > key[j] ? lmax : key[j];
+    // two bits per step: the three candidate prefixes are counted independently
     uint32_t T = 0;
 #pragma unroll
-    for (int b = 31; b >= 0; b--) {
-        const uint32_t t = T | (1u << b);
-        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= kk) T = t;
+    for (int b = 30; b >= 0; b -= 2) {
+        const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
+        const uint32_t c1 = (uint32_t)__popcll(__ballot(lmax >= t1));
+        const uint32_t c2 = (uint32_t)__popcll(__ballot(lmax >= t2));
+        const uint32_t c3 = (uint32_t)__popcll(__ballot(lmax >= t3));
+        T = c3 >= kk ? t3 : (c2 >= kk ? t2 : (c1 >= kk ? t1 : T));
     }
     const uint32_t L = T > 1u ? T : 1u;  // key 0 (nan, -inf) is never selectable
     uint32_t C = 0;
@@ -125,15 +132,13 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
     uint32_t my_key = 0, my_idx = 0xffffffffu, ksel;
     if (C <= 64u) {
         wave_sync();
-        if (lane < C) {
-            const uint2 me = cand[lane];
-            uint32_t rank = 0;
-            for (uint32_t t = 0; t < C; t++) {
-                const uint32_t kt = cand[t].x;
-                rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
-            }
-            if (rank < kk) cand[64 + rank] = me;
+        const uint2 me = lane < C ? cand[lane] : make_uint2(0u, 0u);
+        uint32_t rank = 0;
+        for (uint32_t t = 0; t < C; t++) {  // candidate t's key from lane t's register
+            const uint32_t kt = (uint32_t)__builtin_amdgcn_readlane((int)me.x, (int)t);
+            rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
         }
+        if (lane < C && rank < kk) cand[64 + rank] = me;
         wave_sync();
         ksel = C < kk ? C : kk;
         if (lane < ksel) {

@@ -78,7 +78,7 @@ hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_ga
                                 hipStream_t st);
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
-hipError_t launch_dispatch(const Workspace& ws, uint32_t m, hipStream_t st);
+hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
                                const Workspace& ws, uint32_t m, hipStream_t st);
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m,
