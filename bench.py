@@ -34,10 +34,6 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-DECODE_KERNELS = ("router_logits", "decode_gateup", "decode_down")
-BATCH_KERNELS = ("router_logits", "route", "quantize", "dispatch", "batch_gateup", "batch_down", "batch_combine")
-
-
 def layer_bytes(n_experts_touched, M):
     """Algorithmic HBM bytes of one layer call (each byte counted once): touched experts, the
     shared expert, the f32 router, the shared gate vector, x in and out in f32."""
@@ -58,6 +54,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--fusion", type=int, default=None, choices=(0, 1),
+                    help="force the one-launch decode layer on (1) or off (0); default: the library's choice")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
                     help="finish with three device copies of MIB MiB (a known-size kernel for calibrating "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -85,6 +83,8 @@ def main():
     torch.cuda.synchronize()
     log(f"generated {args.layers} layers ({args.layers * E * EXPERT_BYTES / 1e9:.1f} GB experts) in {time.time() - t0:.1f}s")
     ctx = trmoe.Context(H, E, F, K, m_max)
+    if args.fusion is not None:
+        ctx.set_fusion(args.fusion)
     xs = {M: trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H) for M in ms_list}
     out = torch.empty((m_max, H), dtype=torch.float32, device=dev)
 
@@ -140,8 +140,12 @@ def main():
         # holds the last forward's routing and activations, so every launch does a real call's
         # work on cold weights); the K launches are captured into a HIP graph so that host launch
         # cost does not hide short kernels
+        ctx.set_timing(True)  # the kernels this M launches
+        ctx.forward(weights(0, M), x, out[:M])
+        names = list(ctx.timing())
+        ctx.set_timing(False)
         kern = {}
-        for name in (DECODE_KERNELS if M == 1 else BATCH_KERNELS):
+        for name in names:
             ctx.forward(weights(0, M), x, out[:M])
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -175,7 +179,8 @@ def main():
     tavg = float(np.mean(r["_touched"]))
     gu_bytes = (tavg + 1) * 2 * F * Q4K_ROW_H
     dn_bytes = (tavg + 1) * H * Q4K_ROW_F
-    alg = {"decode_gateup": gu_bytes + 2 * 2 * H + 2 * (H // 32) * 8 + 33 * 2 * (F + F // 16 * 8),
+    alg = {"decode_layer": gu_bytes + dn_bytes + E * H * 4 + H * 4 + H * 4 * 2,
+           "decode_gateup": gu_bytes + 2 * 2 * H + 2 * (H // 32) * 8 + 33 * 2 * (F + F // 16 * 8),
            "decode_down": dn_bytes + (tavg + 1) * 2 * (F + F // 16 * 8) + H * 4,
            "batch_gateup": gu_bytes, "batch_down": dn_bytes,
            "router_logits": E * H * 4 + prim * H * 4 + prim * E * 4}.get(dom)

@@ -172,6 +172,12 @@ int trk_gen_gguf_stack(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t s
 int trk_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, float *out, void *stream);
 
 /* ---- measurement and introspection ------------------------------------------------------ */
+/* M == 1: run the whole layer as one launch when the layer's shape has a fused kernel and the GPU
+ * can hold its grid at once (on by default), or always as the three launches router / gate-up /
+ * down (off).  Both follow exec.rs:1540-1623 with identical results; no counterpart in the
+ * reference, whose decode layer is one pool run. */
+int trk_set_fusion(trk_ctx *ctx, int on);
+
 /* Per-kernel timing (the HIP counterpart of the reference's TR_PROFILE laps, exec.rs:344-430):
  * when on, every kernel a forward launches is bracketed by HIP events on the call's stream. */
 int trk_set_timing(trk_ctx *ctx, int on);
@@ -202,7 +208,8 @@ enum {
     TRK_WS_XS = 12,      /* [rows][H/32] f32 */
     TRK_WS_ACTQ = 13,    /* activation rows of the down input, i8 */
     TRK_WS_ACTS = 14,    /* their folded scales, f32 */
-    TRK_WS_SHLOGIT = 15  /* [M] f32: dot(shexp_gate, x) */
+    TRK_WS_SHLOGIT = 15, /* [M] f32: dot(shexp_gate, x) */
+    TRK_WS_BARRIER_ERR = 16 /* u32: nonzero if a one-launch decode layer ever timed out at a grid barrier */
 };
 int trk_debug_read(trk_ctx *ctx, int which, void *host_dst, size_t bytes);
 

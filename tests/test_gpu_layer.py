@@ -83,6 +83,38 @@ def test_decode_layer(shape, k, hiprec):
     ctx.close()
 
 
+@pytest.mark.parametrize("policy", [None, (1, 10, 0.9, O.BASIS_TOP), (2, 10, 0.8, O.BASIS_ALL)])
+def test_decode_one_launch_matches_three(policy):
+    """The one-launch decode layer (grid barriers) and the three-launch sequence give the same
+    bits, both against the oracle; no barrier ever times out."""
+    say(f"decode one launch vs three, policy {policy}")
+    import torch
+    L, orc, W = layer("full", **FULL)
+    outs = {}
+    for fused in (True, False):
+        ctx = trmoe.Context(L.H, L.E, L.F, 10, 4)
+        ctx.set_fusion(fused)
+        if policy:
+            ctx.set_moe(policy)
+        res = []
+        for t in range(3):
+            x = L.x(1, tid=700 + t)
+            out = torch.empty((1, L.H), dtype=torch.float32, device="cuda")
+            ctx.forward(W, dev(x), out)
+            res.append(host(out)[0].copy())
+            if fused:
+                r = orc.moe_block(x[0], k=10, hiprec=True, policy=policy)
+                ids = ctx.read(trmoe.WS_IDS, 4 * 32, np.uint32)[:len(r["ids"])]
+                assert np.array_equal(ids, r["ids"])
+                w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:len(r["ids"])]
+                compare_out(res[-1], r["out"], np.array_equal(w, r["w"]), f"fused t={t}")
+        assert ctx.read(trmoe.WS_BARRIER_ERR, 4, np.uint32)[0] == 0
+        outs[fused] = res
+        ctx.close()
+    for a, b in zip(outs[True], outs[False]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
                                        ("full", 16, 10)])
 def test_batch_layer_and_dispatch(shape, M, k):

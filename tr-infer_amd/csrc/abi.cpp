@@ -40,11 +40,11 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 }  // namespace
 
 // Kernel ids for trk_get_timing.
-enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DISPATCH, K_B_GATEUP, K_B_DOWN, K_B_COMBINE,
-                K_RMSNORM, K_COUNT };
+enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DEC_LAYER, K_DISPATCH, K_B_GATEUP, K_B_DOWN,
+                K_B_COMBINE, K_RMSNORM, K_COUNT };
 static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
-                                                  "decode_down", "dispatch", "batch_gateup", "batch_down",
-                                                  "batch_combine", "rmsnorm"};
+                                                  "decode_down", "decode_layer", "dispatch", "batch_gateup",
+                                                  "batch_down", "batch_combine", "rmsnorm"};
 
 struct TimedLaunch {
     int kid;
@@ -60,6 +60,8 @@ struct trk_ctx {
     int timing;
     std::vector<TimedLaunch> timed;
     std::vector<hipEvent_t> spare;
+    int fusion = 0;   // decode: one launch per layer (when the shape and the GPU allow it) if set
+    int fused = -1;   // that check for the current policy: -1 not yet made, 0 no, 1 yes
 };
 
 extern "C" const char* trk_last_error(void) { return g_err; }
@@ -140,7 +142,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.yent, yrows * H * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
-        {(void**)&ws.counters, 64},
+        {(void**)&ws.counters, 64 * 4 * 34},  // grid-barrier words, 256 bytes apart
     };
     size_t total = 0;
     for (auto& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
@@ -186,11 +188,13 @@ extern "C" int trk_set_moe(trk_ctx* c, const trk_moe_policy* p) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     if (!p) {
         c->pol = Policy{0, 0, 0, 0, 0.0f};
+        c->fused = -1;
         return TRK_OK;
     }
     int rc = check_policy(c, p);
     if (rc) return rc;
     c->pol = Policy{1, p->min, p->max, p->basis, p->mass};
+    c->fused = -1;
     return TRK_OK;
 }
 
@@ -277,6 +281,18 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     if (m == 1) {
         // logits (and the shared gate's logit), then routing + gate/up in one launch, then down
         const int pair = c->cfg.hiprec ? 1 : 0;
+        if (c->fusion && c->fused < 0)
+            c->fused = launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg, M.shu,
+                                           M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual, true,
+                                           st) == hipSuccess
+                               ? 1
+                               : 0;
+        if (c->fusion && c->fused == 1 && w->router) {
+            TIMED(K_DEC_LAYER, launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
+                                                   M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual,
+                                                   false, st));
+            return TRK_OK;
+        }
         if (rlog)
             TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st));
         else
@@ -338,6 +354,13 @@ extern "C" int trk_get_stats(trk_ctx* c, trk_moe_stats* out, int reset) {
     return TRK_OK;
 }
 
+extern "C" int trk_set_fusion(trk_ctx* c, int on) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    c->fusion = on ? 1 : 0;
+    c->fused = -1;
+    return TRK_OK;
+}
+
 extern "C" int trk_set_timing(trk_ctx* c, int on) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     c->timing = on ? 1 : 0;
@@ -392,6 +415,7 @@ extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes) {
     case TRK_WS_XS: src = ws.xs; cap = rows_x * (ws.H / 32) * 4; break;
     case TRK_WS_ACTQ: src = ws.actq; cap = ws.act_rows * ws.F; break;
     case TRK_WS_ACTS: src = ws.acts; cap = ws.act_rows * (ws.F / 16) * 4; break;
+    case TRK_WS_BARRIER_ERR: src = ws.counters + 2; cap = 4; break;
     case TRK_WS_SHLOGIT: src = ws.shl; cap = M * 4; break;
     default: return fail(TRK_E_INVALID, "unknown workspace buffer %d", which);
     }

@@ -167,6 +167,23 @@ __device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, floa
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Device-coherent word access for data exchanged between workgroups inside one launch:
+// agent-scope atomic loads and stores go to memory directly, past the per-XCD L2, so neither
+// side needs a whole-cache write-back or invalidate.
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_dev(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_devf(const float* p) {
+    return __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_devf(float* p, float v) { st_dev(reinterpret_cast<uint32_t*>(p), __float_as_uint(v)); }
+
 // LDS writes of this wave visible to its own later reads (no workgroup barrier)
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -14,6 +14,7 @@
 //            runs the chain in registers; slot 0 is stored and later slots (routing order,
 //            shared last) are added — tasks C with the combine fused.
 #include "route.hpp"
+#include "router.hpp"
 
 namespace trk {
 
@@ -39,7 +40,7 @@ __device__ __forceinline__ float lane_up(float v) {
 // on every thread once the routing is in LDS, before any weight of a routed slot is requested
 // (the fused layer kernel issues its down-projection prefetch there).  active = false: route
 // and hook only.
-template <int P, int NSB, int NJ, typename Hook>
+template <int P, int NSB, int NJ, bool COH, typename Hook>
 __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, const Mat& shg, const Mat& shu,
                                             const float* __restrict__ x, const float* __restrict__ lg,
                                             const Workspace& ws, uint32_t k, const Policy& pol, uint32_t kcap,
@@ -83,12 +84,12 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
     float shl = 0.0f;
     if (shared) {
         load_rows(shg, shu, 0u, wq);  // the shared expert does not wait for the routing
-        shl = ws.shl[0];
+        shl = COH ? ld_devf(ws.shl) : ws.shl[0];
     }
     if (route && tid < 64) {
         // route this token (wave 0): every routed workgroup repeats it, so no separate launch and
         // no round trip through memory sits between the logits and the expert weights
-        const uint32_t n = route_row<NJ>(lg, E, k, pol, tid, cand, ex, r_ids, r_w);
+        const uint32_t n = route_row<NJ, COH>(lg, E, k, pol, tid, cand, ex, r_ids, r_w);
         if (tid == 0) r_n[0] = n;
         if (publish) {  // one workgroup publishes it (down kernel, introspection)
             wave_sync();
@@ -244,10 +245,23 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             const int32_t qi = cvt_rne(v * inv);
             const int32_t sum = row16_allreduce(qi, [](int32_t a, int32_t b) { return a + b; });
-            dq[p * F + tid] = sat_i8(qi);
-            if (tid == 0) {
-                ds[p * nbf] = sc * wgt;
-                dsu[p * nbf] = sum;
+            if constexpr (COH) {  // 4 lanes' bytes in one device-coherent word (quad_perm gathers)
+                const uint32_t b0 = (uint8_t)sat_i8(qi);
+                const uint32_t b1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b0, 0xF9, 0xf, 0xf, false);
+                const uint32_t b2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b0, 0xFE, 0xf, 0xf, false);
+                const uint32_t b3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b0, 0xFF, 0xf, 0xf, false);
+                if (tid % 4 == 0)
+                    st_dev(reinterpret_cast<uint32_t*>(dq + p * F + tid), b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
+                if (tid == 0) {
+                    st_devf(ds + p * nbf, sc * wgt);
+                    st_dev(reinterpret_cast<uint32_t*>(dsu + p * nbf), (uint32_t)sum);
+                }
+            } else {
+                dq[p * F + tid] = sat_i8(qi);
+                if (tid == 0) {
+                    ds[p * nbf] = sc * wgt;
+                    dsu[p * nbf] = sum;
+                }
             }
             v = __builtin_fmaf(-(float)qi, sc, v);  // residual for the second level (quant.rs:132)
         }
@@ -268,7 +282,7 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
         Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
         uint32_t k, Policy pol, uint32_t kcap) {
     extern __shared__ __align__(16) uint8_t smem[];
-    gateup_unit<P, NSB, NJ>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
+    gateup_unit<P, NSB, NJ, false>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
                             blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoHook{});
 }
 
@@ -467,7 +481,7 @@ __device__ __forceinline__ void down_first(const Mat& down, const Mat& shd, uint
     if (f.live && down.fmt == TRK_FMT_Q4_K) load_half_q4k(f.rowp, q / 2, q % 2, f.hdr, f.qs);
 }
 
-template <int P, int NSB>
+template <int P, int NSB, bool COH>
 __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const Workspace& ws, uint32_t kcap,
                                           uint32_t n, const uint32_t* ids, float* __restrict__ out, int residual,
                                           uint32_t row0, uint8_t* smem, const DownFirst& first) {
@@ -495,7 +509,15 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
             for (int c = 0; c < 4; c++) {
                 const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
                 const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
-                t[c] = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F)[ic % QP];
+                const int4* src = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F) + ic % QP;
+                if constexpr (COH) {
+                    const unsigned long long* w2 = reinterpret_cast<const unsigned long long*>(src);
+                    const unsigned long long lo = ld_dev(w2), hi = ld_dev(w2 + 1);
+                    t[c] = make_int4((int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
+                                     (int)(uint32_t)(hi >> 32));
+                } else {
+                    t[c] = *src;
+                }
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
@@ -510,8 +532,9 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
             for (int c = 0; c < 4; c++) {
                 const uint32_t i = i0 + tid + 256 * c, ic = i < ns ? i : ns - 1;
                 const uint32_t s = ic / SP, a = s < kcap ? s : (uint32_t)SH_SLOT;
-                sc[c] = ws.acts[(size_t)a * SP + ic % SP];
-                su[c] = ws.actsum[(size_t)a * SP + ic % SP];
+                const size_t o = (size_t)a * SP + ic % SP;
+                sc[c] = COH ? ld_devf(ws.acts + o) : ws.acts[o];
+                su[c] = COH ? (int32_t)ld_dev(reinterpret_cast<const uint32_t*>(ws.actsum + o)) : ws.actsum[o];
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
@@ -588,7 +611,151 @@ __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Wor
     const uint32_t row0 = blockIdx.x * DN_R, n = ws.n_sel[0];
     DownFirst first;
     down_first<NSB>(down, shd, kcap, n, ws.ids, row0, first);
-    down_unit<P, NSB>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first);
+    down_unit<P, NSB, false>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first);
+}
+
+// ---- the whole decode layer in one launch ----------------------------------------------------
+//
+// Three phases separated by grid barriers: (1) router logits and the shared gate's logit, one
+// wave per router row; (2) every workgroup routes the token, workgroups with a (slot, strip) unit
+// run it, and every workgroup requests the down-projection weights of its phase-3 rows as soon
+// as the routing is known; (3) down + combine for 4 output rows per workgroup.  Requires the
+// whole grid resident at once (the host checks occupancy); the barriers wait a bounded time.
+
+constexpr uint32_t BARRIER_SPIN = 1u << 16;  // polls before a barrier gives up (~tens of ms)
+constexpr uint32_t BAR_GROUPS = 32;          // workgroups arrive in BAR_GROUPS groups (wg % BAR_GROUPS)
+constexpr uint32_t BAR_LINE = 64;            // u32 words between barrier words (256 bytes)
+
+// Two-level grid barrier on counters that only grow, so no reset is needed between barriers or
+// launches (graph replays included).  A workgroup arrives on its group's counter; the last of a
+// group arrives on the top counter; the last group writes every group's release word, and each
+// workgroup polls its own group's word.  No line sees more than BAR_GROUPS arrivals or more than
+// nwg / BAR_GROUPS pollers.  Words (u32 index into ws.counters): top at 0, time-out flag at 2,
+// group g's counter at BAR_LINE * (1 + g), its release word at BAR_LINE * (1 + g) + 32.
+// Data crossing the barrier is written and read with the device-coherent ld_dev / st_dev, so
+// completing this workgroup's stores (s_waitcnt) before arriving is the whole release: no L2
+// write-back or invalidate (each of those is a whole-cache operation on gfx950).
+__device__ __forceinline__ void grid_barrier(uint32_t* words, uint32_t nwg) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t g = blockIdx.x % BAR_GROUPS, gsize = nwg / BAR_GROUPS;
+        unsigned long long* top = reinterpret_cast<unsigned long long*>(words);
+        unsigned long long* sub = reinterpret_cast<unsigned long long*>(words + BAR_LINE * (1 + g));
+        const unsigned long long* rel = reinterpret_cast<const unsigned long long*>(words + BAR_LINE * (1 + g) + 32);
+        const unsigned long long old =
+                __hip_atomic_fetch_add(sub, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long epoch = old / gsize + 1;  // barriers completed once this one is
+        if (old % gsize == gsize - 1) {
+            const unsigned long long t = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (t % BAR_GROUPS == BAR_GROUPS - 1)
+                for (uint32_t h = 0; h < BAR_GROUPS; h++)
+                    __hip_atomic_store(reinterpret_cast<unsigned long long*>(words + BAR_LINE * (1 + h) + 32), epoch,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        uint32_t spins = 0;
+        while (ld_dev(rel) < epoch) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins == BARRIER_SPIN) {
+                __hip_atomic_fetch_or(words + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int P, int NSB, int NJ, int NSBF>
+__global__ __launch_bounds__(256) void decode_layer_kernel(const float* __restrict__ router,
+                                                          const float* __restrict__ bias,
+                                                          const float* __restrict__ shgv, Mat gate, Mat up,
+                                                          Mat down, Mat shg, Mat shu, Mat shd,
+                                                          const float* __restrict__ x, const float* __restrict__ lg_in,
+                                                          Workspace ws, uint32_t k, Policy pol, uint32_t kcap,
+                                                          float* __restrict__ out, int residual, uint32_t rsm_bytes) {
+    constexpr uint32_t H = NSB * 256;
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t* rsm = smem;              // routing (kept through phase 3)
+    uint8_t* usm = smem + rsm_bytes;  // unit area: gate/up, then down
+    const uint32_t E = ws.E, nwg = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
+    const uint32_t strips = gate.rows / 16;
+
+    // phase 1: logits (attn::dot order, exec.rs:1003-1011) and the shared gate's logit
+    {
+        const uint32_t wv = tid / 64, lane = tid % 64;
+        for (uint32_t row = wg * 4 + wv; row <= E; row += nwg * 4) {
+            if (lg_in && row < E) continue;
+            const float* wr = row < E ? router + (size_t)row * H : shgv;
+            float res[DOT_MR];
+            dot_rows(wr, x, 0, 1, H, lane, res);
+            if (lane == 0) {
+                if (row < E)
+                    st_devf(ws.rlog + row, bias ? res[0] + bias[row] : res[0]);
+                else
+                    st_devf(ws.shl, res[0]);
+            }
+        }
+    }
+    grid_barrier(ws.counters, nwg);
+
+    // phase 2: route, gate/up units, down weights requested
+    const float* lg = lg_in ? lg_in : ws.rlog;
+    const uint32_t units = (kcap + 1) * strips;
+    const bool active = wg < units;
+    const uint32_t row0 = wg * DN_R;
+    DownFirst first;
+    gateup_unit<P, NSB, NJ, true>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, active ? wg / strips : 0u,
+                            active ? wg % strips : 0u, active, true, wg == 0, usm, rsm,
+                            [&](const uint32_t* ids, uint32_t n) {
+                                down_first<NSBF>(down, shd, kcap, n, ids, row0, first);
+                            });
+    grid_barrier(ws.counters, nwg);
+
+    // phase 3: down + combine (exec.rs:1610-1621)
+    const uint32_t* r_ids = reinterpret_cast<const uint32_t*>(rsm);
+    const uint32_t n = r_ids[2 * K_MAX];
+    down_unit<P, NSBF, true>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first);
+}
+
+template <int P, int NSB, int NJ, int NSBF>
+static size_t layer_lds(uint32_t E, uint32_t kcap, bool mass_all, uint32_t& rsm) {
+    rsm = (ROUTE_LDS + (mass_all ? E * 4 : 0) + 15) / 16 * 16;
+    const size_t gu = gu_lds_x<P, NSB>();
+    const size_t slots = kcap + 1, F = NSBF * 256, nbf = F / 16;
+    const size_t dn = slots * (P * F + 16) + slots * P * nbf * 8 + slots * DN_R * 4 + 64;
+    return rsm + (gu > dn ? gu : dn);
+}
+
+// Fused decode layer: returns hipErrorNotSupported when the shape or the GPU cannot hold the
+// grid (the caller then runs the three separate launches).  check_only: answer that (queries the
+// occupancy) without launching.
+hipError_t launch_decode_layer(const float* router, const float* bias, const float* shexp_gate, const Mat& gate,
+                               const Mat& up, const Mat& down, const Mat& sh_gate, const Mat& sh_up,
+                               const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
+                               Policy pol, int pair, uint32_t kcap, float* out, int residual, bool check_only,
+                               hipStream_t st) {
+    const uint32_t H = gate.k, F = gate.rows, E = ws.E;
+    const uint32_t nwg = H / DN_R;
+    if (H != 2048 || F != 512 || E > 512 || !pair || down.fmt != TRK_FMT_Q4_K || sh_down.fmt != TRK_FMT_Q4_K)
+        return hipErrorNotSupported;  // the instantiated shape (BASELINE's layer)
+    if ((kcap + 1) * (F / 16) > nwg || !router || nwg % BAR_GROUPS) return hipErrorNotSupported;
+    const bool mass_all = pol.enabled && pol.basis == TRK_BASIS_ALL;
+    uint32_t rsm = 0;
+    const size_t lds = layer_lds<2, 8, 8, 2>(E, kcap, mass_all, rsm);
+    auto kern = decode_layer_kernel<2, 8, 8, 2>;
+    if (check_only) {  // can the whole grid be resident at once?
+        int per_cu = 0, dev = 0, cus = 0;
+        hipError_t e;
+        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+        if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds)) != hipSuccess) return e;
+        return (uint64_t)per_cu * (uint64_t)cus >= nwg ? hipSuccess : hipErrorNotSupported;
+    }
+    kern<<<nwg, 256, lds, st>>>(router, bias, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, x, rlog, ws, k, pol,
+                                kcap, out, residual, rsm);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair, uint32_t kcap,

@@ -31,15 +31,15 @@ __device__ __forceinline__ float rdl(float v, uint32_t l) {
 // Fallback selection (more than 64 candidates, i.e. many equal logits): each lane sorts its keys
 // (key desc, j asc), then kk rounds of a wave arg-max over the lane heads.  Lane rd < ksel gets
 // the key and index of the rd-th winner; returns ksel.
-template <int NJ>
+template <int NJ, bool COH>
 __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict__ lg, uint32_t E, uint32_t kk,
                                                         uint32_t lane, uint32_t& my_key, uint32_t& my_idx) {
     uint32_t key[NJ], jj[NJ];
     float v[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const uint32_t i = lane + 64u * j;
-        v[j] = lg[i < E ? i : E - 1];
+        const uint32_t i = lane + 64u * j, ic = i < E ? i : E - 1;
+        v[j] = COH ? ld_devf(lg + ic) : lg[ic];
     }
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -84,20 +84,23 @@ __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict_
 // `cand` is 96 entries of LDS for this wave; `ex` (E floats of LDS) is used only for
 // MassBasis::All.
 //
-// Selection: T = the kk-th largest of the 64 lane maxima (a 32-step radix select over ballots) is
-// a lower bound on the kk-th largest key, since the kk lanes with the largest maxima hold kk keys
-// >= T.  The keys >= T (usually a few more than kk) are compacted into LDS in ascending index
-// order; each candidate's rank is the number of candidates with a larger key plus the earlier
-// ones with an equal key, and the candidates of rank < kk are written to their rank's slot.
-template <int NJ>
+// Selection: T = the kk-th largest of the 64 lane maxima, truncated to its top 16 bits (a radix
+// select over ballots), is a lower bound on the kk-th largest key, since the kk lanes with the
+// largest maxima hold kk keys >= T.  The keys >= T (usually a few more than kk) are compacted
+// into LDS in ascending index order; each candidate's rank is the number of candidates with a
+// larger key plus the earlier ones with an equal key, and the candidates of rank < kk are written
+// to their rank's slot.
+// COH: the logits were written earlier in the same launch by other workgroups (device-coherent
+// loads).
+template <int NJ, bool COH = false>
 __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
                               uint2* cand, float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
     // all NJ loads go out together: clamped indices, no per-load branch
     float v[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const uint32_t i = lane + 64u * j;
-        v[j] = lg[i < E ? i : E - 1];
+        const uint32_t i = lane + 64u * j, ic = i < E ? i : E - 1;
+        v[j] = COH ? ld_devf(lg + ic) : lg[ic];
     }
     uint32_t key[NJ];
 #pragma unroll
@@ -106,10 +109,12 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
     uint32_t lmax = key[0];
 #pragma unroll
     for (int j = 1; j < NJ; j++) lmax = lmax > key[j] ? lmax : key[j];
-    // two bits per step: the three candidate prefixes are counted independently
+    // two bits per step over the top 16 bits of the keys: T is the kk-th largest lane maximum
+    // with its low 16 bits cleared, still a lower bound (candidates sharing its top 16 bits join
+    // the ranking); the three candidate prefixes of a step are counted independently
     uint32_t T = 0;
 #pragma unroll
-    for (int b = 30; b >= 0; b -= 2) {
+    for (int b = 30; b >= 16; b -= 2) {
         const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
         const uint32_t c1 = (uint32_t)__popcll(__ballot(lmax >= t1));
         const uint32_t c2 = (uint32_t)__popcll(__ballot(lmax >= t2));
@@ -147,7 +152,7 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
             my_idx = w.y;
         }
     } else {
-        ksel = route_select_rounds<NJ>(lg, E, kk, lane, my_key, my_idx);
+        ksel = route_select_rounds<NJ, COH>(lg, E, kk, lane, my_key, my_idx);
     }
     if (ksel == 0) return 0;  // nothing selectable (the reference would index u32::MAX)
     const float my_tv = lane < ksel ? fkey_inv(my_key) : -__builtin_inff();
@@ -157,7 +162,7 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
     if (pol.enabled) {  // route_mass (router.rs:118-148)
         float denom = 0.0f;
         if (pol.basis == TRK_BASIS_ALL) {
-            for (uint32_t i = lane; i < E; i += 64u) ex[i] = expf_libm(lg[i] - mx);
+            for (uint32_t i = lane; i < E; i += 64u) ex[i] = expf_libm((COH ? ld_devf(lg + i) : lg[i]) - mx);
             wave_sync();
             if (lane == 0)
                 for (uint32_t i = 0; i < E; i++) denom += ex[i];

@@ -61,7 +61,7 @@ struct Workspace {
     float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
-    uint32_t* counters;   // [16] device-scope arrival counters (kept at zero between launches)
+    uint32_t* counters;   // [64 * 34]: grid-barrier words (k_decode.hip), [2] barrier time-out flag
     size_t act_rows;
 };
 
@@ -76,6 +76,11 @@ hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k,
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
                                 const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
                                 hipStream_t st);
+hipError_t launch_decode_layer(const float* router, const float* bias, const float* shexp_gate, const Mat& gate,
+                               const Mat& up, const Mat& down, const Mat& sh_gate, const Mat& sh_up,
+                               const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
+                               Policy pol, int pair, uint32_t kcap, float* out, int residual, bool check_only,
+                               hipStream_t st);
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);

@@ -19,7 +19,7 @@ FMT_Q4_K, FMT_Q6_K = 12, 14
 BASIS_ALL, BASIS_TOP = 0, 1
 K_MAX = 32
 (WS_RLOG, WS_IDS, WS_W, WS_NSEL, WS_ENT_TOK, WS_ENT_W, WS_ENT_EXP, WS_GRP_START, WS_GRP_EXP, WS_NGROUPS, WS_XQ,
- WS_XS, WS_ACTQ, WS_ACTS, WS_SHLOGIT) = range(1, 16)
+ WS_XS, WS_ACTQ, WS_ACTS, WS_SHLOGIT, WS_BARRIER_ERR) = range(1, 17)
 
 
 class TrkError(RuntimeError):
@@ -81,6 +81,7 @@ def lib() -> C.CDLL:
         L.trk_debug_read.argtypes = [vp, i, vp, sz]
         L.trk_launch_kernel.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, C.c_char_p, vp]
         L.trk_set_timing.argtypes = [vp, i]
+        L.trk_set_fusion.argtypes = [vp, i]
         L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
         _lib = L
     return _lib
@@ -157,6 +158,9 @@ class Context:
         s = Stats()
         check(lib().trk_get_stats(self.h, C.byref(s), int(reset)))
         return s.rows, s.experts
+
+    def set_fusion(self, on: bool):
+        check(lib().trk_set_fusion(self.h, int(on)))
 
     def set_timing(self, on: bool):
         check(lib().trk_set_timing(self.h, int(on)))
