@@ -142,7 +142,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.yent, yrows * H * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
-        {(void**)&ws.counters, 64 * 4 * 34},  // grid-barrier words, 256 bytes apart
+        {(void**)&ws.counters, (size_t)BAR_LINE * 4 * (BAR_GROUPS + 2)},
     };
     size_t total = 0;
     for (auto& pc : pieces) total += (pc.bytes + 255) / 256 * 256;

@@ -623,8 +623,6 @@ __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Wor
 // whole grid resident at once (the host checks occupancy); the barriers wait a bounded time.
 
 constexpr uint32_t BARRIER_SPIN = 1u << 16;  // polls before a barrier gives up (~tens of ms)
-constexpr uint32_t BAR_GROUPS = 32;          // workgroups arrive in BAR_GROUPS groups (wg % BAR_GROUPS)
-constexpr uint32_t BAR_LINE = 64;            // u32 words between barrier words (256 bytes)
 
 // Two-level grid barrier on counters that only grow, so no reset is needed between barriers or
 // launches (graph replays included).  A workgroup arrives on its group's counter; the last of a

@@ -33,6 +33,11 @@ struct Item {
 };
 
 // Device workspace (sized at trk_create).
+// grid barrier of the one-launch decode layer: workgroups arrive on BAR_GROUPS counters, BAR_LINE
+// u32 words apart
+constexpr uint32_t BAR_GROUPS = 32;
+constexpr uint32_t BAR_LINE = 64;
+
 struct Workspace {
     uint32_t H, E, F, m_max, k_cap, ent_cap, item_cap;
     int8_t* xq;           // [max(2, m_max)][H]
@@ -61,7 +66,8 @@ struct Workspace {
     float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
-    uint32_t* counters;   // [64 * 34]: grid-barrier words (k_decode.hip), [2] barrier time-out flag
+    uint32_t* counters;   // [BAR_LINE * (BAR_GROUPS + 2)]: grid-barrier words (k_decode.hip): [0..1] top
+                          // counter, [2] time-out flag, group g's counter and release word at BAR_LINE * (1 + g)
     size_t act_rows;
 };
 
