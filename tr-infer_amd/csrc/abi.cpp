@@ -293,11 +293,14 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
                                                    false, st));
             return TRK_OK;
         }
+        // the logits launch also quantises x for gate/up
+        const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, pair};
         if (rlog)
-            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st));
+            TIMED(K_LOGITS,
+                  launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st, &xq));
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, 1, E, H, 0, ws.rlog,
-                                                 ws.shl, st));
+                                                 ws.shl, st, &xq));
         TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
     } else {

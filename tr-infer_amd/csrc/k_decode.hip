@@ -40,7 +40,7 @@ __device__ __forceinline__ float lane_up(float v) {
 // on every thread once the routing is in LDS, before any weight of a routed slot is requested
 // (the fused layer kernel issues its down-projection prefetch there).  active = false: route
 // and hook only.
-template <int P, int NSB, int NJ, bool COH, typename Hook>
+template <int P, int NSB, int NJ, bool COH, bool XPRE, typename Hook>
 __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, const Mat& shg, const Mat& shu,
                                             const float* __restrict__ x, const float* __restrict__ lg,
                                             const Workspace& ws, uint32_t k, const Policy& pol, uint32_t kcap,
@@ -61,13 +61,36 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
     uint2* cand = (uint2*)(r_n + 4);               // [ROUTE_CAND] routing scratch
     float* ex = (float*)(cand + ROUTE_CAND);       // [E] (MassBasis::All only)
 
-    // x first: its loads must not queue behind the (id-dependent) weight loads
+    // x first: its loads must not queue behind the (id-dependent) weight loads.  XPRE: x is
+    // already quantised in ws.xq / xs / xu (the logits launch does it), one block per thread
     float4 xv[8];
     const bool qthread = active && tid >= 64 && tid < 64 + nb;
     if (qthread) {
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)(tid - 64) * 32);
+        const uint32_t b = tid - 64;
+        if constexpr (XPRE) {  // straight into LDS (the routing wave does not touch this area)
+            uint4 pq[P][2];
+            float ps[P], pu[P];
 #pragma unroll
-        for (int i = 0; i < 8; i++) xv[i] = src[i];
+            for (int p = 0; p < P; p++) {
+                const uint4* src = reinterpret_cast<const uint4*>(ws.xq + (size_t)p * H + b * 32);
+                pq[p][0] = src[0];
+                pq[p][1] = src[1];
+                ps[p] = ws.xs[p * nb + b];
+                pu[p] = ws.xu[p * nb + b];
+            }
+            const uint32_t xo = (b / 8) * XSB + (b % 8) * 32;
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                *reinterpret_cast<uint4*>(xq + p * XP + xo) = pq[p][0];
+                *reinterpret_cast<uint4*>(xq + p * XP + xo + 16) = pq[p][1];
+                xs[p * nb + b] = ps[p];
+                xu[p * nb + b] = pu[p];
+            }
+        } else {
+            const float4* src = reinterpret_cast<const float4*>(x + (size_t)b * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = src[i];
+        }
     }
     const uint32_t r = tid / NSB, sb = tid % NSB;
     const bool wthread = r < 32;
@@ -107,7 +130,7 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
         }
     }
     // quantise x per 32 (quantize_pair_blocks, quant.rs:96-108, or QAct::quantize) into LDS
-    if (qthread) {
+    if (!XPRE && qthread) {
         const uint32_t b = tid - 64;
         float v[32], rs[32];
 #pragma unroll
@@ -282,7 +305,7 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
         Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
         uint32_t k, Policy pol, uint32_t kcap) {
     extern __shared__ __align__(16) uint8_t smem[];
-    gateup_unit<P, NSB, NJ, false>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
+    gateup_unit<P, NSB, NJ, false, true>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
                             blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoHook{});
 }
 
@@ -500,46 +523,38 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
 
     {
         // loads first (clamped indices, so no per-lane branch separates them), then the stores:
-        // one memory round trip per chunk of 4 pieces per thread
-        constexpr uint32_t QP = P * F / 16, SP = P * nbf;  // int4 pieces and scales per slot
-        const uint32_t nq = slots * QP, ns = slots * SP;
+        // one memory round trip per chunk of 4 (int4 piece, scale, sum) per thread
+        constexpr uint32_t QP = P * F / 16;  // int4 pieces of a slot = its scales = its sums
+        static_assert(QP == P * nbf, "a 16-byte piece per 16-block");
+        const uint32_t nq = slots * QP;
         for (uint32_t i0 = 0; i0 < nq; i0 += 1024) {
             int4 t[4];
+            float sc[4];
+            int32_t su[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
                 const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
                 const int4* src = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F) + ic % QP;
+                const size_t o = (size_t)a * QP + ic % QP;
                 if constexpr (COH) {
                     const unsigned long long* w2 = reinterpret_cast<const unsigned long long*>(src);
                     const unsigned long long lo = ld_dev(w2), hi = ld_dev(w2 + 1);
                     t[c] = make_int4((int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
                                      (int)(uint32_t)(hi >> 32));
+                    sc[c] = ld_devf(ws.acts + o);
+                    su[c] = (int32_t)ld_dev(reinterpret_cast<const uint32_t*>(ws.actsum + o));
                 } else {
                     t[c] = *src;
+                    sc[c] = ws.acts[o];
+                    su[c] = ws.actsum[o];
                 }
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const uint32_t i = i0 + tid + 256 * c;
-                if (i < nq) *reinterpret_cast<int4*>(aq + (size_t)(i / QP) * SQ + (i % QP) * 16) = t[c];
-            }
-        }
-        for (uint32_t i0 = 0; i0 < ns; i0 += 1024) {
-            float sc[4];
-            int32_t su[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint32_t i = i0 + tid + 256 * c, ic = i < ns ? i : ns - 1;
-                const uint32_t s = ic / SP, a = s < kcap ? s : (uint32_t)SH_SLOT;
-                const size_t o = (size_t)a * SP + ic % SP;
-                sc[c] = COH ? ld_devf(ws.acts + o) : ws.acts[o];
-                su[c] = COH ? (int32_t)ld_dev(reinterpret_cast<const uint32_t*>(ws.actsum + o)) : ws.actsum[o];
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint32_t i = i0 + tid + 256 * c;
-                if (i < ns) {
+                if (i < nq) {
+                    *reinterpret_cast<int4*>(aq + (size_t)(i / QP) * SQ + (i % QP) * 16) = t[c];
                     as[i] = sc[c];
                     au[i] = sc[c] * (float)su[c];
                 }
@@ -704,7 +719,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(const float* __restri
     const bool active = wg < units;
     const uint32_t row0 = wg * DN_R;
     DownFirst first;
-    gateup_unit<P, NSB, NJ, true>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, active ? wg / strips : 0u,
+    gateup_unit<P, NSB, NJ, true, false>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, active ? wg / strips : 0u,
                             active ? wg % strips : 0u, active, true, wg == 0, usm, rsm,
                             [&](const uint32_t* ids, uint32_t n) {
                                 down_first<NSBF>(down, shd, kcap, n, ids, row0, first);

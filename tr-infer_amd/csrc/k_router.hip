@@ -13,13 +13,86 @@
 
 namespace trk {
 
-// grid.x: waves over weight rows ([0, E) router rows + bias, row E = shared gate if shg);
-// grid.y: chunks of DOT_MR activation rows.
+// Quantise a 32-block held by the 4 lanes of a quad (lane q: values 8q..8q+7) as quant_block_regs<32>
+// does (quant.rs:112-166): the block maximum and the integer sum do not depend on the order, so
+// quad all-reduces give the same scale and sum.  qw: this lane's 8 bytes.
+template <bool RESID>
+__device__ __forceinline__ void quant_block_quad(const float (&v)[8], uint32_t (&qw)[2], float& scale, int32_t& sum,
+                                                 float (&resid)[8]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = mx_ps(amax, __builtin_fabsf(v[i]));
+    amax = mx_ps(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xf, 0xf, false)));
+    amax = mx_ps(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xf, 0xf, false)));
+    const float s = amax / 127.0f;
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    int32_t su = 0;
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int i = 4 * w + b;
+            const int32_t qi = cvt_rne(v[i] * inv);
+            su += qi;
+            packed |= (uint32_t)(uint8_t)sat_i8(qi) << (8 * b);
+            if (RESID) resid[i] = __builtin_fmaf(-(float)qi, s, v[i]);
+        }
+        qw[w] = packed;
+    }
+    su += __builtin_amdgcn_mov_dpp(su, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    su += __builtin_amdgcn_mov_dpp(su, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    scale = s;
+    sum = su;
+}
+
+// x of one row (decode) quantised per 32 by the workgroups after the logit rows: four lanes per
+// block; pair = quantize_pair_blocks (quant.rs:96-108), else QAct::quantize.
+__device__ __forceinline__ void quantize_x_row(const float* __restrict__ x, uint32_t H, const XQuant& xq,
+                                               uint32_t qwg) {
+    const uint32_t nb = H / 32, t = qwg * blockDim.x + threadIdx.x, b = t / 4, qd = t % 4;
+    const uint32_t bc = b < nb ? b : nb - 1;
+    const float4* src = reinterpret_cast<const float4*>(x + (size_t)bc * 32 + 8 * qd);
+    const float4 a = src[0], c = src[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+    float r[8], r2[8];
+    uint32_t qw[2];
+    float s;
+    int32_t su;
+    quant_block_quad<true>(v, qw, s, su, r);
+    if (b < nb) {
+        *reinterpret_cast<uint2*>(xq.q + (size_t)b * 32 + 8 * qd) = make_uint2(qw[0], qw[1]);
+        if (qd == 0) {
+            xq.s[b] = s;
+            xq.sum[b] = su;
+            xq.u[b] = s * (float)su;  // gemv.rs:144
+        }
+    }
+    if (xq.pair) {
+        quant_block_quad<false>(r, qw, s, su, r2);
+        if (b < nb) {
+            *reinterpret_cast<uint2*>(xq.q + (size_t)H + (size_t)b * 32 + 8 * qd) = make_uint2(qw[0], qw[1]);
+            if (qd == 0) {
+                xq.s[nb + b] = s;
+                xq.sum[nb + b] = su;
+                xq.u[nb + b] = s * (float)su;
+            }
+        }
+    }
+}
+
+// grid.x: waves over weight rows ([0, E) router rows + bias, row E = shared gate if shg), then
+// (xquant) the workgroups that quantise x; grid.y: chunks of DOT_MR activation rows.
 __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict__ router,
                                                         const float* __restrict__ bias,
                                                         const float* __restrict__ shg,
                                                         const float* __restrict__ x, uint32_t m, uint32_t E,
-                                                        uint32_t H, float* __restrict__ rlog, float* __restrict__ sh) {
+                                                        uint32_t H, float* __restrict__ rlog, float* __restrict__ sh,
+                                                        XQuant xquant, uint32_t qwg0) {
+    if (xquant.q && blockIdx.x >= qwg0) {  // workgroup-uniform
+        quantize_x_row(x, H, xquant, blockIdx.x - qwg0);
+        return;
+    }
     const uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (wave >= E + (shg ? 1u : 0u)) return;
     const float* wr = wave < E ? router + (size_t)wave * H : shg;
@@ -142,11 +215,15 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
 
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
-                                hipStream_t st) {
+                                hipStream_t st, const XQuant* xquant) {
     const uint32_t chunks = (m + DOT_MR - 1) / DOT_MR;
+    const XQuant none{};
+    if (xquant && (m != 1 || gemm_order || H % 32)) return hipErrorInvalidValue;  // one decode row
     if (!gemm_order) {
-        const uint32_t nrow = E + (shexp_gate ? 1 : 0);
-        router_dot_kernel<<<dim3((nrow + 1) / 2, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh);
+        const uint32_t nrow = E + (shexp_gate ? 1 : 0), wgs = (nrow + 1) / 2;
+        const uint32_t qwgs = xquant ? (H / 32 * 4 + 127) / 128 : 0;  // four lanes per 32-block
+        router_dot_kernel<<<dim3(wgs + qwgs, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
+                                                                    xquant ? *xquant : none, wgs);
     } else {
         if (m >= 256)
             router_gemm_kernel<8, 8, 4><<<dim3((E + 31) / 32, (m + 31) / 32), 256, 0, st>>>(router, bias, x, m, E,
@@ -158,7 +235,8 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
             router_gemm_kernel<4, 2, 4><<<dim3((E + 7) / 8, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E, H,
                                                                                        rlog);
         if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
-            router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh);
+            router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh,
+                                                              none, 1);
     }
     return hipGetLastError();
 }

@@ -74,9 +74,17 @@ struct Workspace {
 // ---- launchers (return hipError_t of the launch) ----
 hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t* q, float* s,
                            int32_t* su, float* u, hipStream_t st);
+// x of one row quantised per 32 (pair: coarse + residual) into q [P][H], s / sum / u [P][H/32]
+struct XQuant {
+    int8_t* q;
+    float* s;
+    int32_t* sum;
+    float* u;  // s * (float)sum
+    int pair;
+};
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
-                                hipStream_t st);
+                                hipStream_t st, const XQuant* xquant = nullptr);
 hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
