@@ -99,6 +99,18 @@ def test_router_logits_bit_exact(m):
     assert np.array_equal(host(lg2).view(np.uint32), want2.view(np.uint32))
 
 
+@pytest.mark.parametrize("m", [70, 300])
+def test_router_gemm_tiles_bit_exact(m):
+    # the gemm tiles chosen for 64 <= m < 256 and m >= 256 (smallgemm.rs:8-59 order)
+    say(f"router gemm m={m}")
+    E, H = 512, 2048
+    router = O.gen_normal(1, 1, E * H, 0.02).reshape(E, H)
+    x = O.gen_normal(1, 5, m * H, 1.0).reshape(m, H)
+    lg, _ = trmoe.router_logits(to_dev(router), to_dev(x), gemm_order=True)
+    want = O.gemm_f32_nt(x, router)
+    assert np.array_equal(host(lg).view(np.uint32), want.view(np.uint32))
+
+
 def routing_cases(E=512):
     rng = np.random.default_rng(5)
     lg = [rng.standard_normal((8, E)).astype(np.float32),

@@ -208,6 +208,18 @@ __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_reduce_u32<true>(v); }
 
+// Inclusive prefix sum over the 64 lanes (Kogge-Stone within each row of 16, then the row
+// broadcasts 15 / 31); lanes without a source add 0.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
 // All-reduce within each 16-lane row with DPP: quad_perm [1,0,3,2], quad_perm [2,3,0,1], half-row
 // mirror, row mirror.  The pairing differs from an xor butterfly, so it is only for operations
 // whose result does not depend on the order (max of non-NaN values, integer sums).

@@ -37,136 +37,112 @@ __device__ __forceinline__ uint32_t load_ids(const Workspace& ws, uint32_t t, ui
     return ns;
 }
 
-// single workgroup (DISPATCH_WAVES waves); kc4 = ceil(largest selection / 4)
+// Single workgroup of DISPATCH_WAVES waves, one token per thread per round of DT tokens (ids and
+// weights stay in registers).  Per round each wave ORs its 64 tokens into a per-(wave, expert) lane
+// mask, so a token's rank within its expert is the popcount of the lower lanes' bits plus the
+// counts of the earlier waves and rounds: the reference's token-major order.  Expert starts,
+// group indices and work-item offsets come from one block-wide scan (a DPP scan per wave, then
+// the wave totals).  kc4 = ceil(largest selection / 4).
+constexpr uint32_t DT = DISPATCH_WAVES * 64;  // tokens per round
 __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m, uint32_t kc4) {
-    const uint32_t E = ws.E, tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t E = ws.E, tid = threadIdx.x;
     const uint32_t wv = tid / 64, lane = tid % 64;
     extern __shared__ __align__(16) uint8_t smem[];
-    uint32_t* cnt = (uint32_t*)smem;                  // [E]
-    uint32_t* start = cnt + E;                        // [E]
-    uint32_t* run = start + E;                        // [E]
-    uint32_t* gidx = run + E;                         // [E]
-    uint32_t* off = gidx + E;                         // [W][E]
-    uint32_t* scan_tmp = off + DISPATCH_WAVES * E;    // [2][E]
-    uint32_t* masks = scan_tmp + 2 * E;               // [W][E][2] (64-bit token masks as 2 words)
+    unsigned long long* masks = reinterpret_cast<unsigned long long*>(smem);  // [W][E]
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(masks + DISPATCH_WAVES * E);  // [E]
+    uint32_t* run = cnt + E;                                                  // [E]
+    uint32_t* off = run + E;                                                  // [W][E]
+    uint32_t* wtot = off + DISPATCH_WAVES * E;                                // [W][3]
+    const uint32_t rounds = (m + DT - 1) / DT;
+    const uint32_t ept = (E + DT - 1) / DT;  // experts per thread in the scans (contiguous)
 
-    for (uint32_t e = tid; e < E; e += nt) cnt[e] = 0;
-    __syncthreads();
-    for (uint32_t t = tid; t < m; t += nt) {
-        uint32_t id[K_MAX];
-        const uint32_t ns = load_ids(ws, t, kc4, id);
+    uint32_t id[K_MAX], ns = 0;
+    float wt[K_MAX];
+    auto load_tok = [&](uint32_t r) {
+        const uint32_t t = r * DT + tid;
+        ns = t < m ? load_ids(ws, t, kc4, id) : 0u;
+        if (t < m) {
+#pragma unroll
+            for (uint32_t q = 0; q < K_MAX / 4; q++)
+                if (q < kc4) {
+                    const float4 v = reinterpret_cast<const float4*>(ws.w + (size_t)t * K_MAX)[q];
+                    wt[4 * q] = v.x; wt[4 * q + 1] = v.y; wt[4 * q + 2] = v.z; wt[4 * q + 3] = v.w;
+                }
+        }
+    };
+    auto build_masks = [&]() {  // ends with the masks complete
+        for (uint32_t i = tid; i < DISPATCH_WAVES * E; i += DT) masks[i] = 0ull;
+        __syncthreads();
+        uint32_t* mw = reinterpret_cast<uint32_t*>(masks + wv * E);
 #pragma unroll
         for (uint32_t s = 0; s < K_MAX; s++)
-            if (s < ns) atomicAdd(&cnt[id[s]], 1u);
-    }
-    __syncthreads();
-    // exclusive scans over experts: entry starts, and group index of each non-empty expert
-    // (Hillis-Steele in LDS; E <= 1024)
-    for (uint32_t e = tid; e < E; e += nt) {
-        scan_tmp[e] = cnt[e];
-        scan_tmp[E + e] = cnt[e] ? 1u : 0u;
-    }
-    __syncthreads();
-    for (uint32_t d = 1; d < E; d <<= 1) {
-        uint32_t a[4], b[4];
-        uint32_t j = 0;
-        for (uint32_t e = tid; e < E; e += nt, j++) {
-            a[j] = scan_tmp[e] + (e >= d ? scan_tmp[e - d] : 0u);
-            b[j] = scan_tmp[E + e] + (e >= d ? scan_tmp[E + e - d] : 0u);
-        }
+            if (s < ns) atomicOr(&mw[id[s] * 2 + (lane >> 5)], 1u << (lane & 31));
         __syncthreads();
-        j = 0;
-        for (uint32_t e = tid; e < E; e += nt, j++) {
-            scan_tmp[e] = a[j];
-            scan_tmp[E + e] = b[j];
+    };
+
+    // pass 1: per-expert counts
+    for (uint32_t e = tid; e < E; e += DT) cnt[e] = 0;
+    for (uint32_t r = 0; r < rounds; r++) {
+        load_tok(r);
+        build_masks();
+        for (uint32_t e = tid; e < E; e += DT) {
+            uint32_t c = cnt[e];
+            for (uint32_t w = 0; w < DISPATCH_WAVES; w++) c += popc64(masks[w * E + e]);
+            cnt[e] = c;
         }
-        __syncthreads();
+        if (rounds > 1) __syncthreads();
     }
-    for (uint32_t e = tid; e < E; e += nt) {
-        start[e] = scan_tmp[e] - cnt[e];
-        run[e] = start[e];
-        gidx[e] = scan_tmp[E + e] - (cnt[e] ? 1u : 0u);
-    }
-    const uint32_t n_ent = scan_tmp[E - 1];
-    const uint32_t ng = scan_tmp[2 * E - 1];
     __syncthreads();
 
-    // rank-within-expert scatter, 64 tokens per wave, DISPATCH_WAVES chunks per round
-    const uint32_t nchunks = (m + 63) / 64;
-    for (uint32_t c0 = 0; c0 < nchunks; c0 += DISPATCH_WAVES) {
-        for (uint32_t i = tid; i < DISPATCH_WAVES * E * 2; i += nt) masks[i] = 0;
-        __syncthreads();
-        const uint32_t c = c0 + wv, t = c * 64 + lane;
-        const bool live = c < nchunks && t < m;
-        uint32_t id[K_MAX];
-        const uint32_t ns = live ? load_ids(ws, t, kc4, id) : 0u;
-#pragma unroll
-        for (uint32_t s = 0; s < K_MAX; s++)
-            if (s < ns) atomicOr(&masks[(wv * E + id[s]) * 2 + (lane >> 5)], 1u << (lane & 31));
-        __syncthreads();
-        for (uint32_t e = tid; e < E; e += nt) {
-            uint32_t r = run[e];
-            for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
-                off[w * E + e] = r;
-                r += __popc(masks[(w * E + e) * 2]) + __popc(masks[(w * E + e) * 2 + 1]);
-            }
-            run[e] = r;
-        }
-        __syncthreads();
-        const unsigned long long below = lane ? ((1ull << lane) - 1ull) : 0ull;
-        float wt[K_MAX];
-#pragma unroll
-        for (uint32_t q = 0; q < K_MAX / 4; q++)
-            if (q < kc4 && live) {
-                const float4 v = reinterpret_cast<const float4*>(ws.w + (size_t)t * K_MAX)[q];
-                wt[4 * q] = v.x; wt[4 * q + 1] = v.y; wt[4 * q + 2] = v.z; wt[4 * q + 3] = v.w;
-            }
-#pragma unroll
-        for (uint32_t s = 0; s < K_MAX; s++)
-            if (s < ns) {
-                const uint32_t e = id[s];
-                const unsigned long long mk = (unsigned long long)masks[(wv * E + e) * 2] |
-                                              ((unsigned long long)masks[(wv * E + e) * 2 + 1] << 32);
-                const uint32_t pos = off[wv * E + e] + popc64(mk & below);
-                ws.ent_tok[pos] = t;
-                ws.ent_w[pos] = wt[s];
-                ws.ent_exp[pos] = e;
-                ws.ent_of[(size_t)t * K_MAX + s] = pos;
-            }
-        __syncthreads();
+    // block-wide exclusive scans of (entries, non-empty, items) over the experts
+    uint32_t loc[3] = {0, 0, 0};
+    for (uint32_t i = 0; i < ept; i++) {
+        const uint32_t e = tid * ept + i;
+        const uint32_t c = e < E ? cnt[e] : 0u;
+        loc[0] += c;
+        loc[1] += c ? 1u : 0u;
+        loc[2] += (c + BR - 1) / BR;
     }
-    // group table (only non-empty experts, ascending) and work items
-    for (uint32_t e = tid; e < E; e += nt)
-        if (cnt[e]) {
-            ws.grp_start[gidx[e]] = start[e];
-            ws.grp_exp[gidx[e]] = e;
-        }
-    // items: chunks of BR rows per group, then the shared expert over the tokens
-    for (uint32_t e = tid; e < E; e += nt) scan_tmp[e] = (cnt[e] + BR - 1) / BR;
+    uint32_t inc[3];
+#pragma unroll
+    for (int v = 0; v < 3; v++) {
+        inc[v] = wave_incl_scan_u32(loc[v]);
+        if (lane == 63) wtot[wv * 3 + v] = inc[v];
+    }
     __syncthreads();
-    for (uint32_t d = 1; d < E; d <<= 1) {
-        uint32_t a[4];
-        uint32_t j = 0;
-        for (uint32_t e = tid; e < E; e += nt, j++) a[j] = scan_tmp[e] + (e >= d ? scan_tmp[e - d] : 0u);
-        __syncthreads();
-        j = 0;
-        for (uint32_t e = tid; e < E; e += nt, j++) scan_tmp[e] = a[j];
-        __syncthreads();
-    }
-    const uint32_t n_routed_items = scan_tmp[E - 1];
-    for (uint32_t e = tid; e < E; e += nt) {
-        const uint32_t nc = (cnt[e] + BR - 1) / BR;
-        uint32_t o = scan_tmp[e] - nc;
-        for (uint32_t c = 0; c < nc; c++) {
-            const uint32_t r0 = start[e] + c * BR;
-            const uint32_t nr = cnt[e] - c * BR < BR ? cnt[e] - c * BR : BR;
-            ws.items[o + c] = Item{e, r0, nr, 0};
+    uint32_t base[3] = {0, 0, 0}, tot[3] = {0, 0, 0};
+    for (uint32_t w = 0; w < DISPATCH_WAVES; w++)
+#pragma unroll
+        for (int v = 0; v < 3; v++) {
+            const uint32_t x = wtot[w * 3 + v];
+            if (w < wv) base[v] += x;
+            tot[v] += x;
+        }
+    const uint32_t n_ent = tot[0], ng = tot[1], n_routed_items = tot[2];
+    {
+        uint32_t st = base[0] + inc[0] - loc[0], gi = base[1] + inc[1] - loc[1], it = base[2] + inc[2] - loc[2];
+        for (uint32_t i = 0; i < ept; i++) {
+            const uint32_t e = tid * ept + i;
+            if (e >= E) break;
+            const uint32_t c = cnt[e], nc = (c + BR - 1) / BR;
+            run[e] = st;
+            if (c) {  // group table: non-empty experts ascending; work items of BR rows
+                ws.grp_start[gi] = st;
+                ws.grp_exp[gi] = e;
+                for (uint32_t q = 0; q < nc; q++) {
+                    const uint32_t nr = c - q * BR < BR ? c - q * BR : BR;
+                    ws.items[it + q] = Item{e, st + q * BR, nr, 0};
+                }
+            }
+            st += c;
+            gi += c ? 1u : 0u;
+            it += nc;
         }
     }
-    const uint32_t n_sh = (m + BR - 1) / BR;
-    for (uint32_t c = tid; c < n_sh; c += nt) {
-        const uint32_t r0 = c * BR;
-        ws.items[n_routed_items + c] = Item{NO_EXPERT, r0, m - r0 < BR ? m - r0 : BR, 0};
+    const uint32_t n_sh = (m + BR - 1) / BR;  // the shared expert over the tokens, last
+    for (uint32_t q = tid; q < n_sh; q += DT) {
+        const uint32_t r0 = q * BR;
+        ws.items[n_routed_items + q] = Item{NO_EXPERT, r0, m - r0 < BR ? m - r0 : BR, 0};
     }
     if (tid == 0) {
         ws.grp_start[ng] = n_ent;
@@ -174,12 +150,44 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         ws.n_groups[1] = n_ent;
         ws.n_groups[2] = n_routed_items + n_sh;
     }
+    __syncthreads();
+
+    // pass 2: scatter (the single-round case reuses the masks and the registers of pass 1)
+    const unsigned long long below = lane ? ((1ull << lane) - 1ull) : 0ull;
+    for (uint32_t r = 0; r < rounds; r++) {
+        if (rounds > 1) {
+            load_tok(r);
+            build_masks();
+        }
+        for (uint32_t e = tid; e < E; e += DT) {
+            uint32_t o = run[e];
+            for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
+                off[w * E + e] = o;
+                o += popc64(masks[w * E + e]);
+            }
+            run[e] = o;
+        }
+        __syncthreads();
+        const uint32_t t = r * DT + tid;
+#pragma unroll
+        for (uint32_t s = 0; s < K_MAX; s++)
+            if (s < ns) {
+                const uint32_t e = id[s];
+                const uint32_t pos = off[wv * E + e] + popc64(masks[wv * E + e] & below);
+                ws.ent_tok[pos] = t;
+                ws.ent_w[pos] = wt[s];
+                ws.ent_exp[pos] = e;
+                ws.ent_of[(size_t)t * K_MAX + s] = pos;
+            }
+        if (rounds > 1) __syncthreads();
+    }
 }
 
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st) {
     const size_t E = ws.E;
-    size_t lds = (4 * E + DISPATCH_WAVES * E + 2 * E + DISPATCH_WAVES * E * 2) * 4;
-    dispatch_kernel<<<1, DISPATCH_WAVES * 64, lds, st>>>(ws, m, (kcap + 3) / 4);
+    if (E > 2 * DT) return hipErrorInvalidValue;
+    const size_t lds = DISPATCH_WAVES * E * 8 + (2 * E + DISPATCH_WAVES * E + DISPATCH_WAVES * 3) * 4;
+    dispatch_kernel<<<1, DT, lds, st>>>(ws, m, (kcap + 3) / 4);
     return hipGetLastError();
 }
 

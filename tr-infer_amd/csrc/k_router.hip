@@ -112,26 +112,38 @@ __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict
 // gemm_f32_nt order: output (m, e) has 16 lane chains j, chain j = fma over the steps s of
 // x[m][16s + j] * w[e][16s + j], then the halving tree.  Thread (j, q) of a 256-thread workgroup
 // carries chain j of an RM x RE block of outputs (q = qm * QE + qe); the workgroup tile is
-// (QM*RM) rows x (QE*RE) experts.  x and router chunks of KC columns go through LDS transposed
-// ([k][row]), double-buffered, so a thread reads its RM rows / RE experts at column 16s + j with
-// vector LDS reads.
-template <int RM, int RE, int QM>
+// (QM*RM) rows x (QE*RE) experts.  x and router chunks of KC columns are staged in LDS row-major
+// (float4 global loads, 8-byte LDS stores), and lane j reads column 16s + j of each of its rows.
+// Row pitches are padded so that the four 16-lane groups of a wave that read different rows fall
+// on different bank halves.  The global loads of a chunk are issued two chunks before its math
+// (two register stages); DB: two LDS buffers (one barrier per chunk) instead of one (two).
+__host__ __device__ constexpr int gemm_pad(int d, int kc) {  // floats of padding for row distance d
+    for (int p = 2; p <= 32; p += 2)
+        if (d == 0 || (d * (kc + p)) % 32 == 16) return p;
+    return 4;
+}
+template <int RM, int RE, int QM, int KC, bool DB>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restrict__ router,
                                                          const float* __restrict__ bias,
                                                          const float* __restrict__ x, uint32_t m, uint32_t E,
                                                          uint32_t H, float* __restrict__ rlog) {
-    constexpr int QE = 16 / QM, TM = QM * RM, TE = QE * RE, KC = 64;
-    constexpr int XP = TM + 4, WP = TE + 4;  // padded LDS rows (keep 16-byte alignment)
-    __shared__ __align__(16) float xs[2][KC][XP];
-    __shared__ __align__(16) float wsm[2][KC][WP];
+    constexpr int QE = 16 / QM, TM = QM * RM, TE = QE * RE;
+    // rows between the 16-lane groups of one wave (q = 0..3): x rows differ when qm does
+    constexpr int DX = QE >= 4 ? 0 : RM * (QE == 1 ? 1 : 0) + (QE == 2 ? RM : 0);
+    constexpr int DW = QE == 1 ? 0 : RE;
+    constexpr int XK = KC + gemm_pad(DX, KC), WK = KC + gemm_pad(DW, KC);
+    constexpr int NB = DB ? 2 : 1;
+    __shared__ __align__(16) float xs[NB][TM][XK];
+    __shared__ __align__(16) float wsm[NB][TE][WK];
     const uint32_t tid = threadIdx.x, j = tid % 16, q = tid / 16, qm = q / QE, qe = q % QE;
     const uint32_t m0 = blockIdx.y * TM, e0 = blockIdx.x * TE;
 
     // staging: TM rows of x and TE rows of the router, KC columns each, as float4 along k
     constexpr int XV = TM * KC / 4, WV = TE * KC / 4;  // float4 per chunk
     constexpr int NV = (XV + WV + 255) / 256;
-    float4 st[NV];
-    auto fetch = [&](uint32_t k0) {
+    float4 sa[NV], sb[NV];
+    auto fetch = [&](uint32_t ck, float4 (&st)[NV]) {
+        const uint32_t k0 = ck * KC;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const uint32_t v = tid + 256 * i;
@@ -146,22 +158,18 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
             }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, const float4 (&st)[NV]) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const uint32_t v = tid + 256 * i;
-            if (v < (uint32_t)XV) {
-                const uint32_t r = v / (KC / 4), c4 = v % (KC / 4);
-                xs[buf][4 * c4 + 0][r] = st[i].x;
-                xs[buf][4 * c4 + 1][r] = st[i].y;
-                xs[buf][4 * c4 + 2][r] = st[i].z;
-                xs[buf][4 * c4 + 3][r] = st[i].w;
-            } else if (v < (uint32_t)(XV + WV)) {
-                const uint32_t u = v - XV, r = u / (KC / 4), c4 = u % (KC / 4);
-                wsm[buf][4 * c4 + 0][r] = st[i].x;
-                wsm[buf][4 * c4 + 1][r] = st[i].y;
-                wsm[buf][4 * c4 + 2][r] = st[i].z;
-                wsm[buf][4 * c4 + 3][r] = st[i].w;
+            float* dst = nullptr;
+            if (v < (uint32_t)XV)
+                dst = &xs[buf][v / (KC / 4)][4 * (v % (KC / 4))];
+            else if (v < (uint32_t)(XV + WV))
+                dst = &wsm[buf][(v - XV) / (KC / 4)][4 * ((v - XV) % (KC / 4))];
+            if (dst) {
+                reinterpret_cast<float2*>(dst)[0] = make_float2(st[i].x, st[i].y);
+                reinterpret_cast<float2*>(dst)[1] = make_float2(st[i].z, st[i].w);
             }
         }
     };
@@ -170,35 +178,54 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
     for (int a = 0; a < RM; a++)
 #pragma unroll
         for (int b = 0; b < RE; b++) acc[a][b] = 0.0f;
-    fetch(0);
-    store(0);
-    __syncthreads();
-    const uint32_t nchunk = H / KC;
-    for (uint32_t ck = 0; ck < nchunk; ck++) {
-        const int buf = ck & 1;
-        if (ck + 1 < nchunk) fetch((ck + 1) * KC);
-#pragma unroll
+    auto compute = [&](int buf) {
+#pragma unroll 4
         for (int s4 = 0; s4 < KC / 16; s4++) {
             const uint32_t c = 16 * s4 + j;
             float xv[RM], wv[RE];
 #pragma unroll
-            for (int a = 0; a < RM; a += 4) {
-                const float4 t = *reinterpret_cast<const float4*>(&xs[buf][c][qm * RM + a]);
-                xv[a] = t.x; xv[a + 1] = t.y; xv[a + 2] = t.z; xv[a + 3] = t.w;
-            }
+            for (int a = 0; a < RM; a++) xv[a] = xs[buf][qm * RM + a][c];
 #pragma unroll
-            for (int b = 0; b < RE; b += 2) {
-                const float2 t = *reinterpret_cast<const float2*>(&wsm[buf][c][qe * RE + b]);
-                wv[b] = t.x; wv[b + 1] = t.y;
-            }
+            for (int b = 0; b < RE; b++) wv[b] = wsm[buf][qe * RE + b][c];
 #pragma unroll
             for (int a = 0; a < RM; a++)
 #pragma unroll
                 for (int b = 0; b < RE; b++) acc[a][b] = __builtin_fmaf(xv[a], wv[b], acc[a][b]);
         }
-        if (ck + 1 < nchunk) {
-            store(buf ^ 1);
+    };
+    // chunk c: register stage sa (c even) / sb (c odd), filled two chunks ahead; LDS buffer c % NB
+    const uint32_t nchunk = H / KC;
+    fetch(0, sa);
+    if (nchunk > 1) fetch(1, sb);
+    store(0, sa);
+    __syncthreads();
+    for (uint32_t ck = 0; ck < nchunk; ck += 2) {
+        if (ck + 2 < nchunk) fetch(ck + 2, sa);
+        if constexpr (DB) {
+            if (ck + 1 < nchunk) store(1, sb);  // the other buffer: nobody reads it now
+            compute(0);
             __syncthreads();
+        } else {
+            compute(0);
+            __syncthreads();
+            if (ck + 1 < nchunk) {
+                store(0, sb);
+                __syncthreads();
+            }
+        }
+        if (ck + 1 >= nchunk) break;
+        if (ck + 3 < nchunk) fetch(ck + 3, sb);
+        if constexpr (DB) {
+            if (ck + 2 < nchunk) store(0, sa);
+            compute(1);
+            __syncthreads();
+        } else {
+            compute(0);
+            __syncthreads();
+            if (ck + 2 < nchunk) {
+                store(0, sa);
+                __syncthreads();
+            }
         }
     }
     // halving trees (all lanes of the 16-lane row get each sum); lane j stores every 16th output
@@ -213,6 +240,22 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
         }
 }
 
+// workgroup tiles of the router gemm by batch size (the first entry whose min_m <= m and whose
+// chunk divides H)
+struct GemmCfg {
+    uint32_t min_m, kc;
+    int id;
+};
+static const GemmCfg kGemmCfg[] = {{256, 128, 1}, {64, 256, 5}, {0, 512, 2}, {0, 128, 3}};
+
+template <int RM, int RE, int QM, int KC, bool DB>
+static void launch_gemm_cfg(const float* router, const float* bias, const float* x, uint32_t m, uint32_t E,
+                            uint32_t H, float* rlog, hipStream_t st) {
+    constexpr uint32_t TM = QM * RM, TE = (16 / QM) * RE;
+    router_gemm_kernel<RM, RE, QM, KC, DB><<<dim3((E + TE - 1) / TE, (m + TM - 1) / TM), 256, 0, st>>>(
+            router, bias, x, m, E, H, rlog);
+}
+
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
                                 hipStream_t st, const XQuant* xquant) {
@@ -225,15 +268,18 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         router_dot_kernel<<<dim3(wgs + qwgs, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
                                                                     xquant ? *xquant : none, wgs);
     } else {
-        if (m >= 256)
-            router_gemm_kernel<8, 8, 4><<<dim3((E + 31) / 32, (m + 31) / 32), 256, 0, st>>>(router, bias, x, m, E,
-                                                                                         H, rlog);
-        else if (m >= 64)
-            router_gemm_kernel<4, 4, 4><<<dim3((E + 15) / 16, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E,
-                                                                                         H, rlog);
-        else
-            router_gemm_kernel<4, 2, 4><<<dim3((E + 7) / 8, (m + 15) / 16), 256, 0, st>>>(router, bias, x, m, E, H,
-                                                                                       rlog);
+        int id = 3;
+        for (const GemmCfg& c : kGemmCfg)
+            if (m >= c.min_m && H % c.kc == 0) {
+                id = c.id;
+                break;
+            }
+        switch (id) {
+            case 1: launch_gemm_cfg<4, 4, 4, 128, true>(router, bias, x, m, E, H, rlog, st); break;
+            case 2: launch_gemm_cfg<1, 2, 16, 512, false>(router, bias, x, m, E, H, rlog, st); break;
+            case 5: launch_gemm_cfg<4, 2, 4, 256, true>(router, bias, x, m, E, H, rlog, st); break;
+            default: launch_gemm_cfg<1, 2, 16, 128, true>(router, bias, x, m, E, H, rlog, st); break;
+        }
         if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
             router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh,
                                                               none, 1);
