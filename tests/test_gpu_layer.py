@@ -133,6 +133,7 @@ def test_batch_layer_and_dispatch(shape, M, k):
     assert np.array_equal(ids, r["ids"][:, :k])
     ng, n_ent = ctx.read(trmoe.WS_NGROUPS, 16, np.uint32)[:2]
     assert (ng, n_ent) == (r["n_groups"], r["n_ent"])
+    assert ctx.stats() == (M, n_ent)  # MoeStats: rows and selected experts
     assert np.array_equal(ctx.read(trmoe.WS_ENT_TOK, 4 * n_ent, np.uint32), r["ent_tok"])
     assert np.array_equal(ctx.read(trmoe.WS_ENT_EXP, 4 * n_ent, np.uint32), r["ent_expert"])
     assert np.array_equal(ctx.read(trmoe.WS_GRP_START, 4 * (ng + 1), np.uint32), r["grp_start"])

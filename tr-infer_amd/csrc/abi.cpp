@@ -309,7 +309,8 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
                                                  ws.rlog, ws.shl, st));
-        TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+        // the dispatch kernel counts the routed rows (one atomic per call, not per token)
+        TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
         TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, ws.xu, st));
         TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));

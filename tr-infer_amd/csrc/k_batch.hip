@@ -145,6 +145,10 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         ws.items[n_routed_items + q] = Item{NO_EXPERT, r0, m - r0 < BR ? m - r0 : BR, 0};
     }
     if (tid == 0) {
+        if (ws.stats) {  // MoeStats: rows and selected experts of this call
+            atomicAdd(&ws.stats[0], (unsigned long long)m);
+            atomicAdd(&ws.stats[1], (unsigned long long)n_ent);
+        }
         ws.grp_start[ng] = n_ent;
         ws.n_groups[0] = ng;
         ws.n_groups[1] = n_ent;
