@@ -9,7 +9,9 @@ distinct layers (48 = BASELINE config 5, ~43.5 GB of Q4_K experts resident in HB
 (random-init Q4_K superblocks of the configs' shapes) and are resident before timing starts.
 
 Prints ONE JSON line.  `value` is the M=1 decode layer rate; the other M
-(configs 2 and 3) are reported under "results".
+(configs 2 and 3) are reported under "results", with config 4 (M=3072, Q6_K down projections,
+dynamic-k routing) and config 5 (the 48-layer RMSNorm + residual stack, timed end to end at M=1
+and M=512).
 """
 from __future__ import annotations
 
@@ -51,6 +53,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
+    ap.add_argument("--extra", type=str, default="c4,stack",
+                    help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
+                         "48-layer RMSNorm + residual stack at M=1 and M=512); '' for none")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
@@ -170,6 +175,15 @@ def main():
         log(f"M={M}: {per * 1e3:.1f} us/layer (eager {per_eager * 1e3:.1f}), {M / (per * 1e-3):.0f} tok/s, "
             f"{nbytes / (per * 1e-3) / 1e9:.0f} GB/s, kernels {results[M]['kernels_us']}")
 
+    extras = {}
+    todo = {v for v in args.extra.split(",") if v}
+    if "c4" in todo:
+        extras["C4 M=3072"] = bench_config4(args, layers, dev, stream, trmoe, torch, np)
+    if "stack" in todo:
+        for Ms in (1, 512):
+            extras[f"C5 stack M={Ms}"] = bench_stack(args, layers, ctx if Ms <= m_max else None, Ms, dev, stream,
+                                                     trmoe, torch)
+
     prim = 1 if 1 in results else ms_list[0]
     r = results[prim]
     # roofline of the dominant kernel of the primary workload
@@ -208,6 +222,7 @@ def main():
         "results": {f"M={M}": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()
                                if not k.startswith("_")} for M, res in results.items()},
     }
+    line["results"].update(extras)
     print(json.dumps(line), flush=True)
     if args.copy_cal:
         n = args.copy_cal << 18  # floats
@@ -217,6 +232,90 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"calibration copies: 3 x {args.copy_cal} MiB")
+
+
+def timed_graph(torch, stream, body, reps):
+    """Capture body() once into a HIP graph, replay it once untimed, then `reps` times between
+    events on the launch stream; returns ms per replay."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_config4(args, layers, dev, stream, trmoe, torch, np):
+    """Config 4: M=3072 tokens, gate/up Q4_K and down Q6_K, dynamic-k routing (smallest k whose
+    cumulative router mass reaches 0.9, clamped to 1..10, MassBasis::Top), over the same layer
+    rotation with Q6_K down projections."""
+    M = 3072
+    t0 = time.time()
+    lw = [w.with_down(trmoe.FMT_Q6_K, 1, l, device=dev) for l, w in enumerate(layers)]
+    for w in lw:
+        w.moew.router_bias = None
+    ctx = trmoe.Context(H, E, F, K, M)
+    ctx.set_moe((1, K, 0.9, trmoe.BASIS_TOP))
+    x = trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H)
+    out = torch.empty((M, H), dtype=torch.float32, device=dev)
+    touched, ents = [], []
+    for l in range(len(lw)):
+        ctx.forward(lw[l], x, out)
+        ng, n_ent = ctx.read(trmoe.WS_NGROUPS, 16, np.uint32)[:2]
+        touched.append(int(ng))
+        ents.append(int(n_ent))
+    torch.cuda.synchronize()
+    log(f"config 4: {len(lw)} layers with Q6_K down in {time.time() - t0:.1f}s; "
+        f"mean k {np.mean(ents) / M:.2f}, touched {np.mean(touched):.0f}")
+    steps = min(args.steps, 2 * len(lw))
+
+    def body():
+        for i in range(steps):
+            ctx.forward(lw[i % len(lw)], x, out)
+
+    per = timed_graph(torch, stream, body, 1) / steps
+    dn = H * (F // 256 * 210)  # Q6_K down bytes per expert
+    nbytes = float(np.mean(touched) + 1) * (2 * F * Q4K_ROW_H + dn) + E * H * 4 + H * 4 + M * H * 4 * 2
+    nops = (float(np.mean(ents)) + M) * 3 * 2 * H * F
+    ctx.close()
+    del lw
+    return {"tokens_per_s": round(M / (per * 1e-3), 1), "us_per_layer": round(per * 1e3, 2),
+            "layer_GBps": round(nbytes / (per * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "int8_TOPS": round(nops / (per * 1e-3) / 1e12, 3), "mean_k": round(float(np.mean(ents)) / M, 3),
+            "experts_touched": round(float(np.mean(touched)), 1), "layers": len(layers), "steps": steps}
+
+
+def bench_stack(args, layers, ctx, M, dev, stream, trmoe, torch):
+    """Config 5: the whole stack, h <- h + MoE(RMSNorm(h; eps 1e-6, w ~ U(0.9, 1.1))) for each of
+    the layers in turn, on seeded N(0, 1) rows, timed end to end (one replay = one pass)."""
+    if ctx is None:
+        ctx = trmoe.Context(H, E, F, K, M)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    rms = [torch.rand(H, generator=gen, device=dev) * 0.2 + 0.9 for _ in layers]
+    for w in layers:
+        w.moew.router_bias = None
+    h = trmoe.gen_normal(1, (11 << 32) | M, M * H, 1.0, device=dev).view(M, H)
+
+    def body():
+        for l, w in enumerate(layers):
+            ctx.residual(w, rms[l], 1e-6, h)
+
+    reps = 20 if M == 1 else 3
+    per = timed_graph(torch, stream, body, reps)
+    ok = bool(torch.isfinite(h).all())
+    log(f"config 5 stack M={M}: {per:.3f} ms per pass of {len(layers)} layers")
+    return {"tokens_per_s": round(M / (per * 1e-3), 1), "ms_per_pass": round(per, 4),
+            "us_per_layer": round(per * 1e3 / len(layers), 2), "layers": len(layers), "passes": reps,
+            "finite": ok}
 
 
 def measured_traffic(kernel, m):

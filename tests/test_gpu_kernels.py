@@ -199,3 +199,10 @@ def test_swiglu_and_rmsnorm_bit_exact():
     yn = host(trmoe.rmsnorm(to_dev(x), to_dev(w), 1e-6))
     want = np.stack([O.rmsnorm(x[i], w, 1e-6) for i in range(3)])
     assert np.array_equal(yn.view(np.uint32), want.view(np.uint32))
+    # ragged width: one 1024-wide batch, a 64-wide step, a 16-wide tail and a scalar tail
+    n = 1024 + 64 + 16 + 5
+    x = rng.standard_normal((2, n)).astype(np.float32)
+    w = rng.uniform(0.9, 1.1, n).astype(np.float32)
+    yn = host(trmoe.rmsnorm(to_dev(x), to_dev(w), 1e-6))
+    want = np.stack([O.rmsnorm(x[i], w, 1e-6) for i in range(2)])
+    assert np.array_equal(yn.view(np.uint32), want.view(np.uint32))

@@ -202,6 +202,14 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     const float* xr = x + (size_t)row * n;
     float acc = 0.0f;
     uint32_t i = 0;
+    constexpr int U = 16;  // 64-wide steps whose loads are issued together
+    for (; i + 64 * U <= n; i += 64 * U) {
+        float a[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) a[u] = xr[i + 64 * u + lane];
+#pragma unroll
+        for (int u = 0; u < U; u++) acc = __builtin_fmaf(a[u], a[u], acc);
+    }
     for (; i + 64 <= n; i += 64) {
         float a = xr[i + lane];
         acc = __builtin_fmaf(a, a, acc);
@@ -214,7 +222,18 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     float s = reduce16_lanes(rows4_sum(acc));  // the same value in every lane
     for (; i < n; i++) s += xr[i] * xr[i];
     float r = 1.0f / __builtin_sqrtf(s / (float)n + eps);
-    for (uint32_t j = lane; j < n; j += WAVE) y[(size_t)row * n + j] = w ? (xr[j] * r) * w[j] : xr[j] * r;
+    uint32_t j = lane;
+    for (; j + WAVE * (U - 1) < n; j += WAVE * U) {  // loads first, U per lane
+        float a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            a[u] = xr[j + WAVE * u];
+            b[u] = w ? w[j + WAVE * u] : 1.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) y[(size_t)row * n + j + WAVE * u] = w ? (a[u] * r) * b[u] : a[u] * r;
+    }
+    for (; j < n; j += WAVE) y[(size_t)row * n + j] = w ? (xr[j] * r) * w[j] : xr[j] * r;
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,

@@ -247,6 +247,24 @@ class LayerWeights:
         return cls(H, E, F, router, shg, gate, up, down, sh_gate, sh_up, sh_down, FMT_Q4_K, down_fmt, router_bias)
 
 
+    def with_down(self, down_fmt, seed, layer, device="cuda", stream=None):
+        """The same layer with its routed and shared down projections regenerated in `down_fmt`
+        (config 4: Q4_K gate/up, Q6_K down); every other tensor is shared with this one."""
+        import torch
+        H, E, F = self.H, self.E, self.F
+        db = row_bytes(down_fmt, F)
+        L = lib()
+        st = _stream(stream)
+        down = torch.empty((E, H * db), dtype=torch.uint8, device=device)
+        check(L.trk_gen_gguf_stack(down_fmt, seed, (layer << 32) | 18, 3, E, H, F, 1e-4, 2e-3, _ptr(down),
+                                   down.stride(0), st))
+        sh_down = torch.empty(H * db, dtype=torch.uint8, device=device)
+        check(L.trk_gen_gguf(down_fmt, seed, (layer << 32) | 10, H, F, 1e-4, 2e-3, _ptr(sh_down), st))
+        t = self.tensors
+        return LayerWeights(H, E, F, t["router"], t["shexp_gate"], t["gate"], t["up"], down, t["sh_gate"],
+                            t["sh_up"], sh_down, FMT_Q4_K, down_fmt, t["router_bias"])
+
+
 # ---- kernel-level wrappers (torch tensors on the GPU) ----------------------------------------
 
 def quantize(x, kb, pair=False, stream=None):
