@@ -304,14 +304,16 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
     } else {
+        // the logits launch also quantises x (single level, per 32) for the grouped kernels
+        const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, 0};
         if (rlog)
-            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st));
+            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st,
+                                                 &xq));
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
-                                                 ws.rlog, ws.shl, st));
+                                                 ws.rlog, ws.shl, st, &xq));
         // the dispatch kernel counts the routed rows (one atomic per call, not per token)
         TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
-        TIMED(K_QUANT, launch_quantize(x, m, H, 32, 0, ws.xq, ws.xs, ws.xsum, ws.xu, st));
         TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));
         TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, st));

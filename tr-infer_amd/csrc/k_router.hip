@@ -46,13 +46,16 @@ __device__ __forceinline__ void quant_block_quad(const float (&v)[8], uint32_t (
     sum = su;
 }
 
-// x of one row (decode) quantised per 32 by the workgroups after the logit rows: four lanes per
-// block; pair = quantize_pair_blocks (quant.rs:96-108), else QAct::quantize.
-__device__ __forceinline__ void quantize_x_row(const float* __restrict__ x, uint32_t H, const XQuant& xq,
-                                               uint32_t qwg) {
-    const uint32_t nb = H / 32, t = qwg * blockDim.x + threadIdx.x, b = t / 4, qd = t % 4;
-    const uint32_t bc = b < nb ? b : nb - 1;
-    const float4* src = reinterpret_cast<const float4*>(x + (size_t)bc * 32 + 8 * qd);
+// x quantised per 32 by the workgroups after the logit rows, four lanes per block: one row in
+// pair mode (quantize_pair_blocks, quant.rs:96-108: level 1 at +H / +H/32), else m rows single
+// level (QAct::quantize, quant.rs:76-92, as moe_batch's quant_rows).
+__device__ __forceinline__ void quantize_x_rows(const float* __restrict__ x, uint32_t m, uint32_t H,
+                                                const XQuant& xq, uint32_t qwg) {
+    const uint32_t nb = H / 32, t = qwg * blockDim.x + threadIdx.x, id = t / 4, qd = t % 4;
+    const uint32_t idc = id < m * nb ? id : m * nb - 1;
+    const uint32_t row = idc / nb, b = idc % nb;
+    const bool live = id < m * nb;
+    const float4* src = reinterpret_cast<const float4*>(x + (size_t)row * H + (size_t)b * 32 + 8 * qd);
     const float4 a = src[0], c = src[1];
     const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
     float r[8], r2[8];
@@ -60,22 +63,23 @@ __device__ __forceinline__ void quantize_x_row(const float* __restrict__ x, uint
     float s;
     int32_t su;
     quant_block_quad<true>(v, qw, s, su, r);
-    if (b < nb) {
-        *reinterpret_cast<uint2*>(xq.q + (size_t)b * 32 + 8 * qd) = make_uint2(qw[0], qw[1]);
+    const size_t qo = (size_t)row * H + (size_t)b * 32 + 8 * qd, so = (size_t)row * nb + b;
+    if (live) {
+        *reinterpret_cast<uint2*>(xq.q + qo) = make_uint2(qw[0], qw[1]);
         if (qd == 0) {
-            xq.s[b] = s;
-            xq.sum[b] = su;
-            xq.u[b] = s * (float)su;  // gemv.rs:144
+            xq.s[so] = s;
+            xq.sum[so] = su;
+            xq.u[so] = s * (float)su;  // gemv.rs:144
         }
     }
-    if (xq.pair) {
+    if (xq.pair) {  // m == 1
         quant_block_quad<false>(r, qw, s, su, r2);
-        if (b < nb) {
-            *reinterpret_cast<uint2*>(xq.q + (size_t)H + (size_t)b * 32 + 8 * qd) = make_uint2(qw[0], qw[1]);
+        if (live) {
+            *reinterpret_cast<uint2*>(xq.q + H + qo) = make_uint2(qw[0], qw[1]);
             if (qd == 0) {
-                xq.s[nb + b] = s;
-                xq.sum[nb + b] = su;
-                xq.u[nb + b] = s * (float)su;
+                xq.s[nb + so] = s;
+                xq.sum[nb + so] = su;
+                xq.u[nb + so] = s * (float)su;
             }
         }
     }
@@ -90,7 +94,7 @@ __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict
                                                         uint32_t H, float* __restrict__ rlog, float* __restrict__ sh,
                                                         XQuant xquant, uint32_t qwg0) {
     if (xquant.q && blockIdx.x >= qwg0) {  // workgroup-uniform
-        quantize_x_row(x, H, xquant, blockIdx.x - qwg0);
+        if (blockIdx.y == 0) quantize_x_rows(x, m, H, xquant, blockIdx.x - qwg0);
         return;
     }
     const uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -261,10 +265,10 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
                                 hipStream_t st, const XQuant* xquant) {
     const uint32_t chunks = (m + DOT_MR - 1) / DOT_MR;
     const XQuant none{};
-    if (xquant && (m != 1 || gemm_order || H % 32)) return hipErrorInvalidValue;  // one decode row
+    if (xquant && (H % 32 || (xquant->pair && m != 1))) return hipErrorInvalidValue;  // pair: one decode row
     if (!gemm_order) {
         const uint32_t nrow = E + (shexp_gate ? 1 : 0), wgs = (nrow + 1) / 2;
-        const uint32_t qwgs = xquant ? (H / 32 * 4 + 127) / 128 : 0;  // four lanes per 32-block
+        const uint32_t qwgs = xquant ? (m * (H / 32) * 4 + 127) / 128 : 0;  // four lanes per 32-block
         router_dot_kernel<<<dim3(wgs + qwgs, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
                                                                     xquant ? *xquant : none, wgs);
     } else {
@@ -283,6 +287,11 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
             router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh,
                                                               none, 1);
+        if (xquant) {  // a grid of its own: riding on the chunked dot grid would replicate it
+            const uint32_t qwgs = (m * (H / 32) * 4 + 127) / 128;
+            router_dot_kernel<<<dim3(qwgs, 1), 128, 0, st>>>(nullptr, nullptr, nullptr, x, m, 0, H, nullptr, nullptr,
+                                                             *xquant, 0);
+        }
     }
     return hipGetLastError();
 }
