@@ -116,11 +116,12 @@ def test_decode_one_launch_matches_three(policy):
 
 
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
-                                       ("full", 16, 10)])
+                                       ("full", 16, 10), ("small", 700, 3)])
 def test_batch_layer_and_dispatch(shape, M, k):
+    # M = 700: two rounds of 512 tokens and the split (parallel) scatter
     say(f"batch layer {shape} M={M} k={k}")
     L, orc, W = layer(shape, **(SMALL if shape == "small" else FULL))
-    ctx = trmoe.Context(L.H, L.E, L.F, k, 64)
+    ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))
     import torch
     x = L.x(M, tid=200 + M)
     r = orc.moe_batch(x, k=k, router_dot_max_m=16)

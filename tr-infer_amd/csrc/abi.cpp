@@ -133,7 +133,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.grp_start, (E + 2) * 4},
         {(void**)&ws.grp_exp, (E + 1) * 4},
         {(void**)&ws.n_groups, 16},
-        {(void**)&ws.chunk_cnt, 16},
+        {(void**)&ws.doff, (M + 63) / 64 * E * 4},  // [ceil(m / 64)][E]: dispatch writes only chunks < ceil(m / 64)
         {(void**)&ws.items, (size_t)ws.item_cap * sizeof(Item)},
         {(void**)&ws.actq, ws.act_rows * F},
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},

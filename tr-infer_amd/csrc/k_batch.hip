@@ -44,7 +44,10 @@ __device__ __forceinline__ uint32_t load_ids(const Workspace& ws, uint32_t t, ui
 // group indices and work-item offsets come from one block-wide scan (a DPP scan per wave, then
 // the wave totals).  kc4 = ceil(largest selection / 4).
 constexpr uint32_t DT = DISPATCH_WAVES * 64;  // tokens per round
-__global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m, uint32_t kc4) {
+// split: leave the scatter to scatter_kernel (many workgroups) and store the per-(64-token chunk,
+// expert) first positions in ws.doff instead.
+__global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m, uint32_t kc4,
+                                                                       int split) {
     const uint32_t E = ws.E, tid = threadIdx.x;
     const uint32_t wv = tid / 64, lane = tid % 64;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     uint32_t* run = cnt + E;                                                  // [E]
     uint32_t* off = run + E;                                                  // [W][E]
     uint32_t* wtot = off + DISPATCH_WAVES * E;                                // [W][3]
-    const uint32_t rounds = (m + DT - 1) / DT;
+    const uint32_t rounds = (m + DT - 1) / DT, nchunks = (m + 63) / 64;
     const uint32_t ept = (E + DT - 1) / DT;  // experts per thread in the scans (contiguous)
 
     uint32_t id[K_MAX], ns = 0;
@@ -166,10 +169,18 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         for (uint32_t e = tid; e < E; e += DT) {
             uint32_t o = run[e];
             for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
-                off[w * E + e] = o;
+                if (split) {
+                    const uint32_t ch = r * DISPATCH_WAVES + w;  // 64-token chunk; the last round's
+                    if (ch < nchunks) ws.doff[(size_t)ch * E + e] = o;  // trailing waves hold none
+                } else
+                    off[w * E + e] = o;
                 o += popc64(masks[w * E + e]);
             }
             run[e] = o;
+        }
+        if (split) {
+            if (rounds > 1) __syncthreads();
+            continue;
         }
         __syncthreads();
         const uint32_t t = r * DT + tid;
@@ -187,11 +198,50 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     }
 }
 
+// The scatter of a split dispatch: one wave per 64-token chunk, the same lane-mask ranks.
+__global__ __launch_bounds__(64) void scatter_kernel(Workspace ws, uint32_t m, uint32_t kc4) {
+    const uint32_t E = ws.E, c = blockIdx.x, lane = threadIdx.x, t = c * 64 + lane;
+    extern __shared__ __align__(16) uint8_t smem[];
+    unsigned long long* masks = reinterpret_cast<unsigned long long*>(smem);  // [E]
+    for (uint32_t e = lane; e < E; e += 64) masks[e] = 0ull;
+    uint32_t id[K_MAX];
+    float wt[K_MAX];
+    const uint32_t ns = t < m ? load_ids(ws, t, kc4, id) : 0u;
+    if (t < m) {
+#pragma unroll
+        for (uint32_t q = 0; q < K_MAX / 4; q++)
+            if (q < kc4) {
+                const float4 v = reinterpret_cast<const float4*>(ws.w + (size_t)t * K_MAX)[q];
+                wt[4 * q] = v.x; wt[4 * q + 1] = v.y; wt[4 * q + 2] = v.z; wt[4 * q + 3] = v.w;
+            }
+    }
+    wave_sync();
+    uint32_t* mw = reinterpret_cast<uint32_t*>(masks);
+#pragma unroll
+    for (uint32_t s = 0; s < K_MAX; s++)
+        if (s < ns) atomicOr(&mw[id[s] * 2 + (lane >> 5)], 1u << (lane & 31));
+    wave_sync();
+    const unsigned long long below = lane ? ((1ull << lane) - 1ull) : 0ull;
+#pragma unroll
+    for (uint32_t s = 0; s < K_MAX; s++)
+        if (s < ns) {
+            const uint32_t e = id[s];
+            const uint32_t pos = ws.doff[(size_t)c * E + e] + popc64(masks[e] & below);
+            ws.ent_tok[pos] = t;
+            ws.ent_w[pos] = wt[s];
+            ws.ent_exp[pos] = e;
+            ws.ent_of[(size_t)t * K_MAX + s] = pos;
+        }
+}
+
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st) {
     const size_t E = ws.E;
     if (E > 2 * DT) return hipErrorInvalidValue;
     const size_t lds = DISPATCH_WAVES * E * 8 + (2 * E + DISPATCH_WAVES * E + DISPATCH_WAVES * 3) * 4;
-    dispatch_kernel<<<1, DT, lds, st>>>(ws, m, (kcap + 3) / 4);
+    // from a few hundred tokens on, one workgroup's scattered stores dominate: spread them
+    const int split = m >= 256 ? 1 : 0;
+    dispatch_kernel<<<1, DT, lds, st>>>(ws, m, (kcap + 3) / 4, split);
+    if (split) scatter_kernel<<<(m + 63) / 64, 64, E * 8, st>>>(ws, m, (kcap + 3) / 4);
     return hipGetLastError();
 }
 

@@ -57,7 +57,7 @@ struct Workspace {
     uint32_t* grp_start;  // [E + 2]
     uint32_t* grp_exp;    // [E + 1]
     uint32_t* n_groups;   // [4]: n_groups, n_ent, n_items, pad
-    uint32_t* chunk_cnt;  // dispatch scratch: [chunks][E]
+    uint32_t* doff;       // dispatch: [ceil(m_max / 64)][E] first entry of each (64-token chunk, expert)
     Item* items;          // [item_cap]
     int8_t* actq;         // [act_rows][F] (decode: [33][2][F])
     float* acts;          // [act_rows][F/16]
