@@ -173,10 +173,17 @@ int trk_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double sigma, fl
 
 /* ---- measurement and introspection ------------------------------------------------------ */
 /* M == 1: run the whole layer as one launch when the layer's shape has a fused kernel and the GPU
- * can hold its grid at once (on by default), or always as the three launches router / gate-up /
- * down (off).  Both follow exec.rs:1540-1623 with identical results; no counterpart in the
+ * can hold its grid at once (on), or as the three launches router / gate-up / down (off, the
+ * default).  Both follow exec.rs:1540-1623 with identical results; no counterpart in the
  * reference, whose decode layer is one pool run. */
 int trk_set_fusion(trk_ctx *ctx, int on);
+
+/* M >= 2: grouped work items (one expert's entry rows, at most 16) of at most `rows` rows run on
+ * the streaming GEMV kernels, larger ones on the int8 MFMA tiles.  rows = -1 (the default) picks
+ * 16 for M <= 16 (every item streams) and 4 above; 0 puts every item on the tiles.  Every choice
+ * gives the same bits (moe_batch, exec_batch.rs:1404-1580); no counterpart in the reference,
+ * which runs one grouped kernel per expert matrix. */
+int trk_set_stream_rows(trk_ctx *ctx, int rows);
 
 /* Per-kernel timing (the HIP counterpart of the reference's TR_PROFILE laps, exec.rs:344-430):
  * when on, every kernel a forward launches is bracketed by HIP events on the call's stream. */

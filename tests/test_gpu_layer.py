@@ -44,6 +44,29 @@ def compare_out(got, want, w_equal, ctx=""):
         assert err <= 1e-5 * scale, f"{ctx}: {err} vs scale {scale}"
 
 
+def _libm_expf():
+    import ctypes as C
+    f = C.CDLL("libm.so.6").expf
+    f.restype, f.argtypes = C.c_float, [C.c_float]
+    return f
+
+
+_expf = None
+
+
+def shared_gate_exact(L, x):
+    """True when the host libm's expf, which the oracle's shared-gate sigmoid uses, gives the
+    correctly rounded exp (what the GPU computes) for every row's gate logit."""
+    global _expf
+    if _expf is None:
+        _expf = _libm_expf()
+    for row in np.atleast_2d(x):
+        s = np.float32(O.dot(row, L.shexp_gate))
+        if np.float32(_expf(float(-s))) != np.float32(np.exp(np.float64(-s))):
+            return False
+    return True
+
+
 _layers = {}
 
 
@@ -78,7 +101,7 @@ def test_decode_layer(shape, k, hiprec):
         xq = ctx.read(trmoe.WS_XQ, 2 * L.H, np.int8)
         oq, _, _ = O.quant_pair(x[0], 32) if hiprec else O.quant_rows(x, 32)
         assert np.array_equal(xq[:oq.size], oq.reshape(-1))
-        compare_out(host(out)[0], r["out"], np.array_equal(w, r["w"]), f"{shape} t={t}")
+        compare_out(host(out)[0], r["out"], np.array_equal(w, r["w"]) and shared_gate_exact(L, x), f"{shape} t={t}")
     assert ctx.stats() == (3, 3 * k)
     ctx.close()
 
@@ -107,7 +130,7 @@ def test_decode_one_launch_matches_three(policy):
                 ids = ctx.read(trmoe.WS_IDS, 4 * 32, np.uint32)[:len(r["ids"])]
                 assert np.array_equal(ids, r["ids"])
                 w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:len(r["ids"])]
-                compare_out(res[-1], r["out"], np.array_equal(w, r["w"]), f"fused t={t}")
+                compare_out(res[-1], r["out"], np.array_equal(w, r["w"]) and shared_gate_exact(L, x), f"fused t={t}")
         assert ctx.read(trmoe.WS_BARRIER_ERR, 4, np.uint32)[0] == 0
         outs[fused] = res
         ctx.close()
@@ -141,7 +164,51 @@ def test_batch_layer_and_dispatch(shape, M, k):
     assert np.array_equal(ctx.read(trmoe.WS_GRP_EXP, 4 * ng, np.uint32), r["grp_expert"])
     xq = ctx.read(trmoe.WS_XQ, M * L.H, np.int8).reshape(M, L.H)
     assert np.array_equal(xq, O.quant_rows(x, 32)[0])
-    compare_out(host(out), r["out"], np.array_equal(w, r["w"][:, :k]), f"{shape} M={M}")
+    compare_out(host(out), r["out"], np.array_equal(w, r["w"][:, :k]) and shared_gate_exact(L, x), f"{shape} M={M}")
+    ctx.close()
+
+
+ODD = dict(seed=13, H=768, E=24, F=768)  # 3 superblocks per row: lanes of a row never straddle a wave
+
+
+@pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
+                                       ("full", 16, 10), ("small", 700, 3), ("odd", 9, 5), ("odd", 40, 5)])
+def test_stream_items_match_mfma_tiles(shape, M, k):
+    """Every split of the grouped items between the streaming GEMV and the int8 MFMA tiles gives
+    the same bits, and matches the oracle's moe_batch."""
+    say(f"stream vs mfma items {shape} M={M} k={k}")
+    L, orc, W = layer(shape, **{"small": SMALL, "full": FULL, "odd": ODD}[shape])
+    import torch
+    x = L.x(M, tid=250 + M)
+    r = orc.moe_batch(x, k=k, router_dot_max_m=16)
+    outs = {}
+    for rows in (0, 1, 4, 16, -1):
+        ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))
+        ctx.set_stream_rows(rows)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        outs[rows] = host(out).copy()
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :k]
+        exact = np.array_equal(w, r["w"][:, :k]) and shared_gate_exact(L, x)
+        compare_out(outs[rows], r["out"], exact, f"{shape} M={M} rows={rows}")
+        ctx.close()
+    for rows, o in outs.items():
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"rows={rows}"
+
+
+def test_decode_odd_superblocks():
+    """Decode with 3 superblocks per gate/up row and per down row (no power-of-two lane groups)."""
+    say("decode odd superblocks")
+    L, orc, W = layer("odd", **ODD)
+    ctx = trmoe.Context(L.H, L.E, L.F, 5, 4)
+    import torch
+    for t in range(2):
+        x = L.x(1, tid=120 + t)
+        r = orc.moe_block(x[0], k=5)
+        out = torch.empty((1, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:5]
+        compare_out(host(out)[0], r["out"], np.array_equal(w, r["w"]) and shared_gate_exact(L, x), f"odd t={t}")
     ctx.close()
 
 
@@ -161,7 +228,7 @@ def test_dynamic_k_policy(M):
         r = orc.moe_block(x[0], k=4, policy=pol)
         assert nsel[0] == r["k"]
         w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:r["k"]]
-        compare_out(host(out)[0], r["out"], np.array_equal(w, r["w"]), "decode policy")
+        compare_out(host(out)[0], r["out"], np.array_equal(w, r["w"]) and shared_gate_exact(L, x), "decode policy")
     else:
         r = orc.moe_batch(x, k=4, policy=pol)
         assert np.array_equal(nsel, r["n_sel"])
@@ -170,11 +237,12 @@ def test_dynamic_k_policy(M):
     ctx.close()
 
 
-@pytest.mark.parametrize("M", [1, 6])
-def test_q6k_down(M):
-    say(f"q6k down M={M}")
+@pytest.mark.parametrize("M,rows", [(1, -1), (6, -1), (6, 0), (40, 16)])
+def test_q6k_down(M, rows):
+    say(f"q6k down M={M} stream rows {rows}")
     L, orc, W = layer("q6", seed=4, H=512, E=16, F=256, down_fmt=O.FMT_Q6_K)
-    ctx = trmoe.Context(L.H, L.E, L.F, 3, 8)
+    ctx = trmoe.Context(L.H, L.E, L.F, 3, 64)
+    ctx.set_stream_rows(rows)
     import torch
     x = L.x(M, tid=400)
     out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")

@@ -41,10 +41,14 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 
 // Kernel ids for trk_get_timing.
 enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DEC_LAYER, K_DISPATCH, K_B_GATEUP, K_B_DOWN,
-                K_B_COMBINE, K_RMSNORM, K_COUNT };
+                K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_COUNT };
 static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
                                                   "decode_down", "decode_layer", "dispatch", "batch_gateup",
-                                                  "batch_down", "batch_combine", "rmsnorm"};
+                                                  "batch_down", "stream_gateup", "stream_down", "batch_combine",
+                                                  "rmsnorm"};
+
+// Batch of more than 16 tokens: work items of at most this many rows run on the streaming GEMV.
+static constexpr uint32_t kStreamRows = 4;
 
 struct TimedLaunch {
     int kid;
@@ -62,6 +66,7 @@ struct trk_ctx {
     std::vector<hipEvent_t> spare;
     int fusion = 0;   // decode: one launch per layer (when the shape and the GPU allow it) if set
     int fused = -1;   // that check for the current policy: -1 not yet made, 0 no, 1 yes
+    int stream_rows = -1;  // batch: items of at most this many rows on the streaming GEMV (-1: automatic)
 };
 
 extern "C" const char* trk_last_error(void) { return g_err; }
@@ -315,8 +320,12 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         // the dispatch kernel counts the routed rows (one atomic per call, not per token)
         TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
         TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
-        TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, st));
-        TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, st));
+        // items of few rows on the streaming GEMV, the others on the MFMA tiles (same bits)
+        const uint32_t sr = c->stream_rows >= 0 ? (uint32_t)c->stream_rows : (m <= 16 ? BR : kStreamRows);
+        if (sr > 0) TIMED(K_S_GATEUP, launch_stream_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
+        if (sr < BR) TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
+        if (sr > 0) TIMED(K_S_DOWN, launch_stream_down(M.down, M.shd, ws, m, sr, st));
+        if (sr < BR) TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, sr, st));
         TIMED(K_B_COMBINE, launch_batch_combine(ws, m, out, residual, st));
     }
     return TRK_OK;
@@ -364,6 +373,13 @@ extern "C" int trk_set_fusion(trk_ctx* c, int on) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     c->fusion = on ? 1 : 0;
     c->fused = -1;
+    return TRK_OK;
+}
+
+extern "C" int trk_set_stream_rows(trk_ctx* c, int rows) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    if (rows < -1 || rows > (int)BR) return fail(TRK_E_INVALID, "stream rows (%d) must be in -1..%u", rows, BR);
+    c->stream_rows = rows;
     return TRK_OK;
 }
 

@@ -238,4 +238,11 @@ __device__ __forceinline__ T row16_allreduce(T v, Op op) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_reduce_u32<false>(v); }
 
+// Token (activation row) of entry row `row` of a grouped work item; rows past the item reuse its
+// first row (their outputs are never stored).
+__device__ __forceinline__ uint32_t item_token(const Workspace& ws, const Item& it, bool shared, uint32_t row) {
+    const uint32_t r = row < it.nrows ? row : 0u;
+    return shared ? it.row0 + r : ws.ent_tok[it.row0 + r];
+}
+
 }  // namespace trk

@@ -18,9 +18,7 @@
 
 namespace trk {
 
-constexpr uint32_t BR = 16;  // entry rows per work item: one 16-row MFMA tile
 constexpr uint32_t DISPATCH_WAVES = 8;
-constexpr uint32_t NO_EXPERT = 0xffffffffu;
 
 __device__ __forceinline__ uint32_t popc64(unsigned long long v) { return (uint32_t)__popcll(v); }
 
@@ -267,13 +265,6 @@ __device__ __forceinline__ long unpack8(uint2 p, int h) {
     return (long)(((unsigned long long)hi << 32) | lo);
 }
 
-// Token (activation row) of entry row `row` of an item; rows past the item reuse its first row
-// (their outputs are never stored).
-__device__ __forceinline__ uint32_t item_token(const Workspace& ws, const Item& it, bool shared, uint32_t row) {
-    const uint32_t r = row < it.nrows ? row : 0u;
-    return shared ? it.row0 + r : ws.ent_tok[it.row0 + r];
-}
-
 // Shared by the two grouped kernels.  A workgroup takes one item (<= 16 entry rows of one expert,
 // or <= 16 tokens of the shared expert) and a range of 16-row weight strips, one strip per wave at
 // a time.  The item's int8 activations are staged once in LDS in MFMA operand order (block b,
@@ -338,12 +329,14 @@ constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table
 // gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
 // Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.
 template <int NSB>
-__global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat shg, Mat shu, Workspace ws) {
+__global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat shg, Mat shu, Workspace ws,
+                                                          uint32_t skip_rows) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8;
     const uint32_t F = gate.rows, nbf = F / 16;
     const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
     if (itn >= ws.n_groups[2]) return;
     const Item item = ws.items[itn];
+    if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
     const bool shared = item.expert == NO_EXPERT;
     const uint32_t n_ent = ws.n_groups[1];
     const Mat& G = shared ? shg : gate;
@@ -478,15 +471,15 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
 }
 
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
-                               const Workspace& ws, uint32_t m, hipStream_t st) {
+                               const Workspace& ws, uint32_t m, uint32_t skip_rows, hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32;
     const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_STRIDE * 8 + 32 * 4;
     // a workgroup per (item, 16 strips) once the items fill the GPU; otherwise per (item, 4 strips)
     // so that a wave's chain of dependent weight loads stays short
-    const dim3 grid(m >= 64 ? F / 256 : F / 64, ws.item_cap);
+    const dim3 grid(m >= 64 ? F / 256 : F / 64, grouped_item_rows(ws, m));
     switch (H / 256) {
 #define GU_CASE(n) \
-    case n: batch_gateup_kernel<n><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws); break;
+    case n: batch_gateup_kernel<n><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws, skip_rows); break;
         GU_CASE(1) GU_CASE(2) GU_CASE(3) GU_CASE(4) GU_CASE(5) GU_CASE(6) GU_CASE(7) GU_CASE(8) GU_CASE(9)
         GU_CASE(10) GU_CASE(11) GU_CASE(12) GU_CASE(13) GU_CASE(14) GU_CASE(15) GU_CASE(16)
 #undef GU_CASE
@@ -534,12 +527,13 @@ __device__ __forceinline__ long q6_operand(const Q6Sb& w, int q8) {
 }
 
 template <int NSB, bool Q6>
-__global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws) {
+__global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
     const uint32_t H = down.rows;
     const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
     if (itn >= ws.n_groups[2]) return;
     const Item item = ws.items[itn];
+    if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
     const bool shared = item.expert == NO_EXPERT;
     const uint32_t n_ent = ws.n_groups[1];
     const Mat& D = shared ? shd : down;
@@ -656,16 +650,17 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     (void)NQ;
 }
 
-hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, hipStream_t st) {
+hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t skip_rows,
+                             hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
     const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 8 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
-    const dim3 grid(m >= 64 ? H / 256 : H / 64, ws.item_cap);
+    const dim3 grid(m >= 64 ? H / 256 : H / 64, grouped_item_rows(ws, m));
     const bool q6 = down.fmt == TRK_FMT_Q6_K;
     if (q6 != (sh_down.fmt == TRK_FMT_Q6_K)) return hipErrorInvalidValue;  // one format per layer
     switch (F / 256 * 2 + (q6 ? 1 : 0)) {
 #define DN_CASE(n)                                                                          \
-    case n * 2: batch_down_kernel<n, false><<<grid, 256, lds, st>>>(down, sh_down, ws); break; \
-    case n * 2 + 1: batch_down_kernel<n, true><<<grid, 256, lds, st>>>(down, sh_down, ws); break;
+    case n * 2: batch_down_kernel<n, false><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
+    case n * 2 + 1: batch_down_kernel<n, true><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
         default: return hipErrorInvalidValue;

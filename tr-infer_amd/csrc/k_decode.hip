@@ -13,27 +13,13 @@
 //            row's superblocks, forms the per-16 block dots against the staged activations and
 //            runs the chain in registers; slot 0 is stored and later slots (routing order,
 //            shared last) are added — tasks C with the combine fused.
+#include "gemv.hpp"
 #include "route.hpp"
 #include "router.hpp"
 
 namespace trk {
 
-// gate/up threads: a lane per (row, superblock) of the 32 rows, at least two waves (routing, x)
-#define GU_THREADS(nsb) (32 * (nsb) < 128 ? 128 : 32 * (nsb))
 constexpr int DN_R = 4;      // output rows per down workgroup
-
-__device__ __forceinline__ uint32_t nib(uint32_t w, int h) { return (w >> (4 * h)) & 0x0f0f0f0fu; }
-
-// Lane (row r, superblock sb) of the workgroup: r = tid / NSB.  The per-row epilogue chain runs
-// across the NSB lanes of a row in superblock order, the running f32 accumulators passed one lane
-// up per step (DPP row shift when NSB divides 16).
-template <int NSB>
-__device__ __forceinline__ float lane_up(float v) {
-    if constexpr (16 % NSB == 0)
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
-    else
-        return __shfl_up(v, 1);
-}
 
 // One gate/up unit (slot, strip) on a workgroup of at least GU_THREADS(NSB) threads.  Wave 0
 // routes the token into LDS when `route` is set (always for routed slots).  `hook(r_ids, n)` runs
@@ -92,7 +78,10 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
             for (int i = 0; i < 8; i++) xv[i] = src[i];
         }
     }
-    const uint32_t r = tid / NSB, sb = tid % NSB;
+    // lane (row r, superblock sb); rows never straddle a wave (the chain hands over lane to lane)
+    constexpr uint32_t RPW = 64 / NSB;
+    const uint32_t ln = tid % 64, sb = ln % NSB;
+    const uint32_t r = ln < RPW * NSB ? (tid / 64) * RPW + ln / NSB : 32u;
     const bool wthread = r < 32;
     auto load_rows = [&](const Mat& G, const Mat& U, uint32_t e, uint4* wq) {
         const uint32_t rr = wthread ? r : 0u;
@@ -345,123 +334,6 @@ struct DownLanes {
     static constexpr int UPP = 4 * UPW;      // units per pass of the 256-thread workgroup
 };
 
-// the running accumulator one lane up (towards the next half-superblock of the unit)
-template <int L>
-__device__ __forceinline__ float unit_up(float v) {
-    if constexpr (16 % L == 0)
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
-    else
-        return __shfl_up(v, 1);
-}
-
-// Q4_K half superblock h2 of superblock sb: the 16-byte header and the 64 qs bytes of its four
-// sub-blocks (sub-block j = 4*h2 + jj lives in nibble j%2 of qs[32*(j/2) + i]).
-__device__ __forceinline__ void load_half_q4k(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2, uint4& hdr,
-                                              uint4 (&qs)[4]) {
-    const uint4* p = reinterpret_cast<const uint4*>(rowp + sb * 144);
-    hdr = p[0];
-    const uint4* q = reinterpret_cast<const uint4*>(rowp + sb * 144 + 16 + 64 * h2);
-#pragma unroll
-    for (int i = 0; i < 4; i++) qs[i] = q[i];
-}
-
-// per-block terms of a lane's 8 blocks (blocks 16*sb + 8*h2 + 0..7): exact int dot, t = dd*sx,
-// mm and the activation's u = sx*sum, for P activation rows
-template <int P>
-__device__ __forceinline__ void half_terms_q4k(const uint4& hdr, const uint4 (&qs)[4], uint32_t h2,
-                                               const int8_t* __restrict__ aq /*[P] rows, stride F, at block 0*/,
-                                               uint32_t F, const float* __restrict__ as, const float* __restrict__ au,
-                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
-                                               float (&uv)[P][8]) {
-    const uint32_t* w32 = reinterpret_cast<const uint32_t*>(qs);
-    const float d = h2f((uint16_t)(hdr.x & 0xffff)), dmin = h2f((uint16_t)(hdr.x >> 16));
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        const float4* s4 = reinterpret_cast<const float4*>(as + p * nbf);
-        const float4* u4 = reinterpret_cast<const float4*>(au + p * nbf);
-        const float4 s0 = s4[0], s1 = s4[1], u0 = u4[0], u1 = u4[1];
-        const float sa[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        const float ua[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            tv[p][i] = sa[i];
-            uv[p][i] = ua[i];
-        }
-    }
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-        int sc, mn;
-        // h2 is 0 or 1: select the sub-block's scale/min without indexing by a runtime value
-        int sc0, mn0, sc1, mn1;
-        q4k_scale_min_w(hdr.y, hdr.z, hdr.w, jj, sc0, mn0);
-        q4k_scale_min_w(hdr.y, hdr.z, hdr.w, 4 + jj, sc1, mn1);
-        sc = h2 ? sc1 : sc0;
-        mn = h2 ? mn1 : mn0;
-        float ddv, mm;
-        q4k_dm(d, dmin, sc, mn, ddv, mm);
-        const int c = jj / 2, h = jj % 2;
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const int i = 2 * jj + hh;
-            mmv[i] = mm;
-#pragma unroll
-            for (int p = 0; p < P; p++) {
-                const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
-                int dot = sdot4((int)nib(w32[8 * c + 4 * hh + 0], h), xv.x, 0);
-                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 1], h), xv.y, dot);
-                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 2], h), xv.z, dot);
-                dot = sdot4((int)nib(w32[8 * c + 4 * hh + 3], h), xv.w, dot);
-                dotv[p][i] = (float)dot;
-                tv[p][i] = ddv * tv[p][i];  // t = d * sx (gemv.rs:145)
-            }
-        }
-    }
-}
-
-// Q6_K (210-byte superblocks, 2-byte aligned) half superblock h2: blocks j = 8*h2 + 0..7 use
-// ql[64*h2 + ...], qh[32*h2 + ...], scales[8*h2 + ...] and d — the extension mapping: unsigned
-// 6-bit q, dd = f16(d*sc), mm = f16(-32*dd), one block per scale.
-template <int P>
-__device__ __forceinline__ void half_terms_q6k(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2,
-                                               const int8_t* __restrict__ aq, uint32_t F,
-                                               const float* __restrict__ as, const float* __restrict__ au,
-                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
-                                               float (&uv)[P][8]) {
-    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(rowp + sb * 210);
-    uint16_t ql[32], qh[16], sc2[4];
-#pragma unroll
-    for (int i = 0; i < 32; i++) ql[i] = s2[32 * h2 + i];
-#pragma unroll
-    for (int i = 0; i < 16; i++) qh[i] = s2[64 + 16 * h2 + i];
-#pragma unroll
-    for (int i = 0; i < 4; i++) sc2[i] = s2[96 + 4 * h2 + i];
-    const float d = h2f(s2[104]);
-    auto dl = [&](int o) -> uint32_t { return (uint32_t)ql[o >> 1] | ((uint32_t)ql[(o >> 1) + 1] << 16); };
-    auto dh = [&](int o) -> uint32_t { return (uint32_t)qh[o >> 1] | ((uint32_t)qh[(o >> 1) + 1] << 16); };
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int8_t sc = (int8_t)((sc2[i >> 1] >> ((i & 1) * 8)) & 0xff);
-        const float ddv = f16_round(d * (float)sc);
-        mmv[i] = f16_round(-32.0f * ddv);
-        const int g = i / 2, l0 = 16 * (i % 2);
-#pragma unroll
-        for (int p = 0; p < P; p++) {
-            const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
-            const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
-            int dot = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                uint32_t lo = dl(32 * (g & 1) + l0 + 4 * t);
-                lo = (g >> 1) ? ((lo >> 4) & 0x0f0f0f0fu) : (lo & 0x0f0f0f0fu);
-                const uint32_t hi = (dh(l0 + 4 * t) >> (2 * g)) & 0x03030303u;
-                dot = sdot4((int)(lo | (hi << 4)), xa[t], dot);
-            }
-            dotv[p][i] = (float)dot;
-            tv[p][i] = ddv * as[p * nbf + i];
-            uv[p][i] = au[p * nbf + i];
-        }
-    }
-}
 
 // Work unit u = slot * DN_R + row of a workgroup; slots 0..kcap-1 are the routed slots (those at
 // or past n idle), slot kcap is the shared expert.  Activation rows are staged in LDS with slot

@@ -31,6 +31,8 @@ struct Mat {
 struct Item {
     uint32_t expert, row0, nrows, pad;
 };
+constexpr uint32_t BR = 16;                  // most entry rows of an item: one 16-row MFMA tile
+constexpr uint32_t NO_EXPERT = 0xffffffffu;  // Item::expert of the shared expert's items
 
 // Device workspace (sized at trk_create).
 // grid barrier of the one-launch decode layer: workgroups arrive on BAR_GROUPS counters, BAR_LINE
@@ -98,10 +100,17 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);
+// grouped expert products: the MFMA tiles take the items of more than skip_rows rows, the
+// streaming GEMV the items of at most max_rows rows
+uint32_t grouped_item_rows(const Workspace& ws, uint32_t m);  // grid rows covering every item
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
-                               const Workspace& ws, uint32_t m, hipStream_t st);
+                               const Workspace& ws, uint32_t m, uint32_t skip_rows, hipStream_t st);
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m,
-                             hipStream_t st);
+                             uint32_t skip_rows, hipStream_t st);
+hipError_t launch_stream_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
+                                const Workspace& ws, uint32_t m, uint32_t max_rows, hipStream_t st);
+hipError_t launch_stream_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m,
+                              uint32_t max_rows, hipStream_t st);
 hipError_t launch_batch_combine(const Workspace& ws, uint32_t m, float* out, int residual, hipStream_t st);
 hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t kb, const int8_t* q, const float* s,
                        const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,

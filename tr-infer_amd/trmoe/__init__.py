@@ -82,6 +82,7 @@ def lib() -> C.CDLL:
         L.trk_launch_kernel.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, C.c_char_p, vp]
         L.trk_set_timing.argtypes = [vp, i]
         L.trk_set_fusion.argtypes = [vp, i]
+        L.trk_set_stream_rows.argtypes = [vp, i]
         L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
         _lib = L
     return _lib
@@ -161,6 +162,10 @@ class Context:
 
     def set_fusion(self, on: bool):
         check(lib().trk_set_fusion(self.h, int(on)))
+
+    def set_stream_rows(self, rows: int):
+        """Batch items of at most `rows` rows on the streaming GEMV (-1 automatic, 0 none)."""
+        check(lib().trk_set_stream_rows(self.h, int(rows)))
 
     def set_timing(self, on: bool):
         check(lib().trk_set_timing(self.h, int(on)))
