@@ -61,6 +61,9 @@ def main():
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
     ap.add_argument("--fusion", type=int, default=None, choices=(0, 1),
                     help="force the one-launch decode layer on (1) or off (0); default: the library's choice")
+    ap.add_argument("--stream-rows", type=int, default=None, metavar="ROWS",
+                    help="batch items of at most ROWS rows on the streaming GEMV (-1 the library's choice, "
+                         "0 all on the MFMA tiles)")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
                     help="finish with three device copies of MIB MiB (a known-size kernel for calibrating "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -90,6 +93,8 @@ def main():
     ctx = trmoe.Context(H, E, F, K, m_max)
     if args.fusion is not None:
         ctx.set_fusion(args.fusion)
+    if args.stream_rows is not None:
+        ctx.set_stream_rows(args.stream_rows)
     xs = {M: trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H) for M in ms_list}
     out = torch.empty((m_max, H), dtype=torch.float32, device=dev)
 
@@ -262,6 +267,8 @@ def bench_config4(args, layers, dev, stream, trmoe, torch, np):
     for w in lw:
         w.moew.router_bias = None
     ctx = trmoe.Context(H, E, F, K, M)
+    if args.stream_rows is not None:
+        ctx.set_stream_rows(args.stream_rows)
     ctx.set_moe((1, K, 0.9, trmoe.BASIS_TOP))
     x = trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H)
     out = torch.empty((M, H), dtype=torch.float32, device=dev)
@@ -298,6 +305,8 @@ def bench_stack(args, layers, ctx, M, dev, stream, trmoe, torch):
     the layers in turn, on seeded N(0, 1) rows, timed end to end (one replay = one pass)."""
     if ctx is None:
         ctx = trmoe.Context(H, E, F, K, M)
+        if args.stream_rows is not None:
+            ctx.set_stream_rows(args.stream_rows)
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
     rms = [torch.rand(H, generator=gen, device=dev) * 0.2 + 0.9 for _ in layers]

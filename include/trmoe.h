@@ -180,9 +180,9 @@ int trk_set_fusion(trk_ctx *ctx, int on);
 
 /* M >= 2: grouped work items (one expert's entry rows, at most 16) of at most `rows` rows run on
  * the streaming GEMV kernels, larger ones on the int8 MFMA tiles.  rows = -1 (the default) picks
- * 16 for M <= 16 (every item streams) and 4 above; 0 puts every item on the tiles.  Every choice
- * gives the same bits (moe_batch, exec_batch.rs:1404-1580); no counterpart in the reference,
- * which runs one grouped kernel per expert matrix. */
+ * 16 for M <= 16 (every item streams), 4 while M * k_cap <= 2 * n_expert, else 0 (every item on
+ * the tiles).  Every choice gives the same bits (moe_batch, exec_batch.rs:1404-1580); no
+ * counterpart in the reference, which runs one grouped kernel per expert matrix. */
 int trk_set_stream_rows(trk_ctx *ctx, int rows);
 
 /* Per-kernel timing (the HIP counterpart of the reference's TR_PROFILE laps, exec.rs:344-430):

@@ -47,8 +47,15 @@ static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "qua
                                                   "batch_down", "stream_gateup", "stream_down", "batch_combine",
                                                   "rmsnorm"};
 
-// Batch of more than 16 tokens: work items of at most this many rows run on the streaming GEMV.
-static constexpr uint32_t kStreamRows = 4;
+// Which grouped items run on the streaming GEMV (the rest on the MFMA tiles), when the caller has
+// not chosen: all of them up to 16 tokens; the items of at most 4 rows while the selections
+// average at most two per expert (most routed items hold one or two rows, the shared expert's
+// 16); none beyond, where tail items share their expert's weights with its full tiles and a
+// split costs more than it saves (measured at M = 512 and 3072).
+static uint32_t auto_stream_rows(uint32_t m, uint32_t kcap, uint32_t E) {
+    if (m <= BR) return BR;
+    return (uint64_t)m * kcap <= 2ull * E ? 4u : 0u;
+}
 
 struct TimedLaunch {
     int kid;
@@ -317,11 +324,20 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
                                                  ws.rlog, ws.shl, st, &xq));
-        // the dispatch kernel counts the routed rows (one atomic per call, not per token)
-        TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
-        TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
+        // the dispatch kernel counts the routed rows (one atomic per call, not per token).  Up to 4
+        // tokens one launch routes (a wave per token, one per SIMD) and dispatches; up to 16 the
+        // routing has a launch of its own (spread over CUs) and the dispatch is the small one
+        if (m <= 4 && m * kcap <= 1024) {
+            TIMED(K_DISPATCH, launch_dispatch_small(ws, m, kcap, lg, k, c->pol, st));
+        } else if (m <= 16 && m * kcap <= 1024) {
+            TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
+            TIMED(K_DISPATCH, launch_dispatch_small(ws, m, kcap, nullptr, k, c->pol, st));
+        } else {
+            TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
+            TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
+        }
         // items of few rows on the streaming GEMV, the others on the MFMA tiles (same bits)
-        const uint32_t sr = c->stream_rows >= 0 ? (uint32_t)c->stream_rows : (m <= 16 ? BR : kStreamRows);
+        const uint32_t sr = c->stream_rows >= 0 ? (uint32_t)c->stream_rows : auto_stream_rows(m, kcap, E);
         if (sr > 0) TIMED(K_S_GATEUP, launch_stream_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
         if (sr < BR) TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
         if (sr > 0) TIMED(K_S_DOWN, launch_stream_down(M.down, M.shd, ws, m, sr, st));

@@ -13,6 +13,7 @@
 //   combine:  per token, shared row first, then its entries in ascending expert order (the
 //             reference's overwrite-then-accumulate order, exec_batch.rs:1539-1561).
 #include "common.hpp"
+#include "route.hpp"
 
 #include <type_traits>
 
@@ -230,6 +231,124 @@ __global__ __launch_bounds__(64) void scatter_kernel(Workspace ws, uint32_t m, u
             ws.ent_exp[pos] = e;
             ws.ent_of[(size_t)t * K_MAX + s] = pos;
         }
+}
+
+// Routing and dispatch of a batch of at most 16 tokens in one launch (every expert's group then
+// fits one work item).  One workgroup of 16 waves: wave t routes token t (route_topk /
+// route_mass, router.rs:70-148, as route_kernel does) into ws.ids / w / n_sel; then thread
+// (token, slot) ranks its selection's key (expert, token) against every other key, broadcast
+// from LDS: the rank is the entry's position in moe_batch's order (experts ascending, tokens
+// ascending within one), and the keys of the same expert give its group size.  Group indices
+// come from one block scan of the group-start flags over the sorted keys.
+constexpr uint32_t SMALL_WAVES = 16;
+constexpr uint32_t SMALL_T = SMALL_WAVES * 64;
+template <int NJ>
+__global__ __launch_bounds__(SMALL_T) void dispatch_small_kernel(Workspace ws, uint32_t m, uint32_t kcap,
+                                                               const float* __restrict__ lg, uint32_t k, Policy pol) {
+    const uint32_t E = ws.E, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    extern __shared__ __align__(16) uint8_t smem[];
+    if (lg) {  // route (the scratch below is reused once every wave is past the barrier)
+        uint2* cand = reinterpret_cast<uint2*>(smem) + wv * ROUTE_CAND;                           // [16][96]
+        float* ex = reinterpret_cast<float*>(smem + SMALL_WAVES * ROUTE_CAND * 8) + (size_t)wv * E;  // [16][E]
+        if (wv < m) {
+            const uint32_t n = route_row<NJ>(lg + (size_t)wv * E, E, k, pol, lane, cand, ex,
+                                             ws.ids + (size_t)wv * K_MAX, ws.w + (size_t)wv * K_MAX);
+            if (lane == 0) ws.n_sel[wv] = n;
+        }
+        __syncthreads();  // orders the routing's global stores before the loads below
+    }
+    uint32_t* keys = reinterpret_cast<uint32_t*>(smem);  // [SMALL_T] (expert << 16 | token), ~0 = none
+    uint32_t* skey = keys + SMALL_T;                     // [SMALL_T] keys in entry order
+    float* sw = reinterpret_cast<float*>(skey + SMALL_T);  // [SMALL_T] their routing weights
+    uint32_t* scnt = reinterpret_cast<uint32_t*>(sw + SMALL_T);  // [SMALL_T] their group sizes
+    uint32_t* wtot = scnt + SMALL_T;                     // [16]
+    const uint32_t N = m * kcap, t = tid / kcap, s = tid % kcap;
+    // n_sel: lane i of every wave loads token i's (a per-lane vector load, which sees the routing's
+    // stores), then the wave sums them and each thread takes its token's by a lane shuffle
+    const uint32_t ns_l = lane < m ? ws.n_sel[lane] : 0u;
+    const uint32_t n_ent = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan_u32(ns_l), 63);
+    const uint32_t ns_t = (uint32_t)__shfl((int)ns_l, (int)(t < m ? t : 0));
+    const bool valid = tid < N && s < ns_t;
+    const uint32_t key = valid ? (ws.ids[(size_t)t * K_MAX + s] << 16) | t : 0xffffffffu;
+    const float w = valid ? ws.w[(size_t)t * K_MAX + s] : 0.0f;
+    keys[tid] = key;
+    __syncthreads();
+    uint32_t rank = 0, same = 0;
+    // only the waves holding selections rank (broadcast LDS reads still cost full bandwidth)
+    const uint32_t N16 = wv * 64 < N ? (N + 15) / 16 : 0u;
+    for (uint32_t j = 0; j < N16; j++) {  // keys past N are ~0 from the store above (tid >= N)
+        uint4 kv[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) kv[c] = reinterpret_cast<const uint4*>(keys)[4 * j + c];  // all four in flight
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t ka[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                rank += ka[i] < key ? 1u : 0u;
+                same += (ka[i] >> 16) == (key >> 16) ? 1u : 0u;
+            }
+        }
+    }
+    if (valid) {
+        skey[rank] = key;
+        sw[rank] = w;
+        scnt[rank] = same;
+        ws.ent_of[(size_t)t * K_MAX + s] = rank;
+    }
+    __syncthreads();
+    // entry p = tid: its group starts here when the expert changes
+    const uint32_t p = tid;
+    const uint32_t kp = p < n_ent ? skey[p] : 0u;
+    const bool head = p < n_ent && (p == 0 || (skey[p - 1] >> 16) != (kp >> 16));
+    const uint32_t inc = wave_incl_scan_u32(head ? 1u : 0u);
+    if (lane == 63) wtot[wv] = inc;
+    if (p < n_ent) {
+        ws.ent_tok[p] = kp & 0xffffu;
+        ws.ent_exp[p] = kp >> 16;
+        ws.ent_w[p] = sw[p];
+    }
+    __syncthreads();
+    uint32_t base = 0, ng = 0;
+    for (uint32_t v = 0; v < SMALL_WAVES; v++) {
+        const uint32_t x = wtot[v];
+        base += v < wv ? x : 0u;
+        ng += x;
+    }
+    if (head) {
+        const uint32_t g = base + inc - 1, e = kp >> 16;
+        ws.grp_start[g] = p;
+        ws.grp_exp[g] = e;
+        ws.items[g] = Item{e, p, scnt[p], 0};
+    }
+    if (tid == 0) {
+        ws.items[ng] = Item{NO_EXPERT, 0, m, 0};  // the shared expert over the tokens, last
+        if (ws.stats) {  // MoeStats: rows and selected experts of this call
+            atomicAdd(&ws.stats[0], (unsigned long long)m);
+            atomicAdd(&ws.stats[1], (unsigned long long)n_ent);
+        }
+        ws.grp_start[ng] = n_ent;
+        ws.n_groups[0] = ng;
+        ws.n_groups[1] = n_ent;
+        ws.n_groups[2] = ng + 1;
+    }
+}
+
+hipError_t launch_dispatch_small(const Workspace& ws, uint32_t m, uint32_t kcap, const float* lg, uint32_t k,
+                                 Policy pol, hipStream_t st) {
+    const size_t E = ws.E;
+    if (m > SMALL_WAVES || m * kcap > SMALL_T || E > 1024) return hipErrorInvalidValue;
+    size_t lds = (size_t)SMALL_T * 16 + SMALL_WAVES * 4;
+    if (lg) {
+        const size_t rl = SMALL_WAVES * ROUTE_CAND * 8 +
+                          ((pol.enabled && pol.basis == TRK_BASIS_ALL) ? SMALL_WAVES * E * 4 : 0);
+        lds = lds > rl ? lds : rl;
+    }
+    if (route_nj(ws.E) == 8)
+        dispatch_small_kernel<8><<<1, SMALL_T, lds, st>>>(ws, m, kcap, lg, k, pol);
+    else
+        dispatch_small_kernel<16><<<1, SMALL_T, lds, st>>>(ws, m, kcap, lg, k, pol);
+    return hipGetLastError();
 }
 
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st) {

@@ -100,6 +100,10 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);
+// m <= 16 (m * kcap <= 1024): the same dispatch in one launch with the routing (lg != null) or
+// from ws.ids / w / n_sel (lg == null)
+hipError_t launch_dispatch_small(const Workspace& ws, uint32_t m, uint32_t kcap, const float* lg, uint32_t k,
+                                 Policy pol, hipStream_t st);
 // grouped expert products: the MFMA tiles take the items of more than skip_rows rows, the
 // streaming GEMV the items of at most max_rows rows
 uint32_t grouped_item_rows(const Workspace& ws, uint32_t m);  // grid rows covering every item
