@@ -126,12 +126,32 @@ __host__ __device__ constexpr int gemm_pad(int d, int kc) {  // floats of paddin
         if (d == 0 || (d * (kc + p)) % 32 == 16) return p;
     return 4;
 }
+// The first n_aux workgroups of the grid do the launch's other work, so that it needs no launch of
+// its own: workgroups < n_dot compute the shared gate's logit (always in dot order,
+// exec_batch.rs:1520), a wave per DOT_MR rows; the rest quantise x for the grouped kernels.
 template <int RM, int RE, int QM, int KC, bool DB>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restrict__ router,
                                                          const float* __restrict__ bias,
                                                          const float* __restrict__ x, uint32_t m, uint32_t E,
-                                                         uint32_t H, float* __restrict__ rlog) {
+                                                         uint32_t H, float* __restrict__ rlog,
+                                                         const float* __restrict__ shg, float* __restrict__ sh,
+                                                         XQuant xquant, uint32_t n_dot, uint32_t n_aux) {
     constexpr int QE = 16 / QM, TM = QM * RM, TE = QE * RE;
+    if (blockIdx.x < n_aux) {  // workgroup-uniform
+        if (blockIdx.x < n_dot) {
+            const uint32_t lane = threadIdx.x % WAVE, m0 = (blockIdx.x * 4 + threadIdx.x / WAVE) * DOT_MR;
+            if (m0 < m) {
+                const uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
+                float res[DOT_MR];
+                dot_rows(shg, x, m0, mr, H, lane, res);
+                if (lane == 0)
+                    for (uint32_t r = 0; r < mr; r++) sh[m0 + r] = res[r];
+            }
+        } else {
+            quantize_x_rows(x, m, H, xquant, blockIdx.x - n_dot);
+        }
+        return;
+    }
     // rows between the 16-lane groups of one wave (q = 0..3): x rows differ when qm does
     constexpr int DX = QE >= 4 ? 0 : RM * (QE == 1 ? 1 : 0) + (QE == 2 ? RM : 0);
     constexpr int DW = QE == 1 ? 0 : RE;
@@ -140,7 +160,8 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
     __shared__ __align__(16) float xs[NB][TM][XK];
     __shared__ __align__(16) float wsm[NB][TE][WK];
     const uint32_t tid = threadIdx.x, j = tid % 16, q = tid / 16, qm = q / QE, qe = q % QE;
-    const uint32_t m0 = blockIdx.y * TM, e0 = blockIdx.x * TE;
+    const uint32_t tiles_e = (E + TE - 1) / TE, bx = blockIdx.x - n_aux;
+    const uint32_t m0 = (bx / tiles_e) * TM, e0 = (bx % tiles_e) * TE;
 
     // staging: TM rows of x and TE rows of the router, KC columns each, as float4 along k
     constexpr int XV = TM * KC / 4, WV = TE * KC / 4;  // float4 per chunk
@@ -254,10 +275,12 @@ static const GemmCfg kGemmCfg[] = {{256, 128, 1}, {64, 256, 5}, {0, 512, 2}, {0,
 
 template <int RM, int RE, int QM, int KC, bool DB>
 static void launch_gemm_cfg(const float* router, const float* bias, const float* x, uint32_t m, uint32_t E,
-                            uint32_t H, float* rlog, hipStream_t st) {
+                            uint32_t H, float* rlog, const float* shg, float* sh, const XQuant& xq,
+                            uint32_t n_dot, uint32_t n_aux, hipStream_t st) {
     constexpr uint32_t TM = QM * RM, TE = (16 / QM) * RE;
-    router_gemm_kernel<RM, RE, QM, KC, DB><<<dim3((E + TE - 1) / TE, (m + TM - 1) / TM), 256, 0, st>>>(
-            router, bias, x, m, E, H, rlog);
+    const uint32_t tiles = ((E + TE - 1) / TE) * ((m + TM - 1) / TM);
+    router_gemm_kernel<RM, RE, QM, KC, DB><<<n_aux + tiles, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shg, sh, xq,
+                                                                         n_dot, n_aux);
 }
 
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
@@ -278,19 +301,17 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
                 id = c.id;
                 break;
             }
+        // ahead of the tiles: the shared gate's logit (a wave per DOT_MR rows) and x's quantisation
+        const uint32_t n_dot = shexp_gate ? (chunks + 3) / 4 : 0u;
+        const uint32_t n_aux = n_dot + (xquant ? (m * (H / 32) * 4 + 255) / 256 : 0u);
+        const XQuant& xq = xquant ? *xquant : none;
         switch (id) {
-            case 1: launch_gemm_cfg<4, 4, 4, 128, true>(router, bias, x, m, E, H, rlog, st); break;
-            case 2: launch_gemm_cfg<1, 2, 16, 512, false>(router, bias, x, m, E, H, rlog, st); break;
-            case 5: launch_gemm_cfg<4, 2, 4, 256, true>(router, bias, x, m, E, H, rlog, st); break;
-            default: launch_gemm_cfg<1, 2, 16, 128, true>(router, bias, x, m, E, H, rlog, st); break;
-        }
-        if (shexp_gate)  // the shared gate always uses dot (exec_batch.rs:1520)
-            router_dot_kernel<<<dim3(1, chunks), 64, 0, st>>>(router, nullptr, shexp_gate, x, m, 0, H, rlog, sh,
-                                                              none, 1);
-        if (xquant) {  // a grid of its own: riding on the chunked dot grid would replicate it
-            const uint32_t qwgs = (m * (H / 32) * 4 + 127) / 128;
-            router_dot_kernel<<<dim3(qwgs, 1), 128, 0, st>>>(nullptr, nullptr, nullptr, x, m, 0, H, nullptr, nullptr,
-                                                             *xquant, 0);
+#define GEMM_ARGS router, bias, x, m, E, H, rlog, shexp_gate, sh, xq, n_dot, n_aux, st
+            case 1: launch_gemm_cfg<4, 4, 4, 128, true>(GEMM_ARGS); break;
+            case 2: launch_gemm_cfg<1, 2, 16, 512, false>(GEMM_ARGS); break;
+            case 5: launch_gemm_cfg<4, 2, 4, 256, true>(GEMM_ARGS); break;
+            default: launch_gemm_cfg<1, 2, 16, 128, true>(GEMM_ARGS); break;
+#undef GEMM_ARGS
         }
     }
     return hipGetLastError();
