@@ -80,15 +80,37 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 // entry's strip and the weight fold, 16 lanes per entry.
 template <int NSB>
 __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate, Mat up, Mat shg, Mat shu,
-                                                                       Workspace ws, uint32_t max_rows) {
-    constexpr uint32_t H = NSB * 256, nb = NSB * 8, XSB = 256 + 16, XP = NSB * XSB, RPW = 64 / NSB;
+                                                                       Workspace ws, uint32_t max_rows,
+                                                                       uint32_t xall) {
+    constexpr uint32_t H = NSB * 256, nb = NSB * 8, XSB = 256 + 16, XP = NSB * XSB, RPW = 64 / NSB, PPR = H / 16;
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
+    // xall (a batch of xall <= 16 tokens): every token's x is staged, its loads issued before the
+    // item is known (at most XV pieces and XS scales per thread, checked by the host)
+    constexpr int XV = 8, XS = 4;
+    constexpr uint32_t SCH = 4;  // entry rows staged per pass otherwise
+    v4u xv[XV];
+    float xsv[XS], xuv[XS];
+    if (xall) {
+        const uint32_t np = xall * PPR, ns = xall * nb;
+#pragma unroll
+        for (int c = 0; c < XV; c++) {
+            const uint32_t i = tid + nthr * c, ic = i < np ? i : np - 1;
+            xv[c] = *reinterpret_cast<const v4u*>(ws.xq + (size_t)(ic / PPR) * H + (ic % PPR) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < XS; c++) {
+            const uint32_t i = tid + nthr * c, ic = i < ns ? i : ns - 1;
+            xsv[c] = ws.xs[ic];
+            xuv[c] = ws.xu[ic];
+        }
+    }
     Item item;
     if (!stream_item(ws, blockIdx.y, max_rows, item)) return;
-    const uint32_t F = gate.rows, nbf = F / 16, strip = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t F = gate.rows, nbf = F / 16, strip = blockIdx.x;
     const bool shared = item.expert == NO_EXPERT;
     const uint32_t nr = item.nrows, e = shared ? 0u : item.expert;
 
-    // this lane's weights first: they do not depend on anything staged below
+    // this lane's weights next: they depend on the item only
     const uint32_t ln = tid % 64, sb = ln % NSB;
     const uint32_t r = ln < RPW * NSB ? (tid / 64) * RPW + ln / NSB : 32u;
     const bool wthread = r < 32;
@@ -104,17 +126,41 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate
     for (int i = 0; i < 9; i++) wq[i] = wp[i];
 
     extern __shared__ __align__(16) uint8_t smem[];
-    int8_t* xq = (int8_t*)smem;                 // [nr][NSB][XSB]
-    float* xs = (float*)(smem + nr * XP);       // [nr][nb]
-    float* xu = xs + nr * nb;                   // [nr][nb]
-    float* hres = xu + nr * nb;                 // [nr][32]
-    uint32_t* tok = (uint32_t*)(hres + nr * 32);  // [nr]
-    if (tid < nr) tok[tid] = item_token(ws, item, shared, tid);
-    __syncthreads();
-    stage_rows<true>(ws.xq, ws.xs, ws.xu, tok, nr, H, nb, XP, xq, xs, xu, tid, nthr);
-    __syncthreads();
+    // staged activation rows: every token's (xall), else the item's entries SCH at a time
+    const uint32_t R = xall ? xall : (nr < SCH ? nr : SCH);
+    int8_t* xq = (int8_t*)smem;                   // [R][NSB][XSB]
+    float* xs = (float*)(smem + R * XP);          // [R][nb]
+    float* xu = xs + R * nb;                      // [R][nb]
+    float* hres = xu + R * nb;                    // [nr][32]
+    uint32_t* xrow = (uint32_t*)(hres + nr * 32);  // [nr] staged row of entry i
+    uint32_t* xtok = xrow + nr;                    // [nr] its token
+    if (tid < nr) {
+        const uint32_t t = item_token(ws, item, shared, tid);
+        xrow[tid] = xall ? t : tid;
+        xtok[tid] = t;
+    }
+    if (xall) {
+        const uint32_t np = xall * PPR, ns = xall * nb;
+#pragma unroll
+        for (int c = 0; c < XV; c++) {
+            const uint32_t i = tid + nthr * c;
+            if (i < np) {
+                const uint32_t o = (i % PPR) * 16;
+                *reinterpret_cast<v4u*>(xq + (i / PPR) * XP + o + (o / 256) * 16) = xv[c];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < XS; c++) {
+            const uint32_t i = tid + nthr * c;
+            if (i < ns) {
+                xs[i] = xsv[c];
+                xu[i] = xuv[c];
+            }
+        }
+        __syncthreads();
+    }
 
-    // (dd, mm) of the superblock's 8 sub-blocks and its nibbles, unpacked once for all entries
+    // (dd, mm) of the superblock's 8 sub-blocks
     const float d = h2f((uint16_t)(wq[0].x & 0xffff)), dmin = h2f((uint16_t)(wq[0].x >> 16));
     float ddv[8], mmv[8];
 #pragma unroll
@@ -123,21 +169,19 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate
         q4k_scale_min_w(wq[0].y, wq[0].z, wq[0].w, j, sc, mn);
         q4k_dm(d, dmin, sc, mn, ddv[j], mmv[j]);
     }
-    v4u nq[16];  // [sub-block 2c + h][word pair]: nibble h of qs words 8c .. 8c + 7
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int w = 0; w < 8; w++) nq[(2 * c + h) * 2 + w / 4][w % 4] = nib(wq[1 + 2 * c + w / 4][w % 4], h);
 
     // entries i0 .. i0 + NE - 1 (clamped to nr - 1; a clamped entry's result is not stored)
-    auto run = [&](auto ne_tag, uint32_t i0) {
+    auto run = [&](auto ne_tag, uint32_t i0, uint32_t c0) {
         constexpr int NE = decltype(ne_tag)::value;
+        // the nibbles are extracted per pass, not hoisted out of the entry loop (64 more registers)
+#pragma unroll
+        for (int i = 1; i < 9; i++) asm volatile("" : "+v"(wq[i]));
         float dotv[NE][8], tv[NE][8], uv[NE][8];
 #pragma unroll
         for (int n = 0; n < NE; n++) {
-            const uint32_t i = i0 + n < nr ? i0 + n : nr - 1;
+            // staged row (read from LDS: an index the compiler cannot fold keeps it from hoisting
+            // every entry's x reads ahead, and the registers with them)
+            const uint32_t ie = i0 + n < nr ? i0 + n : i0, i = xrow[ie] - (xall ? 0u : c0);
             const float4* s4 = reinterpret_cast<const float4*>(xs + i * nb + sb * 8);
             const float4* u4 = reinterpret_cast<const float4*>(xu + i * nb + sb * 8);
             const float4 s0 = s4[0], s1 = s4[1], u0 = u4[0], u1 = u4[1];
@@ -157,8 +201,9 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate
                 int d0 = 0, d1 = 0;
 #pragma unroll
                 for (int w = 0; w < 8; w++) {
-                    d0 = sdot4((int)nq[(2 * c) * 2 + w / 4][w % 4], xl[w], d0);
-                    d1 = sdot4((int)nq[(2 * c + 1) * 2 + w / 4][w % 4], xh[w], d1);
+                    const uint32_t qw = wq[1 + 2 * c + w / 4][w % 4];
+                    d0 = sdot4((int)nib(qw, 0), xl[w], d0);
+                    d1 = sdot4((int)nib(qw, 1), xh[w], d1);
                 }
                 dotv[n][2 * c] = (float)d0;
                 dotv[n][2 * c + 1] = (float)d1;
@@ -191,9 +236,19 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate
             for (int n = 0; n < NE; n++)
                 if (i0 + n < nr) hres[(i0 + n) * 32 + r] = acc[n];
     };
-    uint32_t i0 = 0;
-    for (; i0 + 1 < nr; i0 += 2) run(std::integral_constant<int, 2>{}, i0);
-    if (i0 < nr) run(std::integral_constant<int, 1>{}, i0);
+#pragma nounroll
+    for (uint32_t c0 = 0; c0 < nr; c0 += R) {  // one pass when xall or nr <= SCH
+        const uint32_t c1 = nr - c0 < R ? nr : c0 + R;
+        if (!xall) {
+            __syncthreads();  // xtok written; the previous chunk's rows read
+            stage_rows<true>(ws.xq, ws.xs, ws.xu, xtok + c0, c1 - c0, H, nb, XP, xq, xs, xu, tid, nthr);
+            __syncthreads();
+        }
+        uint32_t i0 = c0;
+#pragma nounroll
+        for (; i0 + 1 < c1; i0 += 2) run(std::integral_constant<int, 2>{}, i0, c0);
+        if (i0 < c1) run(std::integral_constant<int, 1>{}, i0, c0);
+    }
     __syncthreads();
 
     // SwiGLU (elem.rs:173), per-16 quantisation of the strip (16 lanes = one DPP row per entry)
@@ -326,12 +381,20 @@ uint32_t grouped_item_rows(const Workspace& ws, uint32_t m) { return item_rows(w
 hipError_t launch_stream_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
                                 const Workspace& ws, uint32_t m, uint32_t max_rows, hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nsb = H / 256, nb = H / 32;
-    const size_t cap = max_rows < BR ? max_rows : BR;
-    const size_t lds = cap * ((size_t)nsb * 272 + (size_t)nb * 8 + 32 * 4 + 4);
+    const size_t cap = max_rows < BR ? max_rows : BR;  // rows of an item here
+    // up to 4 tokens every token's x is staged up front (within the kernel's register budget for
+    // it: 8 pieces and 4 scales per thread)
+    uint32_t xall = m <= 4 ? m : 0u;
+    const uint32_t threads = GU_THREADS(nsb);
+    if ((size_t)xall * (H / 16) > 8u * threads || (size_t)xall * nb > 4u * threads) xall = 0;
+    const size_t rows = xall ? xall : (cap < 4 ? cap : 4);  // staged rows (4 per pass: SCH)
+    const size_t lds = rows * ((size_t)nsb * 272 + (size_t)nb * 8) + cap * (32 * 4 + 8);
     const dim3 grid(F / 16, item_rows(ws, m));
     switch (nsb) {
-#define SG_CASE(n) \
-    case n: stream_gateup_kernel<n><<<grid, GU_THREADS(n), lds, st>>>(gate, up, sh_gate, sh_up, ws, max_rows); break;
+#define SG_CASE(n)                                                                                      \
+    case n:                                                                                             \
+        stream_gateup_kernel<n><<<grid, GU_THREADS(n), lds, st>>>(gate, up, sh_gate, sh_up, ws, max_rows, xall); \
+        break;
         SG_CASE(1) SG_CASE(2) SG_CASE(3) SG_CASE(4) SG_CASE(5) SG_CASE(6) SG_CASE(7) SG_CASE(8)
 #undef SG_CASE
         default: return hipErrorInvalidValue;
