@@ -443,6 +443,51 @@ __device__ __forceinline__ void stage_a(const int8_t* __restrict__ src_rows, con
     }
 }
 
+// ---- gate/up on v_mfma_i32_16x16x64_i8 ------------------------------------------------------
+//
+// A Q4_K superblock's 128 qs bytes are chunk pairs p = 0, 1 of 64 bytes (sub-blocks 4p .. 4p+3:
+// chunk 2p holds 4p / 4p+1 in its low / high nibbles, chunk 2p+1 holds 4p+2 / 4p+3).  Lane (g, r)
+// loads the 16 bytes 64p + 16g .. +15 of row r: the four lanes of a row read 64 contiguous bytes
+// (one 16-byte load each) instead of four scattered 8-byte pieces.  Its low nibbles are 16 values
+// of sub-block 4p + 2 (g / 2), at positions 16 (g % 2) ..; the high nibbles those of the next
+// sub-block.  One 64-wide MFMA per sub-block, with the activation operand zero in the lanes of the
+// other chunk, gives each 32-block's exact dot on its own: the pairing of A and B elements within
+// a lane is all the dot depends on.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i mfma_i8_64(v4i_t a, v4i_t b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
+}
+struct Q4Sb16 {
+    uint4 hdr;
+    v4i_t q[2];  // chunk pair p: bytes 64p + 16g .. +15
+};
+__device__ __forceinline__ void load_q4sb16(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q4Sb16& w) {
+    const uint8_t* p = rowp + sb * 144;
+    w.hdr = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int c = 0; c < 2; c++) w.q[c] = *reinterpret_cast<const v4i_t*>(p + 16 + 64 * c + 16 * g);
+}
+// Activation rows staged as [block][half][row] 16-byte pieces: lane (g, r) reads half g % 2 of a
+// block of entry row r.
+__device__ __forceinline__ void stage_a16(const int8_t* __restrict__ src_rows, const uint32_t* rowoff, uint32_t K,
+                                          v4i_t* As, uint32_t tid) {
+    const uint32_t pieces = K / 16;  // 16-byte pieces per row = (block, half)
+    for (uint32_t i0 = 0; i0 < 16 * pieces; i0 += 2048) {
+        v4i_t v[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * pieces ? i : 16 * pieces - 1;
+            v[c] = *reinterpret_cast<const v4i_t*>(src_rows + (size_t)rowoff[ic / pieces] + (ic % pieces) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + 256 * c;
+            if (i < 16 * pieces) As[(i % pieces) * 16 + i / pieces] = v[c];
+        }
+    }
+}
+
 constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table (16 + 1 against bank conflicts)
 
 // gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
@@ -463,7 +508,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     const uint32_t e = shared ? 0u : item.expert;
 
     extern __shared__ __align__(16) uint8_t smem[];
-    long* As = reinterpret_cast<long*>(smem);                        // [nb][64]
+    v4i_t* As = reinterpret_cast<v4i_t*>(smem);                      // [nb][2 halves][16 rows]
     float* Sx = reinterpret_cast<float*>(smem + nb * 64 * 8);        // [nb][16] activation scales
     float* Su = Sx + nb * 16;                                        // [nb][16] scale * sum
     float2* Dm = reinterpret_cast<float2*>(Su + nb * 16);            // [4 waves][2][16][DM_STRIDE]
@@ -476,7 +521,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
         rowoff[tid] = tok * H;
     }
     __syncthreads();
-    stage_a(ws.xq, rowoff, H, As, tid);
+    stage_a16(ws.xq, rowoff, H, As, tid);
     for (uint32_t i0 = 0; i0 < 16 * nb; i0 += 1024) {
         float a[4], c2[4];
 #pragma unroll
@@ -512,22 +557,24 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
         rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + r) * G.row_bytes;
         ru = U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + r) * U.row_bytes;
     };
-    Q4Sb cg, cu;
+    Q4Sb16 cg, cu;
     {
         const uint8_t *rg, *ru;
         rows_of(0, rg, ru);
-        load_q4sb(rg, 0, g, cg);
-        load_q4sb(ru, 0, g, cu);
+        load_q4sb16(rg, 0, g, cg);
+        load_q4sb16(ru, 0, g, cu);
     }
     float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const v4i_t zero4 = {0, 0, 0, 0};
+    const bool first = g < 2;  // this lane's bytes are of the pair's first chunk
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
-        Q4Sb ng = cg, nu = cu;
+        Q4Sb16 ng = cg, nu = cu;
         if (step + 1 < nstep) {  // the next superblock's loads go out before this one's math
             const uint8_t *rg, *ru;
             rows_of(step + 1, rg, ru);
-            load_q4sb(rg, (step + 1) % NSB, g, ng);
-            load_q4sb(ru, (step + 1) % NSB, g, nu);
+            load_q4sb16(rg, (step + 1) % NSB, g, ng);
+            load_q4sb16(ru, (step + 1) % NSB, g, nu);
         }
         // (dd, mm) of sub-blocks 2g, 2g+1 of row r, gate then up
         wave_sync();
@@ -539,21 +586,41 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
         }
         wave_sync();
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t B = sb * 8 + j;
-            const long a = As[B * 64 + lane];
-            const v4i dg = mfma_i8(a, unpack8(cg.qs[j / 2], j % 2));
-            const v4i du = mfma_i8(a, unpack8(cu.qs[j / 2], j % 2));
-            const float2 mg = dmw[r * DM_STRIDE + j], mu = dmw[(16 + r) * DM_STRIDE + j];
-            const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + 4 * g);
-            const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + 4 * g);
-            const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
+        for (int pp = 0; pp < 2; pp++) {
+            // this lane's activation halves: sub-blocks 4pp + 2 (g / 2) (low nibbles) and the next
+            const uint32_t bl = sb * 8 + 4 * pp + (first ? 0u : 2u);
+            const v4i_t al = As[(bl * 2 + g % 2) * 16 + r], ah = As[((bl + 1) * 2 + g % 2) * 16 + r];
+            const v4i_t wgl = cg.q[pp] & 0x0f0f0f0f, wgh = (cg.q[pp] >> 4) & 0x0f0f0f0f;
+            const v4i_t wul = cu.q[pp] & 0x0f0f0f0f, wuh = (cu.q[pp] >> 4) & 0x0f0f0f0f;
+            v4i dgv[4], duv[4];  // sub-blocks 4pp + 0..3
+            {
+                const v4i_t a0 = first ? al : zero4, a2 = first ? zero4 : al;
+                const v4i_t a1 = first ? ah : zero4, a3 = first ? zero4 : ah;
+                dgv[0] = mfma_i8_64(a0, wgl);
+                duv[0] = mfma_i8_64(a0, wul);
+                dgv[1] = mfma_i8_64(a1, wgh);
+                duv[1] = mfma_i8_64(a1, wuh);
+                dgv[2] = mfma_i8_64(a2, wgl);
+                duv[2] = mfma_i8_64(a2, wul);
+                dgv[3] = mfma_i8_64(a3, wgh);
+                duv[3] = mfma_i8_64(a3, wuh);
+            }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
-                accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
-                accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
-                accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
-                accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * pp + jj;
+                const uint32_t B = sb * 8 + j;
+                const v4i dg = dgv[jj], du = duv[jj];
+                const float2 mg = dmw[r * DM_STRIDE + j], mu = dmw[(16 + r) * DM_STRIDE + j];
+                const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + 4 * g);
+                const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + 4 * g);
+                const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
+                    accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
+                    accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
+                    accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
+                    accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
+                }
             }
         }
         cg = ng;
