@@ -237,11 +237,11 @@ def test_dynamic_k_policy(M):
     ctx.close()
 
 
-@pytest.mark.parametrize("M,rows", [(1, -1), (6, -1), (6, 0), (40, 16)])
+@pytest.mark.parametrize("M,rows", [(1, -1), (6, -1), (6, 0), (40, 16), (80, 0)])
 def test_q6k_down(M, rows):
     say(f"q6k down M={M} stream rows {rows}")
     L, orc, W = layer("q6", seed=4, H=512, E=16, F=256, down_fmt=O.FMT_Q6_K)
-    ctx = trmoe.Context(L.H, L.E, L.F, 3, 64)
+    ctx = trmoe.Context(L.H, L.E, L.F, 3, max(64, M))
     ctx.set_stream_rows(rows)
     import torch
     x = L.x(M, tid=400)

@@ -693,12 +693,22 @@ __device__ __forceinline__ uint32_t ld32_a2(const uint8_t* p) {
     return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
 }
 __device__ __forceinline__ uint2 ld64_a2(const uint8_t* p) { return make_uint2(ld32_a2(p), ld32_a2(p + 4)); }
+// 8 bytes at p + o (p 2-byte aligned) from one 12-byte load at the 4-byte boundary below, shifted
+// by the superblock's misalignment (0 or 2 bytes; the load stays inside the superblock when
+// 2 <= o + 12 - shift <= 210 and o >= shift, as for every ql / qh piece)
+__device__ __forceinline__ uint2 ld64_sh(const uint8_t* pa, uint32_t o, uint32_t sh) {
+    typedef uint32_t v3u __attribute__((ext_vector_type(3)));
+    const v3u v = *reinterpret_cast<const v3u*>(pa + o);
+    return make_uint2(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh));
+}
 __device__ __forceinline__ void load_q6sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q6Sb& w) {
     const uint8_t* p = rowp + sb * 210;
+    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;  // 0 or 2
+    const uint8_t* pa = p - sh;
 #pragma unroll
-    for (int i = 0; i < 4; i++) w.ql[i] = ld64_a2(p + 64 * (i / 2) + 32 * (i % 2) + 8 * g);
+    for (int i = 0; i < 4; i++) w.ql[i] = ld64_sh(pa, 64 * (i / 2) + 32 * (i % 2) + 8 * g, sh);
 #pragma unroll
-    for (int n = 0; n < 2; n++) w.qh[n] = ld64_a2(p + 128 + 32 * n + 8 * g);
+    for (int n = 0; n < 2; n++) w.qh[n] = ld64_sh(pa, 128 + 32 * n + 8 * g, sh);
     w.sc = ld32_a2(p + 192 + 4 * g);
     w.d = *reinterpret_cast<const uint16_t*>(p + 208);
 }
