@@ -722,6 +722,93 @@ __device__ __forceinline__ long q6_operand(const Q6Sb& w, int q8) {
     return (long)(((unsigned long long)(l1 | (h1 << 4)) << 32) | (l0 | (h0 << 4)));
 }
 
+__device__ __forceinline__ v4i mfma_i8_acc(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Q4_K down for items of at most 16 / S rows: S strips share one 16x16 MFMA output.  The rows of
+// A are split into S slots of R = 16 / S; strip s's MFMA sees the item's activation rows in slot s
+// and zeros elsewhere, and the S products of a chunk accumulate into one output.  Output row
+// 4g + i then holds strip 4g / R (of the S) at activation row (4g + i) % R, so lane (g, r) ends
+// with R-row strip g * S / 4 of weight row r, and the f32 epilogue (the VALU bound of this
+// kernel) runs once for S strips instead of once per strip.  Each lane streams the k-group g
+// pieces of its row in all S strips and the header of its own strip, whose (dd, mm) it decodes
+// itself, chunk by chunk.
+template <int NSB, int S>
+__device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const Item& item, uint32_t arow0, uint32_t H,
+                                               const long* As, const float* Sx, const float* Su, const Workspace& ws,
+                                               uint32_t wv, uint32_t lane, uint32_t strips) {
+    constexpr uint32_t R = 16 / S;
+    const uint32_t g = lane / 16, r = lane % 16;
+    const uint32_t own = g * S / 4, orow = (4 * g) % R;  // output strip (of the S) and first act row
+    const uint32_t arl = r % R, sel = r / R;             // act row this lane feeds A, and for which strip
+    const uint32_t nstep = (strips / 4 / S) * NSB;
+    auto row_of = [&](uint32_t step, uint32_t s) -> const uint8_t* {
+        const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + s);
+        return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
+    };
+    struct W {
+        uint4 hdr;
+        uint2 qs[S][4];
+    };
+    auto load = [&](uint32_t step, W& w) {
+        const uint32_t sb = step % NSB;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const uint8_t* p = row_of(step, s) + sb * 144;
+#pragma unroll
+            for (int c = 0; c < 4; c++) w.qs[s][c] = *reinterpret_cast<const uint2*>(p + 16 + 32 * c + 8 * g);
+        }
+        w.hdr = *reinterpret_cast<const uint4*>(row_of(step, own) + sb * 144);
+    };
+    W cw;
+    load(0, cw);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const v4i z = {0, 0, 0, 0};
+    for (uint32_t step = 0; step < nstep; step++) {
+        const uint32_t sb = step % NSB;
+        W nw = cw;
+        if (step + 1 < nstep) load(step + 1, nw);
+#pragma unroll
+        for (int q8 = 0; q8 < 8; q8++) {
+            const uint32_t q = sb * 8 + q8;
+            const long af = As[q * 64 + g * 16 + arl];
+            const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
+            v4i c0 = z, c1 = z;
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const long bw = unpack8(cw.qs[s][q8 / 2], q8 % 2);
+                c0 = mfma_i8_acc(sel == (uint32_t)s ? alo : 0l, bw, c0);
+                c1 = mfma_i8_acc(sel == (uint32_t)s ? ahi : 0l, bw, c1);
+            }
+            const float2 dm = q4k_dm_rt(cw.hdr, q8);  // sub-block q8 = 16-blocks 2 q8, 2 q8 + 1
+            const float4 s0 = *reinterpret_cast<const float4*>(Sx + (2 * q) * 16 + orow);
+            const float4 u0 = *reinterpret_cast<const float4*>(Su + (2 * q) * 16 + orow);
+            const float4 s1 = *reinterpret_cast<const float4*>(Sx + (2 * q + 1) * 16 + orow);
+            const float4 u1 = *reinterpret_cast<const float4*>(Su + (2 * q + 1) * 16 + orow);
+            const float s0a[4] = {s0.x, s0.y, s0.z, s0.w}, u0a[4] = {u0.x, u0.y, u0.z, u0.w};
+            const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[i] = __builtin_fmaf(dm.y, u0a[i], acc[i]);
+                acc[i] = __builtin_fmaf((float)c0[i], dm.x * s0a[i], acc[i]);
+                acc[i] = __builtin_fmaf(dm.y, u1a[i], acc[i]);
+                acc[i] = __builtin_fmaf((float)c1[i], dm.x * s1a[i], acc[i]);
+            }
+        }
+        cw = nw;
+        if (sb == NSB - 1) {
+            const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + own);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t row = orow + i;
+                if (row < item.nrows) ws.yent[(size_t)(arow0 + row) * H + strip * 16 + r] = acc[i];
+                acc[i] = 0.0f;
+            }
+        }
+    }
+}
+
 template <int NSB, bool Q6>
 __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
@@ -766,9 +853,20 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     }
     __syncthreads();
 
+    const uint32_t strips = H / 16 / gridDim.x;
+    if constexpr (!Q6) {
+        // small items: several strips per MFMA output (a wave owns strips / 4 strips)
+        if (item.nrows <= 4 && strips % 16 == 0) {
+            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips);
+            return;
+        }
+        if (item.nrows <= 8 && strips % 8 == 0) {
+            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips);
+            return;
+        }
+    }
     const uint32_t g = lane / 16, r = lane % 16;
     float2* dmw = Dm + wv * 16 * DM_STRIDE;
-    const uint32_t strips = H / 16 / gridDim.x;
     const uint32_t nstep = (strips / 4) * NSB;
     auto row_of = [&](uint32_t step) -> const uint8_t* {
         const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
