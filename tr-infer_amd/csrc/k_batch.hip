@@ -490,6 +490,133 @@ __device__ __forceinline__ void stage_a16(const int8_t* __restrict__ src_rows, c
 
 constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table (16 + 1 against bank conflicts)
 
+__device__ __forceinline__ v4i mfma_i8_64_acc(v4i_t a, v4i_t b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// gate/up for items of at most 16 / S rows, S strips per MFMA output: the activation rows split
+// into S slots of R = 16 / S rows as in the down kernel's down_strips_q4.  Lane (g, r) ends with
+// strip g * S / 4 (of the S) of weight row r at activation rows (4g) % R .. +3; the 16 lanes of
+// one lane group still hold one strip's 16 weight rows, so the per-16 requantisation reduces
+// across the same lanes as with one strip.
+template <int NSB, int S>
+__device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32_t e, const Item& item, bool shared,
+                                              uint32_t n_ent, uint32_t F, const v4i_t* As, const float* Sx,
+                                              const float* Su, const Workspace& ws, uint32_t wv, uint32_t lane,
+                                              uint32_t strips) {
+    constexpr uint32_t R = 16 / S;
+    const uint32_t g = lane / 16, r = lane % 16, nbf = F / 16;
+    const uint32_t own = g * S / 4, orow = (4 * g) % R;
+    const uint32_t arl = r % R, sel = r / R;
+    const uint32_t nstep = (strips / 4 / S) * NSB;
+    float wgt[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = orow + i < item.nrows ? orow + i : 0u;
+        wgt[i] = shared ? sigmoid_libm(ws.shl[item.row0 + row]) : ws.ent_w[item.row0 + row];
+    }
+    auto rowp = [&](const Mat& M, uint32_t step, uint32_t s) -> const uint8_t* {
+        const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + s);
+        return M.ptr + (size_t)e * M.stride + (size_t)(strip * 16 + r) * M.row_bytes + (step % NSB) * 144;
+    };
+    struct W {
+        uint4 hg, hu;
+        v4i_t qg[S][2], qu[S][2];
+    };
+    auto load = [&](uint32_t step, W& w) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const uint8_t* pg = rowp(G, step, s);
+            const uint8_t* pu = rowp(U, step, s);
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                w.qg[s][c] = *reinterpret_cast<const v4i_t*>(pg + 16 + 64 * c + 16 * g);
+                w.qu[s][c] = *reinterpret_cast<const v4i_t*>(pu + 16 + 64 * c + 16 * g);
+            }
+        }
+        w.hg = *reinterpret_cast<const uint4*>(rowp(G, step, own));
+        w.hu = *reinterpret_cast<const uint4*>(rowp(U, step, own));
+    };
+    W cw;
+    load(0, cw);
+    float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const v4i_t zero4 = {0, 0, 0, 0};
+    const v4i z = {0, 0, 0, 0};
+    const bool first = g < 2;
+    for (uint32_t step = 0; step < nstep; step++) {
+        const uint32_t sb = step % NSB;
+        W nw = cw;
+        if (step + 1 < nstep) load(step + 1, nw);
+#pragma unroll
+        for (int pp = 0; pp < 2; pp++) {
+            const uint32_t bl = sb * 8 + 4 * pp + (first ? 0u : 2u);
+            const v4i_t al = As[(bl * 2 + g % 2) * 16 + arl], ah = As[((bl + 1) * 2 + g % 2) * 16 + arl];
+            const v4i_t a0 = first ? al : zero4, a2 = first ? zero4 : al;
+            const v4i_t a1 = first ? ah : zero4, a3 = first ? zero4 : ah;
+            v4i dgv[4] = {z, z, z, z}, duv[4] = {z, z, z, z};
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const bool m = sel == (uint32_t)s;
+                const v4i_t b0 = m ? a0 : zero4, b1 = m ? a1 : zero4, b2 = m ? a2 : zero4, b3 = m ? a3 : zero4;
+                const v4i_t wgl = cw.qg[s][pp] & 0x0f0f0f0f, wgh = (cw.qg[s][pp] >> 4) & 0x0f0f0f0f;
+                const v4i_t wul = cw.qu[s][pp] & 0x0f0f0f0f, wuh = (cw.qu[s][pp] >> 4) & 0x0f0f0f0f;
+                dgv[0] = mfma_i8_64_acc(b0, wgl, dgv[0]);
+                duv[0] = mfma_i8_64_acc(b0, wul, duv[0]);
+                dgv[1] = mfma_i8_64_acc(b1, wgh, dgv[1]);
+                duv[1] = mfma_i8_64_acc(b1, wuh, duv[1]);
+                dgv[2] = mfma_i8_64_acc(b2, wgl, dgv[2]);
+                duv[2] = mfma_i8_64_acc(b2, wul, duv[2]);
+                dgv[3] = mfma_i8_64_acc(b3, wgh, dgv[3]);
+                duv[3] = mfma_i8_64_acc(b3, wuh, duv[3]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * pp + jj;
+                const uint32_t B = sb * 8 + j;
+                const v4i dg = dgv[jj], du = duv[jj];
+                const float2 mg = q4k_dm_rt(cw.hg, j), mu = q4k_dm_rt(cw.hu, j);
+                const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + orow);
+                const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + orow);
+                const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
+                    accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
+                    accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
+                    accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
+                    accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
+                }
+            }
+        }
+        cw = nw;
+        if (sb == NSB - 1) {
+            const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + own);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t row = orow + i;
+                const float v = silu512(accg[i]) * accu[i];
+                const float amax =
+                        row16_allreduce(__builtin_fabsf(v), [](float x, float y) { return mx_ps(x, y); });
+                const float sc = amax / 127.0f;
+                const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+                const int32_t qi = cvt_rne(v * inv);
+                const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
+                if (row < item.nrows) {
+                    const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
+                    ws.actq[(size_t)arow * F + strip * 16 + r] = sat_i8(qi);
+                    if (r == 0) {
+                        const float sf = sc * wgt[i];  // exec_batch.rs:1533-1535
+                        ws.acts[(size_t)arow * nbf + strip] = sf;
+                        ws.actsum[(size_t)arow * nbf + strip] = sum;
+                        ws.actu[(size_t)arow * nbf + strip] = sf * (float)sum;
+                    }
+                }
+                accg[i] = 0.0f;
+                accu[i] = 0.0f;
+            }
+        }
+    }
+}
+
 // gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
 // Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.
 template <int NSB>
@@ -539,6 +666,12 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
             }
         }
     }
+    const uint32_t strips = F / 16 / gridDim.x;  // per workgroup
+    if (item.nrows <= 8 && strips % 8 == 0) {
+        __syncthreads();
+        gateup_strips<NSB, 2>(G, U, e, item, shared, n_ent, F, As, Sx, Su, ws, wv, lane, strips);
+        return;
+    }
     const uint32_t g = lane / 16, r = lane % 16;
     // routing weight of this lane's four entry rows (exec_batch.rs:1533-1535; shared: the gate)
     float wgt[4];
@@ -550,7 +683,6 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     __syncthreads();
 
     float2* dmw = Dm + wv * 2 * 16 * DM_STRIDE;
-    const uint32_t strips = F / 16 / gridDim.x;  // per workgroup
     const uint32_t nstep = (strips / 4) * NSB;   // (strip, superblock) steps of this wave
     auto rows_of = [&](uint32_t step, const uint8_t*& rg, const uint8_t*& ru) {
         const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
