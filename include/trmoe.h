@@ -112,7 +112,9 @@ int trk_moe_forward(trk_ctx *ctx, const trk_moe_w *w, const float *x, const floa
                     float *out, void *stream);
 
 /* Config-5 layer: h[M][H] += MoE(rmsnorm(h; rms_w, eps)).  Composes elem::rmsnorm
- * (elem.rs:255-262), the MoE block and elem::add_inplace (elem.rs:104-118). */
+ * (elem.rs:255-262), the MoE block and elem::add_inplace (elem.rs:104-118).  Below the router
+ * GEMM threshold (and with the one-launch decode layer off) the logits launch normalises h as it
+ * reads it, with the same bits as a separate rmsnorm; otherwise rmsnorm runs as its own launch. */
 int trk_moe_residual(trk_ctx *ctx, const trk_moe_w *w, const float *rms_w, float eps, float *h,
                      uint32_t m, void *stream);
 

@@ -280,6 +280,30 @@ def test_residual_stack(M):
     ctx.close()
 
 
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_residual_norm_in_logits_launch(M):
+    """Below the router GEMM threshold the config-5 layer normalises h inside the logits launch
+    (no rmsnorm launch); the result has the same bits as rmsnorm into a copy and the layer on it
+    (forced here through the one-launch decode setting, which keeps the separate rmsnorm).
+    M = 16 takes the GEMM-order router and the separate rmsnorm on both sides."""
+    say(f"residual norm fused M={M}")
+    import torch
+    L = Layer(seed=31, H=512, E=16, F=256)
+    W = trmoe.LayerWeights.from_host(L)
+    rms = dev(O.gen_uniform(31, 4, 512, 0.9, 1.1))
+    h0 = L.x(M, tid=520)
+    outs = []
+    for fusion in (False, True):
+        ctx = trmoe.Context(512, 16, 256, 3, 16)
+        ctx.set_fusion(fusion)
+        h = dev(h0.copy())
+        for _ in range(2):
+            ctx.residual(W, rms, 1e-6, h)
+        outs.append(host(h).copy())
+        ctx.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def test_prefill_zipf_full_size_sampled():
     """Config 3 (M = 512, Zipf(1.1) routing) at full size: dispatch bit-exact, properties of the
     grouping, and sampled tokens against the oracle (per-token batch arithmetic, gemm-order logits)."""

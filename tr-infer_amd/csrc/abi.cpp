@@ -275,9 +275,10 @@ static hipError_t timed(trk_ctx* c, int kid, hipStream_t st, F&& launch) {
         if (only < 0 || only == (kid)) HIP_TRY(timed(c, kid, st, [&]() { return (expr); })); \
     } while (0)
 
-// The MoE block on x (already normed).  residual: out += moe instead of out = moe.
+// The MoE block on x (already normed, or normed inside the logits launch when norm is set; only
+// the logits launch reads x).  residual: out += moe instead of out = moe.
 static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m, float* out,
-                   int residual, hipStream_t st, int only = -1) {
+                   int residual, hipStream_t st, int only = -1, const XNorm* norm = nullptr) {
     Mats M;
     int rc = check_weights(c, w, M);
     if (rc) return rc;
@@ -309,10 +310,10 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, pair};
         if (rlog)
             TIMED(K_LOGITS,
-                  launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st, &xq));
+                  launch_router_logits(nullptr, nullptr, w->shexp_gate, x, 1, 0, H, 0, nullptr, ws.shl, st, &xq, norm));
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, 1, E, H, 0, ws.rlog,
-                                                 ws.shl, st, &xq));
+                                                 ws.shl, st, &xq, norm));
         TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
     } else {
@@ -320,10 +321,10 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, 0};
         if (rlog)
             TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st,
-                                                 &xq));
+                                                 &xq, norm));
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
-                                                 ws.rlog, ws.shl, st, &xq));
+                                                 ws.rlog, ws.shl, st, &xq, norm));
         // the dispatch kernel counts the routed rows (one atomic per call, not per token).  Up to 4
         // tokens one launch routes (a wave per token, one per SIMD) and dispatches; up to 16 the
         // routing has a launch of its own (spread over CUs) and the dispatch is the small one
@@ -367,6 +368,12 @@ extern "C" int trk_moe_residual(trk_ctx* c, const trk_moe_w* w, const float* rms
     if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
     hipStream_t st = (hipStream_t)stream;
     const int only = -1;
+    // Below the router GEMM threshold (and off the one-launch decode layer, which reads x itself)
+    // the logits launch normalises h where it reads it: no rmsnorm launch, no normed copy
+    if (!c->fusion && m < c->cfg.router_dot_max_m && w->router) {
+        const XNorm nrm{rms_w, eps};
+        return forward(c, w, h, nullptr, m, h, 1, st, only, &nrm);
+    }
     TIMED(K_RMSNORM, launch_rmsnorm(h, rms_w, eps, m, c->cfg.hidden, c->ws.xn, st));
     return forward(c, w, c->ws.xn, nullptr, m, h, 1, st);
 }

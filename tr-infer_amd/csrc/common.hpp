@@ -131,6 +131,38 @@ __device__ __forceinline__ float rows4_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// 1 / sqrt(mean(x^2) + eps) of one row of n floats, in every lane of the wave (elem.rs:255-262):
+// sumsq (elem.rs:224-252) in the dot order, lane j carrying the chain over elements j + 64 i, the
+// 16-wide tail on lanes 0-15, the scalar tail after the reduction.
+__device__ __forceinline__ float row_rms_inv(const float* __restrict__ xr, uint32_t n, float eps, uint32_t lane) {
+    float acc = 0.0f;
+    uint32_t i = 0;
+    constexpr int U = 16;  // 64-wide steps whose loads are issued together
+    for (; i + 64 * U <= n; i += 64 * U) {
+        float a[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) a[u] = xr[i + 64 * u + lane];
+#pragma unroll
+        for (int u = 0; u < U; u++) acc = __builtin_fmaf(a[u], a[u], acc);
+    }
+    for (; i + 64 <= n; i += 64) {
+        float a = xr[i + lane];
+        acc = __builtin_fmaf(a, a, acc);
+    }
+    for (; i + 16 <= n; i += 16)
+        if (lane < 16) {
+            float a = xr[i + lane];
+            acc = __builtin_fmaf(a, a, acc);
+        }
+    float s = reduce16_lanes(rows4_sum(acc));  // the same value in every lane
+    for (; i < n; i++) s += xr[i] * xr[i];
+    return 1.0f / __builtin_sqrtf(s / (float)n + eps);
+}
+// one element of rmsnorm's output: (x * r) * w, or x * r without weights (elem.rs:259-261)
+__device__ __forceinline__ float rms_apply(float x, float r, const float* __restrict__ w, uint32_t j) {
+    return w ? (x * r) * w[j] : x * r;
+}
+
 // ---- Q4_K / Q6_K superblock decoding ------------------------------------------------------------
 // blocks.py:16-22 (_scale_min_k)
 __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int j, int& sc, int& mn) {

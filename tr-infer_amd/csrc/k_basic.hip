@@ -200,28 +200,8 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     uint32_t lane = threadIdx.x % WAVE;
     if (row >= m) return;
     const float* xr = x + (size_t)row * n;
-    float acc = 0.0f;
-    uint32_t i = 0;
-    constexpr int U = 16;  // 64-wide steps whose loads are issued together
-    for (; i + 64 * U <= n; i += 64 * U) {
-        float a[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) a[u] = xr[i + 64 * u + lane];
-#pragma unroll
-        for (int u = 0; u < U; u++) acc = __builtin_fmaf(a[u], a[u], acc);
-    }
-    for (; i + 64 <= n; i += 64) {
-        float a = xr[i + lane];
-        acc = __builtin_fmaf(a, a, acc);
-    }
-    for (; i + 16 <= n; i += 16)
-        if (lane < 16) {
-            float a = xr[i + lane];
-            acc = __builtin_fmaf(a, a, acc);
-        }
-    float s = reduce16_lanes(rows4_sum(acc));  // the same value in every lane
-    for (; i < n; i++) s += xr[i] * xr[i];
-    float r = 1.0f / __builtin_sqrtf(s / (float)n + eps);
+    const float r = row_rms_inv(xr, n, eps, lane);
+    constexpr int U = 16;
     uint32_t j = lane;
     for (; j + WAVE * (U - 1) < n; j += WAVE * U) {  // loads first, U per lane
         float a[U], b[U];

@@ -49,15 +49,34 @@ __device__ __forceinline__ void quant_block_quad(const float (&v)[8], uint32_t (
 // x quantised per 32 by the workgroups after the logit rows, four lanes per block: one row in
 // pair mode (quantize_pair_blocks, quant.rs:96-108: level 1 at +H / +H/32), else m rows single
 // level (QAct::quantize, quant.rs:76-92, as moe_batch's quant_rows).
+// NORM: x is rmsnorm's input; the workgroup's waves first compute the factors of the rows its
+// blocks fall in (rinv: LDS, one per row, at most blockDim.x / 4 / (H / 32) + 2 rows).
+template <bool NORM = false>
 __device__ __forceinline__ void quantize_x_rows(const float* __restrict__ x, uint32_t m, uint32_t H,
-                                                const XQuant& xq, uint32_t qwg) {
+                                                const XQuant& xq, uint32_t qwg, const XNorm& nrm = XNorm{},
+                                                float* rinv = nullptr) {
     const uint32_t nb = H / 32, t = qwg * blockDim.x + threadIdx.x, id = t / 4, qd = t % 4;
     const uint32_t idc = id < m * nb ? id : m * nb - 1;
     const uint32_t row = idc / nb, b = idc % nb;
     const bool live = id < m * nb;
     const float4* src = reinterpret_cast<const float4*>(x + (size_t)row * H + (size_t)b * 32 + 8 * qd);
-    const float4 a = src[0], c = src[1];
-    const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+    const float4 a = src[0], c = src[1];  // in flight while the factors are computed
+    float rr = 1.0f;
+    if constexpr (NORM) {
+        const uint32_t i0 = qwg * blockDim.x / 4, i1 = i0 + blockDim.x / 4 - 1;
+        const uint32_t r0 = (i0 < m * nb ? i0 : m * nb - 1) / nb, r1 = (i1 < m * nb ? i1 : m * nb - 1) / nb;
+        for (uint32_t rw = r0 + threadIdx.x / WAVE; rw <= r1; rw += blockDim.x / WAVE) {
+            const float v = row_rms_inv(x + (size_t)rw * H, H, nrm.eps, threadIdx.x % WAVE);
+            if (threadIdx.x % WAVE == 0) rinv[rw - r0] = v;
+        }
+        __syncthreads();
+        rr = rinv[row - r0];
+    }
+    float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = rms_apply(v[i], rr, nrm.w, b * 32 + 8 * qd + i);
+    }
     float r[8], r2[8];
     uint32_t qw[2];
     float s;
@@ -87,14 +106,18 @@ __device__ __forceinline__ void quantize_x_rows(const float* __restrict__ x, uin
 
 // grid.x: waves over weight rows ([0, E) router rows + bias, row E = shared gate if shg), then
 // (xquant) the workgroups that quantise x; grid.y: chunks of DOT_MR activation rows.
+// NORM: x is rmsnorm's input (the config-5 layer), normalised where it is read: each dot wave
+// computes its rows' factors, each quantising workgroup those of its rows.
+template <bool NORM>
 __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict__ router,
                                                         const float* __restrict__ bias,
                                                         const float* __restrict__ shg,
                                                         const float* __restrict__ x, uint32_t m, uint32_t E,
                                                         uint32_t H, float* __restrict__ rlog, float* __restrict__ sh,
-                                                        XQuant xquant, uint32_t qwg0) {
+                                                        XQuant xquant, uint32_t qwg0, XNorm nrm) {
+    __shared__ float rq[128 / 4 + 2];
     if (xquant.q && blockIdx.x >= qwg0) {  // workgroup-uniform
-        if (blockIdx.y == 0) quantize_x_rows(x, m, H, xquant, blockIdx.x - qwg0);
+        if (blockIdx.y == 0) quantize_x_rows<NORM>(x, m, H, xquant, blockIdx.x - qwg0, nrm, rq);
         return;
     }
     const uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -103,7 +126,19 @@ __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict
     const uint32_t m0 = blockIdx.y * DOT_MR;
     const uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
     float res[DOT_MR];
-    dot_rows(wr, x, m0, mr, H, lane, res);
+    if constexpr (NORM) {
+        if (mr == 1 && H % 64 == 0 && H <= 64 * 32) {  // decode: one pass over the row
+            res[0] = dot_row_norm(wr, x + (size_t)m0 * H, H, lane, nrm.w, nrm.eps);
+        } else {  // the factors first, then the dots normalising as they read
+            float rinv[DOT_MR];
+#pragma unroll
+            for (int r = 0; r < DOT_MR; r++)
+                rinv[r] = (uint32_t)r < mr ? row_rms_inv(x + (size_t)(m0 + r) * H, H, nrm.eps, lane) : 1.0f;
+            dot_rows<true>(wr, x, m0, mr, H, lane, res, rinv, nrm.w);
+        }
+    } else {
+        dot_rows(wr, x, m0, mr, H, lane, res);
+    }
     if (lane == 0)
         for (uint32_t r = 0; r < mr; r++) {
             if (wave < E)
@@ -285,15 +320,21 @@ static void launch_gemm_cfg(const float* router, const float* bias, const float*
 
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
-                                hipStream_t st, const XQuant* xquant) {
+                                hipStream_t st, const XQuant* xquant, const XNorm* norm) {
     const uint32_t chunks = (m + DOT_MR - 1) / DOT_MR;
     const XQuant none{};
     if (xquant && (H % 32 || (xquant->pair && m != 1))) return hipErrorInvalidValue;  // pair: one decode row
+    if (norm && gemm_order) return hipErrorInvalidValue;  // rmsnorm is fused into the dot-order launch only
     if (!gemm_order) {
         const uint32_t nrow = E + (shexp_gate ? 1 : 0), wgs = (nrow + 1) / 2;
         const uint32_t qwgs = xquant ? (m * (H / 32) * 4 + 127) / 128 : 0;  // four lanes per 32-block
-        router_dot_kernel<<<dim3(wgs + qwgs, chunks), 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
-                                                                    xquant ? *xquant : none, wgs);
+        const dim3 grid(wgs + qwgs, chunks);
+        if (norm)
+            router_dot_kernel<true><<<grid, 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
+                                                          xquant ? *xquant : none, wgs, *norm);
+        else
+            router_dot_kernel<false><<<grid, 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
+                                                           xquant ? *xquant : none, wgs, XNorm{});
     } else {
         int id = 3;
         for (const GemmCfg& c : kGemmCfg)

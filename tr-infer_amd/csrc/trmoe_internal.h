@@ -84,9 +84,14 @@ struct XQuant {
     float* u;  // s * (float)sum
     int pair;
 };
+// rmsnorm applied to x inside the logits launch (elem.rs:255-262): weights w (null: none), eps
+struct XNorm {
+    const float* w;
+    float eps;
+};
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
-                                hipStream_t st, const XQuant* xquant = nullptr);
+                                hipStream_t st, const XQuant* xquant = nullptr, const XNorm* norm = nullptr);
 hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
