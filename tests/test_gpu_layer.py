@@ -173,7 +173,7 @@ ODD = dict(seed=13, H=768, E=24, F=768)  # 3 superblocks per row: lanes of a row
 
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
                                        ("full", 16, 10), ("small", 700, 3), ("odd", 9, 5), ("odd", 40, 5),
-                                       ("odd", 80, 5)])
+                                       ("odd", 80, 5), ("small", 100, 3)])
 def test_stream_items_match_mfma_tiles(shape, M, k):
     """Every split of the grouped items between the streaming GEMV and the int8 MFMA tiles gives
     the same bits, and matches the oracle's moe_batch."""
