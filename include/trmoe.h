@@ -38,7 +38,7 @@ typedef enum {
     TRK_E_NOMEM = -5
 } trk_status;
 
-enum { TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
+enum { TRK_FMT_Q8_0 = 8, TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
 enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
 
 /* A stack of `count` weight matrices [rows][k] in GGUF superblocks, row-major, `stride` bytes

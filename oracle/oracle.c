@@ -228,6 +228,7 @@ void orc_dequant_tq(const uint8_t *buf, int rows, int k, int bits, int kb, float
 size_t orc_gguf_row_bytes(int fmt, int K) {
     if (fmt == ORC_FMT_Q4_K) return (size_t)(K / 256) * 144;
     if (fmt == ORC_FMT_Q6_K) return (size_t)(K / 256) * 210;
+    if (fmt == ORC_FMT_Q8_0) return (size_t)(K / 32) * 34;
     return 0;
 }
 
@@ -267,6 +268,21 @@ void orc_q4k_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *dd,
                 dd[o] = orc_f32_to_f16(d * (float)sc[j]);
                 mm[o] = orc_f32_to_f16(-(dmin * (float)mn[j]));
             }
+        }
+}
+
+/* blocks.py:71-78 (q8_0_rows): the signed int8 offset by 128 into an unsigned q, the offset folded
+ * into m = f16(-128 * d) (computed in f32, then rounded), d as stored */
+void orc_q80_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *d, uint16_t *m) {
+    int nb = K / 32;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *blk = raw + ((size_t)r * nb + b) * 34;
+            uint16_t dh = rd16(blk);
+            size_t o = (size_t)r * nb + b;
+            d[o] = dh;
+            m[o] = orc_f32_to_f16(-128.0f * orc_f16_to_f32(dh));
+            for (int i = 0; i < 32; i++) q[(size_t)r * K + (size_t)b * 32 + i] = (uint8_t)((int)(int8_t)blk[2 + i] + 128);
         }
 }
 
@@ -321,6 +337,25 @@ int orc_gguf_to_tq(int fmt, const uint8_t *raw, int rows, int K, int kb, uint8_t
         free(d);
         free(m);
         bits = 4;
+    } else if (fmt == ORC_FMT_Q8_0 && (kb == 32 || kb == 16)) {
+        int n32 = K / 32;
+        uint16_t *d = (uint16_t *)malloc((size_t)rows * n32 * 2), *m = (uint16_t *)malloc((size_t)rows * n32 * 2);
+        orc_q80_rows(raw, rows, K, q, d, m);
+        if (kb == 32) {
+            orc_pack_tq(rows, K, 8, 32, q, d, m, out);
+        } else { /* rows_to_groups (blocks.py:107-113) */
+            uint16_t *d16 = (uint16_t *)malloc((size_t)rows * n32 * 4), *m16 = (uint16_t *)malloc((size_t)rows * n32 * 4);
+            for (size_t i = 0; i < (size_t)rows * n32; i++) {
+                d16[2 * i] = d16[2 * i + 1] = d[i];
+                m16[2 * i] = m16[2 * i + 1] = m[i];
+            }
+            orc_pack_tq(rows, K, 8, 16, q, d16, m16, out);
+            free(d16);
+            free(m16);
+        }
+        free(d);
+        free(m);
+        bits = 8;
     } else if (fmt == ORC_FMT_Q6_K && kb == 16) {
         int n16 = K / 16;
         uint16_t *d = (uint16_t *)malloc((size_t)rows * n16 * 2), *m = (uint16_t *)malloc((size_t)rows * n16 * 2);
@@ -335,7 +370,7 @@ int orc_gguf_to_tq(int fmt, const uint8_t *raw, int rows, int K, int kb, uint8_t
 }
 
 void orc_gguf_dequant(int fmt, const uint8_t *raw, int rows, int K, float *out) {
-    int kb = fmt == ORC_FMT_Q6_K ? 16 : 32;
+    int kb = fmt == ORC_FMT_Q4_K ? 32 : 16;
     size_t tb = orc_tq_matrix_bytes(rows, K, 8, kb);
     uint8_t *tq = (uint8_t *)malloc(tb);
     int bits = orc_gguf_to_tq(fmt, raw, rows, K, kb, tq);
@@ -940,6 +975,21 @@ void orc_gen_gguf(int fmt, uint64_t seed, uint64_t stream, int rows, int K, floa
                   uint8_t *out) {
     size_t sbb = fmt == ORC_FMT_Q6_K ? 210 : 144;
     size_t nsb = (size_t)rows * (K / 256);
+    if (fmt == ORC_FMT_Q8_0) { /* units of 8 blocks (272 bytes): 34 random words, then each d */
+        for (size_t sb = 0; sb < nsb; sb++) {
+            uint8_t *b = out + sb * 272;
+            for (size_t wi = 0; wi < 34; wi++) {
+                uint64_t r = orc_rng_u64(seed, stream, sb * 64 + wi);
+                for (int j = 0; j < 8; j++) b[wi * 8 + j] = (uint8_t)(r >> (8 * j));
+            }
+            for (int c = 0; c < 8; c++) {
+                uint16_t d = orc_f32_to_f16(unif24(orc_rng_u64(seed, stream, sb * 64 + 48 + c), dlo, dhi));
+                b[34 * c] = (uint8_t)(d & 0xff);
+                b[34 * c + 1] = (uint8_t)(d >> 8);
+            }
+        }
+        return;
+    }
     for (size_t sb = 0; sb < nsb; sb++) {
         uint8_t *b = out + sb * sbb;
         size_t nw = (sbb + 7) / 8; /* 18 or 27 draws of 8 random bytes */

@@ -108,6 +108,25 @@ def test_q6k_mapping_bruteforce():
     assert np.allclose(got, want, rtol=0, atol=1e-7 * np.abs(want).max())
 
 
+def test_q80_dequant_closed_form():
+    """Q8_0 through the offset-folded unsigned form (q + 128, m = f16(-128 d)) dequantises to
+    exactly d * int8, ggml's definition of the block; the generator keeps d in its range and puts
+    it at the start of every 34-byte block."""
+    rows, K = 3, 512
+    raw = O.gen_gguf(O.FMT_Q8_0, 9, 5, rows, K).reshape(rows, -1)
+    assert raw.shape[1] == K // 32 * 34 == O.gguf_row_bytes(O.FMT_Q8_0, K)
+    blk = raw.reshape(rows, K // 32, 34)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    assert (d >= np.float16(1e-4)).all() and (d <= np.float16(2e-3)).all()
+    want = (d[:, :, None] * blk[:, :, 2:].view(np.int8).astype(np.float32)).reshape(rows, K)
+    got = O.gguf_dequant(O.FMT_Q8_0, raw, rows, K)
+    assert np.array_equal(got, want)
+    # the TQ form at both block widths holds the same weights
+    for kb in (16, 32):
+        tq, bits = O.gguf_to_tq(O.FMT_Q8_0, raw, rows, K, kb)
+        assert bits == 8 and np.array_equal(O.dequant_tq(tq, rows, K, 8, kb), want)
+
+
 def test_q4k_dequant_bruteforce():
     """Q4_K dequant via (q, f16(d*sc), f16(-dmin*mn)) against an f64 evaluation of ggml's layout."""
     rows, K = 2, 512

@@ -161,4 +161,63 @@ __device__ __forceinline__ void half_terms_q6k(const uint8_t* __restrict__ rowp,
     half_terms_q6k<P>(w, aq, F, as, au, nbf, dotv, tv, mmv, uv);
 }
 
+// Q8_0 (34-byte blocks: f16 d, 32 int8), read in units of 8 blocks (272 bytes, 16-byte aligned):
+// half unit h2 = blocks 4 h2 .. 4 h2 + 3 = bytes 136 h2 .. +135, held as 34 words (8-byte loads).
+// q8_0_rows' unsigned form (blocks.py:71-78): q = int8 + 128, dd = d, mm = f16(-128 d).  The
+// unsigned dot is the signed one plus 128 times the activations' sum, both exact in int32.
+struct Q8Half {
+    uint32_t w[34];
+};
+__device__ __forceinline__ void load_half_q80(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2, Q8Half& w) {
+    const uint2* p = reinterpret_cast<const uint2*>(rowp + sb * 272 + 136 * h2);
+#pragma unroll
+    for (int i = 0; i < 17; i++) {
+        const uint2 v = p[i];
+        w.w[2 * i] = v.x;
+        w.w[2 * i + 1] = v.y;
+    }
+}
+// the 4 bytes at byte o of the half (o a constant once unrolled)
+__device__ __forceinline__ uint32_t q8_word(const Q8Half& w, uint32_t o) {
+    return o % 4 ? __builtin_amdgcn_alignbyte(w.w[o / 4 + 1], w.w[o / 4], o % 4) : w.w[o / 4];
+}
+
+template <int P>
+__device__ __forceinline__ void half_terms_q80(const Q8Half& w, const int8_t* __restrict__ aq, uint32_t F,
+                                               const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {  // 16-block i: half i % 2 of block j = i / 2
+        const uint32_t j = i / 2, o = 34 * j;
+        const float ddv = h2f((uint16_t)((w.w[o / 4] >> (8 * (o % 4))) & 0xffffu));
+        mmv[i] = f16_round(-128.0f * ddv);
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
+            const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
+            int dot = 0, sum = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                dot = sdot4((int)q8_word(w, o + 2 + 16 * (i % 2) + 4 * t), xa[t], dot);
+                sum = sdot4(xa[t], 0x01010101, sum);
+            }
+            dotv[p][i] = (float)(dot + 128 * sum);
+            tv[p][i] = ddv * as[p * nbf + i];
+            uv[p][i] = au[p * nbf + i];
+        }
+    }
+}
+
+template <int P>
+__device__ __forceinline__ void half_terms_q80(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2,
+                                               const int8_t* __restrict__ aq, uint32_t F,
+                                               const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+    Q8Half w;
+    load_half_q80(rowp, sb, h2, w);
+    half_terms_q80<P>(w, aq, F, as, au, nbf, dotv, tv, mmv, uv);
+}
+
 }  // namespace trk

@@ -250,10 +250,29 @@ __device__ __forceinline__ float unif24(uint64_t r, float lo, float hi) {
     return lo + p;
 }
 
-// one thread per 8-byte word of a superblock (18 words for Q4_K, 27 for Q6_K); grid.y runs over
-// the `count` matrices of a stack, matrix e drawing from stream stream0 + e * step
+// one thread per 8-byte word of a superblock (18 words for Q4_K, 27 for Q6_K, 34 for a Q8_0 unit
+// of 8 blocks); grid.y runs over the `count` matrices of a stack, matrix e drawing from stream
+// stream0 + e * step
 __global__ void gen_gguf_kernel(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t step, size_t nsb,
                                 uint64_t stride, float dlo, float dhi, uint8_t* out) {
+    if (fmt == TRK_FMT_Q8_0) {  // as orc_gen_gguf: words at sb * 64 + wi, block c's d at sb * 64 + 48 + c
+        const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (t >= nsb * 34) return;
+        const uint64_t key = mix64(seed ^ mix64(stream0 + (uint64_t)blockIdx.y * step));
+        const size_t sb = t / 34, wi = t % 34;
+        uint8_t* b = out + (size_t)blockIdx.y * stride + sb * 272;
+        const uint64_t r = rng_u64(key, sb * 64 + wi);
+        for (int j = 0; j < 8; j++) {
+            const size_t o = wi * 8 + j, c = o / 34;
+            uint8_t v = (uint8_t)(r >> (8 * j));
+            if (o % 34 < 2) {
+                const uint16_t d = f2h(unif24(rng_u64(key, sb * 64 + 48 + c), dlo, dhi));
+                v = (o % 34) ? (uint8_t)(d >> 8) : (uint8_t)(d & 0xff);
+            }
+            b[o] = v;
+        }
+        return;
+    }
     const size_t sbb = fmt == TRK_FMT_Q6_K ? 210 : 144;
     const size_t nw = (sbb + 7) / 8;
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -284,7 +303,7 @@ hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64
                            uint32_t rows, uint32_t k, float dlo, float dhi, void* out, uint64_t stride,
                            hipStream_t st) {
     const size_t nsb = (size_t)rows * (k / 256);
-    const size_t nw = fmt == TRK_FMT_Q6_K ? 27 : 18;
+    const size_t nw = fmt == TRK_FMT_Q6_K ? 27 : fmt == TRK_FMT_Q8_0 ? 34 : 18;
     const size_t n = nsb * nw;
     gen_gguf_kernel<<<dim3((unsigned)((n + 255) / 256), count), 256, 0, st>>>(fmt, seed, stream0, step, nsb, stride,
                                                                                dlo, dhi, (uint8_t*)out);

@@ -941,8 +941,35 @@ __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const I
     }
 }
 
-template <int NSB, bool Q6>
+// Q8_0 operands of one unit of 8 blocks (272 bytes, 16-byte aligned) for lane (g, r): per block c
+// the 8 value bytes 8g .. 8g + 7 (unit bytes 34c + 2 + 8g: 4-byte aligned for odd c, 2 past it for
+// even c, read by an aligned 12-byte load and alignbyte), and the words holding d of blocks 2g
+// (low half of the word at 68g) and 2g + 1 (high half of the word at 68g + 32).
+struct Q8Sb {
+    uint2 q[8];
+    uint32_t d0, d1;
+};
+__device__ __forceinline__ void load_q8sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q8Sb& w) {
+    const uint8_t* p = rowp + sb * 272;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        if (c % 2) {
+            w.q[c] = *reinterpret_cast<const uint2*>(p + 34 * c + 2 + 8 * g);
+        } else {
+            typedef uint32_t v3u __attribute__((ext_vector_type(3)));
+            const v3u v = *reinterpret_cast<const v3u*>(p + 34 * c + 8 * g);
+            w.q[c] = make_uint2(__builtin_amdgcn_alignbyte(v.y, v.x, 2), __builtin_amdgcn_alignbyte(v.z, v.y, 2));
+        }
+    }
+    w.d0 = *reinterpret_cast<const uint32_t*>(p + 68 * g);
+    w.d1 = *reinterpret_cast<const uint32_t*>(p + 68 * g + 32);
+}
+
+// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
+// q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
+template <int NSB, int FK>
 __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
+    constexpr bool Q6 = FK == 1;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
     const uint32_t H = down.rows;
     const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
@@ -960,19 +987,22 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     float* Sx = reinterpret_cast<float*>(smem + NQ * 64 * 8);        // [nbf][16] folded scales
     float* Su = Sx + nbf * 16;                                       // [nbf][16] scale * sum
     float2* Dm = reinterpret_cast<float2*>(Su + nbf * 16);           // [4 waves][16][DM_STRIDE]
-    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [16]
+    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [nbf][16] sums (Q8_0)
+    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Ss + nbf * 16);   // [16]
 
     if (tid < 16) rowoff[tid] = (arow0 + (tid < item.nrows ? tid : 0u)) * F;
     __syncthreads();
     stage_a(ws.actq, rowoff, F, As, tid);
     for (uint32_t i0 = 0; i0 < 16 * nbf; i0 += 1024) {
         float a[4], c2[4];
+        int32_t c3[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nbf ? i : 16 * nbf - 1;
             const size_t row = rowoff[ic / nbf] / F;
             a[c] = ws.acts[row * nbf + ic % nbf];
             c2[c] = ws.actu[row * nbf + ic % nbf];
+            if constexpr (FK == 2) c3[c] = ws.actsum[row * nbf + ic % nbf];
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -980,13 +1010,14 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
             if (i < 16 * nbf) {
                 Sx[(i % nbf) * 16 + i / nbf] = a[c];
                 Su[(i % nbf) * 16 + i / nbf] = c2[c];
+                if constexpr (FK == 2) Ss[(i % nbf) * 16 + i / nbf] = c3[c];
             }
         }
     }
     __syncthreads();
 
     const uint32_t strips = H / 16 / gridDim.x;
-    if constexpr (!Q6) {
+    if constexpr (FK == 0) {
         // small items: several strips per MFMA output (a wave owns strips / 4 strips)
         if (item.nrows <= 4 && strips % 16 == 0) {
             down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips);
@@ -1004,10 +1035,12 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
         const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
         return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
     };
-    using W = typename std::conditional<Q6, Q6Sb, Q4Sb>::type;
+    using W = typename std::conditional<Q6, Q6Sb, typename std::conditional<FK == 2, Q8Sb, Q4Sb>::type>::type;
     auto load = [&](uint32_t step, W& w) {
         if constexpr (Q6)
             load_q6sb(row_of(step), step % NSB, g, w);
+        else if constexpr (FK == 2)
+            load_q8sb(row_of(step), step % NSB, g, w);
         else
             load_q4sb(row_of(step), step % NSB, g, w);
     };
@@ -1027,6 +1060,14 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
                 const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
                 dmw[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
             }
+        } else if constexpr (FK == 2) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
+                const float dd = h2f((uint16_t)(jj ? cw.d1 >> 16 : cw.d0 & 0xffffu));
+                const float2 v = make_float2(dd, f16_round(-128.0f * dd));
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+            }
         } else {
 #pragma unroll
             for (int jj = 0; jj < 2; jj++) {  // sub-block 2g + jj covers blocks 4g + 2jj, +1
@@ -1044,9 +1085,17 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
             long bw;
             if constexpr (Q6)
                 bw = q6_operand(cw, q8);
+            else if constexpr (FK == 2)
+                bw = (long)(((unsigned long long)cw.q[q8].y << 32) | cw.q[q8].x);
             else
                 bw = unpack8(cw.qs[q8 / 2], q8 % 2);
-            const v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+            v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+            if constexpr (FK == 2) {
+                const int4 t0 = *reinterpret_cast<const int4*>(Ss + (2 * q) * 16 + 4 * g);
+                const int4 t1 = *reinterpret_cast<const int4*>(Ss + (2 * q + 1) * 16 + 4 * g);
+                c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
+                c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
+            }
             const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
             const float4 s0 = *reinterpret_cast<const float4*>(Sx + (2 * q) * 16 + 4 * g);
             const float4 u0 = *reinterpret_cast<const float4*>(Su + (2 * q) * 16 + 4 * g);
@@ -1079,14 +1128,15 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t skip_rows,
                              hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
-    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 8 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
+    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
     const dim3 grid(m >= 64 ? H / 256 : H / 64, grouped_item_rows(ws, m));
-    const bool q6 = down.fmt == TRK_FMT_Q6_K;
-    if (q6 != (sh_down.fmt == TRK_FMT_Q6_K)) return hipErrorInvalidValue;  // one format per layer
-    switch (F / 256 * 2 + (q6 ? 1 : 0)) {
-#define DN_CASE(n)                                                                          \
-    case n * 2: batch_down_kernel<n, false><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
-    case n * 2 + 1: batch_down_kernel<n, true><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
+    if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
+    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : 0;
+    switch (F / 256 * 3 + fk) {
+#define DN_CASE(n)                                                                                    \
+    case n * 3: batch_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;     \
+    case n * 3 + 1: batch_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
+    case n * 3 + 2: batch_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
         default: return hipErrorInvalidValue;
