@@ -115,9 +115,13 @@ __global__ __launch_bounds__(128) void router_dot_kernel(const float* __restrict
                                                         const float* __restrict__ x, uint32_t m, uint32_t E,
                                                         uint32_t H, float* __restrict__ rlog, float* __restrict__ sh,
                                                         XQuant xquant, uint32_t qwg0, XNorm nrm) {
-    __shared__ float rq[128 / 4 + 2];
     if (xquant.q && blockIdx.x >= qwg0) {  // workgroup-uniform
-        if (blockIdx.y == 0) quantize_x_rows<NORM>(x, m, H, xquant, blockIdx.x - qwg0, nrm, rq);
+        if constexpr (NORM) {  // LDS only in this instantiation
+            __shared__ float rq[128 / 4 + 2];
+            if (blockIdx.y == 0) quantize_x_rows<true>(x, m, H, xquant, blockIdx.x - qwg0, nrm, rq);
+        } else {
+            if (blockIdx.y == 0) quantize_x_rows(x, m, H, xquant, blockIdx.x - qwg0);
+        }
         return;
     }
     const uint32_t wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
