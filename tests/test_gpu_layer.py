@@ -139,9 +139,9 @@ def test_decode_one_launch_matches_three(policy):
 
 
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
-                                       ("full", 16, 10), ("small", 700, 3)])
+                                       ("full", 16, 10), ("small", 700, 3), ("small", 2200, 2)])
 def test_batch_layer_and_dispatch(shape, M, k):
-    # M = 700: two rounds of 512 tokens and the split (parallel) scatter
+    # M = 700: the split (parallel) scatter; M = 2200: three rounds of 1024 tokens, 35 chunks
     say(f"batch layer {shape} M={M} k={k}")
     L, orc, W = layer(shape, **(SMALL if shape == "small" else FULL))
     ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))

@@ -44,7 +44,8 @@ __device__ __forceinline__ uint32_t load_ids(const Workspace& ws, uint32_t t, ui
 // the wave totals).  kc4 = ceil(largest selection / 4).
 constexpr uint32_t DT = DISPATCH_WAVES * 64;  // tokens per round
 // split: leave the scatter to scatter_kernel (many workgroups) and store the per-(64-token chunk,
-// expert) first positions in ws.doff instead.
+// expert) first positions in ws.doff instead: pass 1 stores each chunk's counts there, and one
+// prefix per expert over the chunks turns them into positions (no second pass over the tokens).
 __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace ws, uint32_t m, uint32_t kc4,
                                                                        int split) {
     const uint32_t E = ws.E, tid = threadIdx.x;
@@ -89,7 +90,12 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         build_masks();
         for (uint32_t e = tid; e < E; e += DT) {
             uint32_t c = cnt[e];
-            for (uint32_t w = 0; w < DISPATCH_WAVES; w++) c += popc64(masks[w * E + e]);
+            for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
+                const uint32_t pc = popc64(masks[w * E + e]);
+                const uint32_t ch = r * DISPATCH_WAVES + w;  // 64-token chunk
+                if (split && ch < nchunks) ws.doff[(size_t)ch * E + e] = pc;  // its count, for now
+                c += pc;
+            }
             cnt[e] = c;
         }
         if (rounds > 1) __syncthreads();
@@ -158,6 +164,23 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     }
     __syncthreads();
 
+    if (split) {  // the chunk counts become each chunk's first position per expert
+        for (uint32_t e = tid; e < E; e += DT) {
+            uint32_t o = run[e];
+            for (uint32_t ch0 = 0; ch0 < nchunks; ch0 += 16) {  // 16 counts requested at once
+                uint32_t c[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) c[j] = ch0 + j < nchunks ? ws.doff[(size_t)(ch0 + j) * E + e] : 0u;
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (ch0 + j < nchunks) {
+                        ws.doff[(size_t)(ch0 + j) * E + e] = o;
+                        o += c[j];
+                    }
+            }
+        }
+        return;
+    }
     // pass 2: scatter (the single-round case reuses the masks and the registers of pass 1)
     const unsigned long long below = lane ? ((1ull << lane) - 1ull) : 0ull;
     for (uint32_t r = 0; r < rounds; r++) {
@@ -168,18 +191,10 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         for (uint32_t e = tid; e < E; e += DT) {
             uint32_t o = run[e];
             for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
-                if (split) {
-                    const uint32_t ch = r * DISPATCH_WAVES + w;  // 64-token chunk; the last round's
-                    if (ch < nchunks) ws.doff[(size_t)ch * E + e] = o;  // trailing waves hold none
-                } else
-                    off[w * E + e] = o;
+                off[w * E + e] = o;
                 o += popc64(masks[w * E + e]);
             }
             run[e] = o;
-        }
-        if (split) {
-            if (rounds > 1) __syncthreads();
-            continue;
         }
         __syncthreads();
         const uint32_t t = r * DT + tid;
