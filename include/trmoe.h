@@ -38,14 +38,14 @@ typedef enum {
     TRK_E_NOMEM = -5
 } trk_status;
 
-enum { TRK_FMT_Q8_0 = 8, TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
+enum { TRK_FMT_Q5_1 = 7, TRK_FMT_Q8_0 = 8, TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
 enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
 
 /* A stack of `count` weight matrices [rows][k] in GGUF superblocks, row-major, `stride` bytes
  * apart.  Replaces tr_model::weights::TqMat {ptr, rows, k, codec, count, stride}
  * (crates/tr-model/src/weights.rs:14-35): `fmt` names the GGUF block format read directly on
  * the GPU where the CPU path reads its TQ re-layout.  Gate/up: Q4_K.  Down (routed and shared
- * alike): Q4_K, Q6_K or Q8_0 (blocks.py:71-78).  Q4_K and Q8_0 stacks are 16-byte aligned,
+ * alike): Q4_K, Q6_K, Q8_0 or Q5_1 (blocks.py:57-78).  Q4_K, Q8_0 and Q5_1 stacks are 16-byte aligned,
  * Q6_K 2-byte aligned. */
 typedef struct {
     const void *ptr;
@@ -165,7 +165,7 @@ int trk_add_inplace(float *y, const float *a, size_t n, void *stream);
 
 /* ---- synthetic data (bit-identical to the test oracle's generator) ---------------------- */
 /* GGUF superblocks of a [rows][k] matrix: d (and dmin) ~ U(dlo, dhi) as f16, all other bytes
- * uniform; fmt Q4_K, Q6_K or Q8_0 (Q8_0: every block's d). */
+ * uniform; fmt Q4_K, Q6_K, Q8_0 or Q5_1 (Q8_0 / Q5_1: every block's d, Q5_1 m = -16 U). */
 int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
                  float dhi, void *out, void *stream);
 /* The same for a stack of `count` matrices `stride` bytes apart, matrix e drawing from stream

@@ -229,6 +229,7 @@ size_t orc_gguf_row_bytes(int fmt, int K) {
     if (fmt == ORC_FMT_Q4_K) return (size_t)(K / 256) * 144;
     if (fmt == ORC_FMT_Q6_K) return (size_t)(K / 256) * 210;
     if (fmt == ORC_FMT_Q8_0) return (size_t)(K / 32) * 34;
+    if (fmt == ORC_FMT_Q5_1) return (size_t)(K / 32) * 24;
     return 0;
 }
 
@@ -286,6 +287,24 @@ void orc_q80_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *d, 
         }
 }
 
+/* blocks.py:57-68 (q5_1_rows): element i of a block is the low (i < 16) or high (i >= 16) nibble
+ * of qs[i % 16] with bit i of qh as its fifth bit; d and m as stored */
+void orc_q51_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *d, uint16_t *m) {
+    int nb = K / 32;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *blk = raw + ((size_t)r * nb + b) * 24;
+            size_t o = (size_t)r * nb + b;
+            d[o] = rd16(blk);
+            m[o] = rd16(blk + 2);
+            uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) | ((uint32_t)blk[7] << 24);
+            for (int i = 0; i < 32; i++) {
+                uint8_t nib = i < 16 ? (blk[8 + i] & 0x0f) : (blk[8 + i - 16] >> 4);
+                q[(size_t)r * K + (size_t)b * 32 + i] = (uint8_t)(nib | (((qh >> i) & 1u) << 4));
+            }
+        }
+}
+
 /* Q6_K (ggml block_q6_K: ql[128] qh[64] scales[16] int8, d f16) -> 6-bit unsigned q with
  * per-16 (dd, mm) = (f16(d*sc), -32*dd).  Extension: follows the offset-folding of q8_0_rows
  * (blocks.py:71-78); the reference itself has no Q6_K converter. */
@@ -337,25 +356,28 @@ int orc_gguf_to_tq(int fmt, const uint8_t *raw, int rows, int K, int kb, uint8_t
         free(d);
         free(m);
         bits = 4;
-    } else if (fmt == ORC_FMT_Q8_0 && (kb == 32 || kb == 16)) {
-        int n32 = K / 32;
+    } else if ((fmt == ORC_FMT_Q8_0 || fmt == ORC_FMT_Q5_1) && (kb == 32 || kb == 16)) {
+        int n32 = K / 32, nbits = fmt == ORC_FMT_Q8_0 ? 8 : 5;
         uint16_t *d = (uint16_t *)malloc((size_t)rows * n32 * 2), *m = (uint16_t *)malloc((size_t)rows * n32 * 2);
-        orc_q80_rows(raw, rows, K, q, d, m);
+        if (fmt == ORC_FMT_Q8_0)
+            orc_q80_rows(raw, rows, K, q, d, m);
+        else
+            orc_q51_rows(raw, rows, K, q, d, m);
         if (kb == 32) {
-            orc_pack_tq(rows, K, 8, 32, q, d, m, out);
+            orc_pack_tq(rows, K, nbits, 32, q, d, m, out);
         } else { /* rows_to_groups (blocks.py:107-113) */
             uint16_t *d16 = (uint16_t *)malloc((size_t)rows * n32 * 4), *m16 = (uint16_t *)malloc((size_t)rows * n32 * 4);
             for (size_t i = 0; i < (size_t)rows * n32; i++) {
                 d16[2 * i] = d16[2 * i + 1] = d[i];
                 m16[2 * i] = m16[2 * i + 1] = m[i];
             }
-            orc_pack_tq(rows, K, 8, 16, q, d16, m16, out);
+            orc_pack_tq(rows, K, nbits, 16, q, d16, m16, out);
             free(d16);
             free(m16);
         }
         free(d);
         free(m);
-        bits = 8;
+        bits = nbits;
     } else if (fmt == ORC_FMT_Q6_K && kb == 16) {
         int n16 = K / 16;
         uint16_t *d = (uint16_t *)malloc((size_t)rows * n16 * 2), *m = (uint16_t *)malloc((size_t)rows * n16 * 2);
@@ -975,6 +997,25 @@ void orc_gen_gguf(int fmt, uint64_t seed, uint64_t stream, int rows, int K, floa
                   uint8_t *out) {
     size_t sbb = fmt == ORC_FMT_Q6_K ? 210 : 144;
     size_t nsb = (size_t)rows * (K / 256);
+    if (fmt == ORC_FMT_Q5_1) { /* units of 8 blocks (192 bytes): 24 random words, then each d, m */
+        for (size_t sb = 0; sb < nsb; sb++) {
+            uint8_t *b = out + sb * 192;
+            for (size_t wi = 0; wi < 24; wi++) {
+                uint64_t r = orc_rng_u64(seed, stream, sb * 64 + wi);
+                for (int j = 0; j < 8; j++) b[wi * 8 + j] = (uint8_t)(r >> (8 * j));
+            }
+            for (int c = 0; c < 8; c++) {
+                uint64_t rd = orc_rng_u64(seed, stream, sb * 64 + 48 + c);
+                uint16_t d = orc_f32_to_f16(unif24(rd, dlo, dhi));
+                uint16_t m = orc_f32_to_f16(-16.0f * unif24(rd >> 24, dlo, dhi));
+                b[24 * c] = (uint8_t)(d & 0xff);
+                b[24 * c + 1] = (uint8_t)(d >> 8);
+                b[24 * c + 2] = (uint8_t)(m & 0xff);
+                b[24 * c + 3] = (uint8_t)(m >> 8);
+            }
+        }
+        return;
+    }
     if (fmt == ORC_FMT_Q8_0) { /* units of 8 blocks (272 bytes): 34 random words, then each d */
         for (size_t sb = 0; sb < nsb; sb++) {
             uint8_t *b = out + sb * 272;

@@ -39,6 +39,7 @@ extern "C" {
 #define ORC_FMT_Q4_K 12
 #define ORC_FMT_Q6_K 14
 #define ORC_FMT_Q8_0 8
+#define ORC_FMT_Q5_1 7
 
 /* ---- half precision (IEEE binary16, round-to-nearest-even) ------------------------------ */
 float orc_f16_to_f32(uint16_t h);
@@ -64,6 +65,8 @@ void orc_q4k_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *dd,
 void orc_q6k_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *dd, uint16_t *mm);
 /* Q8_0 (34-byte blocks: f16 d, 32 int8) -> u8 q = int8 + 128, d, m = f16(-128 d) per 32 (blocks.py:71-78) */
 void orc_q80_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *d, uint16_t *m);
+/* Q5_1 (24-byte blocks: f16 d, f16 m, u32 qh, 16 qs) -> 5-bit q, d, m per 32 (blocks.py:57-68) */
+void orc_q51_rows(const uint8_t *raw, int rows, int K, uint8_t *q, uint16_t *d, uint16_t *m);
 /* Whole matrix GGUF -> TQ(bits, kb) bytes; returns bits, or -1 on an unsupported (fmt, kb). */
 int orc_gguf_to_tq(int fmt, const uint8_t *raw, int rows, int K, int kb, uint8_t *out);
 size_t orc_gguf_row_bytes(int fmt, int K);

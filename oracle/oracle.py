@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 FMT_Q4_K = 12
 FMT_Q6_K = 14
 FMT_Q8_0 = 8
+FMT_Q5_1 = 7
 MOE_K_MAX = 32
 BASIS_ALL = 0
 BASIS_TOP = 1
@@ -178,7 +179,7 @@ def gguf_row_bytes(fmt, K):
 
 
 def gguf_to_tq(fmt, raw, rows, K, kb):
-    bits = 8 if fmt in (FMT_Q6_K, FMT_Q8_0) else 4
+    bits = {FMT_Q6_K: 8, FMT_Q8_0: 8, FMT_Q5_1: 5}.get(fmt, 4)
     out = np.zeros(tq_matrix_bytes(rows, K, bits, kb), np.uint8)
     got = lib().orc_gguf_to_tq(fmt, _p(np.ascontiguousarray(raw, np.uint8)), rows, K, kb, _p(out))
     if got != bits:
@@ -342,7 +343,7 @@ class OracleLayer:
         self.sh_gate, self.gate_bits = gguf_to_tq(gate_fmt, sh_gate_raw, F, H, 32)
         self.sh_up, _ = gguf_to_tq(gate_fmt, sh_up_raw, F, H, 32)
         self.sh_down, self.sh_down_bits = gguf_to_tq(down_fmt, sh_down_raw, H, F, 16)
-        self.down_bits = 8 if down_fmt in (FMT_Q6_K, FMT_Q8_0) else 4
+        self.down_bits = {FMT_Q6_K: 8, FMT_Q8_0: 8, FMT_Q5_1: 5}.get(down_fmt, 4)
         self._gate_ptrs = (C.c_void_p * E)()
         self._up_ptrs = (C.c_void_p * E)()
         self._down_ptrs = (C.c_void_p * E)()

@@ -43,7 +43,7 @@ def ulp_diff(a, b):
     return np.abs(a - b)
 
 
-@pytest.mark.parametrize("fmt,rows,K", [(O.FMT_Q4_K, 33, 2048), (O.FMT_Q6_K, 17, 512), (O.FMT_Q8_0, 9, 768)])
+@pytest.mark.parametrize("fmt,rows,K", [(O.FMT_Q4_K, 33, 2048), (O.FMT_Q6_K, 17, 512), (O.FMT_Q8_0, 9, 768), (O.FMT_Q5_1, 9, 768)])
 def test_generator_bytes_match_oracle(fmt, rows, K):
     say(f"gen_gguf fmt={fmt} rows={rows} K={K}")
     g = host(trmoe.gen_gguf(fmt, 7, (3 << 32) | 99, rows, K))

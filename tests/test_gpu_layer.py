@@ -254,13 +254,15 @@ def test_q6k_down(M, rows):
     ctx.close()
 
 
+@pytest.mark.parametrize("fmt", [O.FMT_Q8_0, O.FMT_Q5_1])
 @pytest.mark.parametrize("M", [1, 6, 40, 80])
-def test_q80_down(M):
-    """Q8_0 downs (the reference's q8_0_rows form: q = int8 + 128, m = f16(-128 d)) on every down
-    kernel: the decode path (M = 1), and for batches every split between the streaming GEMV and
-    the MFMA tiles gives the same bits, within tolerance of the oracle's TQ8_16 GEMV."""
-    say(f"q8_0 down M={M}")
-    L, orc, W = layer("q8", seed=6, H=512, E=16, F=256, down_fmt=O.FMT_Q8_0)
+def test_q80_q51_down(fmt, M):
+    """Q8_0 and Q5_1 downs (the reference's q8_0_rows / q5_1_rows forms: q = int8 + 128 with
+    m = f16(-128 d); 5-bit q with d, m as stored) on every down kernel: the decode path (M = 1),
+    and for batches every split between the streaming GEMV and the MFMA tiles gives the same
+    bits, within tolerance of the oracle's TQ8_16 / TQ5_16 GEMV."""
+    say(f"down fmt={fmt} M={M}")
+    L, orc, W = layer(f"dfmt{fmt}", seed=6, H=512, E=16, F=256, down_fmt=fmt)
     import torch
     x = L.x(M, tid=410)
     r = orc.moe_block(x[0], k=3) if M == 1 else orc.moe_batch(x, k=3)
@@ -274,7 +276,7 @@ def test_q80_down(M):
         outs.append(host(out).copy())
         exact = M > 1 and np.array_equal(ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :3],
                                          r["w"][:, :3]) and shared_gate_exact(L, x)
-        compare_out(outs[-1], want, exact, f"q8_0 M={M} rows={rows}")
+        compare_out(outs[-1], want, exact, f"fmt={fmt} M={M} rows={rows}")
         ctx.close()
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))

@@ -127,6 +127,29 @@ def test_q80_dequant_closed_form():
         assert bits == 8 and np.array_equal(O.dequant_tq(tq, rows, K, 8, kb), want)
 
 
+def test_q51_dequant_bruteforce():
+    """Q5_1 through q5_1_rows' form against an evaluation of ggml's layout: element i of a block
+    is nibble i % 16 of qs (low for i < 16, high after) with bit i of qh on top, w = d q + m."""
+    rows, K = 2, 512
+    raw = O.gen_gguf(O.FMT_Q5_1, 9, 6, rows, K).reshape(rows, -1)
+    assert raw.shape[1] == K // 32 * 24 == O.gguf_row_bytes(O.FMT_Q5_1, K)
+    want = np.zeros((rows, K), np.float32)
+    for r in range(rows):
+        for b in range(K // 32):
+            blk = raw[r, 24 * b:24 * b + 24]
+            d, m = (np.float32(v) for v in blk[:4].view(np.float16))
+            qh = int(blk[4:8].view(np.uint32)[0])
+            for i in range(32):
+                nib = (int(blk[8 + i % 16]) >> (4 * (i // 16))) & 15
+                q = nib | (((qh >> i) & 1) << 4)
+                want[r, 32 * b + i] = np.float32(d * np.float32(q)) + m
+    got = O.gguf_dequant(O.FMT_Q5_1, raw, rows, K)
+    assert np.array_equal(got, want)
+    for kb in (16, 32):
+        tq, bits = O.gguf_to_tq(O.FMT_Q5_1, raw, rows, K, kb)
+        assert bits == 5 and np.array_equal(O.dequant_tq(tq, rows, K, 5, kb), want)
+
+
 def test_q4k_dequant_bruteforce():
     """Q4_K dequant via (q, f16(d*sc), f16(-dmin*mn)) against an f64 evaluation of ggml's layout."""
     rows, K = 2, 512

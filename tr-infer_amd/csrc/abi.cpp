@@ -35,6 +35,7 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
     if (fmt == TRK_FMT_Q4_K) return k / 256 * 144;
     if (fmt == TRK_FMT_Q6_K) return k / 256 * 210;
     if (fmt == TRK_FMT_Q8_0) return k / 256 * 272;
+    if (fmt == TRK_FMT_Q5_1) return k / 256 * 192;
     return 0;
 }
 
@@ -216,14 +217,15 @@ static int make_mat(const trk_mat& m, uint32_t rows, uint32_t k, bool down_ok_q6
     if (!m.ptr) return fail(TRK_E_INVALID, "%s: null weight pointer", name);
     if (m.rows != rows || m.k != k)
         return fail(TRK_E_INVALID, "%s: shape [%u][%u], expected [%u][%u]", name, m.rows, m.k, rows, k);
-    if (!(m.fmt == TRK_FMT_Q4_K || (down_ok_q6 && (m.fmt == TRK_FMT_Q6_K || m.fmt == TRK_FMT_Q8_0))))
+    if (!(m.fmt == TRK_FMT_Q4_K || (down_ok_q6 && (m.fmt == TRK_FMT_Q6_K || m.fmt == TRK_FMT_Q8_0 || m.fmt == TRK_FMT_Q5_1))))
         return fail(TRK_E_INVALID, "%s: unsupported format %u", name, m.fmt);
     if (m.count < min_count) return fail(TRK_E_INVALID, "%s: %u matrices, need %u", name, m.count, min_count);
     uint32_t rb = row_bytes(m.fmt, k);
     uint64_t mb = (uint64_t)rb * rows;
     if (m.count > 1 && m.stride < mb) return fail(TRK_E_INVALID, "%s: stride %llu below matrix bytes %llu", name,
                                                   (unsigned long long)m.stride, (unsigned long long)mb);
-    // Q4_K superblocks and Q8_0 units of 8 blocks (272 bytes) are read with 16- and 8-byte loads
+    // Q4_K superblocks and Q8_0 / Q5_1 units of 8 blocks (272 / 192 bytes) are read with 16- and
+    // 8-byte loads
     uint64_t align = m.fmt == TRK_FMT_Q6_K ? 2 : 16;
     if ((uintptr_t)m.ptr % align || (m.count > 1 && m.stride % align))
         return fail(TRK_E_INVALID, "%s: pointer/stride must be %llu-byte aligned", name, (unsigned long long)align);
@@ -562,7 +564,7 @@ extern "C" int trk_add_inplace(float* y, const float* a, size_t n, void* stream)
 extern "C" int trk_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream_id, uint32_t rows, uint32_t k, float dlo,
                             float dhi, void* out, void* stream) {
     if (!out) return fail(TRK_E_INVALID, "null argument");
-    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K || fmt == TRK_FMT_Q8_0) || k % 256)
+    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K || fmt == TRK_FMT_Q8_0 || fmt == TRK_FMT_Q5_1) || k % 256)
         return fail(TRK_E_INVALID, "bad format/k");
     if (rows == 0) return TRK_OK;
     HIP_TRY(launch_gen_gguf(fmt, seed, stream_id, 0, 1, rows, k, dlo, dhi, out, 0, (hipStream_t)stream));
@@ -573,7 +575,7 @@ extern "C" int trk_gen_gguf_stack(uint32_t fmt, uint64_t seed, uint64_t stream0,
                                   uint32_t count, uint32_t rows, uint32_t k, float dlo, float dhi, void* out,
                                   uint64_t stride, void* stream) {
     if (!out) return fail(TRK_E_INVALID, "null argument");
-    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K || fmt == TRK_FMT_Q8_0) || k % 256)
+    if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K || fmt == TRK_FMT_Q8_0 || fmt == TRK_FMT_Q5_1) || k % 256)
         return fail(TRK_E_INVALID, "bad format/k");
     const uint64_t mb = (uint64_t)rows * (k / 256) * (fmt == TRK_FMT_Q6_K ? 210 : 144);
     if (count > 1 && stride < mb) return fail(TRK_E_INVALID, "stride %llu below matrix bytes %llu",

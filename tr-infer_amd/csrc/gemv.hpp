@@ -220,4 +220,66 @@ __device__ __forceinline__ void half_terms_q80(const uint8_t* __restrict__ rowp,
     half_terms_q80<P>(w, aq, F, as, au, nbf, dotv, tv, mmv, uv);
 }
 
+// Q5_1 (24-byte blocks: f16 d, f16 m, u32 qh, 16 bytes qs), read in units of 8 blocks (192 bytes,
+// 16-byte aligned): half unit h2 = blocks 4 h2 .. 4 h2 + 3 = 24 words.  q5_1_rows (blocks.py:57-68):
+// element i is nibble i % 16 of qs (low for i < 16) with bit i of qh as its fifth bit; dd = d,
+// mm = m as stored.
+struct Q51Half {
+    uint32_t w[24];
+};
+__device__ __forceinline__ void load_half_q51(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2, Q51Half& w) {
+    const uint4* p = reinterpret_cast<const uint4*>(rowp + sb * 192 + 96 * h2);
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const uint4 v = p[i];
+        w.w[4 * i] = v.x;
+        w.w[4 * i + 1] = v.y;
+        w.w[4 * i + 2] = v.z;
+        w.w[4 * i + 3] = v.w;
+    }
+}
+// four fifth bits (bits 0-3 of h4) moved to bit 4 of bytes 0-3: h4 * (1 + 2^7 + 2^14 + 2^21) puts
+// bit b at bit 8b (the 16 partial products land on distinct bits, so nothing carries)
+__device__ __forceinline__ uint32_t q5_hi4(uint32_t h4) { return ((h4 * 0x204081u) & 0x01010101u) << 4; }
+
+template <int P>
+__device__ __forceinline__ void half_terms_q51(const Q51Half& w, const int8_t* __restrict__ aq, uint32_t F,
+                                               const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {  // 16-block i: elements 16 (i % 2) .. +15 of block j = i / 2
+        const int j = i / 2, hf = i % 2;
+        const float ddv = h2f((uint16_t)(w.w[6 * j] & 0xffffu));
+        mmv[i] = h2f((uint16_t)(w.w[6 * j] >> 16));
+        const uint32_t qh = w.w[6 * j + 1];
+        uint32_t qw[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            qw[t] = ((w.w[6 * j + 2 + t] >> (4 * hf)) & 0x0f0f0f0fu) | q5_hi4((qh >> (16 * hf + 4 * t)) & 0xfu);
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const int4 xv = *reinterpret_cast<const int4*>(aq + p * F + i * 16);
+            const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
+            int dot = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) dot = sdot4((int)qw[t], xa[t], dot);
+            dotv[p][i] = (float)dot;
+            tv[p][i] = ddv * as[p * nbf + i];
+            uv[p][i] = au[p * nbf + i];
+        }
+    }
+}
+
+template <int P>
+__device__ __forceinline__ void half_terms_q51(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t h2,
+                                               const int8_t* __restrict__ aq, uint32_t F,
+                                               const float* __restrict__ as, const float* __restrict__ au,
+                                               uint32_t nbf, float (&dotv)[P][8], float (&tv)[P][8], float (&mmv)[8],
+                                               float (&uv)[P][8]) {
+    Q51Half w;
+    load_half_q51(rowp, sb, h2, w);
+    half_terms_q51<P>(w, aq, F, as, au, nbf, dotv, tv, mmv, uv);
+}
+
 }  // namespace trk

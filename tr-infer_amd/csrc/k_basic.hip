@@ -255,6 +255,25 @@ __device__ __forceinline__ float unif24(uint64_t r, float lo, float hi) {
 // stream0 + e * step
 __global__ void gen_gguf_kernel(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64_t step, size_t nsb,
                                 uint64_t stride, float dlo, float dhi, uint8_t* out) {
+    if (fmt == TRK_FMT_Q5_1) {  // as orc_gen_gguf: words at sb * 64 + wi, block c's d, m at sb * 64 + 48 + c
+        const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (t >= nsb * 24) return;
+        const uint64_t key = mix64(seed ^ mix64(stream0 + (uint64_t)blockIdx.y * step));
+        const size_t sb = t / 24, wi = t % 24;
+        uint8_t* b = out + (size_t)blockIdx.y * stride + sb * 192;
+        const uint64_t r = rng_u64(key, sb * 64 + wi);
+        for (int j = 0; j < 8; j++) {
+            const size_t o = wi * 8 + j, c = o / 24;
+            uint8_t v = (uint8_t)(r >> (8 * j));
+            if (o % 24 < 4) {
+                const uint64_t rd = rng_u64(key, sb * 64 + 48 + c);
+                const uint16_t h = o % 24 < 2 ? f2h(unif24(rd, dlo, dhi)) : f2h(-16.0f * unif24(rd >> 24, dlo, dhi));
+                v = (o % 2) ? (uint8_t)(h >> 8) : (uint8_t)(h & 0xff);
+            }
+            b[o] = v;
+        }
+        return;
+    }
     if (fmt == TRK_FMT_Q8_0) {  // as orc_gen_gguf: words at sb * 64 + wi, block c's d at sb * 64 + 48 + c
         const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
         if (t >= nsb * 34) return;
@@ -303,7 +322,7 @@ hipError_t launch_gen_gguf(uint32_t fmt, uint64_t seed, uint64_t stream0, uint64
                            uint32_t rows, uint32_t k, float dlo, float dhi, void* out, uint64_t stride,
                            hipStream_t st) {
     const size_t nsb = (size_t)rows * (k / 256);
-    const size_t nw = fmt == TRK_FMT_Q6_K ? 27 : fmt == TRK_FMT_Q8_0 ? 34 : 18;
+    const size_t nw = fmt == TRK_FMT_Q6_K ? 27 : fmt == TRK_FMT_Q8_0 ? 34 : fmt == TRK_FMT_Q5_1 ? 24 : 18;
     const size_t n = nsb * nw;
     gen_gguf_kernel<<<dim3((unsigned)((n + 255) / 256), count), 256, 0, st>>>(fmt, seed, stream0, step, nsb, stride,
                                                                                dlo, dhi, (uint8_t*)out);

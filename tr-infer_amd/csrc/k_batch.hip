@@ -13,6 +13,7 @@
 //   combine:  per token, shared row first, then its entries in ascending expert order (the
 //             reference's overwrite-then-accumulate order, exec_batch.rs:1539-1561).
 #include "common.hpp"
+#include "gemv.hpp"
 #include "route.hpp"
 
 #include <type_traits>
@@ -980,7 +981,34 @@ __device__ __forceinline__ void load_q8sb(const uint8_t* __restrict__ rowp, uint
     w.d1 = *reinterpret_cast<const uint32_t*>(p + 68 * g + 32);
 }
 
-// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
+// Q5_1 operands of one unit of 8 blocks (192 bytes, 16-byte aligned) for lane (g, r): per block c
+// the 8 qs bytes whose low (g < 2) or high (g >= 2) nibbles are elements 8g .. 8g + 7, the block's
+// qh, and the (d, m) words of blocks 2g and 2g + 1.
+struct Q51Sb {
+    uint2 qs[8];
+    uint32_t qh[8];
+    uint32_t dm0, dm1;
+};
+__device__ __forceinline__ void load_q51sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q51Sb& w) {
+    const uint8_t* p = rowp + sb * 192;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        w.qs[c] = *reinterpret_cast<const uint2*>(p + 24 * c + 8 + 8 * (g % 2));
+        w.qh[c] = *reinterpret_cast<const uint32_t*>(p + 24 * c + 4);
+    }
+    w.dm0 = *reinterpret_cast<const uint32_t*>(p + 48 * g);
+    w.dm1 = *reinterpret_cast<const uint32_t*>(p + 48 * g + 24);
+}
+// elements 8g .. 8g + 7 of block q8 as 8 bytes (q5_1_rows, blocks.py:57-68); q5_hi4 puts four qh
+// bits at bit 4 of four bytes
+__device__ __forceinline__ long q51_operand(const Q51Sb& w, int q8, uint32_t g) {
+    const uint32_t sh = g < 2 ? 0u : 4u, h8 = (w.qh[q8] >> (8 * g)) & 0xffu;
+    const uint32_t lo = ((w.qs[q8].x >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 & 0xfu);
+    const uint32_t hi = ((w.qs[q8].y >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 >> 4);
+    return (long)(((unsigned long long)hi << 32) | lo);
+}
+
+// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
 // q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
 template <int NSB, int FK>
 __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
@@ -1050,12 +1078,16 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
         const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
         return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
     };
-    using W = typename std::conditional<Q6, Q6Sb, typename std::conditional<FK == 2, Q8Sb, Q4Sb>::type>::type;
+    using W = typename std::conditional<
+            Q6, Q6Sb,
+            typename std::conditional<FK == 2, Q8Sb, typename std::conditional<FK == 3, Q51Sb, Q4Sb>::type>::type>::type;
     auto load = [&](uint32_t step, W& w) {
         if constexpr (Q6)
             load_q6sb(row_of(step), step % NSB, g, w);
         else if constexpr (FK == 2)
             load_q8sb(row_of(step), step % NSB, g, w);
+        else if constexpr (FK == 3)
+            load_q51sb(row_of(step), step % NSB, g, w);
         else
             load_q4sb(row_of(step), step % NSB, g, w);
     };
@@ -1074,6 +1106,14 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
             for (int i = 0; i < 4; i++) {
                 const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
                 dmw[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
+            }
+        } else if constexpr (FK == 3) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
+                const uint32_t dm = jj ? cw.dm1 : cw.dm0;
+                const float2 v = make_float2(h2f((uint16_t)(dm & 0xffffu)), h2f((uint16_t)(dm >> 16)));
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
             }
         } else if constexpr (FK == 2) {
 #pragma unroll
@@ -1102,6 +1142,8 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
                 bw = q6_operand(cw, q8);
             else if constexpr (FK == 2)
                 bw = (long)(((unsigned long long)cw.q[q8].y << 32) | cw.q[q8].x);
+            else if constexpr (FK == 3)
+                bw = q51_operand(cw, q8, g);
             else
                 bw = unpack8(cw.qs[q8 / 2], q8 % 2);
             v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
@@ -1146,12 +1188,13 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
     const dim3 grid(m >= 64 ? H / 256 : H / 64, grouped_item_rows(ws, m));
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
-    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : 0;
-    switch (F / 256 * 3 + fk) {
+    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
+    switch (F / 256 * 4 + fk) {
 #define DN_CASE(n)                                                                                    \
-    case n * 3: batch_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;     \
-    case n * 3 + 1: batch_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
-    case n * 3 + 2: batch_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
+    case n * 4: batch_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;     \
+    case n * 4 + 1: batch_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
+    case n * 4 + 2: batch_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
+    case n * 4 + 3: batch_down_kernel<n, 3><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
         default: return hipErrorInvalidValue;

@@ -386,7 +386,7 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
     const uint32_t slots = kcap + 1, units = slots * DN_R;
     const uint32_t wv = tid / 64, ln = tid % 64, q = ln % DL::L;
     const uint32_t sb = q / 2, h2 = q % 2;
-    const bool q4 = down.fmt == TRK_FMT_Q4_K, q8 = down.fmt == TRK_FMT_Q8_0;
+    const bool q4 = down.fmt == TRK_FMT_Q4_K, q8 = down.fmt == TRK_FMT_Q8_0, q5 = down.fmt == TRK_FMT_Q5_1;
 
     int8_t* aq = (int8_t*)smem;                                // [slots][SQ]
     float* as = (float*)(smem + (size_t)slots * SQ);           // [slots][P][nbf] folded scale
@@ -454,6 +454,8 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
             half_terms_q4k<P>(hdr, qs, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
         else if (q8)
             half_terms_q80<P>(rowp, sb, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
+        else if (q5)
+            half_terms_q51<P>(rowp, sb, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
         else
             half_terms_q6k<P>(rowp, sb, h2, a, F, sa, ua, nbf, dotv, tv, mmv, uv);
         // the chain (gemv.rs:141-148) over the unit's lanes in block order

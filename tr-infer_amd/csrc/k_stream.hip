@@ -282,7 +282,7 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void stream_gateup_kernel(Mat gate
 // L = 2 * NSBF lanes, half a superblock each, in chain order (rows never straddle a wave); each
 // lane holds its half superblock and runs every entry of the item against it, two at a time.
 // Outputs are the per-entry rows of yent, combined later in the reference's order.
-// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0
+// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1
 template <int NSBF, int FK>
 __global__ __launch_bounds__(256) void stream_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t max_rows) {
     constexpr uint32_t F = NSBF * 256, nbf = NSBF * 16, L = 2 * NSBF, RPW = 64 / L, RPB = 4 * RPW, SQ = F + 16;
@@ -297,12 +297,17 @@ __global__ __launch_bounds__(256) void stream_down_kernel(Mat down, Mat shd, Wor
     const uint32_t rowc = row < H ? row : H - 1;
     const uint8_t* rowp = (shared ? shd.ptr : down.ptr) + (size_t)e * (shared ? shd.stride : down.stride) +
                           (size_t)rowc * (shared ? shd.row_bytes : down.row_bytes);
-    using W = typename std::conditional<FK == 1, Q6Half, typename std::conditional<FK == 2, Q8Half, v4u[5]>::type>::type;
+    using W = typename std::conditional<
+            FK == 1, Q6Half,
+            typename std::conditional<FK == 2, Q8Half,
+                                      typename std::conditional<FK == 3, Q51Half, v4u[5]>::type>::type>::type;
     W w;
     if constexpr (FK == 1) {
         load_half_q6k(rowp, sb, h2, w);
     } else if constexpr (FK == 2) {
         load_half_q80(rowp, sb, h2, w);
+    } else if constexpr (FK == 3) {
+        load_half_q51(rowp, sb, h2, w);
     } else {
         const v4u* p = reinterpret_cast<const v4u*>(rowp + sb * 144);
         w[0] = p[0];
@@ -333,6 +338,8 @@ __global__ __launch_bounds__(256) void stream_down_kernel(Mat down, Mat shd, Wor
                 half_terms_q6k<1>(w, a, F, as + i * nbf + b0, au + i * nbf + b0, nbf, dotv[n], tv[n], mmv, uv[n]);
             } else if constexpr (FK == 2) {
                 half_terms_q80<1>(w, a, F, as + i * nbf + b0, au + i * nbf + b0, nbf, dotv[n], tv[n], mmv, uv[n]);
+            } else if constexpr (FK == 3) {
+                half_terms_q51<1>(w, a, F, as + i * nbf + b0, au + i * nbf + b0, nbf, dotv[n], tv[n], mmv, uv[n]);
             } else {
                 const uint4 hdr = make_uint4(w[0].x, w[0].y, w[0].z, w[0].w);
                 const uint4 qs[4] = {make_uint4(w[1].x, w[1].y, w[1].z, w[1].w),
@@ -411,16 +418,17 @@ hipError_t launch_stream_down(const Mat& down, const Mat& sh_down, const Workspa
                               uint32_t max_rows, hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nsbf = F / 256, nbf = F / 16;
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
-    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : 0;
+    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
     const size_t cap = max_rows < BR ? max_rows : BR;
     const size_t lds = cap * ((size_t)F + 16 + (size_t)nbf * 8 + 4);
     const uint32_t rpb = 4 * (64 / (2 * nsbf));  // rows per workgroup
     const dim3 grid((H + rpb - 1) / rpb, item_rows(ws, m));
-    switch (nsbf * 3 + fk) {
+    switch (nsbf * 4 + fk) {
 #define SD_CASE(n)                                                                                        \
-    case n * 3: stream_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break;     \
-    case n * 3 + 1: stream_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break; \
-    case n * 3 + 2: stream_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break;
+    case n * 4: stream_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break;     \
+    case n * 4 + 1: stream_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break; \
+    case n * 4 + 2: stream_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break; \
+    case n * 4 + 3: stream_down_kernel<n, 3><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break;
         SD_CASE(1) SD_CASE(2) SD_CASE(3) SD_CASE(4) SD_CASE(5) SD_CASE(6) SD_CASE(7) SD_CASE(8)
 #undef SD_CASE
         default: return hipErrorInvalidValue;

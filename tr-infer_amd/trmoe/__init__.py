@@ -15,7 +15,7 @@ PKG_ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(PKG_ROOT, "libtrmoe.so")
 HEADER = os.path.join(os.path.dirname(PKG_ROOT), "include", "trmoe.h")
 
-FMT_Q4_K, FMT_Q6_K, FMT_Q8_0 = 12, 14, 8
+FMT_Q4_K, FMT_Q6_K, FMT_Q8_0, FMT_Q5_1 = 12, 14, 8, 7
 BASIS_ALL, BASIS_TOP = 0, 1
 K_MAX = 32
 (WS_RLOG, WS_IDS, WS_W, WS_NSEL, WS_ENT_TOK, WS_ENT_W, WS_ENT_EXP, WS_GRP_START, WS_GRP_EXP, WS_NGROUPS, WS_XQ,
@@ -101,7 +101,7 @@ def header_functions() -> list[str]:
 
 
 def row_bytes(fmt: int, k: int) -> int:
-    return k // 256 * {FMT_Q4_K: 144, FMT_Q6_K: 210, FMT_Q8_0: 272}[fmt]
+    return k // 256 * {FMT_Q4_K: 144, FMT_Q6_K: 210, FMT_Q8_0: 272, FMT_Q5_1: 192}[fmt]
 
 
 def _ptr(t):
