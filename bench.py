@@ -55,7 +55,8 @@ def main():
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
     ap.add_argument("--extra", type=str, default="c4,stack",
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
-                         "48-layer RMSNorm + residual stack at M=1 and M=512); '' for none")
+                         "48-layer RMSNorm + residual stack at M=1 and M=512); q80 / q51: the layer at M=1 "
+                         "and M=512 with Q8_0 / Q5_1 downs; '' for none")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
@@ -184,6 +185,10 @@ def main():
     todo = {v for v in args.extra.split(",") if v}
     if "c4" in todo:
         extras["C4 M=3072"] = bench_config4(args, layers, dev, stream, trmoe, torch, np)
+    for key, fmt, nm in (("q80", trmoe.FMT_Q8_0, "Q8_0"), ("q51", trmoe.FMT_Q5_1, "Q5_1")):
+        if key in todo:
+            for Md, res in bench_down_format(args, layers, fmt, nm, dev, stream, trmoe, torch).items():
+                extras[f"{nm} down M={Md}"] = res
     if "stack" in todo:
         for Ms in (1, 512):
             extras[f"C5 stack M={Ms}"] = bench_stack(args, layers, ctx if Ms <= m_max else None, Ms, dev, stream,
@@ -298,6 +303,34 @@ def bench_config4(args, layers, dev, stream, trmoe, torch, np):
             "hbm_frac": round(nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "int8_TOPS": round(nops / (per * 1e-3) / 1e12, 3), "mean_k": round(float(np.mean(ents)) / M, 3),
             "experts_touched": round(float(np.mean(touched)), 1), "layers": len(layers), "steps": steps}
+
+
+def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
+    """The layer with its down projections (routed and shared) regenerated in another GGUF format,
+    at M=1 (no router bias) and M=512 (the Zipf bias), over the same layer rotation."""
+    lw = [w.with_down(fmt, 1, l, device=dev) for l, w in enumerate(layers)]
+    bias = torch.from_numpy(trmoe.zipf_bias(1, E)).to(dev)
+    out_res = {}
+    for M in (1, 512):
+        for w in lw:
+            w.moew.router_bias = bias.data_ptr() if M >= 64 else None
+        ctx = trmoe.Context(H, E, F, K, M)
+        x = trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H)
+        out = torch.empty((M, H), dtype=torch.float32, device=dev)
+        ctx.forward(lw[0], x, out)
+        steps = min(args.steps, 2 * len(lw))
+
+        def body():
+            for i in range(steps):
+                ctx.forward(lw[i % len(lw)], x, out)
+
+        per = timed_graph(torch, stream, body, 1) / steps
+        ctx.close()
+        out_res[M] = {"tokens_per_s": round(M / (per * 1e-3), 1), "us_per_layer": round(per * 1e3, 2),
+                      "layers": len(lw), "steps": steps}
+        log(f"{name} down M={M}: {per * 1e3:.1f} us/layer")
+    del lw
+    return out_res
 
 
 def bench_stack(args, layers, ctx, M, dev, stream, trmoe, torch):
