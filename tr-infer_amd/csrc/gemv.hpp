@@ -239,8 +239,9 @@ __device__ __forceinline__ void load_half_q51(const uint8_t* __restrict__ rowp, 
     }
 }
 // four fifth bits (bits 0-3 of h4) moved to bit 4 of bytes 0-3: h4 * (1 + 2^7 + 2^14 + 2^21) puts
-// bit b at bit 8b (the 16 partial products land on distinct bits, so nothing carries)
-__device__ __forceinline__ uint32_t q5_hi4(uint32_t h4) { return ((h4 * 0x204081u) & 0x01010101u) << 4; }
+// bit b at bit 8b (the 16 partial products land on distinct bits, so nothing carries); both
+// factors fit 24 bits, so the full-rate 24-bit multiply gives the product
+__device__ __forceinline__ uint32_t q5_hi4(uint32_t h4) { return (__umul24(h4, 0x204081u) & 0x01010101u) << 4; }
 
 template <int P>
 __device__ __forceinline__ void half_terms_q51(const Q51Half& w, const int8_t* __restrict__ aq, uint32_t F,
