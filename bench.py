@@ -315,6 +315,8 @@ def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
         for w in lw:
             w.moew.router_bias = bias.data_ptr() if M >= 64 else None
         ctx = trmoe.Context(H, E, F, K, M)
+        if args.stream_rows is not None:
+            ctx.set_stream_rows(args.stream_rows)
         x = trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H)
         out = torch.empty((M, H), dtype=torch.float32, device=dev)
         ctx.forward(lw[0], x, out)
