@@ -72,7 +72,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU: the MoE block on one MI355X; "
-                                   "multi-GPU sharding is design-only (see DESIGN.md)", "n_gpus": args.gpus}))
+                                   "multi-GPU sharding is not built (expert parallelism over RCCL is a "
+                                   "design only)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
