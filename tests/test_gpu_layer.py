@@ -254,15 +254,16 @@ def test_q6k_down(M, rows):
     ctx.close()
 
 
+@pytest.mark.parametrize("F", [256, 768])  # 768: three 256-value units per down row
 @pytest.mark.parametrize("fmt", [O.FMT_Q8_0, O.FMT_Q5_1])
 @pytest.mark.parametrize("M", [1, 6, 40, 80])
-def test_q80_q51_down(fmt, M):
+def test_q80_q51_down(fmt, M, F):
     """Q8_0 and Q5_1 downs (the reference's q8_0_rows / q5_1_rows forms: q = int8 + 128 with
     m = f16(-128 d); 5-bit q with d, m as stored) on every down kernel: the decode path (M = 1),
     and for batches every split between the streaming GEMV and the MFMA tiles gives the same
     bits, within tolerance of the oracle's TQ8_16 / TQ5_16 GEMV."""
-    say(f"down fmt={fmt} M={M}")
-    L, orc, W = layer(f"dfmt{fmt}", seed=6, H=512, E=16, F=256, down_fmt=fmt)
+    say(f"down fmt={fmt} M={M} F={F}")
+    L, orc, W = layer(f"dfmt{fmt}F{F}", seed=6, H=512, E=16, F=F, down_fmt=fmt)
     import torch
     x = L.x(M, tid=410)
     r = orc.moe_block(x[0], k=3) if M == 1 else orc.moe_batch(x, k=3)
