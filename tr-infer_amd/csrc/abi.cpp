@@ -54,14 +54,11 @@ static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "qua
 // average at most two per expert (most routed items hold one or two rows, the shared expert's
 // 16); none beyond, where tail items share their expert's weights with its full tiles and a
 // split costs more than it saves (measured at M = 512 and 3072).
-// Items of at most this many rows take the streaming kernels.  Q5_1 downs cost the MFMA tiles the
-// most per 32-chunk (operands built from nibbles and qh bits), so their small items stream at any
-// batch size (M=512 Zipf layer 627 -> 571 us); for the other formats only while few rows share
-// an expert.
-static uint32_t auto_stream_rows(uint32_t m, uint32_t kcap, uint32_t E, uint32_t down_fmt) {
+// Items of at most this many rows take the streaming kernels: every item up to BR tokens, items of
+// up to 4 rows while few rows share an expert, none beyond.
+static uint32_t auto_stream_rows(uint32_t m, uint32_t kcap, uint32_t E) {
     if (m <= BR) return BR;
-    if ((uint64_t)m * kcap <= 2ull * E) return 4u;
-    return down_fmt == TRK_FMT_Q5_1 ? 4u : 0u;
+    return (uint64_t)m * kcap <= 2ull * E ? 4u : 0u;
 }
 
 struct TimedLaunch {
@@ -349,7 +346,7 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
             TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         }
         // items of few rows on the streaming GEMV, the others on the MFMA tiles (same bits)
-        const uint32_t sr = c->stream_rows >= 0 ? (uint32_t)c->stream_rows : auto_stream_rows(m, kcap, E, M.down.fmt);
+        const uint32_t sr = c->stream_rows >= 0 ? (uint32_t)c->stream_rows : auto_stream_rows(m, kcap, E);
         if (sr > 0) TIMED(K_S_GATEUP, launch_stream_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
         if (sr < BR) TIMED(K_B_GATEUP, launch_batch_gateup(M.gate, M.up, M.shg, M.shu, ws, m, sr, st));
         if (sr > 0) TIMED(K_S_DOWN, launch_stream_down(M.down, M.shd, ws, m, sr, st));

@@ -982,29 +982,35 @@ __device__ __forceinline__ void load_q8sb(const uint8_t* __restrict__ rowp, uint
 }
 
 // Q5_1 operands of one unit of 8 blocks (192 bytes, 16-byte aligned) for lane (g, r): per block c
-// the 8 qs bytes whose low (g < 2) or high (g >= 2) nibbles are elements 8g .. 8g + 7, the block's
-// qh, and the (d, m) words of blocks 2g and 2g + 1.
+// one 16-byte load, at block byte 4 for even g (qh, qs 0-11) and 8 for odd g (qs 0-15), so a lane
+// holds the qs bytes whose low (g < 2) or high (g >= 2) nibbles are elements 8g .. 8g + 7; an odd
+// lane takes qh from its even partner 16 lanes away (permlane16 swap) when the operand is built,
+// not at load time, so the loads stay in flight.  Plus the (d, m) words of blocks 2g and 2g + 1.
 struct Q51Sb {
-    uint2 qs[8];
-    uint32_t qh[8];
+    uint4 v[8];
     uint32_t dm0, dm1;
 };
 __device__ __forceinline__ void load_q51sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q51Sb& w) {
     const uint8_t* p = rowp + sb * 192;
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-        w.qs[c] = *reinterpret_cast<const uint2*>(p + 24 * c + 8 + 8 * (g % 2));
-        w.qh[c] = *reinterpret_cast<const uint32_t*>(p + 24 * c + 4);
-    }
+    for (int c = 0; c < 8; c++) w.v[c] = *reinterpret_cast<const uint4*>(p + 24 * c + (g % 2 ? 8 : 4));
     w.dm0 = *reinterpret_cast<const uint32_t*>(p + 48 * g);
     w.dm1 = *reinterpret_cast<const uint32_t*>(p + 48 * g + 24);
 }
 // elements 8g .. 8g + 7 of block q8 as 8 bytes (q5_1_rows, blocks.py:57-68); q5_hi4 puts four qh
-// bits at bit 4 of four bytes
+// bits at bit 4 of four bytes.  The swap pairs lane groups 0/1 and 2/3 and leaves, in an odd
+// group's lanes, their own first word in one result and the partner's (qh) in the other: the
+// partner's is the one that differs (if they are equal, either is qh).
 __device__ __forceinline__ long q51_operand(const Q51Sb& w, int q8, uint32_t g) {
-    const uint32_t sh = g < 2 ? 0u : 4u, h8 = (w.qh[q8] >> (8 * g)) & 0xffu;
-    const uint32_t lo = ((w.qs[q8].x >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 & 0xfu);
-    const uint32_t hi = ((w.qs[q8].y >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 >> 4);
+    const uint4 v = w.v[q8];
+    const bool odd = g % 2;
+    const auto sw = __builtin_amdgcn_permlane16_swap(v.x, v.x, false, false);
+    const uint32_t other = sw[0] == v.x ? sw[1] : sw[0];
+    const uint32_t qh = odd ? other : v.x;
+    const uint32_t qlo = odd ? v.z : v.y, qhi = odd ? v.w : v.z;
+    const uint32_t sh = g < 2 ? 0u : 4u, h8 = (qh >> (8 * g)) & 0xffu;
+    const uint32_t lo = ((qlo >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 & 0xfu);
+    const uint32_t hi = ((qhi >> sh) & 0x0f0f0f0fu) | q5_hi4(h8 >> 4);
     return (long)(((unsigned long long)hi << 32) | lo);
 }
 
