@@ -828,19 +828,14 @@ hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gat
 // input is quantised per 16, so each 32-byte activation chunk feeds two MFMAs with the other
 // half of its k-groups zeroed, giving the exact dot of each 16-block.
 
-// Q6_K operands of one superblock for lane (g, r), read with 2-byte loads (superblocks are only
-// 2-byte aligned): ql bytes 64n + 32s + 8g (n, s in {0, 1}), qh bytes 128 + 32n + 8g, the
-// scales of blocks 4g .. 4g+3 (this lane decodes them) and d.
+// Q6_K operands of one superblock for lane (g, r) (superblocks are only 2-byte aligned, so each
+// piece comes from an aligned load and byte alignment): ql bytes 64n + 32s + 8g (n, s in {0, 1}),
+// qh bytes 128 + 32n + 8g, the scales of blocks 4g .. 4g+3 (this lane decodes them) and d.
 struct Q6Sb {
     uint2 ql[4], qh[2];
     uint32_t sc;  // int8 scales of blocks 4g .. 4g+3
     uint16_t d;
 };
-__device__ __forceinline__ uint32_t ld32_a2(const uint8_t* p) {
-    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
-    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
-}
-__device__ __forceinline__ uint2 ld64_a2(const uint8_t* p) { return make_uint2(ld32_a2(p), ld32_a2(p + 4)); }
 // 8 bytes at p + o (p 2-byte aligned) from one 12-byte load at the 4-byte boundary below, shifted
 // by the superblock's misalignment (0 or 2 bytes; the load stays inside the superblock when
 // 2 <= o + 12 - shift <= 210 and o >= shift, as for every ql / qh piece)
@@ -857,7 +852,10 @@ __device__ __forceinline__ void load_q6sb(const uint8_t* __restrict__ rowp, uint
     for (int i = 0; i < 4; i++) w.ql[i] = ld64_sh(pa, 64 * (i / 2) + 32 * (i % 2) + 8 * g, sh);
 #pragma unroll
     for (int n = 0; n < 2; n++) w.qh[n] = ld64_sh(pa, 128 + 32 * n + 8 * g, sh);
-    w.sc = ld32_a2(p + 192 + 4 * g);
+    // the 4 scale bytes 192 + 4g: one 8-byte load that stays inside the superblock (at 188 + 4g
+    // when p is 4-byte aligned, else at the 4-byte boundary 2 below 192 + 4g), then the bytes
+    const uint2 sv = *reinterpret_cast<const uint2*>(sh ? pa + 192 + 4 * g : p + 188 + 4 * g);
+    w.sc = sh ? __builtin_amdgcn_alignbyte(sv.y, sv.x, 2) : sv.y;
     w.d = *reinterpret_cast<const uint16_t*>(p + 208);
 }
 // 8 consecutive 6-bit values e = 32*q8 + 8g .. +7 of the superblock (q8 compile-time)
