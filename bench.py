@@ -55,8 +55,8 @@ def main():
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
     ap.add_argument("--extra", type=str, default="c4,stack",
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
-                         "48-layer RMSNorm + residual stack at M=1 and M=512); q80 / q51: the layer at M=1 "
-                         "and M=512 with Q8_0 / Q5_1 downs; '' for none")
+                         "48-layer RMSNorm + residual stack at M=1 and M=512); q80 / q51 / q6k: the layer at "
+                         "M=1 and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
@@ -186,7 +186,8 @@ def main():
     todo = {v for v in args.extra.split(",") if v}
     if "c4" in todo:
         extras["C4 M=3072"] = bench_config4(args, layers, dev, stream, trmoe, torch, np)
-    for key, fmt, nm in (("q80", trmoe.FMT_Q8_0, "Q8_0"), ("q51", trmoe.FMT_Q5_1, "Q5_1")):
+    for key, fmt, nm in (("q80", trmoe.FMT_Q8_0, "Q8_0"), ("q51", trmoe.FMT_Q5_1, "Q5_1"),
+                         ("q6k", trmoe.FMT_Q6_K, "Q6_K")):
         if key in todo:
             for Md, res in bench_down_format(args, layers, fmt, nm, dev, stream, trmoe, torch).items():
                 extras[f"{nm} down M={Md}"] = res
