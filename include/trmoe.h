@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TRK_ABI_VERSION 1
+#define TRK_ABI_VERSION 2
 #define TRK_MOE_K_MAX 32 /* router.rs:6 MOE_K_MAX */
 
 typedef enum {
@@ -35,7 +35,9 @@ typedef enum {
     TRK_E_POLICY = -2,   /* MoePolicy::validate (router.rs:32-44) */
     TRK_E_CAPACITY = -3, /* more rows than the context was created for */
     TRK_E_HIP = -4,      /* a HIP runtime call failed */
-    TRK_E_NOMEM = -5
+    TRK_E_NOMEM = -5,
+    TRK_E_TIMEOUT = -6   /* a device-side wait of the one-launch decode layer gave up (bounded spin):
+                            the outputs of the calls since the last trk_get_stats are invalid */
 } trk_status;
 
 enum { TRK_FMT_Q5_1 = 7, TRK_FMT_Q8_0 = 8, TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
@@ -120,8 +122,21 @@ int trk_moe_forward(trk_ctx *ctx, const trk_moe_w *w, const float *x, const floa
 int trk_moe_residual(trk_ctx *ctx, const trk_moe_w *w, const float *rms_w, float eps, float *h,
                      uint32_t m, void *stream);
 
-/* Read (and optionally reset) the routing counters; synchronises the device. */
-int trk_get_stats(trk_ctx *ctx, trk_moe_stats *out, int reset);
+/* Read (and optionally reset) the routing counters, ordered after the work queued on `stream`
+ * (synchronises that stream only).  Returns TRK_E_TIMEOUT, with the counters filled, when a
+ * device-side wait of the one-launch decode layer timed out since the last call (and clears that
+ * flag): the outputs of those calls are invalid.  Replaces MoeStats::snapshot (exec.rs:593-595). */
+int trk_get_stats(trk_ctx *ctx, trk_moe_stats *out, int reset, void *stream);
+
+/* Router-mass profiling: MoeStats::profile_start (exec.rs:567-573) zeroes the profile and turns it
+ * on; every later forward then adds each row's router::mass_profile (router.rs:152-166: the
+ * cumulative softmax mass of its best 1..32 experts, fixed point 1e-6) to it, as
+ * MoeStats::profile_row (exec.rs:582-592) does.  trk_profile_report (exec.rs:575-581) writes the
+ * mean cumulative mass of the best k experts, k = 1..32, to cum[32] (host memory) and the number of
+ * profiled rows to *rows, ordered after `stream` (synchronises it); on = 0 in trk_profile_start
+ * turns profiling off. */
+int trk_profile_start(trk_ctx *ctx, int on, void *stream);
+int trk_profile_report(trk_ctx *ctx, double *cum, uint64_t *rows, void *stream);
 
 /* Message of the last error on this thread (static storage). */
 const char *trk_last_error(void);
@@ -203,7 +218,7 @@ int trk_get_timing(trk_ctx *ctx, const char **names, double *ms, uint64_t *launc
 int trk_launch_kernel(trk_ctx *ctx, const trk_moe_w *w, const float *x, const float *rlog, uint32_t m,
                       float *out, const char *name, void *stream);
 
-/* Copy an internal workspace buffer of the last forward to host memory (synchronises). */
+/* Copy an internal workspace buffer of the last forward to host memory. */
 enum {
     TRK_WS_RLOG = 1,     /* [M][E] f32 */
     TRK_WS_IDS = 2,      /* [M][32] u32 */
@@ -222,7 +237,8 @@ enum {
     TRK_WS_SHLOGIT = 15, /* [M] f32: dot(shexp_gate, x) */
     TRK_WS_BARRIER_ERR = 16 /* u32: nonzero if a one-launch decode layer ever timed out at a grid barrier */
 };
-int trk_debug_read(trk_ctx *ctx, int which, void *host_dst, size_t bytes);
+/* Ordered after the work queued on `stream` (synchronises that stream only). */
+int trk_debug_read(trk_ctx *ctx, int which, void *host_dst, size_t bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -174,6 +174,26 @@ def q6k_rows(raw, rows, K):
     return q, dd, mm
 
 
+def q80_rows(raw, rows, K):
+    """blocks.py:71-78 q8_0_rows: (q = int8 + 128, d, m = f16(-128 d)) per 32."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    q = np.zeros((rows, K), np.uint8)
+    d = np.zeros((rows, K // 32), np.uint16)
+    m = np.zeros((rows, K // 32), np.uint16)
+    lib().orc_q80_rows(_p(raw), rows, K, _p(q), _p(d), _p(m))
+    return q, d, m
+
+
+def q51_rows(raw, rows, K):
+    """blocks.py:57-68 q5_1_rows: (5-bit q, d, m as stored) per 32."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    q = np.zeros((rows, K), np.uint8)
+    d = np.zeros((rows, K // 32), np.uint16)
+    m = np.zeros((rows, K // 32), np.uint16)
+    lib().orc_q51_rows(_p(raw), rows, K, _p(q), _p(d), _p(m))
+    return q, d, m
+
+
 def gguf_row_bytes(fmt, K):
     return lib().orc_gguf_row_bytes(fmt, K)
 

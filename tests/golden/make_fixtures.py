@@ -3,10 +3,12 @@
 Run once, in the build container, where the reference checkout exists:
     python tests/golden/make_fixtures.py /root/reference
 
-It imports the reference's `python/trpack/blocks.py` (q4k_rows, rows_to_groups) and
+It imports the reference's `python/trpack/blocks.py` (q4k_rows, q8_0_rows, q5_1_rows,
+rows_to_groups) and
 `python/trpack/codec.py` (pack_tq) — both numpy-only — and records their outputs on small,
-seeded inputs.  These are the only pins for the Q4_K scale/min bit layout and the TQ byte layout
-that do not depend on this repository's own reading of them.  The fixtures are data only
+seeded inputs.  These are the only pins for the Q4_K scale/min bit layout, the (q, d, m) forms of
+the Q8_0 / Q5_1 conversions and the TQ byte layout that do not depend on this repository's own
+reading of them.  The fixtures are data only
 (inputs and expected outputs); the tests never import the reference.
 """
 from __future__ import annotations
@@ -76,6 +78,38 @@ def main(ref_root: str) -> None:
     ])
     out["f16_in"] = f
     out["f16_out"] = f.astype(np.float16).view(np.uint16)
+
+    # --- Q8_0 / Q5_1 rows (the real model's down formats): random blocks plus edge cases -------
+    rows, K = 5, 256
+    nb = K // 32
+    raw8 = rng.integers(0, 256, size=(rows, nb * 34), dtype=np.uint8)
+    raw5 = rng.integers(0, 256, size=(rows, nb * 24), dtype=np.uint8)
+    for r in range(rows):
+        for b in range(nb):
+            d = np.float16(rng.uniform(1e-4, 2e-3))
+            m = np.float16(-rng.uniform(1e-3, 3e-2))
+            raw8[r, 34 * b:34 * b + 2] = np.frombuffer(d.tobytes(), np.uint8)
+            raw5[r, 24 * b:24 * b + 2] = np.frombuffer(d.tobytes(), np.uint8)
+            raw5[r, 24 * b + 2:24 * b + 4] = np.frombuffer(m.tobytes(), np.uint8)
+    # row 3: d near the f16 limit (-128 d overflows f16 to -inf), a subnormal d, d = 0, d = -0;
+    # row 4: int8 extremes -128 / 127 / 0 / -1
+    for b, dv in enumerate([65504.0, 600.0, 512.0, 6e-8, 0.0, -0.0, -3.0, 1.0]):
+        raw8[3, 34 * b:34 * b + 2] = np.frombuffer(np.float16(dv).tobytes(), np.uint8)
+        raw5[3, 24 * b:24 * b + 2] = np.frombuffer(np.float16(dv).tobytes(), np.uint8)
+    raw8[4, 2:34] = 0x80
+    raw8[4, 36:68] = 0x7F
+    raw8[4, 70:102] = 0x00
+    raw8[4, 104:136] = 0xFF
+    # Q5_1 qh: all ones, all zeros, alternating, one bit per half
+    raw5[4, 4:8] = 0xFF
+    raw5[4, 24 + 4:24 + 8] = 0x00
+    raw5[4, 48 + 4:48 + 8] = 0xAA
+    raw5[4, 72 + 4:72 + 8] = [0x01, 0x00, 0x01, 0x00]
+    q8, d8, m8 = blocks.q8_0_rows(raw8, K)
+    q5, d5, m5 = blocks.q5_1_rows(raw5, K)
+    out["q80_raw"], out["q80_q"], out["q80_d"], out["q80_m"] = raw8, q8, d8.view(np.uint16), m8.view(np.uint16)
+    out["q51_raw"], out["q51_q"], out["q51_d"], out["q51_m"] = raw5, q5, d5.view(np.uint16), m5.view(np.uint16)
+
 
     path = os.path.join(HERE, "blocks_codec.npz")
     np.savez_compressed(path, **out)

@@ -51,3 +51,21 @@ def test_build_flags_keep_numerics_contract():
     for flag in ("-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt", "-packed-fp32-ops",
                  "--offload-arch=$(ARCH)"):
         assert flag in mk
+
+
+def test_generator_rejects_undersized_stride():
+    """trk_gen_gguf_stack sizes each matrix by its own format (Q8_0: 272 B and Q5_1: 192 B per 256
+    values), so a stride one piece short is refused before anything is written."""
+    L = trmoe.lib()
+    rows, k = 4, 512
+    for fmt in (trmoe.FMT_Q4_K, trmoe.FMT_Q6_K, trmoe.FMT_Q8_0, trmoe.FMT_Q5_1):
+        need = rows * trmoe.row_bytes(fmt, k)
+        rc = L.trk_gen_gguf_stack(fmt, 1, 0, 1, 2, rows, k, 1e-4, 2e-3, C.c_void_p(256), need - 16, None)
+        assert rc == -1 and b"stride" in L.trk_last_error(), fmt
+
+
+def test_stats_and_profile_reject_null_arguments():
+    L = trmoe.lib()
+    assert L.trk_get_stats(None, None, 0, None) == -1
+    assert L.trk_profile_report(None, None, None, None) == -1
+    assert L.trk_profile_start(None, 1, None) == -1

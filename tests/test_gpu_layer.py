@@ -44,6 +44,17 @@ def compare_out(got, want, w_equal, ctx=""):
         assert err <= 1e-5 * scale, f"{ctx}: {err} vs scale {scale}"
 
 
+def ulp(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+def slot_of(ids, toks, exps):
+    """Slot index of expert exps[i] in token toks[i]'s selection (ids [M][k])."""
+    return np.array([int(np.flatnonzero(ids[t] == e)[0]) for t, e in zip(toks, exps)], np.int64)
+
+
 def _libm_expf():
     import ctypes as C
     f = C.CDLL("libm.so.6").expf
@@ -139,7 +150,7 @@ def test_decode_one_launch_matches_three(policy):
 
 
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
-                                       ("full", 16, 10), ("small", 700, 3), ("small", 2200, 2)])
+                                       ("full", 8, 10), ("full", 16, 10), ("small", 700, 3), ("small", 2200, 2)])
 def test_batch_layer_and_dispatch(shape, M, k):
     # M = 700: the split (parallel) scatter; M = 2200: three rounds of 1024 tokens, 35 chunks
     say(f"batch layer {shape} M={M} k={k}")
@@ -162,6 +173,14 @@ def test_batch_layer_and_dispatch(shape, M, k):
     assert np.array_equal(ctx.read(trmoe.WS_ENT_EXP, 4 * n_ent, np.uint32), r["ent_expert"])
     assert np.array_equal(ctx.read(trmoe.WS_GRP_START, 4 * (ng + 1), np.uint32), r["grp_start"])
     assert np.array_equal(ctx.read(trmoe.WS_GRP_EXP, 4 * ng, np.uint32), r["grp_expert"])
+    # ent_w: the routing weights in entry order (exact where the GPU's weights equal the oracle's,
+    # which differ by at most 1 ulp of libm expf otherwise)
+    ent_w = ctx.read(trmoe.WS_ENT_W, 4 * n_ent, np.float32)
+    if np.array_equal(w, r["w"][:, :k]):
+        assert np.array_equal(ent_w.view(np.uint32), r["ent_w"].view(np.uint32))
+    else:
+        assert ulp(ent_w, r["ent_w"]).max() <= 3  # w = e / sum, e from libm expf (1 ulp)
+    assert np.array_equal(ent_w.view(np.uint32), w[r["ent_tok"], slot_of(ids, r["ent_tok"], r["ent_expert"])].view(np.uint32))
     xq = ctx.read(trmoe.WS_XQ, M * L.H, np.int8).reshape(M, L.H)
     assert np.array_equal(xq, O.quant_rows(x, 32)[0])
     compare_out(host(out), r["out"], np.array_equal(w, r["w"][:, :k]) and shared_gate_exact(L, x), f"{shape} M={M}")
@@ -234,24 +253,51 @@ def test_dynamic_k_policy(M):
         r = orc.moe_batch(x, k=4, policy=pol)
         assert np.array_equal(nsel, r["n_sel"])
         assert 1 <= nsel.min() and nsel.max() <= 8
-        compare_out(host(out), r["out"], False, "batch policy")
+        ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+        exact = shared_gate_exact(L, x)
+        for t in range(M):
+            assert np.array_equal(ids[t, :nsel[t]], r["ids"][t, :nsel[t]])
+            exact = exact and np.array_equal(w[t, :nsel[t]], r["w"][t, :nsel[t]])
+        compare_out(host(out), r["out"], exact, "batch policy")
     ctx.close()
 
 
-@pytest.mark.parametrize("M,rows", [(1, -1), (6, -1), (6, 0), (40, 16), (80, 0)])
-def test_q6k_down(M, rows):
-    say(f"q6k down M={M} stream rows {rows}")
-    L, orc, W = layer("q6", seed=4, H=512, E=16, F=256, down_fmt=O.FMT_Q6_K)
-    ctx = trmoe.Context(L.H, L.E, L.F, 3, max(64, M))
-    ctx.set_stream_rows(rows)
+def routing_exact(ctx, r, M, k, L, x):
+    """True when the GPU's routing weights (and shared gate) equal the oracle's bit for bit: the
+    outputs must then be identical too."""
+    if M == 1:
+        w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:len(r["w"])]
+        same = np.array_equal(w, r["w"])
+    else:
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :k]
+        same = np.array_equal(w, r["w"][:, :k])
+    return same and shared_gate_exact(L, x)
+
+
+@pytest.mark.parametrize("F", [256, 768])  # 768: three 256-value units per down row
+@pytest.mark.parametrize("M", [1, 6, 40, 80])
+def test_q6k_down(M, F):
+    """Q6_K downs (unsigned 6-bit q, dd = f16(d sc), mm = f16(-32 dd)) on every down kernel: the
+    decode path (M = 1), and for batches every split between the streaming GEMV and the MFMA tiles
+    gives the same bits, identical to the oracle's TQ8_16 path where the routing weights agree."""
+    say(f"q6k down M={M} F={F}")
+    L, orc, W = layer(f"q6F{F}", seed=4, H=512, E=16, F=F, down_fmt=O.FMT_Q6_K)
     import torch
     x = L.x(M, tid=400)
-    out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
-    ctx.forward(W, dev(x), out)
     r = orc.moe_block(x[0], k=3) if M == 1 else orc.moe_batch(x, k=3)
     want = r["out"][None] if M == 1 else r["out"]
-    compare_out(host(out), want, False, f"q6k M={M}")
-    ctx.close()
+    outs = []
+    for rows in ((-1,) if M == 1 else (0, 1, 4, 16, -1)):
+        ctx = trmoe.Context(L.H, L.E, L.F, 3, max(64, M))
+        ctx.set_stream_rows(rows)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        outs.append(host(out).copy())
+        compare_out(outs[-1], want, routing_exact(ctx, r, M, 3, L, x), f"q6k M={M} F={F} rows={rows}")
+        ctx.close()
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
 
 
 @pytest.mark.parametrize("F", [256, 768])  # 768: three 256-value units per down row
@@ -275,9 +321,7 @@ def test_q80_q51_down(fmt, M, F):
         out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
         ctx.forward(W, dev(x), out)
         outs.append(host(out).copy())
-        exact = M > 1 and np.array_equal(ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :3],
-                                         r["w"][:, :3]) and shared_gate_exact(L, x)
-        compare_out(outs[-1], want, exact, f"fmt={fmt} M={M} rows={rows}")
+        compare_out(outs[-1], want, routing_exact(ctx, r, M, 3, L, x), f"fmt={fmt} M={M} rows={rows}")
         ctx.close()
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
@@ -374,4 +418,145 @@ def test_prefill_zipf_full_size_sampled():
         r = orc.moe_batch(xt, k=10, router_dot_max_m=0)
         assert np.array_equal(r["ids"][0, :10], ids[t])
         compare_out(got[t], r["out"][0], False, f"token {t}")
+    ctx.close()
+
+
+def full_layer_on_gpu(seed, layer_idx, down_fmt=O.FMT_Q4_K, bias=None):
+    """A BASELINE-shape layer (H 2048, E 512, F 512) generated on the GPU, with the host's lazy twin
+    for the oracle.  The router and shared-gate vector are uploaded from the host: f32 normals may
+    differ by an ulp between the host's and the GPU's libm."""
+    import torch
+    H, E, F = 2048, 512, 512
+    L = Layer(seed=seed, H=H, E=E, F=F, layer=layer_idx, down_fmt=down_fmt, bias=bias, lazy=True)
+    W = trmoe.LayerWeights.generate(seed, layer_idx, H, E, F, down_fmt=down_fmt,
+                                    router_bias=None if bias is None else dev(bias))
+    W.tensors["router"].copy_(dev(L.router.reshape(-1)))
+    W.tensors["shexp_gate"].copy_(dev(L.shexp_gate))
+    torch.cuda.synchronize()
+    for e in (0, 511):  # the GPU generator and the host generator produce the same bytes
+        assert np.array_equal(host(W.tensors["down"][e]), L.down(e))
+    return L, W
+
+
+def test_config4_full_shape():
+    """BASELINE config 4 at its own shape: M = 3072, Q4_K gate/up with Q6_K downs, dynamic-k
+    routing MoePolicy{min 1, max 10, mass 0.9, basis Top}.  Every token's n_sel and ids against
+    route_mass (router.rs:118-148) on the GPU's logits, the whole dispatch against the stable sort
+    of exec_batch.rs:1428-1462, sampled logits rows against gemm_f32_nt, and sampled tokens'
+    outputs against moe_batch (bit-identical where the routing weights agree)."""
+    say("config 4 full shape M=3072")
+    import torch
+    M, k, pol = 3072, 10, (1, 10, 0.9, O.BASIS_TOP)
+    L, W = full_layer_on_gpu(1, 0, down_fmt=O.FMT_Q6_K)
+    ctx = trmoe.Context(L.H, L.E, L.F, k, M)
+    ctx.set_moe(pol)
+    x = L.x(M, tid=640)
+    out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+    ctx.forward(W, dev(x), out)
+    torch.cuda.synchronize()
+    rlog = ctx.read(trmoe.WS_RLOG, M * L.E * 4, np.float32).reshape(M, L.E)
+    ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+    w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+    nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+    say("config 4: routing every token")
+    w_exact = np.ones(M, bool)
+    for t in range(M):
+        oi, ow = O.route_mass(rlog[t], *pol)
+        assert nsel[t] == len(oi), t
+        assert np.array_equal(ids[t, :nsel[t]], oi), t
+        # w = e / sum with e = exp(v - max): a 1-ulp difference of libm's expf in e (and in the
+        # sum) moves the quotient by at most 3 ulps
+        assert ulp(w[t, :nsel[t]], ow).max() <= 3, t
+        w_exact[t] = np.array_equal(w[t, :nsel[t]], ow)
+    assert 1 <= nsel.min() and nsel.max() <= 10 and 3 < nsel.mean() < 10
+    say("config 4: dispatch")
+    ng, n_ent = ctx.read(trmoe.WS_NGROUPS, 16, np.uint32)[:2]
+    assert n_ent == nsel.sum()
+    tok = np.repeat(np.arange(M), nsel)
+    slot = np.concatenate([np.arange(n) for n in nsel])
+    exp = ids[tok, slot]
+    order = np.lexsort((tok, exp))  # stable sort of token-major entries by expert
+    assert np.array_equal(ctx.read(trmoe.WS_ENT_TOK, 4 * n_ent, np.uint32), tok[order])
+    assert np.array_equal(ctx.read(trmoe.WS_ENT_EXP, 4 * n_ent, np.uint32), exp[order])
+    ent_w = ctx.read(trmoe.WS_ENT_W, 4 * n_ent, np.float32)
+    assert np.array_equal(ent_w.view(np.uint32), w[tok, slot][order].view(np.uint32))
+    sizes = np.bincount(exp, minlength=L.E)
+    gs = np.concatenate([[0], np.cumsum(sizes[sizes > 0])]).astype(np.uint32)
+    assert ng == (sizes > 0).sum()
+    assert np.array_equal(ctx.read(trmoe.WS_GRP_START, 4 * (ng + 1), np.uint32), gs)
+    assert np.array_equal(ctx.read(trmoe.WS_GRP_EXP, 4 * ng, np.uint32), np.flatnonzero(sizes).astype(np.uint32))
+    assert ctx.stats() == (M, n_ent)
+    got = host(out)
+    assert np.isfinite(got).all()
+    orc = L.oracle()
+    for t in (0, 1, 1000, 2047, 3071):
+        say(f"config 4: token {t}")
+        xt = x[t:t + 1]
+        assert np.array_equal(rlog[t].view(np.uint32), orc.logits(xt, dot_rows=False)[0].view(np.uint32))
+        r = orc.moe_batch(xt, k=k, policy=pol, router_dot_max_m=0)
+        assert np.array_equal(r["ids"][0, :nsel[t]], ids[t, :nsel[t]])
+        compare_out(got[t], r["out"][0], bool(w_exact[t]) and shared_gate_exact(L, xt), f"C4 token {t}")
+    ctx.close()
+
+
+def test_config5_residual_full_m512():
+    """BASELINE config 5 at M = 512 over two full-size layers: h <- h + MoE(rmsnorm(h)) through
+    trk_moe_residual (rmsnorm_kernel, then the GEMM-order router).  After each layer, sampled rows
+    against orc_rmsnorm + orc_moe_batch from the GPU's own input rows (elem.rs:255-262,
+    exec_batch.rs:1404-1580); bit-identical where the routing weights agree."""
+    say("config 5 M=512, two full layers")
+    import torch
+    M, k = 512, 10
+    ctx = trmoe.Context(2048, 512, 512, k, M)
+    h = dev(Layer(seed=1, H=2048, E=4, F=256, lazy=True).x(M, tid=660))
+    for l in range(2):
+        L, W = full_layer_on_gpu(1, l)
+        rms = O.gen_uniform(1, (l << 32) | 4, 2048, 0.9, 1.1)
+        h_in = host(h).copy()
+        ctx.residual(W, dev(rms), 1e-6, h)
+        torch.cuda.synchronize()
+        h_out = host(h)
+        assert np.isfinite(h_out).all()
+        ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)[:, :k]
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :k]
+        orc = L.oracle()
+        for t in (0, 255, 511):
+            say(f"config 5: layer {l} row {t}")
+            xn = O.rmsnorm(h_in[t], rms, 1e-6)[None]
+            r = orc.moe_batch(xn, k=k, router_dot_max_m=0)
+            assert np.array_equal(r["ids"][0, :k], ids[t])
+            want = (h_in[t] + r["out"][0]).astype(np.float32)
+            exact = np.array_equal(r["w"][0, :k], w[t]) and shared_gate_exact(L, xn)
+            compare_out(h_out[t], want, exact, f"C5 layer {l} row {t}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("M", [1, 37])
+def test_mass_profile(M):
+    """MoeStats's router-mass profile (exec.rs:566-591, router.rs:152-166) on the GPU: the mean
+    cumulative mass of the best 1..32 experts over every routed row, against the oracle's
+    mass_profile in the same fixed point (1e-6 per row; the GPU's exp may differ from libm's expf
+    by an ulp, so a row's fixed-point value may differ by a unit or two)."""
+    say(f"mass profile M={M}")
+    import torch
+    L, orc, W = layer("small", **SMALL)
+    ctx = trmoe.Context(L.H, L.E, L.F, 4, 64)
+    ctx.profile_start()
+    want = np.zeros(32)
+    rows = 0
+    for it in range(3):
+        x = L.x(M, tid=680 + it)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        lg = orc.logits(x, M < 16)
+        for t in range(M):
+            want += np.floor(O.mass_profile(lg[t]).astype(np.float64) * 1e6)
+            rows += 1
+    cum, n = ctx.profile_report()
+    assert n == rows
+    assert np.abs(cum - want * 1e-6 / rows).max() <= 3e-6
+    assert np.all(np.diff(cum) >= -1e-12) and cum[-1] <= 1.0 + 1e-6
+    ctx.profile_start(False)
+    ctx.forward(W, dev(L.x(M, tid=690)), out)
+    assert ctx.profile_report()[1] == rows  # off: nothing added
     ctx.close()

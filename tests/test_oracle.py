@@ -54,6 +54,19 @@ def test_q4k_rows_golden(gold):
     assert np.array_equal(mm, gold["q4k_mm"])
 
 
+@pytest.mark.parametrize("fmt", ["q80", "q51"])
+def test_q80_q51_rows_golden(gold, fmt):
+    """orc_q80_rows / orc_q51_rows against the reference's q8_0_rows / q5_1_rows (blocks.py:57-78)
+    on seeded blocks and edge cases: d where -128 d overflows f16, subnormal, zero and negative d,
+    int8 extremes, qh all ones / zeros / alternating."""
+    raw = gold[fmt + "_raw"]
+    rows, K = raw.shape[0], raw.shape[1] // (34 if fmt == "q80" else 24) * 32
+    q, d, m = (O.q80_rows if fmt == "q80" else O.q51_rows)(raw, rows, K)
+    assert np.array_equal(q, gold[fmt + "_q"])
+    assert np.array_equal(d, gold[fmt + "_d"])
+    assert np.array_equal(m, gold[fmt + "_m"])
+
+
 def test_q4k_to_tq_bytes_golden(gold):
     raw = gold["q4k_raw"]
     rows, K = raw.shape[0], raw.shape[1] // 144 * 256
@@ -188,6 +201,33 @@ def test_quant_block_known_answers():
     # all zeros: scale 0, inv 0, q 0
     q, s, su = O.quant_block(np.zeros(16, np.float32))
     assert s == 0.0 and su == 0 and not q.any()
+
+
+def test_quant_multiplies_by_the_rounded_inverse():
+    """quant.rs:158-160 rounds x * f32(127 / amax), not x / f32(amax / 127): blocks where the two
+    forms give different int8 values are found by search, and the oracle must give the first."""
+    rng = np.random.default_rng(17)
+    hits = 0
+    for kb in (16, 32):
+        # values aimed at the rounding boundaries: x = f32((j + 1/2) * amax / 127), a few ulps apart
+        n = 20000
+        amax0 = rng.uniform(0.01, 50, n).astype(np.float32)
+        j = rng.integers(-126, 126, (n, kb - 1))
+        aim = ((j + 0.5) * amax0[:, None].astype(np.float64) / 127).astype(np.float32)
+        aim = (aim.view(np.int32) + rng.integers(-2, 3, aim.shape).astype(np.int32)).view(np.float32)
+        x = np.concatenate([amax0[:, None], aim], 1).astype(np.float32)
+        amax = np.abs(x).max(1, keepdims=True)
+        inv = np.float32(127) / amax
+        by_inv = np.rint(x * inv).astype(np.int32)
+        by_div = np.rint(x / (amax / np.float32(127))).astype(np.int32)
+        differ = np.flatnonzero((by_inv != by_div).any(1))
+        assert differ.size > 0
+        q, s, su = O.quant_rows(x[differ], kb)
+        assert np.array_equal(q.reshape(-1, kb).astype(np.int32), by_inv[differ])
+        assert not np.array_equal(q.reshape(-1, kb).astype(np.int32), by_div[differ])
+        assert np.array_equal(su.reshape(-1), by_inv[differ].sum(1))
+        hits += differ.size
+    assert hits >= 10
 
 
 def test_quant_invariants_and_pair_residual():

@@ -43,11 +43,11 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 
 // Kernel ids for trk_get_timing.
 enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DEC_LAYER, K_DISPATCH, K_B_GATEUP, K_B_DOWN,
-                K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_COUNT };
+                K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_PROFILE, K_COUNT };
 static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
                                                   "decode_down", "decode_layer", "dispatch", "batch_gateup",
                                                   "batch_down", "stream_gateup", "stream_down", "batch_combine",
-                                                  "rmsnorm"};
+                                                  "rmsnorm", "mass_profile"};
 
 // Which grouped items run on the streaming GEMV (the rest on the MFMA tiles), when the caller has
 // not chosen: all of them up to 16 tokens; the items of at most 4 rows while the selections
@@ -78,6 +78,7 @@ struct trk_ctx {
     int fusion = 0;   // decode: one launch per layer (when the shape and the GPU allow it) if set
     int fused = -1;   // that check for the current policy: -1 not yet made, 0 no, 1 yes
     int stream_rows = -1;  // batch: items of at most this many rows on the streaming GEMV (-1: automatic)
+    int profile = 0;       // MoeStats::profile: add every routed row's mass profile to ws.prof
 };
 
 extern "C" const char* trk_last_error(void) { return g_err; }
@@ -121,16 +122,19 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
     ws.F = F;
     ws.m_max = cfg->m_max;
     ws.k_cap = k_cap;
-    ws.ent_cap = (uint32_t)(M * k_cap);
-    ws.item_cap = E + (ws.ent_cap + 15) / 16 + (uint32_t)((M + 15) / 16) + 1;  // items of <= 16 rows
-    ws.act_rows = std::max<size_t>((size_t)(TRK_MOE_K_MAX + 1) * 2, (size_t)ws.ent_cap + M);
+    const geo::Caps caps{H, E, F, cfg->m_max, k_cap};
+    if (geo::ent_cap(caps) > 0xffffffffull || geo::item_cap(caps) > 0xffffffffull)
+        return fail(TRK_E_INVALID, "m_max * k_cap (%u * %u) too large", cfg->m_max, k_cap);
+    ws.ent_cap = (uint32_t)geo::ent_cap(caps);
+    ws.item_cap = (uint32_t)geo::item_cap(caps);  // items of <= 16 rows
+    ws.act_rows = geo::act_rows(caps);
 
     // carve one allocation (256-byte aligned pieces)
     struct Piece {
         void** p;
         size_t bytes;
     };
-    const size_t yrows = (size_t)ws.ent_cap + M;
+    const size_t yrows = geo::yent_rows(caps);
     Piece pieces[] = {
         {(void**)&ws.xq, rows_x * H},
         {(void**)&ws.xs, rows_x * (H / 32) * 4},
@@ -149,7 +153,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.grp_start, (E + 2) * 4},
         {(void**)&ws.grp_exp, (E + 1) * 4},
         {(void**)&ws.n_groups, 16},
-        {(void**)&ws.doff, (M + 63) / 64 * E * 4},  // [ceil(m / 64)][E]: dispatch writes only chunks < ceil(m / 64)
+        {(void**)&ws.doff, geo::doff_elems(cfg->m_max, E) * 4},  // [ceil(m / 64)][E] per-chunk offsets
         {(void**)&ws.items, (size_t)ws.item_cap * sizeof(Item)},
         {(void**)&ws.actq, ws.act_rows * F},
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
@@ -158,6 +162,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.yent, yrows * H * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
+        {(void**)&ws.prof, (K_MAX + 1) * 8},
         {(void**)&ws.counters, (size_t)BAR_LINE * 4 * (BAR_GROUPS + 2)},
     };
     size_t total = 0;
@@ -299,19 +304,30 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     const uint32_t kcap = c->pol.enabled ? c->pol.max : k;
     const float* lg = rlog ? rlog : ws.rlog;
     const int gemm_order = m >= c->cfg.router_dot_max_m ? 1 : 0;
+    // every grid below and every workspace extent its kernels index, checked on the host
+    if (const char* why = geo::check_call(geo::Caps{H, E, ws.F, ws.m_max, ws.k_cap}, m, kcap))
+        return fail(TRK_E_INVALID, "launch geometry: %s", why);
     if (m == 1) {
         // logits (and the shared gate's logit), then routing + gate/up in one launch, then down
         const int pair = c->cfg.hiprec ? 1 : 0;
-        if (c->fusion && c->fused < 0)
-            c->fused = launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg, M.shu,
-                                           M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual, true,
-                                           st) == hipSuccess
-                               ? 1
-                               : 0;
-        if (c->fusion && c->fused == 1 && w->router) {
+        // the one-launch layer where this layer's shape and formats have one (checked per call: the
+        // down format may change from layer to layer) and the GPU holds its grid (asked once per
+        // policy, which sets the LDS size)
+        bool fuse = false;
+        if (c->fusion && w->router && decode_layer_supported(M.gate, M.down, M.shd, E, pair, kcap)) {
+            if (c->fused < 0)
+                c->fused = launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
+                                               M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual, true,
+                                               st) == hipSuccess
+                                   ? 1
+                                   : 0;
+            fuse = c->fused == 1;
+        }
+        if (fuse) {
             TIMED(K_DEC_LAYER, launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
                                                    M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual,
                                                    false, st));
+            if (c->profile) TIMED(K_PROFILE, launch_mass_profile(lg, m, E, ws.prof, st));
             return TRK_OK;
         }
         // the logits launch also quantises x for gate/up
@@ -353,6 +369,9 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         if (sr < BR) TIMED(K_B_DOWN, launch_batch_down(M.down, M.shd, ws, m, sr, st));
         TIMED(K_B_COMBINE, launch_batch_combine(ws, m, out, residual, st));
     }
+    // MoeStats::profile_row on every routed row (exec.rs:1552, exec_batch.rs:1456), off the layer's
+    // critical path
+    if (c->profile) TIMED(K_PROFILE, launch_mass_profile(lg, m, E, ws.prof, st));
     return TRK_OK;
 }
 
@@ -386,17 +405,45 @@ extern "C" int trk_moe_residual(trk_ctx* c, const trk_moe_w* w, const float* rms
     return forward(c, w, c->ws.xn, nullptr, m, h, 1, st);
 }
 
-extern "C" int trk_get_stats(trk_ctx* c, trk_moe_stats* out, int reset) {
+extern "C" int trk_get_stats(trk_ctx* c, trk_moe_stats* out, int reset, void* stream) {
     if (!c || !out) return fail(TRK_E_INVALID, "null argument");
+    hipStream_t st = (hipStream_t)stream;
     unsigned long long v[2];
-    HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(v, c->ws.stats, sizeof v, hipMemcpyDeviceToHost));
+    uint32_t timed_out = 0;
+    HIP_TRY(hipMemcpyAsync(v, c->ws.stats, sizeof v, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&timed_out, c->ws.counters + 2, 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
     out->rows = v[0];
     out->experts = v[1];
-    if (reset) {
-        HIP_TRY(hipMemset(c->ws.stats, 0, sizeof v));
-        HIP_TRY(hipDeviceSynchronize());
+    if (reset) HIP_TRY(hipMemsetAsync(c->ws.stats, 0, sizeof v, st));
+    if (timed_out) {
+        HIP_TRY(hipMemsetAsync(c->ws.counters + 2, 0, 4, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        return fail(TRK_E_TIMEOUT, "a device-side wait of the one-launch decode layer timed out: the outputs of "
+                                   "the calls since the last trk_get_stats are invalid");
     }
+    if (reset) HIP_TRY(hipStreamSynchronize(st));
+    return TRK_OK;
+}
+
+extern "C" int trk_profile_start(trk_ctx* c, int on, void* stream) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    // MoeStats::profile_start (exec.rs:567-573): zero the sums, then count
+    if (on) HIP_TRY(hipMemsetAsync(c->ws.prof, 0, (K_MAX + 1) * sizeof(unsigned long long), (hipStream_t)stream));
+    c->profile = on ? 1 : 0;
+    return TRK_OK;
+}
+
+extern "C" int trk_profile_report(trk_ctx* c, double* cum, uint64_t* rows, void* stream) {
+    if (!c || !cum || !rows) return fail(TRK_E_INVALID, "null argument");
+    hipStream_t st = (hipStream_t)stream;
+    unsigned long long v[K_MAX + 1];
+    HIP_TRY(hipMemcpyAsync(v, c->ws.prof, sizeof v, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    // MoeStats::profile_report (exec.rs:575-581): fixed point 1e-6, mean over the profiled rows
+    const unsigned long long n = v[K_MAX];
+    *rows = n;
+    for (int j = 0; j < K_MAX; j++) cum[j] = n ? (double)v[j] * 1e-6 / (double)n : 0.0;
     return TRK_OK;
 }
 
@@ -447,7 +494,7 @@ extern "C" int trk_get_timing(trk_ctx* c, const char** names, double* ms, uint64
     return n;
 }
 
-extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes) {
+extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes, void* stream) {
     if (!c || !host) return fail(TRK_E_INVALID, "null argument");
     const Workspace& ws = c->ws;
     const void* src = nullptr;
@@ -473,8 +520,8 @@ extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes) {
     default: return fail(TRK_E_INVALID, "unknown workspace buffer %d", which);
     }
     if (bytes > cap) return fail(TRK_E_INVALID, "read of %zu bytes above the buffer's %zu", bytes, cap);
-    HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
     return TRK_OK;
 }
 
@@ -579,7 +626,7 @@ extern "C" int trk_gen_gguf_stack(uint32_t fmt, uint64_t seed, uint64_t stream0,
     if (!out) return fail(TRK_E_INVALID, "null argument");
     if (!(fmt == TRK_FMT_Q4_K || fmt == TRK_FMT_Q6_K || fmt == TRK_FMT_Q8_0 || fmt == TRK_FMT_Q5_1) || k % 256)
         return fail(TRK_E_INVALID, "bad format/k");
-    const uint64_t mb = (uint64_t)rows * (k / 256) * (fmt == TRK_FMT_Q6_K ? 210 : 144);
+    const uint64_t mb = (uint64_t)rows * row_bytes(fmt, k);
     if (count > 1 && stride < mb) return fail(TRK_E_INVALID, "stride %llu below matrix bytes %llu",
                                               (unsigned long long)stride, (unsigned long long)mb);
     if (count > 65535) return fail(TRK_E_INVALID, "count (%u) above 65535", count);

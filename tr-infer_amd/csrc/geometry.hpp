@@ -1,0 +1,93 @@
+// Launch geometry and workspace extents of the MoE kernels, as plain host arithmetic (no HIP
+// types), shared by the launchers, the workspace sizing of trk_create and a CPU-only check that
+// sweeps shapes (tests/geometry_check.cpp).  Every grid a launcher builds and every workspace
+// extent a kernel indexes is computed here, so a grid that addresses strips past F or a buffer
+// sized below what a dispatch writes shows up on the host, without a GPU.
+#pragma once
+
+#include <stdint.h>
+
+namespace trk {
+namespace geo {
+
+constexpr uint32_t KMAX = 32;      // router.rs:6 MOE_K_MAX: stride of the per-token id / weight rows
+constexpr uint32_t ITEM_ROWS = 16; // rows of a grouped work item (one 16-row MFMA tile)
+constexpr uint32_t CHUNK = 64;     // tokens per dispatch chunk (one wave's lane mask)
+constexpr uint32_t DN_R = 4;       // output rows per decode down workgroup
+
+struct Caps {  // what trk_create sizes for (m_max rows, k_cap selections per token)
+    uint32_t H, E, F, m_max, k_cap;
+};
+
+inline uint64_t ent_cap(const Caps& c) { return (uint64_t)c.m_max * c.k_cap; }
+// work items: every non-empty expert's entries in items of <= 16 rows (at most E + entries / 16 of
+// them), then the shared expert's tokens in items of <= 16
+inline uint64_t item_cap(const Caps& c) {
+    return c.E + (ent_cap(c) + ITEM_ROWS - 1) / ITEM_ROWS + (c.m_max + ITEM_ROWS - 1) / ITEM_ROWS + 1;
+}
+inline uint64_t items_max(uint32_t E, uint32_t m, uint32_t kcap) {
+    const uint64_t ent = (uint64_t)m * kcap;
+    const uint64_t nonempty = ent < E ? ent : E;
+    return nonempty + ent / ITEM_ROWS + (m + ITEM_ROWS - 1) / ITEM_ROWS;
+}
+// activation rows of the down input: one per entry and one per token (shared), and the decode
+// slots (K_MAX routed + the shared one, two levels each)
+inline uint64_t act_rows(const Caps& c) {
+    const uint64_t a = ent_cap(c) + c.m_max, d = (uint64_t)(KMAX + 1) * 2;
+    return a > d ? a : d;
+}
+inline uint64_t yent_rows(const Caps& c) { return ent_cap(c) + c.m_max; }
+// dispatch chunks of 64 tokens, and the per-(chunk, expert) offsets the split dispatch writes
+inline uint32_t chunks(uint32_t m) { return (m + CHUNK - 1) / CHUNK; }
+inline uint64_t doff_elems(uint32_t m, uint32_t E) { return (uint64_t)chunks(m) * E; }
+inline bool dispatch_split(uint32_t m) { return m >= 256; }
+
+// MFMA gate/up: grid.x column blocks of F / 16 / grid.x strips, four waves taking every fourth
+inline uint32_t mfma_gateup_cols(uint32_t m, uint32_t F) { return m >= 64 ? F / 256 : F / 64; }
+inline uint32_t mfma_gateup_strips(uint32_t m, uint32_t F) { return F / 16 / mfma_gateup_cols(m, F); }
+// MFMA down: grid.x blocks of 256 or 64 output rows, four waves of 16-row strips
+inline uint32_t mfma_down_cols(uint32_t m, uint32_t H) { return m >= 64 ? H / 256 : H / 64; }
+inline uint32_t mfma_down_rows(uint32_t m, uint32_t H) { return H / mfma_down_cols(m, H); }
+// streaming down: 4 waves of 64 / (2 NSB) units of 2 NSB lanes (half a superblock each)
+inline uint32_t stream_down_rows_per_wg(uint32_t F) { return 4 * (64 / (2 * (F / 256))); }
+inline uint32_t stream_down_cols(uint32_t H, uint32_t F) {
+    const uint32_t r = stream_down_rows_per_wg(F);
+    return (H + r - 1) / r;
+}
+// decode: gate/up (F / 16 strips, kcap + 1 slots), down H / 4 workgroups
+inline uint32_t decode_gateup_strips(uint32_t F) { return F / 16; }
+inline uint32_t decode_down_wgs(uint32_t H) { return H / DN_R; }
+
+// Every invariant a call of m rows with kcap selections per token relies on; returns nullptr when
+// they hold, else what failed.
+inline const char* check_call(const Caps& c, uint32_t m, uint32_t kcap) {
+    if (c.H == 0 || c.H % 256 || c.F == 0 || c.F % 256) return "H and F must be multiples of 256";
+    if (m == 0 || m > c.m_max) return "m outside 1..m_max";
+    if (kcap == 0 || kcap > c.k_cap || kcap > KMAX) return "kcap outside 1..k_cap";
+    if ((uint64_t)m * kcap > ent_cap(c)) return "entries above the entry capacity";
+    if (items_max(c.E, m, kcap) > item_cap(c)) return "work items above the item capacity";
+    if ((uint64_t)m * kcap + m > act_rows(c) || (uint64_t)m * kcap + m > yent_rows(c))
+        return "activation rows above capacity";
+    if (doff_elems(m, c.E) > doff_elems(c.m_max, c.E)) return "dispatch offsets above capacity";
+    {  // MFMA gate/up: the column blocks tile F's strips exactly, four waves each
+        const uint32_t cols = mfma_gateup_cols(m, c.F), s = mfma_gateup_strips(m, c.F);
+        if (cols == 0 || cols * s * 16 != c.F || s % 4) return "MFMA gate/up grid does not tile F";
+    }
+    {  // MFMA down: the row blocks tile H exactly, 16-row strips over four waves
+        const uint32_t cols = mfma_down_cols(m, c.H), r = mfma_down_rows(m, c.H);
+        if (cols == 0 || cols * r != c.H || r % 64) return "MFMA down grid does not tile H";
+    }
+    {  // streaming down: the row blocks cover H (the kernel guards rows past H)
+        const uint32_t r = stream_down_rows_per_wg(c.F);
+        if (r == 0 || (uint64_t)stream_down_cols(c.H, c.F) * r < c.H) return "stream down grid does not cover H";
+    }
+    if (m == 1) {  // decode: slots 0..kcap-1 and the shared slot, strips of F, rows of H
+        if (decode_gateup_strips(c.F) * 16 != c.F) return "decode gate/up strips do not tile F";
+        if (decode_down_wgs(c.H) * DN_R != c.H) return "decode down workgroups do not tile H";
+        if ((uint64_t)(KMAX + 1) * 2 > act_rows(c)) return "decode activation slots above capacity";
+    }
+    return nullptr;
+}
+
+}  // namespace geo
+}  // namespace trk

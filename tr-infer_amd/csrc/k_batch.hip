@@ -372,9 +372,10 @@ hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipSt
     if (E > 2 * DT) return hipErrorInvalidValue;
     const size_t lds = DISPATCH_WAVES * E * 8 + (2 * E + DISPATCH_WAVES * E + DISPATCH_WAVES * 3) * 4;
     // from a few hundred tokens on, one workgroup's scattered stores dominate: spread them
-    const int split = m >= 256 ? 1 : 0;
+    const int split = geo::dispatch_split(m) ? 1 : 0;
+    if (split && geo::doff_elems(m, ws.E) > geo::doff_elems(ws.m_max, ws.E)) return hipErrorInvalidValue;
     dispatch_kernel<<<1, DT, lds, st>>>(ws, m, (kcap + 3) / 4, split);
-    if (split) scatter_kernel<<<(m + 63) / 64, 64, E * 8, st>>>(ws, m, (kcap + 3) / 4);
+    if (split) scatter_kernel<<<geo::chunks(m), 64, E * 8, st>>>(ws, m, (kcap + 3) / 4);
     return hipGetLastError();
 }
 
@@ -810,7 +811,7 @@ hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gat
     const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_STRIDE * 8 + 32 * 4;
     // a workgroup per (item, 16 strips) once the items fill the GPU; otherwise per (item, 4 strips)
     // so that a wave's chain of dependent weight loads stays short
-    const dim3 grid(m >= 64 ? F / 256 : F / 64, grouped_item_rows(ws, m));
+    const dim3 grid(geo::mfma_gateup_cols(m, F), grouped_item_rows(ws, m));
     switch (H / 256) {
 #define GU_CASE(n) \
     case n: batch_gateup_kernel<n><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws, skip_rows); break;
@@ -1190,7 +1191,7 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
                              hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
     const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
-    const dim3 grid(m >= 64 ? H / 256 : H / 64, grouped_item_rows(ws, m));
+    const dim3 grid(geo::mfma_down_cols(m, H), grouped_item_rows(ws, m));
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
     const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
     switch (F / 256 * 4 + fk) {

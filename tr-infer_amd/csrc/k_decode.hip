@@ -608,6 +608,15 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(const float* __restri
     down_unit<P, NSBF, true>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first);
 }
 
+// The shape the one-launch layer is instantiated for (BASELINE's layer: H = 2048, F = 512, E <= 512,
+// two-level activations, Q4_K down) with a grid of H / 4 workgroups that covers every gate/up unit.
+bool decode_layer_supported(const Mat& gate, const Mat& down, const Mat& sh_down, uint32_t E, int pair,
+                            uint32_t kcap) {
+    const uint32_t H = gate.k, F = gate.rows, nwg = H / DN_R;
+    return H == 2048 && F == 512 && E <= 512 && pair && down.fmt == TRK_FMT_Q4_K && sh_down.fmt == TRK_FMT_Q4_K &&
+           (kcap + 1) * (F / 16) <= nwg && nwg % BAR_GROUPS == 0;
+}
+
 template <int P, int NSB, int NJ, int NSBF>
 static size_t layer_lds(uint32_t E, uint32_t kcap, bool mass_all, uint32_t& rsm) {
     rsm = (ROUTE_LDS + (mass_all ? E * 4 : 0) + 15) / 16 * 16;
@@ -625,11 +634,9 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
                                const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
                                Policy pol, int pair, uint32_t kcap, float* out, int residual, bool check_only,
                                hipStream_t st) {
-    const uint32_t H = gate.k, F = gate.rows, E = ws.E;
+    const uint32_t H = gate.k, E = ws.E;
     const uint32_t nwg = H / DN_R;
-    if (H != 2048 || F != 512 || E > 512 || !pair || down.fmt != TRK_FMT_Q4_K || sh_down.fmt != TRK_FMT_Q4_K)
-        return hipErrorNotSupported;  // the instantiated shape (BASELINE's layer)
-    if ((kcap + 1) * (F / 16) > nwg || !router || nwg % BAR_GROUPS) return hipErrorNotSupported;
+    if (!decode_layer_supported(gate, down, sh_down, E, pair, kcap) || !router) return hipErrorNotSupported;
     const bool mass_all = pol.enabled && pol.basis == TRK_BASIS_ALL;
     uint32_t rsm = 0;
     const size_t lds = layer_lds<2, 8, 8, 2>(E, kcap, mass_all, rsm);

@@ -394,4 +394,58 @@ hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k,
     return hipGetLastError();
 }
 
+// router::mass_profile (router.rs:152-166) of each logit row, added to MoeStats's fixed-point sums
+// as MoeStats::profile_row does (exec.rs:582-592): prof[j] += (u64)(cum[j] * 1e6) for j < 32,
+// prof[32] += 1.  One wave per row: the top-32 come from route_row's selection (the insertion
+// order of topk_sorted), the denominator over all logits is summed in index order by one lane.
+template <int NJ>
+__global__ __launch_bounds__(256) void mass_profile_kernel(const float* __restrict__ logits, uint32_t m, uint32_t E,
+                                                          unsigned long long* __restrict__ prof) {
+    __shared__ uint2 cand[4][ROUTE_CAND];
+    __shared__ uint32_t top_i[4][K_MAX];
+    __shared__ float top_w[4][K_MAX];
+    extern __shared__ float ex_all[];  // [4][E]
+    const uint32_t wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const uint32_t row = blockIdx.x * 4 + wv;
+    if (row >= m) return;
+    const float* lg = logits + (size_t)row * E;
+    const uint32_t kk = E < (uint32_t)K_MAX ? E : (uint32_t)K_MAX;
+    const Policy none{0, 0, 0, 0, 0.0f};
+    const uint32_t n = route_row<NJ>(lg, E, kk, none, lane, cand[wv], nullptr, top_i[wv], top_w[wv]);
+    wave_sync();
+    // topk_sorted's values in order; slots it leaves unfilled stay -inf (router.rs:155-158)
+    const float tv = lane < n ? lg[top_i[wv][lane]] : -__builtin_inff();
+    const float mx = rdl(tv, 0);
+    float* ex = ex_all + (size_t)wv * E;
+    for (uint32_t i = lane; i < E; i += WAVE) ex[i] = expf_libm(lg[i] - mx);
+    wave_sync();
+    float denom = 0.0f;
+    if (lane == 0)
+        for (uint32_t i = 0; i < E; i++) denom += ex[i];
+    denom = rdl(denom, 0);
+    const float e = lane < kk ? expf_libm(tv - mx) / denom : 0.0f;
+    float mass = 0.0f, mine = 0.0f;
+    for (uint32_t j = 0; j < (uint32_t)K_MAX; j++) {  // cum[j] = mass of the best j + 1
+        if (j < kk) mass += rdl(e, j);
+        if (lane == j) mine = mass;
+    }
+    if (lane < (uint32_t)K_MAX) {
+        // (m as f64 * 1e6) as u64: truncation, NaN and negatives to 0, saturating
+        const double d = (double)mine * 1e6;
+        const unsigned long long fx =
+                !(d > 0.0) ? 0ull : (d >= 18446744073709551615.0 ? ~0ull : (unsigned long long)d);
+        atomicAdd(&prof[lane], fx);
+    }
+    if (lane == 0) atomicAdd(&prof[K_MAX], 1ull);
+}
+
+hipError_t launch_mass_profile(const float* logits, uint32_t m, uint32_t E, unsigned long long* prof, hipStream_t st) {
+    const size_t lds = (size_t)4 * E * sizeof(float);
+    if (E <= 512)
+        mass_profile_kernel<8><<<(m + 3) / 4, 256, lds, st>>>(logits, m, E, prof);
+    else
+        mass_profile_kernel<16><<<(m + 3) / 4, 256, lds, st>>>(logits, m, E, prof);
+    return hipGetLastError();
+}
+
 }  // namespace trk

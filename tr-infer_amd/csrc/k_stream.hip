@@ -421,8 +421,7 @@ hipError_t launch_stream_down(const Mat& down, const Mat& sh_down, const Workspa
     const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
     const size_t cap = max_rows < BR ? max_rows : BR;
     const size_t lds = cap * ((size_t)F + 16 + (size_t)nbf * 8 + 4);
-    const uint32_t rpb = 4 * (64 / (2 * nsbf));  // rows per workgroup
-    const dim3 grid((H + rpb - 1) / rpb, item_rows(ws, m));
+    const dim3 grid(geo::stream_down_cols(H, F), item_rows(ws, m));
     switch (nsbf * 4 + fk) {
 #define SD_CASE(n)                                                                                        \
     case n * 4: stream_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, max_rows); break;     \

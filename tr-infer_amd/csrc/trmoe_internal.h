@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "../../include/trmoe.h"
+#include "geometry.hpp"
 
 namespace trk {
 
@@ -68,6 +69,7 @@ struct Workspace {
     float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
+    unsigned long long* prof;   // [33] router-mass profile: fixed-point sums per k, then the row count
     uint32_t* counters;   // [BAR_LINE * (BAR_GROUPS + 2)]: grid-barrier words (k_decode.hip): [0..1] top
                           // counter, [2] time-out flag, group g's counter and release word at BAR_LINE * (1 + g)
     size_t act_rows;
@@ -92,6 +94,8 @@ struct XNorm {
 hipError_t launch_router_logits(const float* router, const float* bias, const float* shexp_gate, const float* x,
                                 uint32_t m, uint32_t E, uint32_t H, int gemm_order, float* rlog, float* sh,
                                 hipStream_t st, const XQuant* xquant = nullptr, const XNorm* norm = nullptr);
+hipError_t launch_mass_profile(const float* logits, uint32_t m, uint32_t E, unsigned long long* prof,
+                               hipStream_t st);
 hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k, Policy pol, uint32_t* ids,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
@@ -102,6 +106,8 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
                                const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
                                Policy pol, int pair, uint32_t kcap, float* out, int residual, bool check_only,
                                hipStream_t st);
+bool decode_layer_supported(const Mat& gate, const Mat& down, const Mat& sh_down, uint32_t E, int pair,
+                            uint32_t kcap);
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
                               uint32_t kcap, float* out, int residual, hipStream_t st);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);

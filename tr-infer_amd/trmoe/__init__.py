@@ -67,7 +67,9 @@ def lib() -> C.CDLL:
         L.trk_set_moe.argtypes = [vp, C.POINTER(Policy)]
         L.trk_moe_forward.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, vp]
         L.trk_moe_residual.argtypes = [vp, C.POINTER(MoeW), vp, f, vp, u32, vp]
-        L.trk_get_stats.argtypes = [vp, C.POINTER(Stats), i]
+        L.trk_get_stats.argtypes = [vp, C.POINTER(Stats), i, vp]
+        L.trk_profile_start.argtypes = [vp, i, vp]
+        L.trk_profile_report.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_uint64), vp]
         L.trk_router_logits.argtypes = [vp, vp, vp, vp, u32, u32, u32, i, vp, vp, vp]
         L.trk_route.argtypes = [vp, u32, u32, u32, C.POINTER(Policy), vp, vp, vp, vp]
         L.trk_quantize.argtypes = [vp, u32, u32, u32, i, vp, vp, vp, vp]
@@ -78,7 +80,7 @@ def lib() -> C.CDLL:
         L.trk_gen_gguf.argtypes = [u32, u64, u64, u32, u32, f, f, vp, vp]
         L.trk_gen_gguf_stack.argtypes = [u32, u64, u64, u64, u32, u32, u32, f, f, vp, u64, vp]
         L.trk_gen_normal.argtypes = [u64, u64, sz, C.c_double, vp, vp]
-        L.trk_debug_read.argtypes = [vp, i, vp, sz]
+        L.trk_debug_read.argtypes = [vp, i, vp, sz, vp]
         L.trk_launch_kernel.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, C.c_char_p, vp]
         L.trk_set_timing.argtypes = [vp, i]
         L.trk_set_fusion.argtypes = [vp, i]
@@ -155,10 +157,24 @@ class Context:
     def residual(self, w: "LayerWeights", rms_w, eps, h, stream=None):
         check(lib().trk_moe_residual(self.h, C.byref(w.moew), _ptr(rms_w), eps, _ptr(h), h.shape[0], _stream(stream)))
 
-    def stats(self, reset=False):
+    def stats(self, reset=False, stream=None):
+        """(rows, experts) routed since the last reset (MoeStats::snapshot); raises on TRK_E_TIMEOUT."""
         s = Stats()
-        check(lib().trk_get_stats(self.h, C.byref(s), int(reset)))
+        check(lib().trk_get_stats(self.h, C.byref(s), int(reset), _stream(stream)))
         return s.rows, s.experts
+
+    def profile_start(self, on=True, stream=None):
+        """MoeStats::profile_start: zero the router-mass profile and collect it on later forwards."""
+        check(lib().trk_profile_start(self.h, int(on), _stream(stream)))
+
+    def profile_report(self, stream=None):
+        """MoeStats::profile_report: (mean cumulative mass of the best 1..32 experts, rows profiled)."""
+        import numpy as np
+        cum = np.zeros(K_MAX, np.float64)
+        rows = C.c_uint64()
+        check(lib().trk_profile_report(self.h, cum.ctypes.data_as(C.POINTER(C.c_double)), C.byref(rows),
+                                       _stream(stream)))
+        return cum, rows.value
 
     def set_fusion(self, on: bool):
         check(lib().trk_set_fusion(self.h, int(on)))
@@ -181,10 +197,10 @@ class Context:
             check(n)
         return {names[i].decode(): (ms[i], int(cnt[i])) for i in range(min(n, cap))}
 
-    def read(self, which, nbytes, dtype):
+    def read(self, which, nbytes, dtype, stream=None):
         import numpy as np
         buf = np.zeros(nbytes, np.uint8)
-        check(lib().trk_debug_read(self.h, which, buf.ctypes.data_as(C.c_void_p), nbytes))
+        check(lib().trk_debug_read(self.h, which, buf.ctypes.data_as(C.c_void_p), nbytes, _stream(stream)))
         return buf.view(dtype)
 
 
