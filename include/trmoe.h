@@ -122,6 +122,19 @@ int trk_moe_forward(trk_ctx *ctx, const trk_moe_w *w, const float *x, const floa
 int trk_moe_residual(trk_ctx *ctx, const trk_moe_w *w, const float *rms_w, float eps, float *h,
                      uint32_t m, void *stream);
 
+/* trk_moe_forward without a context and without allocating anything: no counterpart in the
+ * reference.  For callers that cannot allocate (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  cfg gives the layer shape as for trk_create (m_max is
+ * ignored: the workspace is laid out for this call's m), policy the routing (NULL = top
+ * n_expert_used).  The workspace lives in a static device array of TRK_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; a call whose workspace does not fit returns TRK_E_CAPACITY (at
+ * H = 2048, E = 512, F = 512, k = 10 that is M above 64).  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (several host threads or streams) race.  MoeStats are not counted
+ * and the one-launch decode layer is not used.  Results are those of trk_moe_forward. */
+#define TRK_NOALLOC_SCRATCH_BYTES (16u << 20)
+int trk_moe_forward_noalloc(const trk_cfg *cfg, const trk_moe_policy *policy, const trk_moe_w *w, const float *x,
+                            const float *rlog, uint32_t m, float *out, void *stream);
+
 /* Read (and optionally reset) the routing counters, ordered after the work queued on `stream`
  * (synchronises that stream only).  Returns TRK_E_TIMEOUT, with the counters filled, when a
  * device-side wait of the one-launch decode layer timed out since the last call (and clears that

@@ -69,3 +69,14 @@ def test_stats_and_profile_reject_null_arguments():
     assert L.trk_get_stats(None, None, 0, None) == -1
     assert L.trk_profile_report(None, None, None, None) == -1
     assert L.trk_profile_start(None, 1, None) == -1
+
+
+def test_noalloc_rejects_a_workspace_above_the_scratch():
+    """trk_moe_forward_noalloc lays its workspace out on the host and refuses a call whose workspace
+    does not fit the static scratch before touching a GPU."""
+    L = trmoe.lib()
+    cfg = trmoe.Cfg(2048, 512, 512, 10, 0, 0, 16, 1)
+    rc = L.trk_moe_forward_noalloc(C.byref(cfg), None, None, C.c_void_p(256), None, 4096, C.c_void_p(256), None)
+    assert rc == -3 and b"scratch" in L.trk_last_error()
+    bad = trmoe.Cfg(2000, 512, 512, 10, 0, 0, 16, 1)
+    assert L.trk_moe_forward_noalloc(C.byref(bad), None, None, C.c_void_p(256), None, 1, C.c_void_p(256), None) == -1

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -97,39 +98,37 @@ static int check_policy(const trk_ctx* c, const trk_moe_policy* p) {
     return TRK_OK;
 }
 
-extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
-    if (!cfg || !out) return fail(TRK_E_INVALID, "trk_create: null argument");
+// Shape checks of a layer configuration (trk_create and the no-allocation entry point); k_cap
+// comes back resolved (0 = n_expert_used).
+static int check_cfg(const trk_cfg* cfg, uint32_t m_max, uint32_t& k_cap) {
     const uint32_t H = cfg->hidden, E = cfg->n_expert, F = cfg->n_ff, k = cfg->n_expert_used;
     if (H == 0 || H % 256 || F == 0 || F % 256)
         return fail(TRK_E_INVALID, "hidden (%u) and n_ff (%u) must be positive multiples of 256", H, F);
     if (E == 0 || E > 1024) return fail(TRK_E_INVALID, "n_expert (%u) must be in 1..1024", E);
     if (k < 1 || k > TRK_MOE_K_MAX || k > E) return fail(TRK_E_INVALID, "n_expert_used (%u) must be in 1..min(32, E)", k);
-    if (cfg->m_max == 0) return fail(TRK_E_INVALID, "m_max must be positive");
-    uint32_t k_cap = cfg->k_cap ? cfg->k_cap : k;
+    if (m_max == 0) return fail(TRK_E_INVALID, "m_max must be positive");
+    k_cap = cfg->k_cap ? cfg->k_cap : k;
     if (k_cap < k || k_cap > TRK_MOE_K_MAX) return fail(TRK_E_INVALID, "k_cap (%u) must be in n_expert_used..32", k_cap);
+    const geo::Caps caps{H, E, F, m_max, k_cap};
+    if (geo::ent_cap(caps) > 0xffffffffull || geo::item_cap(caps) > 0xffffffffull)
+        return fail(TRK_E_INVALID, "m_max * k_cap (%u * %u) too large", m_max, k_cap);
+    return TRK_OK;
+}
 
-    trk_ctx* c = new (std::nothrow) trk_ctx();
-    if (!c) return fail(TRK_E_NOMEM, "host allocation failed");
-    c->cfg = *cfg;
-    if (!c->cfg.router_dot_max_m) c->cfg.router_dot_max_m = 16;
-    c->pol = Policy{0, 0, 0, 0, 0.0f};
-    HIP_TRY(hipGetDevice(&c->device));
-
-    Workspace& ws = c->ws;
-    const size_t M = cfg->m_max, rows_x = std::max<size_t>(2, M);
+// The workspace of a layer configuration for m_max rows: sizes, then 256-byte aligned pieces cut
+// from base (nullptr: sizes only).  Returns the bytes the pieces take.
+static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max, uint32_t k_cap, char* base) {
+    const uint32_t H = cfg.hidden, E = cfg.n_expert, F = cfg.n_ff;
+    const size_t M = m_max, rows_x = std::max<size_t>(2, M);
     ws.H = H;
     ws.E = E;
     ws.F = F;
-    ws.m_max = cfg->m_max;
+    ws.m_max = m_max;
     ws.k_cap = k_cap;
-    const geo::Caps caps{H, E, F, cfg->m_max, k_cap};
-    if (geo::ent_cap(caps) > 0xffffffffull || geo::item_cap(caps) > 0xffffffffull)
-        return fail(TRK_E_INVALID, "m_max * k_cap (%u * %u) too large", cfg->m_max, k_cap);
+    const geo::Caps caps{H, E, F, m_max, k_cap};
     ws.ent_cap = (uint32_t)geo::ent_cap(caps);
     ws.item_cap = (uint32_t)geo::item_cap(caps);  // items of <= 16 rows
     ws.act_rows = geo::act_rows(caps);
-
-    // carve one allocation (256-byte aligned pieces)
     struct Piece {
         void** p;
         size_t bytes;
@@ -153,7 +152,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.grp_start, (E + 2) * 4},
         {(void**)&ws.grp_exp, (E + 1) * 4},
         {(void**)&ws.n_groups, 16},
-        {(void**)&ws.doff, geo::doff_elems(cfg->m_max, E) * 4},  // [ceil(m / 64)][E] per-chunk offsets
+        {(void**)&ws.doff, geo::doff_elems(m_max, E) * 4},  // [ceil(m / 64)][E] per-chunk offsets
         {(void**)&ws.items, (size_t)ws.item_cap * sizeof(Item)},
         {(void**)&ws.actq, ws.act_rows * F},
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
@@ -165,8 +164,28 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         {(void**)&ws.prof, (K_MAX + 1) * 8},
         {(void**)&ws.counters, (size_t)BAR_LINE * 4 * (BAR_GROUPS + 2)},
     };
-    size_t total = 0;
-    for (auto& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
+    size_t off = 0;
+    for (auto& pc : pieces) {
+        *pc.p = base ? base + off : nullptr;
+        off += (pc.bytes + 255) / 256 * 256;
+    }
+    return off;
+}
+
+extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
+    if (!cfg || !out) return fail(TRK_E_INVALID, "trk_create: null argument");
+    uint32_t k_cap = 0;
+    int rc = check_cfg(cfg, cfg->m_max, k_cap);
+    if (rc) return rc;
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device));
+    trk_ctx* c = new (std::nothrow) trk_ctx();
+    if (!c) return fail(TRK_E_NOMEM, "host allocation failed");
+    c->cfg = *cfg;
+    if (!c->cfg.router_dot_max_m) c->cfg.router_dot_max_m = 16;
+    c->pol = Policy{0, 0, 0, 0, 0.0f};
+    c->device = device;
+    const size_t total = layout_workspace(c->ws, c->cfg, cfg->m_max, k_cap, nullptr);
     hipError_t e = hipMalloc(&c->block, total);
     if (e != hipSuccess) {
         delete c;
@@ -178,11 +197,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
         delete c;
         return fail(TRK_E_HIP, "workspace clear: %s", hipGetErrorString(e));
     }
-    size_t off = 0;
-    for (auto& pc : pieces) {
-        *pc.p = (char*)c->block + off;
-        off += (pc.bytes + 255) / 256 * 256;
-    }
+    layout_workspace(c->ws, c->cfg, cfg->m_max, k_cap, (char*)c->block);
     e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(c->block);
@@ -379,6 +394,69 @@ extern "C" int trk_moe_forward(trk_ctx* c, const trk_moe_w* w, const float* x, c
                                float* out, void* stream) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     return forward(c, w, x, rlog, m, out, 0, (hipStream_t)stream);
+}
+
+// ---- the layer without a context and without allocating ------------------------------------
+//
+// The workspace lives in one file-scope device array, `scratch`, of TRK_NOALLOC_SCRATCH_BYTES; every
+// GPU the library runs on holds its own copy until the process ends.  Host code never uses the
+// array's name as an address: on a device's first call hipGetSymbolAddress gives that device's
+// address, kept per device, and only that address reaches the kernels.  Nothing in the sequence
+// reads the workspace before writing it in the same call (routing, dispatch, activations and
+// per-entry outputs are all produced before they are consumed), so no clear is needed; the
+// MoeStats counters, the mass profile and the one-launch layer's barrier words belong to a
+// context and are not used here.  Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) uint8_t scratch[TRK_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+constexpr int SCRATCH_DEVICES = 64;
+static void* g_scratch_ptr[SCRATCH_DEVICES];  // device address of `scratch`, per device
+
+static int scratch_of_current_device(void** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCRATCH_DEVICES) return fail(TRK_E_INVALID, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(TRK_E_HIP, "hipGetSymbolAddress gave no address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TRK_OK;
+}
+
+extern "C" int trk_moe_forward_noalloc(const trk_cfg* cfg, const trk_moe_policy* policy, const trk_moe_w* w,
+                                       const float* x, const float* rlog, uint32_t m, float* out, void* stream) {
+    if (!cfg) return fail(TRK_E_INVALID, "null configuration");
+    if (m == 0) return TRK_OK;
+    uint32_t k_cap = 0;
+    int rc = check_cfg(cfg, m, k_cap);
+    if (rc) return rc;
+    trk_ctx c;  // host-side bookkeeping on the stack; its event lists stay empty (timing off)
+    c.cfg = *cfg;
+    c.cfg.m_max = m;
+    if (!c.cfg.router_dot_max_m) c.cfg.router_dot_max_m = 16;
+    c.pol = Policy{0, 0, 0, 0, 0.0f};
+    c.block = nullptr;
+    c.timing = 0;
+    const size_t need = layout_workspace(c.ws, c.cfg, m, k_cap, nullptr);
+    if (need > TRK_NOALLOC_SCRATCH_BYTES)
+        return fail(TRK_E_CAPACITY, "workspace for M=%u needs %zu bytes, above the static scratch of %zu bytes", m,
+                    need, (size_t)TRK_NOALLOC_SCRATCH_BYTES);
+    if (policy) {
+        if ((rc = check_policy(&c, policy))) return rc;
+        c.pol = Policy{1, policy->min, policy->max, policy->basis, policy->mass};
+    }
+    void* base = nullptr;
+    if ((rc = scratch_of_current_device(&base))) return rc;
+    layout_workspace(c.ws, c.cfg, m, k_cap, (char*)base);
+    c.ws.stats = nullptr;  // MoeStats, the mass profile and the barrier words belong to a context
+    c.ws.prof = nullptr;
+    c.ws.counters = nullptr;
+    HIP_TRY(hipGetDevice(&c.device));
+    return forward(&c, w, x, rlog, m, out, 0, (hipStream_t)stream);
 }
 
 extern "C" int trk_launch_kernel(trk_ctx* c, const trk_moe_w* w, const float* x, const float* rlog, uint32_t m,

@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
         L.trk_set_moe.argtypes = [vp, C.POINTER(Policy)]
         L.trk_moe_forward.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, vp]
         L.trk_moe_residual.argtypes = [vp, C.POINTER(MoeW), vp, f, vp, u32, vp]
+        L.trk_moe_forward_noalloc.argtypes = [C.POINTER(Cfg), C.POINTER(Policy), C.POINTER(MoeW), vp, vp, u32, vp,
+                                              vp]
         L.trk_get_stats.argtypes = [vp, C.POINTER(Stats), i, vp]
         L.trk_profile_start.argtypes = [vp, i, vp]
         L.trk_profile_report.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_uint64), vp]
@@ -284,6 +286,19 @@ class LayerWeights:
         t = self.tensors
         return LayerWeights(H, E, F, t["router"], t["shexp_gate"], t["gate"], t["up"], down, t["sh_gate"],
                             t["sh_up"], sh_down, FMT_Q4_K, down_fmt, t["router_bias"])
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def forward_noalloc(hidden, n_expert, n_ff, k, w: "LayerWeights", x, out, policy=None, k_cap=0, router_dot_max_m=16,
+                    hiprec=True, rlog=None, stream=None):
+    """trk_moe_forward_noalloc: the layer without a context, its workspace in the library's static
+    device scratch (no allocation)."""
+    cfg = Cfg(hidden, n_expert, n_ff, k, 0, k_cap, router_dot_max_m, int(hiprec))
+    p = C.byref(Policy(*policy)) if policy is not None else None
+    check(lib().trk_moe_forward_noalloc(C.byref(cfg), p, C.byref(w.moew), _ptr(x), _ptr(rlog), x.shape[0], _ptr(out),
+                                        _stream(stream)))
 
 
 # ---- kernel-level wrappers (torch tensors on the GPU) ----------------------------------------
