@@ -77,7 +77,6 @@ struct trk_ctx {
     std::vector<TimedLaunch> timed;
     std::vector<hipEvent_t> spare;
     int fusion = 0;   // decode: one launch per layer (when the shape and the GPU allow it) if set
-    int fused = -1;   // that check for the current policy: -1 not yet made, 0 no, 1 yes
     int stream_rows = -1;  // batch: items of at most this many rows on the streaming GEMV (-1: automatic)
     int profile = 0;       // MoeStats::profile: add every routed row's mass profile to ws.prof
 };
@@ -224,13 +223,11 @@ extern "C" int trk_set_moe(trk_ctx* c, const trk_moe_policy* p) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     if (!p) {
         c->pol = Policy{0, 0, 0, 0, 0.0f};
-        c->fused = -1;
         return TRK_OK;
     }
     int rc = check_policy(c, p);
     if (rc) return rc;
     c->pol = Policy{1, p->min, p->max, p->basis, p->mass};
-    c->fused = -1;
     return TRK_OK;
 }
 
@@ -325,19 +322,12 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     if (m == 1) {
         // logits (and the shared gate's logit), then routing + gate/up in one launch, then down
         const int pair = c->cfg.hiprec ? 1 : 0;
-        // the one-launch layer where this layer's shape and formats have one (checked per call: the
-        // down format may change from layer to layer) and the GPU holds its grid (asked once per
-        // policy, which sets the LDS size)
-        bool fuse = false;
-        if (c->fusion && w->router && decode_layer_supported(M.gate, M.down, M.shd, E, pair, kcap)) {
-            if (c->fused < 0)
-                c->fused = launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
-                                               M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual, true,
-                                               st) == hipSuccess
-                                   ? 1
-                                   : 0;
-            fuse = c->fused == 1;
-        }
+        // the one-launch layer where this layer's shape has one (checked per call: the formats may
+        // change from layer to layer)
+        const bool fuse = c->fusion && ws.counters &&
+                          launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
+                                              M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual, true,
+                                              st) == hipSuccess;
         if (fuse) {
             TIMED(K_DEC_LAYER, launch_decode_layer(w->router, w->router_bias, w->shexp_gate, M.gate, M.up, M.down, M.shg,
                                                    M.shu, M.shd, x, rlog, ws, k, c->pol, pair, kcap, out, residual,
@@ -528,7 +518,6 @@ extern "C" int trk_profile_report(trk_ctx* c, double* cum, uint64_t* rows, void*
 extern "C" int trk_set_fusion(trk_ctx* c, int on) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     c->fusion = on ? 1 : 0;
-    c->fused = -1;
     return TRK_OK;
 }
 

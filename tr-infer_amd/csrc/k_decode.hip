@@ -22,16 +22,19 @@ namespace trk {
 constexpr int DN_R = 4;      // output rows per down workgroup
 
 // One gate/up unit (slot, strip) on a workgroup of at least GU_THREADS(NSB) threads.  Wave 0
-// routes the token into LDS when `route` is set (always for routed slots).  `hook(r_ids, n)` runs
-// on every thread once the routing is in LDS, before any weight of a routed slot is requested
-// (the fused layer kernel issues its down-projection prefetch there).  active = false: route
-// and hook only.
-template <int P, int NSB, int NJ, bool COH, bool XPRE, typename Hook>
+// routes the token into LDS when `route` is set (always for routed slots).  `pre()` runs on every
+// thread after the unit's first loads are issued (x; the shared expert's weights) and before the
+// logits or the shared gate's logit are read (the pipelined layer waits there for the router
+// workgroups).  `hook(r_ids, n)` runs on every thread once the routing is in LDS, before any
+// weight of a routed slot is requested.  active = false: route and hook only.  pub: with publish,
+// a counter raised once the published routing is visible device-wide (COH stores).
+template <int P, int NSB, int NJ, bool COH, bool XPRE, typename Pre, typename Hook>
 __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, const Mat& shg, const Mat& shu,
                                             const float* __restrict__ x, const float* __restrict__ lg,
                                             const Workspace& ws, uint32_t k, const Policy& pol, uint32_t kcap,
                                             uint32_t slot, uint32_t strip, bool active, bool route, bool publish,
-                                            uint8_t* smem, uint8_t* rsm, Hook&& hook) {
+                                            uint8_t* smem, uint8_t* rsm, Pre&& pre, Hook&& hook,
+                                            uint32_t* pub = nullptr) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8, XSB = 256 + 16, XP = NSB * XSB;
     const uint32_t F = gate.rows, E = ws.E;
     const uint32_t tid = threadIdx.x;
@@ -94,27 +97,59 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
     };
     uint4 wq[9];
     float shl = 0.0f;
-    if (shared) {
-        load_rows(shg, shu, 0u, wq);  // the shared expert does not wait for the routing
-        shl = COH ? ld_devf(ws.shl) : ws.shl[0];
+    if (shared) load_rows(shg, shu, 0u, wq);  // the shared expert does not wait for the routing
+    pre();
+    if (shared) shl = COH ? ld_devf(ws.shl) : ws.shl[0];
+    // route this token (wave 0): every routed workgroup repeats it, so no separate launch and no
+    // round trip through memory sits between the logits and the expert weights.  Without a mass
+    // policy the selection alone fixes every slot's expert: the workgroup then requests its slot's
+    // weights before wave 0 works out the routing weights
+    const bool early = route && !pol.enabled;  // workgroup-uniform
+    uint32_t my_key = 0, my_idx = 0, ksel = 0;
+    if (route && tid < 64) {
+        ksel = route_select<NJ, COH>(lg, E, k, pol, tid, cand, my_key, my_idx);
+        if (early) {
+            if (tid < ksel) r_ids[tid] = my_idx;
+            if (tid == 0) r_n[0] = ksel;  // top-k: the count is the selection's size
+        }
+    }
+    bool loaded = false;
+    if (early) {
+        __syncthreads();
+        if (active && !shared && slot < r_n[0]) {
+            load_rows(gate, up, r_ids[slot], wq);
+            loaded = true;
+        }
     }
     if (route && tid < 64) {
-        // route this token (wave 0): every routed workgroup repeats it, so no separate launch and
-        // no round trip through memory sits between the logits and the expert weights
-        const uint32_t n = route_row<NJ, COH>(lg, E, k, pol, tid, cand, ex, r_ids, r_w);
+        const uint32_t n = route_weights<COH>(lg, E, k, pol, tid, ex, ksel, my_key, my_idx, r_ids, r_w);
         if (tid == 0) r_n[0] = n;
         if (publish) {  // one workgroup publishes it (down kernel, introspection)
             wave_sync();
             if (tid < n) {
-                ws.ids[tid] = r_ids[tid];
-                ws.w[tid] = r_w[tid];
+                if constexpr (COH) {
+                    st_dev(ws.ids + tid, r_ids[tid]);
+                    st_devf(ws.w + tid, r_w[tid]);
+                } else {
+                    ws.ids[tid] = r_ids[tid];
+                    ws.w[tid] = r_w[tid];
+                }
             }
             if (tid == 0) {
-                ws.n_sel[0] = n;
+                if constexpr (COH)
+                    st_dev(ws.n_sel, n);
+                else
+                    ws.n_sel[0] = n;
                 if (ws.stats) {
                     atomicAdd(&ws.stats[0], 1ull);
                     atomicAdd(&ws.stats[1], (unsigned long long)n);
                 }
+            }
+            if (pub) {  // this wave's stores are complete before the counter moves
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_waitcnt(0);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (tid == 0) __hip_atomic_fetch_add(pub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
@@ -161,7 +196,7 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
     float wgt = 0.0f;
     if (!shared) {
         if (slot >= r_n[0]) return;  // workgroup-uniform
-        load_rows(gate, up, r_ids[slot], wq);
+        if (!loaded) load_rows(gate, up, r_ids[slot], wq);
         wgt = r_w[slot];
     }
 
@@ -191,23 +226,35 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
 #pragma unroll
         for (int p = 0; p < P; p++) tv[p][j] = ddv * tv[p][j];  // t = d * sx (gemv.rs:145)
     }
+    // sub-block pairs (2c, 2c+1): the nibbles once for both levels
 #pragma unroll
-    for (int p = 0; p < P; p++) {
+    for (int c = 0; c < 4; c++) {
+        int4 xa[P][4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int4* xa = reinterpret_cast<const int4*>(xq + p * XP + sb * XSB + 64 * c);  // sub-blocks 2c, 2c+1
-            const int4 x0 = xa[0], x1 = xa[1], x2 = xa[2], x3 = xa[3];
-            const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-            int d0 = 0, d1 = 0;
+        for (int p = 0; p < P; p++) {
+            const int4* src = reinterpret_cast<const int4*>(xq + p * XP + sb * XSB + 64 * c);
 #pragma unroll
-            for (int w = 0; w < 8; w++) {
-                const uint32_t qw = w32[4 + 8 * c + w];
-                d0 = sdot4((int)nib(qw, 0), xl[w], d0);
-                d1 = sdot4((int)nib(qw, 1), xh[w], d1);
+            for (int i = 0; i < 4; i++) xa[p][i] = src[i];
+        }
+        int d0[P], d1[P];
+#pragma unroll
+        for (int p = 0; p < P; p++) d0[p] = d1[p] = 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t qw = w32[4 + 8 * c + w];
+            const int lo = (int)nib(qw, 0), hi = (int)nib(qw, 1);
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                const int xl = w < 4 ? (&xa[p][0].x)[w] : (&xa[p][1].x)[w - 4];
+                const int xh = w < 4 ? (&xa[p][2].x)[w] : (&xa[p][3].x)[w - 4];
+                d0[p] = sdot4(lo, xl, d0[p]);
+                d1[p] = sdot4(hi, xh, d1[p]);
             }
-            dotv[p][2 * c] = (float)d0;
-            dotv[p][2 * c + 1] = (float)d1;
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            dotv[p][2 * c] = (float)d0[p];
+            dotv[p][2 * c + 1] = (float)d1[p];
         }
     }
     // the chain (gemv.rs:141-148) in block order: superblock sb continues where sb-1 stopped
@@ -288,6 +335,9 @@ constexpr uint32_t ROUTE_LDS = K_MAX * 8 + 16 + ROUTE_CAND * 8;  // + E floats f
 struct NoHook {
     __device__ void operator()(const uint32_t*, uint32_t) const {}
 };
+struct NoPre {
+    __device__ void operator()() const {}
+};
 
 template <int P, int NSB, int NJ>
 __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
@@ -295,7 +345,7 @@ __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
         uint32_t k, Policy pol, uint32_t kcap) {
     extern __shared__ __align__(16) uint8_t smem[];
     gateup_unit<P, NSB, NJ, false, true>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
-                            blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoHook{});
+                            blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoPre{}, NoHook{});
 }
 
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
@@ -507,47 +557,32 @@ __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Wor
 
 // ---- the whole decode layer in one launch ----------------------------------------------------
 //
-// Three phases separated by grid barriers: (1) router logits and the shared gate's logit, one
-// wave per router row; (2) every workgroup routes the token, workgroups with a (slot, strip) unit
-// run it, and every workgroup requests the down-projection weights of its phase-3 rows as soon
-// as the routing is known; (3) down + combine for 4 output rows per workgroup.  Requires the
-// whole grid resident at once (the host checks occupancy); the barriers wait a bounded time.
+// One grid, four roles by workgroup index, in dependency order:
+//   [0, nA)              router logits (attn::dot order, exec.rs:1003-1011) and the shared gate's
+//                        logit, a wave per router row;
+//   next S = F / 16      the shared expert's gate/up strips: they need no routing, so their weights
+//                        are requested at once (only the sigmoid fold waits for the gate's logit);
+//   next kcap * S        the routed gate/up units (slot, strip): each waits for the router
+//                        workgroups, routes the token itself (no round trip through memory between
+//                        the logits and the expert weights) and runs its unit; unit (0, 0) also
+//                        publishes the routing;
+//   last H / DN_R        down + combine for DN_R output rows each: waits for the published routing,
+//                        requests its down weights at once, then waits for every gate/up unit.
+// A workgroup only waits on workgroups of lower index, which the dispatcher places first, so the
+// grid need not be resident at once.  The waits are counters in ws.counters, raised by the waited-on
+// workgroups once their device-coherent stores (st_dev: past the per-XCD L2s) are complete; the last
+// workgroup to finish zeroes them for the next launch.  Every wait is bounded: on time-out it raises
+// the flag at ws.counters[2] (trk_get_stats reports it) and carries on.
 
-constexpr uint32_t BARRIER_SPIN = 1u << 16;  // polls before a barrier gives up (~tens of ms)
+constexpr uint32_t PIPE_A = BAR_LINE, PIPE_R = 2 * BAR_LINE, PIPE_B = 3 * BAR_LINE, PIPE_D = 4 * BAR_LINE;
+constexpr uint32_t PIPE_SPIN = 1u << 16;  // polls before a wait gives up (tens of ms)
 
-// Two-level grid barrier on counters that only grow, so no reset is needed between barriers or
-// launches (graph replays included).  A workgroup arrives on its group's counter; the last of a
-// group arrives on the top counter; the last group writes every group's release word, and each
-// workgroup polls its own group's word.  No line sees more than BAR_GROUPS arrivals or more than
-// nwg / BAR_GROUPS pollers.  Words (u32 index into ws.counters): top at 0, time-out flag at 2,
-// group g's counter at BAR_LINE * (1 + g), its release word at BAR_LINE * (1 + g) + 32.
-// Data crossing the barrier is written and read with the device-coherent ld_dev / st_dev, so
-// completing this workgroup's stores (s_waitcnt) before arriving is the whole release: no L2
-// write-back or invalidate (each of those is a whole-cache operation on gfx950).
-__device__ __forceinline__ void grid_barrier(uint32_t* words, uint32_t nwg) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
+__device__ __forceinline__ void pipe_wait(uint32_t* words, uint32_t which, uint32_t target) {
     if (threadIdx.x == 0) {
-        const uint32_t g = blockIdx.x % BAR_GROUPS, gsize = nwg / BAR_GROUPS;
-        unsigned long long* top = reinterpret_cast<unsigned long long*>(words);
-        unsigned long long* sub = reinterpret_cast<unsigned long long*>(words + BAR_LINE * (1 + g));
-        const unsigned long long* rel = reinterpret_cast<const unsigned long long*>(words + BAR_LINE * (1 + g) + 32);
-        const unsigned long long old =
-                __hip_atomic_fetch_add(sub, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long epoch = old / gsize + 1;  // barriers completed once this one is
-        if (old % gsize == gsize - 1) {
-            const unsigned long long t = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (t % BAR_GROUPS == BAR_GROUPS - 1)
-                for (uint32_t h = 0; h < BAR_GROUPS; h++)
-                    __hip_atomic_store(reinterpret_cast<unsigned long long*>(words + BAR_LINE * (1 + h) + 32), epoch,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
         uint32_t spins = 0;
-        while (ld_dev(rel) < epoch) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++spins == BARRIER_SPIN) {
+        while (ld_dev(words + which) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == PIPE_SPIN) {
                 __hip_atomic_fetch_or(words + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
@@ -556,25 +591,34 @@ __device__ __forceinline__ void grid_barrier(uint32_t* words, uint32_t nwg) {
     __syncthreads();
 }
 
+// raise counter `which` once every thread's stores of this workgroup are complete
+__device__ __forceinline__ void pipe_signal(uint32_t* words, uint32_t which) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(words + which, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int P, int NSB, int NJ, int NSBF>
-__global__ __launch_bounds__(256) void decode_layer_kernel(const float* __restrict__ router,
-                                                          const float* __restrict__ bias,
-                                                          const float* __restrict__ shgv, Mat gate, Mat up,
-                                                          Mat down, Mat shg, Mat shu, Mat shd,
-                                                          const float* __restrict__ x, const float* __restrict__ lg_in,
-                                                          Workspace ws, uint32_t k, Policy pol, uint32_t kcap,
-                                                          float* __restrict__ out, int residual, uint32_t rsm_bytes) {
+__global__ __launch_bounds__(256) void decode_pipe_kernel(const float* __restrict__ router,
+                                                         const float* __restrict__ bias,
+                                                         const float* __restrict__ shgv, Mat gate, Mat up, Mat down,
+                                                         Mat shg, Mat shu, Mat shd, const float* __restrict__ x,
+                                                         const float* __restrict__ lg_in, Workspace ws, uint32_t k,
+                                                         Policy pol, uint32_t kcap, float* __restrict__ out,
+                                                         int residual, uint32_t rsm_bytes, uint32_t nA) {
     constexpr uint32_t H = NSB * 256;
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t* rsm = smem;              // routing (kept through phase 3)
-    uint8_t* usm = smem + rsm_bytes;  // unit area: gate/up, then down
+    uint8_t* rsm = smem;              // routing
+    uint8_t* usm = smem + rsm_bytes;  // unit area: gate/up or down
     const uint32_t E = ws.E, nwg = gridDim.x, wg = blockIdx.x, tid = threadIdx.x;
-    const uint32_t strips = gate.rows / 16;
+    const uint32_t S = gate.rows / 16, gu = S * (kcap + 1);
+    uint32_t* cw = ws.counters;
 
-    // phase 1: logits (attn::dot order, exec.rs:1003-1011) and the shared gate's logit
-    {
+    if (wg < nA) {
         const uint32_t wv = tid / 64, lane = tid % 64;
-        for (uint32_t row = wg * 4 + wv; row <= E; row += nwg * 4) {
+        for (uint32_t row = wg * 4 + wv; row <= E; row += nA * 4) {
             if (lg_in && row < E) continue;
             const float* wr = row < E ? router + (size_t)row * H : shgv;
             float res[DOT_MR];
@@ -586,39 +630,42 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(const float* __restri
                     st_devf(ws.shl, res[0]);
             }
         }
+        pipe_signal(cw, PIPE_A);
+    } else if (wg < nA + gu) {
+        const uint32_t u = wg - nA;
+        const uint32_t slot = u < S ? kcap : u / S - 1, strip = u % S;  // the shared strips first
+        const float* lg = lg_in ? lg_in : ws.rlog;
+        gateup_unit<P, NSB, NJ, true, false>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, slot, strip, true, false,
+                                             slot == 0 && strip == 0, usm, rsm,
+                                             [&]() { pipe_wait(cw, PIPE_A, nA); }, NoHook{}, cw + PIPE_R);
+        pipe_signal(cw, PIPE_B);
+    } else {
+        const uint32_t row0 = (wg - nA - gu) * DN_R;
+        uint32_t* r_ids = reinterpret_cast<uint32_t*>(rsm);  // [K_MAX] ids, then n
+        pipe_wait(cw, PIPE_R, 1);
+        if (tid < kcap) r_ids[tid] = ld_dev(ws.ids + tid);
+        if (tid == 0) r_ids[K_MAX] = ld_dev(ws.n_sel);
+        __syncthreads();
+        const uint32_t n = r_ids[K_MAX];
+        DownFirst first;
+        down_first<NSBF>(down, shd, kcap, n, r_ids, row0, first);  // in flight during the wait
+        pipe_wait(cw, PIPE_B, gu);
+        down_unit<P, NSBF, true>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first);
     }
-    grid_barrier(ws.counters, nwg);
-
-    // phase 2: route, gate/up units, down weights requested
-    const float* lg = lg_in ? lg_in : ws.rlog;
-    const uint32_t units = (kcap + 1) * strips;
-    const bool active = wg < units;
-    const uint32_t row0 = wg * DN_R;
-    DownFirst first;
-    gateup_unit<P, NSB, NJ, true, false>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, active ? wg / strips : 0u,
-                            active ? wg % strips : 0u, active, true, wg == 0, usm, rsm,
-                            [&](const uint32_t* ids, uint32_t n) {
-                                down_first<NSBF>(down, shd, kcap, n, ids, row0, first);
-                            });
-    grid_barrier(ws.counters, nwg);
-
-    // phase 3: down + combine (exec.rs:1610-1621)
-    const uint32_t* r_ids = reinterpret_cast<const uint32_t*>(rsm);
-    const uint32_t n = r_ids[2 * K_MAX];
-    down_unit<P, NSBF, true>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first);
+    __syncthreads();
+    if (tid == 0) {  // the last workgroup out zeroes the counters for the next launch
+        const uint32_t done = __hip_atomic_fetch_add(cw + PIPE_D, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == nwg - 1) {
+            st_dev(cw + PIPE_A, 0u);
+            st_dev(cw + PIPE_R, 0u);
+            st_dev(cw + PIPE_B, 0u);
+            st_dev(cw + PIPE_D, 0u);
+        }
+    }
 }
 
-// The shape the one-launch layer is instantiated for (BASELINE's layer: H = 2048, F = 512, E <= 512,
-// two-level activations, Q4_K down) with a grid of H / 4 workgroups that covers every gate/up unit.
-bool decode_layer_supported(const Mat& gate, const Mat& down, const Mat& sh_down, uint32_t E, int pair,
-                            uint32_t kcap) {
-    const uint32_t H = gate.k, F = gate.rows, nwg = H / DN_R;
-    return H == 2048 && F == 512 && E <= 512 && pair && down.fmt == TRK_FMT_Q4_K && sh_down.fmt == TRK_FMT_Q4_K &&
-           (kcap + 1) * (F / 16) <= nwg && nwg % BAR_GROUPS == 0;
-}
-
-template <int P, int NSB, int NJ, int NSBF>
-static size_t layer_lds(uint32_t E, uint32_t kcap, bool mass_all, uint32_t& rsm) {
+template <int P, int NSB, int NSBF>
+static size_t pipe_lds(uint32_t E, uint32_t kcap, bool mass_all, uint32_t& rsm) {
     rsm = (ROUTE_LDS + (mass_all ? E * 4 : 0) + 15) / 16 * 16;
     const size_t gu = gu_lds_x<P, NSB>();
     const size_t slots = kcap + 1, F = NSBF * 256, nbf = F / 16;
@@ -626,32 +673,66 @@ static size_t layer_lds(uint32_t E, uint32_t kcap, bool mass_all, uint32_t& rsm)
     return rsm + (gu > dn ? gu : dn);
 }
 
-// Fused decode layer: returns hipErrorNotSupported when the shape or the GPU cannot hold the
-// grid (the caller then runs the three separate launches).  check_only: answer that (queries the
-// occupancy) without launching.
+// The shapes the one-launch layer is instantiated for (H / 256, F / 256): BASELINE's layer
+// (2048, 512) and the test shapes (512, 256), (768, 768).
+static int pipe_shape(uint32_t H, uint32_t F) {
+    if (H == 2048 && F == 512) return 0;
+    if (H == 512 && F == 256) return 1;
+    if (H == 768 && F == 768) return 2;
+    return -1;
+}
+
+bool decode_layer_supported(const Mat& gate, const Mat& down, const Mat& sh_down, uint32_t E, int pair,
+                            uint32_t kcap) {
+    (void)pair;
+    (void)kcap;
+    return pipe_shape(gate.k, gate.rows) >= 0 && E <= 1024 && down.fmt == sh_down.fmt && gate.k % DN_R == 0;
+}
+
+template <int P, int NSB, int NJ, int NSBF>
+static hipError_t launch_pipe(const float* router, const float* bias, const float* shexp_gate, const Mat& gate,
+                              const Mat& up, const Mat& down, const Mat& sh_gate, const Mat& sh_up, const Mat& sh_down,
+                              const float* x, const float* rlog, const Workspace& ws, uint32_t k, Policy pol,
+                              uint32_t kcap, float* out, int residual, hipStream_t st) {
+    const uint32_t H = gate.k, F = gate.rows, E = ws.E;
+    const bool mass_all = pol.enabled && pol.basis == TRK_BASIS_ALL;
+    uint32_t rsm = 0;
+    const size_t lds = pipe_lds<P, NSB, NSBF>(E, kcap, mass_all, rsm);
+    const uint32_t nA = rlog ? 1u : (E + 1 + 3) / 4;
+    const uint32_t nwg = nA + (F / 16) * (kcap + 1) + H / DN_R;
+    decode_pipe_kernel<P, NSB, NJ, NSBF><<<nwg, 256, lds, st>>>(router, bias, shexp_gate, gate, up, down, sh_gate,
+                                                                sh_up, sh_down, x, rlog, ws, k, pol, kcap, out,
+                                                                residual, rsm, nA);
+    return hipGetLastError();
+}
+
+// The whole layer in one launch: hipErrorNotSupported when the shape has no instantiation (the
+// caller then runs the three separate launches).  check_only: answer that without launching.
 hipError_t launch_decode_layer(const float* router, const float* bias, const float* shexp_gate, const Mat& gate,
                                const Mat& up, const Mat& down, const Mat& sh_gate, const Mat& sh_up,
                                const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
                                Policy pol, int pair, uint32_t kcap, float* out, int residual, bool check_only,
                                hipStream_t st) {
-    const uint32_t H = gate.k, E = ws.E;
-    const uint32_t nwg = H / DN_R;
-    if (!decode_layer_supported(gate, down, sh_down, E, pair, kcap) || !router) return hipErrorNotSupported;
-    const bool mass_all = pol.enabled && pol.basis == TRK_BASIS_ALL;
-    uint32_t rsm = 0;
-    const size_t lds = layer_lds<2, 8, 8, 2>(E, kcap, mass_all, rsm);
-    auto kern = decode_layer_kernel<2, 8, 8, 2>;
-    if (check_only) {  // can the whole grid be resident at once?
-        int per_cu = 0, dev = 0, cus = 0;
-        hipError_t e;
-        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
-        if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds)) != hipSuccess) return e;
-        return (uint64_t)per_cu * (uint64_t)cus >= nwg ? hipSuccess : hipErrorNotSupported;
+    const int shp = pipe_shape(gate.k, gate.rows);
+    if (!decode_layer_supported(gate, down, sh_down, ws.E, pair, kcap) || !ws.counters || shp < 0 ||
+        (!router && !rlog))
+        return hipErrorNotSupported;
+    if (check_only) return hipSuccess;
+    const bool nj16 = route_nj(ws.E) == 16;
+#define PIPE_ARGS router, bias, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, x, rlog, ws, k, pol, kcap, out, residual, st
+#define PIPE_SHAPE(P, NSB, NSBF) \
+    return nj16 ? launch_pipe<P, NSB, 16, NSBF>(PIPE_ARGS) : launch_pipe<P, NSB, 8, NSBF>(PIPE_ARGS);
+    if (pair) {
+        if (shp == 0) PIPE_SHAPE(2, 8, 2)
+        if (shp == 1) PIPE_SHAPE(2, 2, 1)
+        PIPE_SHAPE(2, 3, 3)
+    } else {
+        if (shp == 0) PIPE_SHAPE(1, 8, 2)
+        if (shp == 1) PIPE_SHAPE(1, 2, 1)
+        PIPE_SHAPE(1, 3, 3)
     }
-    kern<<<nwg, 256, lds, st>>>(router, bias, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, x, rlog, ws, k, pol,
-                                kcap, out, residual, rsm);
-    return hipGetLastError();
+#undef PIPE_SHAPE
+#undef PIPE_ARGS
 }
 
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair, uint32_t kcap,

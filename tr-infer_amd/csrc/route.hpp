@@ -92,9 +92,10 @@ __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict_
 // to their rank's slot.
 // COH: the logits were written earlier in the same launch by other workgroups (device-coherent
 // loads).
+// Selection: lane j < ksel gets the key and index of the j-th winner (my_key, my_idx); returns ksel.
 template <int NJ, bool COH = false>
-__device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
-                              uint2* cand, float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
+__device__ uint32_t route_select(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol,
+                                 uint32_t lane, uint2* cand, uint32_t& my_key, uint32_t& my_idx) {
     // all NJ loads go out together: clamped indices, no per-load branch
     float v[NJ];
 #pragma unroll
@@ -134,14 +135,25 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
         }
         C += (uint32_t)__popcll(m);
     }
-    uint32_t my_key = 0, my_idx = 0xffffffffu, ksel;
+    my_key = 0;
+    my_idx = 0xffffffffu;
+    uint32_t ksel;
     if (C <= 64u) {
         wave_sync();
         const uint2 me = lane < C ? cand[lane] : make_uint2(0u, 0u);
         uint32_t rank = 0;
-        for (uint32_t t = 0; t < C; t++) {  // candidate t's key from lane t's register
-            const uint32_t kt = (uint32_t)__builtin_amdgcn_readlane((int)me.x, (int)t);
-            rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
+        if (C <= 16u) {  // the usual case: 16 independent lane reads, no loop
+            // lanes >= C hold key 0, below every candidate's key (>= 1), so they add nothing
+#pragma unroll
+            for (uint32_t t = 0; t < 16u; t++) {
+                const uint32_t kt = (uint32_t)__builtin_amdgcn_readlane((int)me.x, (int)t);
+                rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
+            }
+        } else {
+            for (uint32_t t = 0; t < C; t++) {  // candidate t's key from lane t's register
+                const uint32_t kt = (uint32_t)__builtin_amdgcn_readlane((int)me.x, (int)t);
+                rank += (kt > me.x || (kt == me.x && t < lane)) ? 1u : 0u;
+            }
         }
         if (lane < C && rank < kk) cand[64 + rank] = me;
         wave_sync();
@@ -154,6 +166,16 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
     } else {
         ksel = route_select_rounds<NJ, COH>(lg, E, kk, lane, my_key, my_idx);
     }
+    return ksel;
+}
+
+// Weights of a selection (route_select's per-lane winners): exp of (v - max), the mass loop of
+// route_mass, the renormalisation.  Lanes < count write ids_out / w_out; returns count.
+template <bool COH = false>
+__device__ uint32_t route_weights(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol,
+                                  uint32_t lane, float* ex, uint32_t ksel, uint32_t my_key, uint32_t my_idx,
+                                  uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
+    const uint32_t kk = pol.enabled ? pol.max : k;
     if (ksel == 0) return 0;  // nothing selectable (the reference would index u32::MAX)
     const float my_tv = lane < ksel ? fkey_inv(my_key) : -__builtin_inff();
     const float mx = rdl(my_tv, 0);
@@ -179,13 +201,29 @@ __device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t
         }
     }
     if (count > ksel) count = ksel;
-    float sum = 0.0f;  // renorm (router.rs:93-104)
-    for (uint32_t j = 0; j < count; j++) sum += rdl(e, j);
+    float sum = 0.0f;  // renorm (router.rs:93-104): the sequential f32 sum, four lane reads at a time
+    for (uint32_t j0 = 0; j0 < count; j0 += 4) {
+        float ev[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) ev[i] = rdl(e, j0 + i < 64u ? j0 + i : 63u);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++)
+            if (j0 + i < count) sum += ev[i];
+    }
     if (lane < count) {
         ids_out[lane] = my_idx;
         w_out[lane] = e / sum;
     }
     return count;
+}
+
+// One token on one whole wave: selection, then weights.
+template <int NJ, bool COH = false>
+__device__ uint32_t route_row(const float* __restrict__ lg, uint32_t E, uint32_t k, const Policy& pol, uint32_t lane,
+                              uint2* cand, float* ex, uint32_t* __restrict__ ids_out, float* __restrict__ w_out) {
+    uint32_t my_key, my_idx;
+    const uint32_t ksel = route_select<NJ, COH>(lg, E, k, pol, lane, cand, my_key, my_idx);
+    return route_weights<COH>(lg, E, k, pol, lane, ex, ksel, my_key, my_idx, ids_out, w_out);
 }
 
 constexpr uint32_t ROUTE_CAND = 96;  // LDS entries (uint2) of route_row's candidate lists per wave
