@@ -57,7 +57,7 @@ def main():
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
                          "48-layer RMSNorm + residual stack at M=1 and M=512); q80 / q51 / q6k: the layer at "
                          "M=1 and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
     ap.add_argument("--fusion", type=int, default=None, choices=(0, 1),
@@ -219,7 +219,7 @@ def main():
 
     cpu = None
     if not args.no_cpu and prim == 1:
-        cpu = cpu_baseline(layers[0], xs[1], args.cpu_seconds)
+        cpu = cpu_baseline(layers[0], xs[1], args.cpu_seconds, trmoe.zipf_bias(1, E))
 
     line = {
         "metric": "MoE-layer tokens/s (decode M=1; M=4/8/16/512 in results)",
@@ -377,9 +377,31 @@ def measured_traffic(kernel, m):
         return None
 
 
-def cpu_baseline(w, x_dev, seconds):
-    """The oracle (a scalar C restatement of the reference's CPU moe_block) on layer 0, timed on
-    this host over a bounded number of tokens."""
+def host_info(cpus):
+    """CPU model and the NUMA nodes of the CPUs the baseline's threads are pinned to."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nodes = set()
+    for c in cpus:
+        try:
+            nodes.update(int(d[4:]) for d in os.listdir(f"/sys/devices/system/cpu/cpu{c}") if d.startswith("node"))
+        except (OSError, ValueError):
+            pass
+    return model, sorted(nodes)
+
+
+def cpu_baseline(w, x_dev, seconds, bias=None):
+    """The reference's CPU MoE layer timed on this host: moe_block (decode, M = 1) and moe_batch
+    (M = 512) restated with AVX-512 VNNI over a pool of pinned threads (one tile of at most 16
+    cores, the reference's T = 1 layout; oracle/cpu_moe.c), on layer 0's weights.  Each leg runs for
+    about `seconds`.  A host without AVX-512 VNNI times the scalar C oracle on one core instead."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -391,24 +413,62 @@ def cpu_baseline(w, x_dev, seconds):
                         t["sh_down"].cpu().numpy())
     x0 = x_dev.cpu().numpy()[0]
     rng = np.random.default_rng(0)
-    xs = [x0] + [(x0 * rng.choice([-1.0, 1.0], H)).astype(np.float32) for _ in range(63)]
-    for xx in xs[:4]:  # weight re-layout is offline in the reference: do it before timing
-        orc.ensure(O.route_topk(orc.logits(xx, True)[0], K)[0])
-    n, t0 = 0, time.perf_counter()
-    while n < len(xs) and (time.perf_counter() - t0 < seconds or n < 2):
-        orc.ensure(O.route_topk(orc.logits(xs[n], True)[0], K)[0])
-        ts = time.perf_counter()
-        orc.moe_block(xs[n], k=K, hiprec=True)
-        n += 1
-        t0 += 0  # conversion time excluded below
-        if n == 1:
-            spent = time.perf_counter() - ts
-        else:
+    xs = [x0] + [(x0 * rng.choice([-1.0, 1.0], H)).astype(np.float32) for _ in range(255)]
+    vnni = O.cpu_have_vnni()
+    if not vnni:
+        for xx in xs[:64]:  # weight re-layout is offline in the reference: do it before timing
+            orc.ensure(O.route_topk(orc.logits(xx, True)[0], K)[0])
+        n, spent = 0, 0.0
+        while n < 64 and (spent < seconds or n < 2):
+            ts = time.perf_counter()
+            orc.moe_block(xs[n], k=K, hiprec=True)
             spent += time.perf_counter() - ts
-    return {"value": round(n / spent, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n} decode tokens (M=1) of layer 0 through the scalar C oracle (moe_block with pair "
-                      f"quantisation; Q4_K->TQ re-layout done beforehand, as the reference packs offline)",
-            "seconds": round(spent, 2)}
+            n += 1
+        return {"value": round(n / spent, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"{n} decode tokens (M=1) of layer 0 through the scalar C oracle (this host has no "
+                          f"AVX-512 VNNI)", "seconds": round(spent, 2)}
+
+    # weight re-layout (GGUF -> TQ) is offline in the reference: every expert before timing
+    t0 = time.perf_counter()
+    orc.ensure(range(E))
+    conv = time.perf_counter() - t0
+    cm = O.CpuMoe(0)
+    try:
+        amx = bool(cm.L.cpu_amx_available())
+        model, nodes = host_info(cm.cpus)
+        # decode: M = 1 tokens one after another (moe_block, exec.rs:1540-1623)
+        for xx in xs[:4]:
+            cm.block(orc, xx, K)
+        n, spent = 0, 0.0
+        while spent < seconds / 2 or n < 8:
+            ts = time.perf_counter()
+            cm.block(orc, xs[n % len(xs)], K)
+            spent += time.perf_counter() - ts
+            n += 1
+        # batch: M = 512 with the Zipf router bias the GPU leg uses (moe_batch, exec_batch.rs:1404-1580)
+        orc.router_bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        xb = np.ascontiguousarray(rng.standard_normal((512, H)), np.float32)
+        cm.batch(orc, xb, K)
+        nb, sb = 0, 0.0
+        while sb < seconds / 2 or nb < 1:
+            ts = time.perf_counter()
+            cm.batch(orc, xb, K)
+            sb += time.perf_counter() - ts
+            nb += 1
+        orc.router_bias = None
+    finally:
+        threads, cpus = cm.threads, cm.cpus
+        cm.close()
+    return {"value": round(n / spent, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "m512_tokens_per_s": round(nb * 512 / sb, 1),
+            "sample": f"{n} decode tokens (M=1, moe_block, {len(xs)} distinct inputs in turn) and {nb} batch(es) of M=512 (moe_batch, Zipf-biased "
+                      f"router) of layer 0 through the AVX-512 VNNI restatement of the reference's CPU path "
+                      f"(oracle/cpu_moe.c) on one tile of {threads} pinned threads; GGUF->TQ re-layout of all "
+                      f"{E} experts done beforehand ({conv:.1f} s), as the reference packs offline",
+            "host": {"cpu": model, "cpus": cpus, "numa_nodes": nodes, "avx512_vnni": True,
+                     "amx": "available, unused: the reference's routed experts run VNNI" if amx else
+                            "unavailable -> VNNI timed"},
+            "seconds": round(spent + sb, 2)}
 
 
 if __name__ == "__main__":

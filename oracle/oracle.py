@@ -457,3 +457,83 @@ class OracleLayer:
                     ent_expert=ent_expert[:n_ent].copy(), grp_start=grp_start[:ng + 1].copy(),
                     grp_expert=grp_expert[:ng].copy(), grp_order=grp_order[:ng].copy(), n_ent=n_ent, n_groups=ng,
                     rlog=rlog, stats=(st.rows, st.experts))
+
+
+# ---- the timed CPU baseline (libcpumoe.so: AVX-512 VNNI, threaded) ----------------------------
+
+CPU_LIB_PATH = os.path.join(HERE, "libcpumoe.so")
+_cpu = None
+
+
+def cpu_lib() -> C.CDLL:
+    """libcpumoe.so (cpu_moe.c): the reference's CPU MoE path on AVX-512 VNNI over a pinned pool."""
+    global _cpu
+    if _cpu is None:
+        if not os.path.exists(CPU_LIB_PATH):
+            build()
+        L = C.CDLL(CPU_LIB_PATH)
+        vp = C.c_void_p
+        L.cpu_have_vnni.restype = C.c_int
+        L.cpu_amx_available.restype = C.c_int
+        L.cpu_pool_create.restype = vp
+        L.cpu_pool_create.argtypes = [C.c_int]
+        L.cpu_pool_destroy.argtypes = [vp]
+        L.cpu_pool_size.argtypes = [vp]
+        L.cpu_pool_cpu.argtypes = [vp, C.c_int]
+        L.cpu_moe_block.argtypes = [vp, C.POINTER(MoeW), vp, C.c_int, C.POINTER(Policy), C.c_int, vp, vp, vp]
+        L.cpu_moe_batch.argtypes = [vp, C.POINTER(MoeW), vp, C.c_int, C.c_int, C.POINTER(Policy), C.c_int, vp]
+        _cpu = L
+    return _cpu
+
+
+def cpu_have_vnni() -> bool:
+    return bool(cpu_lib().cpu_have_vnni())
+
+
+class CpuMoe:
+    """A pool of `threads` pinned threads (0: one per allowed CPU, at most 16 = one tile) running
+    the VNNI restatement of moe_block / moe_batch on an OracleLayer's TQ weights."""
+
+    def __init__(self, threads=0):
+        self.L = cpu_lib()
+        if not self.L.cpu_have_vnni():
+            raise RuntimeError("this host has no AVX-512 VNNI")
+        self.p = self.L.cpu_pool_create(threads)
+        self.threads = self.L.cpu_pool_size(self.p)
+        self.cpus = [self.L.cpu_pool_cpu(self.p, i) for i in range(self.threads)]
+
+    def close(self):
+        if self.p:
+            self.L.cpu_pool_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def block(self, layer, x, k=10, policy=None, hiprec=True):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(layer.H, np.float32)
+        ids = np.zeros(MOE_K_MAX, np.uint32)
+        w = np.zeros(MOE_K_MAX, np.float32)
+        pol = Policy(*policy) if policy else None
+        W = layer._w()
+        n = self.L.cpu_moe_block(self.p, C.byref(W), _p(x), k, C.byref(pol) if pol else None, int(hiprec), _p(out),
+                                 _p(ids), _p(w))
+        if n < 0:
+            raise RuntimeError("cpu_moe_block failed")
+        return dict(out=out, ids=ids[:n].copy(), w=w[:n].copy(), k=n)
+
+    def batch(self, layer, x, k=10, policy=None, router_dot_max_m=16):
+        x = np.ascontiguousarray(x, np.float32)
+        M = x.shape[0]
+        out = np.zeros((M, layer.H), np.float32)
+        pol = Policy(*policy) if policy else None
+        W = layer._w()
+        n = self.L.cpu_moe_batch(self.p, C.byref(W), _p(x), M, k, C.byref(pol) if pol else None, router_dot_max_m,
+                                 _p(out))
+        if n < 0:
+            raise RuntimeError("cpu_moe_batch failed")
+        return dict(out=out, n_ent=n)
