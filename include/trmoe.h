@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TRK_ABI_VERSION 2
+#define TRK_ABI_VERSION 3
 #define TRK_MOE_K_MAX 32 /* router.rs:6 MOE_K_MAX */
 
 typedef enum {
@@ -41,6 +41,13 @@ typedef enum {
 } trk_status;
 
 enum { TRK_FMT_Q5_1 = 7, TRK_FMT_Q8_0 = 8, TRK_FMT_Q4_K = 12, TRK_FMT_Q6_K = 14 }; /* GGML type ids (python/trpack/blocks.py:11) */
+/* The reference's packed TQ codecs (crates/tr-format/src/codec.rs:1-46, Codec {bits, kb}):
+ * fmt = bits << 8 | kb.  A TQ matrix is ceil(rows / 16) strips of k / kb blocks, each block
+ * d[16] f16 | m[16] f16 | q | (5-bit) high-bit plane, exactly as trpack writes it. */
+enum {
+    TRK_FMT_TQ4_16 = 0x410, TRK_FMT_TQ4_32 = 0x420, TRK_FMT_TQ5_16 = 0x510,
+    TRK_FMT_TQ5_32 = 0x520, TRK_FMT_TQ8_16 = 0x810, TRK_FMT_TQ8_32 = 0x820
+};
 enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
 
 /* A stack of `count` weight matrices [rows][k] in GGUF superblocks, row-major, `stride` bytes
@@ -48,7 +55,8 @@ enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
  * (crates/tr-model/src/weights.rs:14-35): `fmt` names the GGUF block format read directly on
  * the GPU where the CPU path reads its TQ re-layout.  Gate/up: Q4_K.  Down (routed and shared
  * alike): Q4_K, Q6_K, Q8_0 or Q5_1 (blocks.py:57-78).  Q4_K, Q8_0 and Q5_1 stacks are 16-byte aligned,
- * Q6_K 2-byte aligned. */
+ * Q6_K 2-byte aligned.  trk_gemv also takes a TQ codec (TRK_FMT_TQ*, 4-byte aligned): then the
+ * matrix is the reference's packed strips, exactly as trpack writes them. */
 typedef struct {
     const void *ptr;
     uint32_t rows, k;
@@ -174,13 +182,21 @@ int trk_route(const float *logits, uint32_t m, uint32_t n_expert, uint32_t k, co
 int trk_quantize(const float *x, uint32_t m, uint32_t k, uint32_t kb, int pair, int8_t *q, float *scale,
                  int32_t *sum, void *stream);
 
-/* y[rows[i]][r] (+)= W_item[r] . x_i for int8 activation rows x (gemv_tq_rows / gemm_tq_rows,
- * gemv.rs:25-78) on a GGUF matrix.  The activation block is 32 for k = W.k rows read as gate/up
- * and 16 for down-style use: kb must be 32 (Q4_K only) or 16 (Q4_K, Q6_K).  pair: rows come in
- * (coarse, residual) pairs, m counts physical rows.  rows: NULL = identity. */
-int trk_gemv(const trk_mat *w, uint32_t item, uint32_t kb, const int8_t *q, const float *scale,
-             const int32_t *sum, uint32_t m, int pair, float *y, uint32_t ldy, const uint32_t *rows,
-             int accumulate, void *stream);
+/* y[rows[i] * ldy + r] (+)= W_item[r] . x_i for the rows r of 16-row strips [s0, s1) and int8
+ * activation rows x: gemv_tq_rows / gemm_tq_rows (gemv.rs:16-78) with w = the strip-s0 pointer of
+ * matrix `item`.  Any number of activation rows (gemm_tq_rows' chunking is internal); logical
+ * rows are written in order, so a row map with repeats accumulates as the reference's does.
+ *   w->fmt  a TQ codec (kb must equal the codec's, gemv.rs:27; k a multiple of kb), or a GGUF
+ *           block format (k a multiple of 256) read as its TQ conversion: Q4_K with kb 32 or 16,
+ *           Q6_K with kb 16, Q8_0 / Q5_1 with kb 32 or 16 (blocks.py:57-113);
+ *   s1      at most ceil(rows / 16).  TQ writes every row of each strip (zero padding rows
+ *           included, as the reference's 16-wide stores do); GGUF writes rows < w->rows;
+ *   pair    rows come in (coarse, residual) pairs, m counts physical rows;
+ *   rows    NULL = identity (logical row i to y row i).
+ * q: 16-byte aligned, [m][k]; scale / sum: [m][k / kb]. */
+int trk_gemv(const trk_mat *w, uint32_t item, uint32_t s0, uint32_t s1, uint32_t kb, const int8_t *q,
+             const float *scale, const int32_t *sum, uint32_t m, int pair, float *y, uint32_t ldy,
+             const uint32_t *rows, int accumulate, void *stream);
 
 /* y = silu(g) * u (elem::swiglu_vec, elem.rs:173-175) over n floats. */
 int trk_swiglu(const float *g, const float *u, float *y, size_t n, void *stream);

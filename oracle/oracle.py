@@ -242,21 +242,26 @@ def quant_pair(x, kb):
     return q, s, su
 
 
-def gemv_tq(w, k, bits, kb, rows_out, q, s, su, pair=False, y=None, rows=None, accumulate=False, gemm=True):
-    """y[mi][r] (+)= W x_mi over all strips; q/s/su as returned by quant_rows/quant_pair."""
+def gemv_tq(w, k, bits, kb, rows_out, q, s, su, pair=False, y=None, rows=None, accumulate=False, gemm=True,
+            s0=0, s1=None, ldy=None):
+    """y[mi][r] (+)= W x_mi over strips [s0, s1) (default: all rows_out // 16) of a packed TQ
+    matrix w (the whole matrix: the strip-s0 pointer is taken here, as the reference's callers
+    do); q/s/su as returned by quant_rows/quant_pair."""
     q = np.ascontiguousarray(q, np.int8)
     s = np.ascontiguousarray(s, np.float32)
     su = np.ascontiguousarray(su, np.int32)
     m = q.shape[0]
     logical = m // 2 if pair else m
-    ldy = rows_out
+    s1 = rows_out // 16 if s1 is None else s1
+    ldy = rows_out if ldy is None else ldy
     if y is None:
-        y = np.zeros((logical if rows is None else int(np.max(rows)) + 1, rows_out), np.float32)
+        y = np.zeros((logical if rows is None else int(np.max(rows)) + 1, ldy), np.float32)
     qa = QAct(m, k, kb, _p(q), _p(s), _p(su), int(pair))
     rp = _p(np.ascontiguousarray(rows, np.uint32)) if rows is not None else None
+    w = np.ascontiguousarray(w, np.uint8)
+    off = s0 * (k // kb) * lib().orc_tq_block_bytes(bits, kb)
     fn = lib().orc_gemm_tq_rows if gemm else lib().orc_gemv_tq_rows
-    fn(_p(np.ascontiguousarray(w, np.uint8)), k, bits, kb, 0, rows_out // 16, C.byref(qa), _p(y), ldy, rp,
-       int(accumulate))
+    fn(C.c_void_p(w.ctypes.data + off), k, bits, kb, s0, s1, C.byref(qa), _p(y), ldy, rp, int(accumulate))
     return y
 
 

@@ -80,3 +80,27 @@ def test_noalloc_rejects_a_workspace_above_the_scratch():
     assert rc == -3 and b"scratch" in L.trk_last_error()
     bad = trmoe.Cfg(2000, 512, 512, 10, 0, 0, 16, 1)
     assert L.trk_moe_forward_noalloc(C.byref(bad), None, None, C.c_void_p(256), None, 1, C.c_void_p(256), None) == -1
+
+
+def test_gemv_rejects_bad_codecs_and_ranges():
+    """gemv_tq_rows' contract (gemv.rs:16-40): kb equal to the codec's, k a multiple of kb, strips
+    inside the matrix; GGUF formats with the kb their TQ conversion has."""
+    L = trmoe.lib()
+
+    def call(fmt, rows, k, kb, s0=0, s1=1, m=1, pair=0, q=64, ldy=4096):
+        mat = trmoe.Mat(C.c_void_p(256), rows, k, fmt, 1, 0)
+        return L.trk_gemv(C.byref(mat), 0, s0, s1, kb, C.c_void_p(q), C.c_void_p(64), C.c_void_p(64), m, pair,
+                          C.c_void_p(64), ldy, None, 0, None)
+
+    assert call(trmoe.FMT_TQ4_32, 64, 2560, 16) == -1 and b"codec" in L.trk_last_error()
+    assert call(trmoe.FMT_TQ5_16, 64, 648, 16) == -1 and b"multiple of kb" in L.trk_last_error()
+    assert call(trmoe.FMT_TQ8_16, 40, 640, 16, s0=0, s1=4) == -1 and b"strips" in L.trk_last_error()
+    assert call(trmoe.FMT_TQ8_16, 40, 640, 16, s0=2, s1=1) == -1
+    assert call(trmoe.FMT_Q6_K, 64, 512, 32) == -1 and b"unsupported" in L.trk_last_error()
+    assert call(trmoe.FMT_Q8_0, 64, 640, 32) == -1 and b"256" in L.trk_last_error()
+    assert call(trmoe.FMT_Q5_1, 64, 512, 16, q=72) == -1 and b"aligned" in L.trk_last_error()
+    assert call(trmoe.FMT_TQ4_16, 64, 640, 16, m=3, pair=1) == -1 and b"twos" in L.trk_last_error()
+    assert call(trmoe.FMT_TQ4_16, 64, 640, 16, s1=4, m=2, ldy=63) == -1 and b"ldy" in L.trk_last_error()
+    # within the contract and with nothing to do: no device work, status OK
+    assert call(trmoe.FMT_TQ5_16, 2560, 640, 16, s0=7, s1=7) == 0
+    assert call(trmoe.FMT_Q4_K, 64, 2048, 32, m=0) == 0

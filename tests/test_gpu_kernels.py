@@ -153,35 +153,94 @@ def test_route_matches_oracle(policy, E):
     assert worst <= 1  # libm expf vs correctly rounded exp
 
 
-GEMV_CASES = [(O.FMT_Q4_K, 32, 64, 2048, False, 3), (O.FMT_Q4_K, 32, 48, 512, True, 2),
-              (O.FMT_Q4_K, 16, 96, 512, True, 2), (O.FMT_Q4_K, 16, 32, 256, False, 5),
-              (O.FMT_Q6_K, 16, 64, 512, False, 3), (O.FMT_Q6_K, 16, 32, 256, True, 2)]
+def act_rows(x, kb, pair):
+    """int8 activation rows as the reference quantises them: one row each, or (coarse, residual)
+    pairs (quant.rs:36-53)."""
+    if not pair:
+        return O.quant_rows(x, kb)
+    qs = [O.quant_pair(x[i], kb) for i in range(x.shape[0])]
+    return tuple(np.concatenate([a[c] for a in qs]) for c in range(3))
 
 
-@pytest.mark.parametrize("fmt,kb,rows,K,pair,m", GEMV_CASES)
-def test_gemv_mirror_bit_exact(fmt, kb, rows, K, pair, m):
-    say(f"gemv fmt={fmt} kb={kb} rows={rows} K={K} pair={pair} m={m}")
+def gemv_check(w_dev, w_tq, rows, K, fmt, bits, kb, x, pair, strips):
+    """trk_gemv against the oracle's gemm_tq_rows on the same TQ bytes: identity rows, then a row
+    map with repeats (accumulate and overwrite) into a wider y (ldy > rows)."""
+    q, s, su = act_rows(x, kb, pair)
+    m = x.shape[0]
+    nstrips = (rows + 15) // 16
+    s0, s1 = strips if strips else (0, nstrips)
+    width = 16 * nstrips  # the oracle stores whole strips
+    cut = width if fmt in trmoe.TQ_FMTS else rows  # GGUF rows past `rows` are never written
+    want = O.gemv_tq(w_tq, K, bits, kb, width, q, s, su, pair=pair, s0=s0, s1=s1)
+    y = trmoe.gemv(w_dev, rows, K, fmt, 0, 1, kb, to_dev(q), to_dev(s), to_dev(su), pair=pair, s0=s0, s1=s1,
+                   y=to_dev(np.zeros((m, width), np.float32)), ldy=width)
+    got = host(y)
+    assert np.array_equal(got[:, :cut].view(np.uint32), want[:, :cut].view(np.uint32))
+    assert not got[:, cut:].any()
+    # a row map with repeats: logical rows in order onto 3 y rows of pitch width + 5
+    rmap = np.array([(2 * i + 1) % 3 for i in range(m)], np.uint32)
+    ldy = width + 5
+    for acc in (True, False):
+        base = np.arange(3 * ldy, dtype=np.float32).reshape(3, ldy) * 0.25
+        want2 = O.gemv_tq(w_tq, K, bits, kb, width, q, s, su, pair=pair, y=base.copy(), rows=rmap,
+                          accumulate=acc, s0=s0, s1=s1, ldy=ldy)
+        y2 = trmoe.gemv(w_dev, rows, K, fmt, 0, 1, kb, to_dev(q), to_dev(s), to_dev(su), pair=pair,
+                        y=to_dev(base.copy()), ldy=ldy, rowmap=to_dev(rmap.view(np.int32)), accumulate=acc,
+                        s0=s0, s1=s1)
+        got2 = host(y2)
+        c0, c1 = 16 * s0, min(16 * s1, cut)
+        assert np.array_equal(got2[:, c0:c1].view(np.uint32), want2[:, c0:c1].view(np.uint32)), acc
+        keep = np.ones(ldy, bool)
+        keep[c0:c1] = False
+        assert np.array_equal(got2[:, keep], base[:, keep]), acc
+
+
+# GGUF matrices read as their TQ conversion: every format and kb, sub-ranges of strips, rows not
+# a multiple of 16, one to nine activation rows (passes of four), pairs
+GEMV_GGUF_CASES = [(O.FMT_Q4_K, 32, 64, 2048, False, 3, None), (O.FMT_Q4_K, 32, 48, 512, True, 4, (1, 3)),
+                   (O.FMT_Q4_K, 16, 96, 512, True, 6, (1, 5)), (O.FMT_Q4_K, 16, 40, 256, False, 5, None),
+                   (O.FMT_Q6_K, 16, 64, 512, False, 3, (2, 4)), (O.FMT_Q6_K, 16, 40, 2048, True, 2, None),
+                   (O.FMT_Q8_0, 32, 64, 512, False, 9, None), (O.FMT_Q8_0, 16, 48, 768, True, 4, (1, 3)),
+                   (O.FMT_Q5_1, 32, 64, 1024, False, 1, None), (O.FMT_Q5_1, 16, 80, 512, False, 7, (2, 5))]
+
+
+@pytest.mark.parametrize("fmt,kb,rows,K,pair,m,strips", GEMV_GGUF_CASES)
+def test_gemv_gguf_bit_exact(fmt, kb, rows, K, pair, m, strips):
+    say(f"gemv gguf fmt={fmt} kb={kb} rows={rows} K={K} pair={pair} m={m} strips={strips}")
     raw = O.gen_gguf(fmt, 3, 40 + fmt + kb, rows, K)
     tq, bits = O.gguf_to_tq(fmt, raw, rows, K, kb)
-    x = O.gen_normal(3, 41, m * K, 1.0).reshape(m, K)
-    if pair:
-        qs = [O.quant_pair(x[i], kb) for i in range(m)]
-        q = np.concatenate([a[0] for a in qs])
-        s = np.concatenate([a[1] for a in qs])
-        su = np.concatenate([a[2] for a in qs])
-    else:
-        q, s, su = O.quant_rows(x, kb)
-    want = O.gemv_tq(tq, K, bits, kb, rows, q, s, su, pair=pair)
-    y = trmoe.gemv(to_dev(raw), rows, K, fmt, 0, 1, kb, to_dev(q), to_dev(s), to_dev(su), pair=pair)
-    assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
-    # row map + accumulate (gemm_tq_rows with rows, accumulate = true)
-    logical = m
-    rmap = np.array([(3 * i + 1) % (logical + 2) for i in range(logical)], np.uint32)
-    base = np.ones((logical + 2, rows), np.float32)
-    want2 = O.gemv_tq(tq, K, bits, kb, rows, q, s, su, pair=pair, y=base.copy(), rows=rmap, accumulate=True)
-    y2 = trmoe.gemv(to_dev(raw), rows, K, fmt, 0, 1, kb, to_dev(q), to_dev(s), to_dev(su), pair=pair,
-                    y=to_dev(base.copy()), rowmap=to_dev(rmap.view(np.int32)), accumulate=True)
-    assert np.array_equal(host(y2).view(np.uint32), want2.view(np.uint32))
+    x = O.gen_normal(3, 41 + m, m * K, 1.0).reshape(m, K)
+    gemv_check(to_dev(raw), tq, rows, K, fmt, bits, kb, x, pair, strips)
+
+
+def random_tq(seed, rows, K, bits, kb):
+    """A packed TQ matrix (codec.rs:1-46) of uniform q and f16 scales / mins of real magnitudes."""
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 1 << bits, (rows, K), dtype=np.uint8)
+    nb = K // kb
+    d = (rng.uniform(1e-4, 3e-3, (rows, nb)) * rng.choice([-1, 1], (rows, nb))).astype(np.float16)
+    m = (-d.astype(np.float32) * rng.uniform(0, 1 << (bits - 1), (rows, nb))).astype(np.float16)
+    return O.pack_tq(q, d, m, bits, kb)
+
+
+# The reference's own packed codecs: its real expert shapes (gate TQ4_32 [640][2560], down
+# TQ5_16 [2560][640], python/tests/test_blocks_real.py:23-26), k not a multiple of 256, ragged
+# slices (33 blocks), padded strips, sub-ranges, pairs and row maps
+GEMV_TQ_CASES = [(4, 32, 640, 2560, False, 1, None), (5, 16, 2560, 640, False, 1, None),
+                 (5, 16, 2560, 640, True, 2, (40, 100)), (4, 16, 40, 80, False, 5, None),
+                 (8, 16, 64, 96, False, 9, (1, 3)), (8, 32, 48, 2048, True, 6, None),
+                 (5, 32, 100, 320, False, 3, None), (4, 32, 64, 1056, False, 4, (0, 2)),
+                 (8, 16, 2560, 640, False, 2, (3, 160))]
+
+
+@pytest.mark.parametrize("bits,kb,rows,K,pair,m,strips", GEMV_TQ_CASES)
+def test_gemv_tq_bit_exact(bits, kb, rows, K, pair, m, strips):
+    say(f"gemv tq bits={bits} kb={kb} rows={rows} K={K} pair={pair} m={m} strips={strips}")
+    fmt = (bits << 8) | kb
+    tq = random_tq(7 + bits + kb + m, rows, K, bits, kb)
+    assert tq.size == trmoe.matrix_bytes(fmt, rows, K)
+    x = O.gen_normal(4, 50 + m, m * K, 1.0).reshape(m, K)
+    gemv_check(to_dev(tq), tq, rows, K, fmt, bits, kb, x, pair, strips)
 
 
 def test_swiglu_and_rmsnorm_bit_exact():

@@ -639,20 +639,41 @@ extern "C" int trk_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb,
     return TRK_OK;
 }
 
-extern "C" int trk_gemv(const trk_mat* w, uint32_t item, uint32_t kb, const int8_t* q, const float* scale,
-                        const int32_t* sum, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
-                        int accumulate, void* stream) {
+extern "C" int trk_gemv(const trk_mat* w, uint32_t item, uint32_t s0, uint32_t s1, uint32_t kb, const int8_t* q,
+                        const float* scale, const int32_t* sum, uint32_t m, int pair, float* y, uint32_t ldy,
+                        const uint32_t* rows, int accumulate, void* stream) {
     if (!w || !q || !scale || !sum || !y) return fail(TRK_E_INVALID, "null argument");
-    if (!w->ptr || w->k == 0 || w->k % 256 || w->rows == 0) return fail(TRK_E_INVALID, "bad matrix");
-    if (!((w->fmt == TRK_FMT_Q4_K && (kb == 32 || kb == 16)) || (w->fmt == TRK_FMT_Q6_K && kb == 16)))
-        return fail(TRK_E_INVALID, "unsupported (fmt %u, kb %u)", w->fmt, kb);
+    if (!w->ptr || w->k == 0 || w->rows == 0) return fail(TRK_E_INVALID, "bad matrix");
+    const bool tq = fmt_is_tq(w->fmt);
+    uint64_t pitch, mbytes;  // row (GGUF) or strip (TQ) bytes, matrix bytes
+    if (tq) {
+        // gemv_tq_rows asserts xq.kb == c.kb (gemv.rs:27); blocks never straddle k
+        if (kb != tq_kb(w->fmt)) return fail(TRK_E_INVALID, "kb %u differs from the codec's %u", kb, tq_kb(w->fmt));
+        if (w->k % kb) return fail(TRK_E_INVALID, "k %u is not a multiple of kb %u", w->k, kb);
+        if ((uintptr_t)w->ptr % 4 || (w->count > 1 && w->stride % 4)) return fail(TRK_E_INVALID, "TQ matrix must be 4-byte aligned");
+        pitch = (uint64_t)(w->k / kb) * tq_block_bytes(w->fmt);
+        mbytes = pitch * ((w->rows + 15) / 16);
+    } else {
+        const bool ok = ((w->fmt == TRK_FMT_Q4_K || w->fmt == TRK_FMT_Q8_0 || w->fmt == TRK_FMT_Q5_1) && (kb == 32 || kb == 16)) ||
+                        (w->fmt == TRK_FMT_Q6_K && kb == 16);
+        if (!ok) return fail(TRK_E_INVALID, "unsupported (fmt %u, kb %u)", w->fmt, kb);
+        if (w->k % 256) return fail(TRK_E_INVALID, "k %u is not a multiple of 256", w->k);
+        const uint32_t al = w->fmt == TRK_FMT_Q6_K ? 2 : 16;
+        if ((uintptr_t)w->ptr % al || (w->count > 1 && w->stride % al)) return fail(TRK_E_INVALID, "matrix misaligned");
+        pitch = row_bytes(w->fmt, w->k);
+        mbytes = pitch * w->rows;
+    }
     if (item >= (w->count ? w->count : 1)) return fail(TRK_E_INVALID, "item %u out of range", item);
+    if (w->count > 1 && w->stride < mbytes) return fail(TRK_E_INVALID, "stride below the matrix size");
+    const uint32_t strips = (w->rows + 15) / 16;
+    if (s0 > s1 || s1 > strips) return fail(TRK_E_INVALID, "strips [%u, %u) outside [0, %u)", s0, s1, strips);
     if (pair && m % 2) return fail(TRK_E_INVALID, "pair rows come in twos");
-    if (ldy < w->rows && !(m == (pair ? 2u : 1u) && !rows)) return fail(TRK_E_INVALID, "ldy below rows");
-    uint32_t rb = row_bytes(w->fmt, w->k);
-    Mat M{(const uint8_t*)w->ptr, w->count > 1 ? w->stride : (uint64_t)rb * w->rows, w->rows, w->k, w->fmt, rb};
-    if (m == 0) return TRK_OK;
-    HIP_TRY(launch_gemv(M, item, kb, q, scale, sum, m, pair, y, ldy, rows, accumulate, (hipStream_t)stream));
+    if ((uintptr_t)q % 16) return fail(TRK_E_INVALID, "q must be 16-byte aligned");
+    const uint32_t r_hi = tq ? 16 * s1 : (16 * s1 < w->rows ? 16 * s1 : w->rows);
+    if (ldy < r_hi && !(m == (pair ? 2u : 1u) && !rows)) return fail(TRK_E_INVALID, "ldy %u below row %u", ldy, r_hi);
+    if (m == 0 || s0 == s1) return TRK_OK;
+    Mat M{(const uint8_t*)w->ptr, w->count > 1 ? w->stride : mbytes, w->rows, w->k, w->fmt, (uint32_t)pitch};
+    HIP_TRY(launch_gemv(M, item, s0, s1, kb, q, scale, sum, m, pair, y, ldy, rows, accumulate, (hipStream_t)stream));
     return TRK_OK;
 }
 

@@ -86,94 +86,6 @@ hipError_t launch_quantize(const float* x, uint32_t m, uint32_t k, uint32_t kb, 
 }
 
 // ============================================================================================
-// kernel-level GEMV mirror (gemv.rs:25-78) on GGUF rows: one thread per (output row, logical
-// activation row), blocks in ascending order with the per-block epilogue of gemv.rs:141-148.
-// Reference semantics, not a fast path.
-// ============================================================================================
-
-__device__ __forceinline__ void block_dm(const uint8_t* wrow, uint32_t fmt, int kb, int b, float& dd, float& mm) {
-    if (fmt == TRK_FMT_Q4_K) {
-        int j32 = kb == 32 ? b : b / 2;
-        const uint8_t* hdr = wrow + (size_t)(j32 / 8) * 144;
-        int sc, mn;
-        q4k_scale_min(hdr + 4, j32 % 8, sc, mn);
-        q4k_dm(h2f(ld16(hdr)), h2f(ld16(hdr + 2)), sc, mn, dd, mm);
-    } else {  // Q6_K, kb = 16
-        const uint8_t* sbp = wrow + (size_t)(b / 16) * 210;
-        float d = h2f(ld16(sbp + 208));
-        int8_t sc = (int8_t)sbp[192 + b % 16];
-        dd = f16_round(d * (float)sc);
-        mm = f16_round(-32.0f * dd);
-    }
-}
-
-__device__ __forceinline__ int block_q(const uint8_t* wrow, uint32_t fmt, int kb, int b, int i) {
-    if (fmt == TRK_FMT_Q4_K) {
-        int e = b * kb + i;  // element index in the row
-        int sb = e / 256, j = (e % 256) / 32, ii = e % 32;
-        const uint8_t* qs = wrow + (size_t)sb * 144 + 16;
-        uint8_t byte = qs[(j / 2) * 32 + ii];
-        return (j & 1) ? (byte >> 4) : (byte & 15);
-    }
-    int e = b * kb + i;
-    int sb = e / 256, r = e % 256;
-    int n = r / 128, g = (r % 128) / 32, l = r % 32;
-    const uint8_t* p = wrow + (size_t)sb * 210;
-    uint8_t lo = p[64 * n + l + ((g & 1) ? 32 : 0)];
-    int nib = (g >> 1) ? (lo >> 4) : (lo & 15);
-    int hi = (p[128 + 32 * n + l] >> (2 * g)) & 3;
-    return nib | (hi << 4);
-}
-
-__global__ void gemv_mirror_kernel(Mat w, uint32_t item, uint32_t kb, const int8_t* __restrict__ q,
-                                   const float* __restrict__ s, const int32_t* __restrict__ su, uint32_t m,
-                                   int pair, float* __restrict__ y, uint32_t ldy, const uint32_t* __restrict__ rows,
-                                   int accumulate) {
-    uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-    uint32_t logical = blockIdx.y;
-    if (r >= w.rows) return;
-    const uint8_t* wrow = w.ptr + (size_t)item * w.stride + (size_t)r * w.row_bytes;
-    uint32_t K = w.k, nb = K / kb, per = pair ? 2 : 1;
-    float acc[2] = {0.0f, 0.0f};
-    for (uint32_t b = 0; b < nb; b++) {
-        float dd, mm;
-        block_dm(wrow, w.fmt, kb, b, dd, mm);
-        for (uint32_t p = 0; p < per; p++) {
-            uint32_t mi = logical * per + p;
-            const int8_t* xp = q + (size_t)mi * K + (size_t)b * kb;
-            int dot = 0;
-            for (uint32_t i = 0; i < kb; i++) dot += block_q(wrow, w.fmt, kb, b, i) * (int)xp[i];
-            float sx = s[(size_t)mi * nb + b];
-            float u = sx * (float)su[(size_t)mi * nb + b];
-            float t = dd * sx;
-            acc[p] = __builtin_fmaf(mm, u, acc[p]);
-            acc[p] = __builtin_fmaf((float)dot, t, acc[p]);
-        }
-    }
-    float v = pair ? acc[0] + acc[1] : acc[0];
-    size_t yr = rows ? rows[logical] : logical;
-    float* yp = y + yr * ldy + r;
-    *yp = accumulate ? *yp + v : v;
-}
-
-hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t kb, const int8_t* q, const float* s,
-                       const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
-                       int accumulate, hipStream_t st) {
-    uint32_t logical = pair ? m / 2 : m;
-    // rows of one call go in sequence so that a row map with repeats accumulates in order
-    for (uint32_t i = 0; i < logical; i++) {
-        dim3 g((w.rows + 127) / 128, 1);
-        const int8_t* qi = q + (size_t)i * (pair ? 2 : 1) * w.k;
-        const float* si = s + (size_t)i * (pair ? 2 : 1) * (w.k / kb);
-        const int32_t* sui = su + (size_t)i * (pair ? 2 : 1) * (w.k / kb);
-        const uint32_t* ri = rows ? rows + i : nullptr;
-        float* yi = rows ? y : y + (size_t)i * ldy;
-        gemv_mirror_kernel<<<g, 128, 0, st>>>(w, item, kb, qi, si, sui, pair ? 2 : 1, pair, yi, ldy, ri, accumulate);
-    }
-    return hipGetLastError();
-}
-
-// ============================================================================================
 // elementwise (elem.rs)
 // ============================================================================================
 

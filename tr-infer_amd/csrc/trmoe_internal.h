@@ -19,6 +19,19 @@ struct Policy {
     float mass;
 };
 
+// TQ codecs (codec.rs:1-46): fmt = bits << 8 | kb
+__host__ __device__ inline bool fmt_is_tq(uint32_t fmt) {
+    return fmt == TRK_FMT_TQ4_16 || fmt == TRK_FMT_TQ4_32 || fmt == TRK_FMT_TQ5_16 || fmt == TRK_FMT_TQ5_32 ||
+           fmt == TRK_FMT_TQ8_16 || fmt == TRK_FMT_TQ8_32;
+}
+__host__ __device__ inline uint32_t tq_bits(uint32_t fmt) { return fmt >> 8; }
+__host__ __device__ inline uint32_t tq_kb(uint32_t fmt) { return fmt & 0xff; }
+// Codec::block_bytes: a 64-byte header (d[16], m[16] f16), 16 x kb q values, 5-bit: 2 kb plane bytes
+__host__ __device__ inline uint32_t tq_block_bytes(uint32_t fmt) {
+    const uint32_t b = tq_bits(fmt), kb = tq_kb(fmt);
+    return 64 + (b == 8 ? 16 * kb : 8 * kb) + (b == 5 ? 2 * kb : 0);
+}
+
 // A weight stack as the kernels take it.
 struct Mat {
     const uint8_t* ptr;
@@ -127,9 +140,10 @@ hipError_t launch_stream_gateup(const Mat& gate, const Mat& up, const Mat& sh_ga
 hipError_t launch_stream_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m,
                               uint32_t max_rows, hipStream_t st);
 hipError_t launch_batch_combine(const Workspace& ws, uint32_t m, float* out, int residual, hipStream_t st);
-hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t kb, const int8_t* q, const float* s,
-                       const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy, const uint32_t* rows,
-                       int accumulate, hipStream_t st);
+// Mat for a TQ matrix: row_bytes holds the bytes of one 16-row strip
+hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t s0, uint32_t s1, uint32_t kb, const int8_t* q,
+                       const float* s, const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy,
+                       const uint32_t* rows, int accumulate, hipStream_t st);
 hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
                           hipStream_t st);

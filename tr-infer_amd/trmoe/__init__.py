@@ -16,6 +16,9 @@ LIB_PATH = os.path.join(PKG_ROOT, "libtrmoe.so")
 HEADER = os.path.join(os.path.dirname(PKG_ROOT), "include", "trmoe.h")
 
 FMT_Q4_K, FMT_Q6_K, FMT_Q8_0, FMT_Q5_1 = 12, 14, 8, 7
+# the reference's TQ codecs (codec.rs:1-46): bits << 8 | kb
+FMT_TQ4_16, FMT_TQ4_32, FMT_TQ5_16, FMT_TQ5_32, FMT_TQ8_16, FMT_TQ8_32 = 0x410, 0x420, 0x510, 0x520, 0x810, 0x820
+TQ_FMTS = (FMT_TQ4_16, FMT_TQ4_32, FMT_TQ5_16, FMT_TQ5_32, FMT_TQ8_16, FMT_TQ8_32)
 BASIS_ALL, BASIS_TOP = 0, 1
 K_MAX = 32
 (WS_RLOG, WS_IDS, WS_W, WS_NSEL, WS_ENT_TOK, WS_ENT_W, WS_ENT_EXP, WS_GRP_START, WS_GRP_EXP, WS_NGROUPS, WS_XQ,
@@ -75,7 +78,7 @@ def lib() -> C.CDLL:
         L.trk_router_logits.argtypes = [vp, vp, vp, vp, u32, u32, u32, i, vp, vp, vp]
         L.trk_route.argtypes = [vp, u32, u32, u32, C.POINTER(Policy), vp, vp, vp, vp]
         L.trk_quantize.argtypes = [vp, u32, u32, u32, i, vp, vp, vp, vp]
-        L.trk_gemv.argtypes = [C.POINTER(Mat), u32, u32, vp, vp, vp, u32, i, vp, u32, vp, i, vp]
+        L.trk_gemv.argtypes = [C.POINTER(Mat), u32, u32, u32, u32, vp, vp, vp, u32, i, vp, u32, vp, i, vp]
         L.trk_swiglu.argtypes = [vp, vp, vp, sz, vp]
         L.trk_rmsnorm.argtypes = [vp, vp, f, u32, u32, vp, vp]
         L.trk_add_inplace.argtypes = [vp, vp, sz, vp]
@@ -106,6 +109,19 @@ def header_functions() -> list[str]:
 
 def row_bytes(fmt: int, k: int) -> int:
     return k // 256 * {FMT_Q4_K: 144, FMT_Q6_K: 210, FMT_Q8_0: 272, FMT_Q5_1: 192}[fmt]
+
+
+def tq_block_bytes(fmt: int) -> int:
+    """Codec::block_bytes (codec.rs:22-29)."""
+    bits, kb = fmt >> 8, fmt & 0xFF
+    return 64 + (16 * kb if bits == 8 else 8 * kb) + (2 * kb if bits == 5 else 0)
+
+
+def matrix_bytes(fmt: int, rows: int, k: int) -> int:
+    """Bytes of one [rows][k] matrix: TQ strips (rows padded to 16) or GGUF rows."""
+    if fmt in TQ_FMTS:
+        return (rows + 15) // 16 * (k // (fmt & 0xFF)) * tq_block_bytes(fmt)
+    return rows * row_bytes(fmt, k)
 
 
 def _ptr(t):
@@ -337,15 +353,20 @@ def route(logits, k, policy=None, stream=None):
 
 
 def gemv(wt, rows, k, fmt, item, count, kb, q, s, su, pair=False, y=None, ldy=None, rowmap=None, accumulate=False,
-         stream=None):
+         s0=0, s1=None, stream=None):
+    """trk_gemv over strips [s0, s1) (all strips by default) of matrix `item` of a stack of
+    `count` [rows][k] matrices in `fmt` (GGUF or TQ) held in `wt`."""
     import torch
     m = q.shape[0]
     logical = m // 2 if pair else m
+    strips = (rows + 15) // 16
+    s1 = strips if s1 is None else s1
+    width = 16 * strips if fmt in TQ_FMTS else rows
     if y is None:
-        y = torch.zeros((logical, rows), dtype=torch.float32, device=q.device)
-    mat = Mat(wt.data_ptr(), rows, k, fmt, count, rows * row_bytes(fmt, k))
-    check(lib().trk_gemv(C.byref(mat), item, kb, _ptr(q), _ptr(s), _ptr(su), m, int(pair), _ptr(y),
-                         ldy if ldy is not None else rows, _ptr(rowmap), int(accumulate), _stream(stream)))
+        y = torch.zeros((logical, width), dtype=torch.float32, device=q.device)
+    mat = Mat(wt.data_ptr(), rows, k, fmt, count, matrix_bytes(fmt, rows, k))
+    check(lib().trk_gemv(C.byref(mat), item, s0, s1, kb, _ptr(q), _ptr(s), _ptr(su), m, int(pair), _ptr(y),
+                         ldy if ldy is not None else width, _ptr(rowmap), int(accumulate), _stream(stream)))
     return y
 
 
