@@ -495,6 +495,34 @@ def cpu_have_vnni() -> bool:
     return bool(cpu_lib().cpu_have_vnni())
 
 
+class TQOracleLayer(OracleLayer):
+    """A layer whose experts are already the reference's packed TQ strips (what trpack writes):
+    gate / up [E] arrays of a kb-32 codec, down [E] of a kb-16 codec, used as they are."""
+
+    def __init__(self, H, E, F, router, shexp_gate, gate_tq, up_tq, down_tq, sh_gate, sh_up, sh_down, gate_bits,
+                 down_bits, router_bias=None):
+        self.H, self.E, self.F = H, E, F
+        self.router = np.ascontiguousarray(router, np.float32)
+        self.router_bias = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
+        self.shexp_gate = np.ascontiguousarray(shexp_gate, np.float32)
+        self.gate_fmt = self.down_fmt = None
+        self.gate_bits, self.down_bits, self.sh_down_bits = gate_bits, down_bits, down_bits
+        self.sh_gate, self.sh_up, self.sh_down = (np.ascontiguousarray(a, np.uint8) for a in (sh_gate, sh_up, sh_down))
+        self._gate_ptrs = (C.c_void_p * E)()
+        self._up_ptrs = (C.c_void_p * E)()
+        self._down_ptrs = (C.c_void_p * E)()
+        self._tq = {}
+        for e in range(E):
+            g, u, d = (np.ascontiguousarray(a[e], np.uint8) for a in (gate_tq, up_tq, down_tq))
+            self._tq[e] = (g, u, d)
+            self._gate_ptrs[e] = g.ctypes.data
+            self._up_ptrs[e] = u.ctypes.data
+            self._down_ptrs[e] = d.ctypes.data
+
+    def ensure(self, experts):
+        pass
+
+
 class CpuMoe:
     """A pool of `threads` pinned threads (0: one per allowed CPU, at most 16 = one tile) running
     the VNNI restatement of moe_block / moe_batch on an OracleLayer's TQ weights."""

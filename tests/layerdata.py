@@ -83,3 +83,40 @@ class Layer:
         """[E][bytes] contiguous expert stack (what the GPU library takes)."""
         idx = {"gate": 0, "up": 1, "down": 2}[which]
         return np.stack([self.expert(e)[idx] for e in range(self.E)])
+
+
+def random_tq(rng, rows, K, bits, kb):
+    """One packed TQ matrix (codec.rs:1-46): uniform q, f16 d > 0 and m = -d * U(0, 2^(bits-1)),
+    the sign pattern of weights converted from GGUF (d * sc >= 0, -(dmin * mn) <= 0)."""
+    q = rng.integers(0, 1 << bits, (rows, K), dtype=np.uint8)
+    nb = K // kb
+    d = rng.uniform(5e-4, 3e-3, (rows, nb)).astype(np.float16)
+    m = (-d.astype(np.float32) * rng.uniform(0, 1 << (bits - 1), (rows, nb))).astype(np.float16)
+    return O.pack_tq(q, d, m, bits, kb)
+
+
+class TQLayer:
+    """A layer whose experts are the reference's packed TQ strips: gate / up [E][F][H] in a kb-32
+    codec, down [E][H][F] in a kb-16 codec (the real packs: TQ4_32 / TQ5_16), shared expert alike."""
+
+    def __init__(self, seed=1, H=2560, E=32, F=640, gate_bits=4, down_bits=5, bias=None):
+        rng = np.random.default_rng(seed)
+        self.H, self.E, self.F, self.seed = H, E, F, seed
+        self.gate_bits, self.down_bits = gate_bits, down_bits
+        self.gate_fmt, self.down_fmt = (gate_bits << 8) | 32, (down_bits << 8) | 16
+        self.router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        self.shexp_gate = (rng.standard_normal(H) * 0.02).astype(np.float32)
+        self.bias = bias
+        self.gate = np.stack([random_tq(rng, F, H, gate_bits, 32) for _ in range(E)])
+        self.up = np.stack([random_tq(rng, F, H, gate_bits, 32) for _ in range(E)])
+        self.down = np.stack([random_tq(rng, H, F, down_bits, 16) for _ in range(E)])
+        self.sh_gate = random_tq(rng, F, H, gate_bits, 32)
+        self.sh_up = random_tq(rng, F, H, gate_bits, 32)
+        self.sh_down = random_tq(rng, H, F, down_bits, 16)
+
+    def oracle(self):
+        return O.TQOracleLayer(self.H, self.E, self.F, self.router, self.shexp_gate, self.gate, self.up, self.down,
+                               self.sh_gate, self.sh_up, self.sh_down, self.gate_bits, self.down_bits, self.bias)
+
+    def x(self, M, tid=0, sigma=1.0):
+        return O.gen_normal(self.seed, stream(0, 900 + tid), M * self.H, sigma).reshape(M, self.H)

@@ -44,11 +44,13 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 
 // Kernel ids for trk_get_timing.
 enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DEC_LAYER, K_DISPATCH, K_B_GATEUP, K_B_DOWN,
-                K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_PROFILE, K_COUNT };
+                K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_PROFILE, K_TQ_GATEUP, K_TQ_ACT, K_TQ_DOWN,
+                K_TQ_COMBINE, K_COUNT };
 static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
                                                   "decode_down", "decode_layer", "dispatch", "batch_gateup",
                                                   "batch_down", "stream_gateup", "stream_down", "batch_combine",
-                                                  "rmsnorm", "mass_profile"};
+                                                  "rmsnorm", "mass_profile", "tq_gateup", "tq_act", "tq_down",
+                                                  "tq_combine"};
 
 // Which grouped items run on the streaming GEMV (the rest on the MFMA tiles), when the caller has
 // not chosen: all of them up to 16 tokens; the items of at most 4 rows while the selections
@@ -101,8 +103,9 @@ static int check_policy(const trk_ctx* c, const trk_moe_policy* p) {
 // comes back resolved (0 = n_expert_used).
 static int check_cfg(const trk_cfg* cfg, uint32_t m_max, uint32_t& k_cap) {
     const uint32_t H = cfg->hidden, E = cfg->n_expert, F = cfg->n_ff, k = cfg->n_expert_used;
-    if (H == 0 || H % 256 || F == 0 || F % 256)
-        return fail(TRK_E_INVALID, "hidden (%u) and n_ff (%u) must be positive multiples of 256", H, F);
+    // n_ff: a multiple of 256 for GGUF experts (checked per call), of 16 for TQ experts
+    if (H == 0 || H % 256 || F == 0 || F % 16)
+        return fail(TRK_E_INVALID, "hidden (%u) must be a positive multiple of 256 and n_ff (%u) of 16", H, F);
     if (E == 0 || E > 1024) return fail(TRK_E_INVALID, "n_expert (%u) must be in 1..1024", E);
     if (k < 1 || k > TRK_MOE_K_MAX || k > E) return fail(TRK_E_INVALID, "n_expert_used (%u) must be in 1..min(32, E)", k);
     if (m_max == 0) return fail(TRK_E_INVALID, "m_max must be positive");
@@ -158,6 +161,7 @@ static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max
         {(void**)&ws.actsum, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.actu, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.yent, yrows * H * 4},
+        {(void**)&ws.hgu, yrows * 2 * F * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
         {(void**)&ws.prof, (K_MAX + 1) * 8},
@@ -236,19 +240,34 @@ static int make_mat(const trk_mat& m, uint32_t rows, uint32_t k, bool down_ok_q6
     if (!m.ptr) return fail(TRK_E_INVALID, "%s: null weight pointer", name);
     if (m.rows != rows || m.k != k)
         return fail(TRK_E_INVALID, "%s: shape [%u][%u], expected [%u][%u]", name, m.rows, m.k, rows, k);
-    if (!(m.fmt == TRK_FMT_Q4_K || (down_ok_q6 && (m.fmt == TRK_FMT_Q6_K || m.fmt == TRK_FMT_Q8_0 || m.fmt == TRK_FMT_Q5_1))))
-        return fail(TRK_E_INVALID, "%s: unsupported format %u", name, m.fmt);
     if (m.count < min_count) return fail(TRK_E_INVALID, "%s: %u matrices, need %u", name, m.count, min_count);
-    uint32_t rb = row_bytes(m.fmt, k);
-    uint64_t mb = (uint64_t)rb * rows;
+    uint64_t pitch, mb, align;
+    if (fmt_is_tq(m.fmt)) {
+        // the reference's packed strips: gate/up blocks of 32 values (x is quantised per 32), down
+        // blocks of 16 (the SwiGLU output is quantised per 16), exec.rs:1563-1606
+        const uint32_t kb = tq_kb(m.fmt);
+        if (kb != (down_ok_q6 ? 16u : 32u))
+            return fail(TRK_E_INVALID, "%s: TQ codec with kb %u, this projection needs kb %u", name, kb, down_ok_q6 ? 16u : 32u);
+        if (k % kb) return fail(TRK_E_INVALID, "%s: k %u is not a multiple of kb %u", name, k, kb);
+        pitch = (uint64_t)(k / kb) * tq_block_bytes(m.fmt);  // one 16-row strip
+        mb = pitch * ((rows + 15) / 16);
+        align = 16;  // blocks are read with 16-byte loads
+    } else {
+        if (!(m.fmt == TRK_FMT_Q4_K || (down_ok_q6 && (m.fmt == TRK_FMT_Q6_K || m.fmt == TRK_FMT_Q8_0 || m.fmt == TRK_FMT_Q5_1))))
+            return fail(TRK_E_INVALID, "%s: unsupported format %u", name, m.fmt);
+        if (k % 256 || rows % 256)
+            return fail(TRK_E_INVALID, "%s: GGUF experts need rows and k multiples of 256 ([%u][%u])", name, rows, k);
+        pitch = row_bytes(m.fmt, k);
+        mb = pitch * rows;
+        // Q4_K superblocks and Q8_0 / Q5_1 units of 8 blocks (272 / 192 bytes) are read with 16- and
+        // 8-byte loads
+        align = m.fmt == TRK_FMT_Q6_K ? 2 : 16;
+    }
     if (m.count > 1 && m.stride < mb) return fail(TRK_E_INVALID, "%s: stride %llu below matrix bytes %llu", name,
                                                   (unsigned long long)m.stride, (unsigned long long)mb);
-    // Q4_K superblocks and Q8_0 / Q5_1 units of 8 blocks (272 / 192 bytes) are read with 16- and
-    // 8-byte loads
-    uint64_t align = m.fmt == TRK_FMT_Q6_K ? 2 : 16;
     if ((uintptr_t)m.ptr % align || (m.count > 1 && m.stride % align))
         return fail(TRK_E_INVALID, "%s: pointer/stride must be %llu-byte aligned", name, (unsigned long long)align);
-    out = Mat{(const uint8_t*)m.ptr, m.count > 1 ? m.stride : mb, rows, k, m.fmt, rb};
+    out = Mat{(const uint8_t*)m.ptr, m.count > 1 ? m.stride : mb, rows, k, m.fmt, (uint32_t)pitch};
     return TRK_OK;
 }
 
@@ -268,6 +287,12 @@ static int check_weights(trk_ctx* c, const trk_moe_w* w, Mats& M) {
     if ((rc = make_mat(w->sh_down, H, F, true, 1, "sh_down", M.shd))) return rc;
     if (M.shd.fmt != M.down.fmt) return fail(TRK_E_INVALID, "sh_down: format %u, down: %u (one down format per layer)",
                                              M.shd.fmt, M.down.fmt);
+    // one gate/up format per layer; TQ and GGUF experts are not mixed within a layer
+    if (M.up.fmt != M.gate.fmt || M.shg.fmt != M.gate.fmt || M.shu.fmt != M.gate.fmt)
+        return fail(TRK_E_INVALID, "gate/up: formats %u/%u (shared %u/%u) differ (one gate/up format per layer)",
+                    M.gate.fmt, M.up.fmt, M.shg.fmt, M.shu.fmt);
+    if (fmt_is_tq(M.gate.fmt) != fmt_is_tq(M.down.fmt))
+        return fail(TRK_E_INVALID, "gate/up and down: TQ and GGUF experts in one layer");
     return TRK_OK;
 }
 
@@ -316,9 +341,43 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
     const uint32_t kcap = c->pol.enabled ? c->pol.max : k;
     const float* lg = rlog ? rlog : ws.rlog;
     const int gemm_order = m >= c->cfg.router_dot_max_m ? 1 : 0;
+    const bool tq = fmt_is_tq(M.gate.fmt);
     // every grid below and every workspace extent its kernels index, checked on the host
-    if (const char* why = geo::check_call(geo::Caps{H, E, ws.F, ws.m_max, ws.k_cap}, m, kcap))
+    if (const char* why = geo::check_call(geo::Caps{H, E, ws.F, ws.m_max, ws.k_cap}, m, kcap, tq))
         return fail(TRK_E_INVALID, "launch geometry: %s", why);
+    if (tq) {
+        // the layer on the reference's packed TQ experts (k_tq.hip): the logits launch quantises x
+        // (two levels at M = 1 with hiprec), routing and dispatch as below, then the grouped TQ
+        // GEMVs, SwiGLU + quantisation + fold between them, and the combine
+        const int pair = m == 1 && c->cfg.hiprec ? 1 : 0;
+        const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, pair};
+        if (rlog)
+            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st,
+                                                 &xq, norm));
+        else
+            TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H,
+                                                 m == 1 ? 0 : gemm_order, ws.rlog, ws.shl, st, &xq, norm));
+        if (m == 1) {
+            TIMED(K_ROUTE, launch_route(lg, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+        } else if (m <= 4 && m * kcap <= 1024) {
+            TIMED(K_DISPATCH, launch_dispatch_small(ws, m, kcap, lg, k, c->pol, st));
+        } else if (m <= 16 && m * kcap <= 1024) {
+            TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
+            TIMED(K_DISPATCH, launch_dispatch_small(ws, m, kcap, nullptr, k, c->pol, st));
+        } else {
+            TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
+            TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
+        }
+        TIMED(K_TQ_GATEUP, launch_tq_gateup(M.gate, M.up, M.shg, M.shu, ws, ws.hgu, m, kcap, pair, st));
+        TIMED(K_TQ_ACT, launch_tq_act(ws, ws.hgu, m, kcap, pair, st));
+        TIMED(K_TQ_DOWN, launch_tq_down(M.down, M.shd, ws, m, kcap, pair, st));
+        if (m == 1)
+            TIMED(K_TQ_COMBINE, launch_tq_combine(ws, out, residual, st));
+        else
+            TIMED(K_B_COMBINE, launch_batch_combine(ws, m, out, residual, st));
+        if (c->profile) TIMED(K_PROFILE, launch_mass_profile(lg, m, E, ws.prof, st));
+        return TRK_OK;
+    }
     if (m == 1) {
         // logits (and the shared gate's logit), then routing + gate/up in one launch, then down
         const int pair = c->cfg.hiprec ? 1 : 0;

@@ -58,10 +58,16 @@ inline uint32_t stream_down_cols(uint32_t H, uint32_t F) {
 inline uint32_t decode_gateup_strips(uint32_t F) { return F / 16; }
 inline uint32_t decode_down_wgs(uint32_t H) { return H / DN_R; }
 
+// TQ layer (k_tq.hip): gate/up strips of 16 over F twice (gate, up), down strips of 16 over H;
+// grid.y: the decode slots (kcap + 1) or the work items
+inline uint32_t tq_gateup_tiles(uint32_t F) { return 2 * F / 16; }
+inline uint32_t tq_down_tiles(uint32_t H) { return H / 16; }
+
 // Every invariant a call of m rows with kcap selections per token relies on; returns nullptr when
-// they hold, else what failed.
-inline const char* check_call(const Caps& c, uint32_t m, uint32_t kcap) {
-    if (c.H == 0 || c.H % 256 || c.F == 0 || c.F % 256) return "H and F must be multiples of 256";
+// they hold, else what failed.  tq: the experts are TQ strips (k_tq.hip), not GGUF superblocks.
+inline const char* check_call(const Caps& c, uint32_t m, uint32_t kcap, bool tq = false) {
+    if (c.H == 0 || c.H % 256) return "H must be a multiple of 256";
+    if (c.F == 0 || c.F % (tq ? 16 : 256)) return tq ? "F must be a multiple of 16" : "F must be a multiple of 256";
     if (m == 0 || m > c.m_max) return "m outside 1..m_max";
     if (kcap == 0 || kcap > c.k_cap || kcap > KMAX) return "kcap outside 1..k_cap";
     if ((uint64_t)m * kcap > ent_cap(c)) return "entries above the entry capacity";
@@ -69,6 +75,13 @@ inline const char* check_call(const Caps& c, uint32_t m, uint32_t kcap) {
     if ((uint64_t)m * kcap + m > act_rows(c) || (uint64_t)m * kcap + m > yent_rows(c))
         return "activation rows above capacity";
     if (doff_elems(m, c.E) > doff_elems(c.m_max, c.E)) return "dispatch offsets above capacity";
+    if (tq) {
+        if (tq_gateup_tiles(c.F) * 16 != 2 * c.F || tq_down_tiles(c.H) * 16 != c.H) return "TQ strips do not tile F / H";
+        // decode: slots 0..kcap (the shared one last) in h / yent rows and in the [33][2] act rows
+        if (m == 1 && ((uint64_t)kcap + 1 > yent_rows(c) || (uint64_t)(KMAX + 1) * 2 > act_rows(c)))
+            return "decode slots above capacity";
+        return nullptr;
+    }
     {  // MFMA gate/up: the column blocks tile F's strips exactly, four waves each
         const uint32_t cols = mfma_gateup_cols(m, c.F), s = mfma_gateup_strips(m, c.F);
         if (cols == 0 || cols * s * 16 != c.F || s % 4) return "MFMA gate/up grid does not tile F";

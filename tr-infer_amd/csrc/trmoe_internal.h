@@ -80,6 +80,7 @@ struct Workspace {
     int32_t* actsum;
     float* actu;          // [act_rows][F/16]: folded scale * (float)sum
     float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
+    float* hgu;           // [ent_cap + m_max][2F] gate / up outputs of the TQ layer
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
     unsigned long long* prof;   // [33] router-mass profile: fixed-point sums per k, then the row count
@@ -144,6 +145,14 @@ hipError_t launch_batch_combine(const Workspace& ws, uint32_t m, float* out, int
 hipError_t launch_gemv(const Mat& w, uint32_t item, uint32_t s0, uint32_t s1, uint32_t kb, const int8_t* q,
                        const float* s, const int32_t* su, uint32_t m, int pair, float* y, uint32_t ldy,
                        const uint32_t* rows, int accumulate, hipStream_t st);
+// the layer on TQ experts (k_tq.hip): gate/up into h [rows][2F], SwiGLU + quantisation + fold,
+// down into yent, and (decode) the slot-order combine
+hipError_t launch_tq_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
+                            float* h, uint32_t m, uint32_t kcap, int pair, hipStream_t st);
+hipError_t launch_tq_act(const Workspace& ws, const float* h, uint32_t m, uint32_t kcap, int pair, hipStream_t st);
+hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
+                          hipStream_t st);
+hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st);
 hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
                           hipStream_t st);

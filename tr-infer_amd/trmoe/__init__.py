@@ -230,17 +230,17 @@ class LayerWeights:
         self.H, self.E, self.F = H, E, F
         self.tensors = dict(router=router, shexp_gate=shexp_gate, gate=gate, up=up, down=down, sh_gate=sh_gate,
                             sh_up=sh_up, sh_down=sh_down, router_bias=router_bias)
-        gb, db = row_bytes(gate_fmt, H), row_bytes(down_fmt, F)
+        gm, dmb = matrix_bytes(gate_fmt, F, H), matrix_bytes(down_fmt, H, F)
 
-        def mat(t, rows, k, fmt, count, rb):
-            return Mat(t.data_ptr(), rows, k, fmt, count, rows * rb)
+        def mat(t, rows, k, fmt, count, mb):
+            return Mat(t.data_ptr(), rows, k, fmt, count, mb)
 
         self.moew = MoeW(router.data_ptr() if router is not None else None,
                          router_bias.data_ptr() if router_bias is not None else None, shexp_gate.data_ptr(),
-                         mat(gate, F, H, gate_fmt, E, gb), mat(up, F, H, gate_fmt, E, gb), mat(down, H, F, down_fmt, E, db),
-                         mat(sh_gate, F, H, gate_fmt, 1, gb), mat(sh_up, F, H, gate_fmt, 1, gb),
-                         mat(sh_down, H, F, down_fmt, 1, db))
-        self.bytes_per_expert = 2 * F * gb + H * db
+                         mat(gate, F, H, gate_fmt, E, gm), mat(up, F, H, gate_fmt, E, gm), mat(down, H, F, down_fmt, E, dmb),
+                         mat(sh_gate, F, H, gate_fmt, 1, gm), mat(sh_up, F, H, gate_fmt, 1, gm),
+                         mat(sh_down, H, F, down_fmt, 1, dmb))
+        self.bytes_per_expert = 2 * gm + dmb
 
     @classmethod
     def from_host(cls, layer, device="cuda"):
@@ -255,6 +255,20 @@ class LayerWeights:
                    dev(layer.stacked("up")), dev(layer.stacked("down")), dev(layer.sh_gate), dev(layer.sh_up),
                    dev(layer.sh_down), layer.gate_fmt, layer.down_fmt,
                    None if layer.bias is None else dev(layer.bias))
+
+    @classmethod
+    def from_tq(cls, H, E, F, router, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, gate_fmt, down_fmt,
+                router_bias=None, device="cuda"):
+        """Upload a layer whose experts are the reference's packed TQ strips (host arrays: gate /
+        up / down as [E][matrix bytes], the shared expert's as one matrix each), unchanged."""
+        import numpy as np
+        import torch
+
+        def dev(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        return cls(H, E, F, dev(router), dev(shexp_gate), dev(gate), dev(up), dev(down), dev(sh_gate), dev(sh_up),
+                   dev(sh_down), gate_fmt, down_fmt, None if router_bias is None else dev(router_bias))
 
     @classmethod
     def generate(cls, seed, layer, H, E, F, down_fmt=FMT_Q4_K, router_bias=None, device="cuda", stream=None):
