@@ -53,10 +53,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
-    ap.add_argument("--extra", type=str, default="c4,stack",
+    ap.add_argument("--extra", type=str, default="c4,stack,tq",
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
-                         "48-layer RMSNorm + residual stack at M=1 and M=512); q80 / q51 / q6k: the layer at "
-                         "M=1 and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
+                         "48-layer RMSNorm + residual stack at M=1 and M=512); tq: the layer on packed TQ "
+                         "experts at the real shape (H=2560, F=640) at M=1 and M=512; q80 / q51 / q6k: the "
+                         "layer at M=1 and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
+    ap.add_argument("--tq-layers", type=int, default=24,
+                    help="layers in the rotation of the TQ extra (1.78 GB of experts each)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
@@ -191,6 +194,9 @@ def main():
         if key in todo:
             for Md, res in bench_down_format(args, layers, fmt, nm, dev, stream, trmoe, torch).items():
                 extras[f"{nm} down M={Md}"] = res
+    if "tq" in todo:
+        for Mt, res in bench_tq(args, dev, stream, trmoe, torch, np).items():
+            extras[f"TQ real shape M={Mt}"] = res
     if "stack" in todo:
         for Ms in (1, 512):
             extras[f"C5 stack M={Ms}"] = bench_stack(args, layers, ctx if Ms <= m_max else None, Ms, dev, stream,
@@ -335,6 +341,89 @@ def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
         log(f"{name} down M={M}: {per * 1e3:.1f} us/layer")
     del lw
     return out_res
+
+
+def gen_tq_stack(torch, trmoe, count, rows, k, fmt, dev, gen):
+    """A stack of `count` packed TQ matrices on the GPU (codec.rs:1-46): uniform q bytes (and
+    5-bit planes), each block's f16 d in [5e-4, 3e-3] and m = -d * U(0, 2^(bits-1)), the sign
+    pattern of converted GGUF weights."""
+    mb = trmoe.matrix_bytes(fmt, rows, k)
+    bb, bits = trmoe.tq_block_bytes(fmt), fmt >> 8
+    t = torch.randint(0, 256, (count, mb), dtype=torch.uint8, device=dev, generator=gen)
+    blocks = t.view(count, mb // bb, bb)
+    d = torch.empty((count, mb // bb, 16), device=dev).uniform_(5e-4, 3e-3, generator=gen)
+    m = -d * torch.empty_like(d).uniform_(0, float(1 << (bits - 1)), generator=gen)
+    blocks[:, :, 0:32] = d.half().view(torch.uint8)
+    blocks[:, :, 32:64] = m.half().view(torch.uint8)
+    return t
+
+
+def bench_tq(args, dev, stream, trmoe, torch, np):
+    """The layer on the reference's own packed TQ experts at the real expert shape: H = 2560,
+    F = 640, E = 512, top-10, gate/up TQ4_32 and down TQ5_16 (python/tests/test_blocks_real.py:
+    23-26), over a rotation of args.tq_layers layers (synthetic packs generated on the GPU), at M = 1
+    and M = 512 (Zipf-biased router)."""
+    Ht, Et, Ft = 2560, 512, 640
+    gf, df = trmoe.FMT_TQ4_32, trmoe.FMT_TQ5_16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    t0 = time.time()
+    lw = []
+    for _ in range(args.tq_layers):
+        router = torch.randn((Et, Ht), device=dev, generator=gen) * 0.02
+        shg = torch.randn(Ht, device=dev, generator=gen) * 0.02
+        gate, up = (gen_tq_stack(torch, trmoe, Et, Ft, Ht, gf, dev, gen) for _ in range(2))
+        down = gen_tq_stack(torch, trmoe, Et, Ht, Ft, df, dev, gen)
+        sg, su = (gen_tq_stack(torch, trmoe, 1, Ft, Ht, gf, dev, gen)[0] for _ in range(2))
+        sd = gen_tq_stack(torch, trmoe, 1, Ht, Ft, df, dev, gen)[0]
+        lw.append(trmoe.LayerWeights(Ht, Et, Ft, router, shg, gate, up, down, sg, su, sd, gf, df))
+    torch.cuda.synchronize()
+    per_expert = 2 * trmoe.matrix_bytes(gf, Ft, Ht) + trmoe.matrix_bytes(df, Ht, Ft)
+    log(f"TQ layers: {len(lw)} x {Et} experts ({len(lw) * Et * per_expert / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
+    bias = torch.from_numpy(trmoe.zipf_bias(1, Et)).to(dev)
+    res = {}
+    for M in (1, 512):
+        for w in lw:
+            w.moew.router_bias = bias.data_ptr() if M >= 64 else None
+        ctx = trmoe.Context(Ht, Et, Ft, K, M)
+        x = torch.randn((M, Ht), device=dev, generator=gen)
+        out = torch.empty((M, Ht), dtype=torch.float32, device=dev)
+        touched = []
+        for w in lw:
+            ctx.forward(w, x, out)
+            ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+            nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+            touched.append(len(np.unique(np.concatenate([ids[t, :nsel[t]] for t in range(M)]))))
+        steps = min(args.steps, 2 * len(lw))
+
+        def body():
+            for i in range(steps):
+                ctx.forward(lw[i % len(lw)], x, out)
+
+        per = timed_graph(torch, stream, body, 1) / steps
+        ctx.set_timing(True)
+        ctx.forward(lw[0], x, out)
+        names = list(ctx.timing())
+        ctx.set_timing(False)
+        kern = {}
+        for name in names:
+            ctx.forward(lw[0], x, out)
+
+            def kbody():
+                for i in range(steps):
+                    ctx.launch_kernel(name, lw[i % len(lw)], x, out)
+
+            kern[name] = round(timed_graph(torch, stream, kbody, 1) / steps * 1e3, 2)
+        ctx.close()
+        nbytes = (float(np.mean(touched)) + 1) * per_expert + Et * Ht * 4 + M * Ht * 8
+        res[M] = {"tokens_per_s": round(M / (per * 1e-3), 1), "us_per_layer": round(per * 1e3, 2),
+                  "layer_GBps": round(nbytes / (per * 1e-3) / 1e9, 1),
+                  "hbm_frac": round(nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "experts_touched": round(float(np.mean(touched)), 1), "kernels_us": kern, "layers": len(lw),
+                  "steps": steps}
+        log(f"TQ real shape M={M}: {per * 1e3:.1f} us/layer, {M / (per * 1e-3):.0f} tok/s, kernels {kern}")
+    del lw
+    return res
 
 
 def bench_stack(args, layers, ctx, M, dev, stream, trmoe, torch):
