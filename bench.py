@@ -204,24 +204,12 @@ def main():
 
     prim = 1 if 1 in results else ms_list[0]
     r = results[prim]
-    # roofline of the dominant kernel of the primary workload
-    kern = r["_kern"]
-    dom = max(kern, key=lambda k: kern[k][0])
-    avg_ms = kern[dom][0] / kern[dom][1]
-    tavg = float(np.mean(r["_touched"]))
-    gu_bytes = (tavg + 1) * 2 * F * Q4K_ROW_H
-    dn_bytes = (tavg + 1) * H * Q4K_ROW_F
-    alg = {"decode_layer": gu_bytes + dn_bytes + E * H * 4 + H * 4 + H * 4 * 2,
-           "decode_gateup": gu_bytes + 2 * 2 * H + 2 * (H // 32) * 8 + 33 * 2 * (F + F // 16 * 8),
-           "decode_down": dn_bytes + (tavg + 1) * 2 * (F + F // 16 * 8) + H * 4,
-           "batch_gateup": gu_bytes, "batch_down": dn_bytes,
-           "router_logits": E * H * 4 + prim * H * 4 + prim * E * 4}.get(dom)
-    roof = None
-    if alg:
-        ach = alg / (avg_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, prim),
-                "alg_bytes_per_launch": int(alg), "avg_launch_us": round(avg_ms * 1e3, 2)}
+    # roofline of the dominant kernel of the primary workload, and of every other M
+    roofs = {M: roofline(M, res, np) for M, res in results.items()}
+    roof = roofs[prim]
+    for M, res in results.items():
+        if M != prim:
+            res["roofline"] = roofs[M]
 
     cpu = None
     if not args.no_cpu and prim == 1:
@@ -451,6 +439,33 @@ def bench_stack(args, layers, ctx, M, dev, stream, trmoe, torch):
     return {"tokens_per_s": round(M / (per * 1e-3), 1), "ms_per_pass": round(per, 4),
             "us_per_layer": round(per * 1e3 / len(layers), 2), "layers": len(layers), "passes": reps,
             "finite": ok}
+
+
+def roofline(M, res, np):
+    """The roofline object of the dominant kernel of one M's layer: algorithmic bytes per launch
+    (touched experts' weights, each byte once, plus the activations the kernel moves) over its
+    average isolated launch time, against the 8 TB/s HBM peak; traffic from the counter passes."""
+    kern = res["_kern"]
+    dom = max(kern, key=lambda k: kern[k][0])
+    avg_ms = kern[dom][0] / kern[dom][1]
+    tavg = float(np.mean(res["_touched"]))
+    nent = float(np.mean(res["_ents"]))
+    gu_bytes = (tavg + 1) * 2 * F * Q4K_ROW_H
+    dn_bytes = (tavg + 1) * H * Q4K_ROW_F
+    xq = M * (H + H // 32 * 12)                # int8 x rows with their scale, sum and u
+    act = (nent + M) * (F + F // 16 * 12)      # int8 SwiGLU rows with their scale, sum and u
+    alg = {"decode_layer": gu_bytes + dn_bytes + E * H * 4 + H * 4 + H * 4 * 2,
+           "decode_gateup": gu_bytes + 2 * 2 * H + 2 * (H // 32) * 8 + 33 * 2 * (F + F // 16 * 8),
+           "decode_down": dn_bytes + (tavg + 1) * 2 * (F + F // 16 * 8) + H * 4,
+           "batch_gateup": gu_bytes + xq + act, "batch_down": dn_bytes + act + (nent + M) * H * 4,
+           "stream_gateup": gu_bytes + xq + act, "stream_down": dn_bytes + act + (nent + M) * H * 4,
+           "router_logits": E * H * 4 + M * H * 4 + M * E * 4}.get(dom)
+    if not alg:
+        return None
+    ach = alg / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, M),
+            "alg_bytes_per_launch": int(alg), "avg_launch_us": round(avg_ms * 1e3, 2)}
 
 
 def measured_traffic(kernel, m):

@@ -272,6 +272,21 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_reduc
 
 // Token (activation row) of entry row `row` of a grouped work item; rows past the item reuse its
 // first row (their outputs are never stored).
+// XCD-aware order of a grouped launch's (column block, item) workgroups.  The dispatcher deals
+// workgroup ids round robin to the 8 XCDs (id % 8), each with its own L2.  Here XCD x takes a
+// contiguous run of the live ids [0, gridDim.x * n_items) in dispatch order, so the consecutive
+// items of one expert (each re-reads that expert's weights) run on one XCD close in time and
+// share its L2.  A bijection on the live ids; false for the ids past them.
+__device__ __forceinline__ bool xcd_order(uint32_t n_items, uint32_t& col, uint32_t& itn) {
+    const uint32_t gx = gridDim.x, id = blockIdx.x + gx * blockIdx.y, T = gx * n_items;
+    if (id >= T) return false;
+    const uint32_t x = id % 8, slot = id / 8, base = T / 8, rem = T % 8;
+    const uint32_t nid = x * base + (x < rem ? x : rem) + slot;
+    col = nid % gx;
+    itn = nid / gx;
+    return true;
+}
+
 __device__ __forceinline__ uint32_t item_token(const Workspace& ws, const Item& it, bool shared, uint32_t row) {
     const uint32_t r = row < it.nrows ? row : 0u;
     return shared ? it.row0 + r : ws.ent_tok[it.row0 + r];

@@ -520,7 +520,7 @@ template <int NSB, int S>
 __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32_t e, const Item& item, bool shared,
                                               uint32_t n_ent, uint32_t F, const v4i_t* As, const float* Sx,
                                               const float* Su, const Workspace& ws, uint32_t wv, uint32_t lane,
-                                              uint32_t strips) {
+                                              uint32_t strips, uint32_t bx) {
     constexpr uint32_t R = 16 / S;
     const uint32_t g = lane / 16, r = lane % 16, nbf = F / 16;
     const uint32_t own = g * S / 4, orow = (4 * g) % R;
@@ -533,7 +533,7 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
         wgt[i] = shared ? sigmoid_libm(ws.shl[item.row0 + row]) : ws.ent_w[item.row0 + row];
     }
     auto rowp = [&](const Mat& M, uint32_t step, uint32_t s) -> const uint8_t* {
-        const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + s);
+        const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + s);
         return M.ptr + (size_t)e * M.stride + (size_t)(strip * 16 + r) * M.row_bytes + (step % NSB) * 144;
     };
     struct W {
@@ -606,7 +606,7 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
         }
         cw = nw;
         if (sb == NSB - 1) {
-            const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + own);
+            const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + own);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = orow + i;
@@ -641,8 +641,9 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
                                                           uint32_t skip_rows) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8;
     const uint32_t F = gate.rows, nbf = F / 16;
-    const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-    if (itn >= ws.n_groups[2]) return;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    uint32_t bx, itn;  // column block and item, in XCD order
+    if (!xcd_order(ws.n_groups[2], bx, itn)) return;
     const Item item = ws.items[itn];
     if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
     const bool shared = item.expert == NO_EXPERT;
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     const uint32_t strips = F / 16 / gridDim.x;  // per workgroup
     if (item.nrows <= 8 && strips % 8 == 0) {
         __syncthreads();
-        gateup_strips<NSB, 2>(G, U, e, item, shared, n_ent, F, As, Sx, Su, ws, wv, lane, strips);
+        gateup_strips<NSB, 2>(G, U, e, item, shared, n_ent, F, As, Sx, Su, ws, wv, lane, strips, bx);
         return;
     }
     const uint32_t g = lane / 16, r = lane % 16;
@@ -702,7 +703,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     float2* dmw = Dm + wv * 2 * 16 * DM_STRIDE;
     const uint32_t nstep = (strips / 4) * NSB;   // (strip, superblock) steps of this wave
     auto rows_of = [&](uint32_t step, const uint8_t*& rg, const uint8_t*& ru) {
-        const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+        const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
         rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + r) * G.row_bytes;
         ru = U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + r) * U.row_bytes;
     };
@@ -777,7 +778,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
         if (sb == NSB - 1) {
             // SwiGLU (elem.rs:173) and per-16 quantisation across the 16 lanes holding one entry's
             // strip (lanes 16g .. 16g+15, one DPP row)
-            const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+            const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = 4 * g + i;
@@ -884,14 +885,14 @@ __device__ __forceinline__ v4i mfma_i8_acc(long a, long b, v4i c) {
 template <int NSB, int S>
 __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const Item& item, uint32_t arow0, uint32_t H,
                                                const long* As, const float* Sx, const float* Su, const Workspace& ws,
-                                               uint32_t wv, uint32_t lane, uint32_t strips) {
+                                               uint32_t wv, uint32_t lane, uint32_t strips, uint32_t bx) {
     constexpr uint32_t R = 16 / S;
     const uint32_t g = lane / 16, r = lane % 16;
     const uint32_t own = g * S / 4, orow = (4 * g) % R;  // output strip (of the S) and first act row
     const uint32_t arl = r % R, sel = r / R;             // act row this lane feeds A, and for which strip
     const uint32_t nstep = (strips / 4 / S) * NSB;
     auto row_of = [&](uint32_t step, uint32_t s) -> const uint8_t* {
-        const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + s);
+        const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + s);
         return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
     };
     struct W {
@@ -945,7 +946,7 @@ __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const I
         }
         cw = nw;
         if (sb == NSB - 1) {
-            const uint32_t strip = blockIdx.x * strips + wv + 4 * ((step / NSB) * S + own);
+            const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + own);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = orow + i;
@@ -1020,8 +1021,9 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     constexpr bool Q6 = FK == 1;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
     const uint32_t H = down.rows;
-    const uint32_t itn = blockIdx.y, tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-    if (itn >= ws.n_groups[2]) return;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    uint32_t bx, itn;  // column block and item, in XCD order
+    if (!xcd_order(ws.n_groups[2], bx, itn)) return;
     const Item item = ws.items[itn];
     if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
     const bool shared = item.expert == NO_EXPERT;
@@ -1068,11 +1070,11 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     if constexpr (FK == 0) {
         // small items: several strips per MFMA output (a wave owns strips / 4 strips)
         if (item.nrows <= 4 && strips % 16 == 0) {
-            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips);
+            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
             return;
         }
         if (item.nrows <= 8 && strips % 8 == 0) {
-            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips);
+            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
             return;
         }
     }
@@ -1080,7 +1082,7 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     float2* dmw = Dm + wv * 16 * DM_STRIDE;
     const uint32_t nstep = (strips / 4) * NSB;
     auto row_of = [&](uint32_t step) -> const uint8_t* {
-        const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+        const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
         return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
     };
     using W = typename std::conditional<
@@ -1175,7 +1177,7 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
         }
         cw = nw;
         if (sb == NSB - 1) {
-            const uint32_t strip = blockIdx.x * strips + wv + 4 * (step / NSB);
+            const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = 4 * g + i;
