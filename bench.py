@@ -113,7 +113,7 @@ def main():
     for M in ms_list:
         x = xs[M]
         # pre-pass: the experts each layer touches for this input (for the algorithmic bytes)
-        touched, ents = [], []
+        touched, ents, maxg = [], [], []
         for l in range(args.layers):
             ctx.forward(weights(l, M), x, out[:M])
             ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
@@ -121,6 +121,7 @@ def main():
             sel = np.concatenate([ids[t, :nsel[t]] for t in range(M)])
             touched.append(len(np.unique(sel)))
             ents.append(int(nsel.sum()))
+            maxg.append(int(np.bincount(sel).max()))
         for i in range(args.warmup):
             ctx.forward(weights(i % args.layers, M), x, out[:M])
         torch.cuda.synchronize()
@@ -181,6 +182,9 @@ def main():
             mfma_frac=nops / (per * 1e-3) / 1e12 / INT8_PEAK_TOPS, experts_touched=float(np.mean(touched)),
             layer_MB=nbytes / 1e6,
             kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in kern.items()},
+            largest_group=float(np.mean(maxg)),
+            routing=("Zipf(1.1) load: per-rank router bias fitted to Plackett-Luce top-10 inclusion "
+                     "(trmoe/zipf_bias_table.json)" if M >= 512 else "router logits only (no bias)"),
             _kern=kern, _touched=touched, _ents=ents)
         log(f"M={M}: {per * 1e3:.1f} us/layer (eager {per_eager * 1e3:.1f}), {M / (per * 1e-3):.0f} tok/s, "
             f"{nbytes / (per * 1e-3) / 1e9:.0f} GB/s, kernels {results[M]['kernels_us']}")

@@ -431,24 +431,48 @@ def rng_u64(seed: int, stream_id: int, idx: int) -> int:
     return _mix64((key + idx * 0xD1B54A32D192ED03) & _M64)
 
 
-# Scale of the Zipf log-probabilities in the router bias.  Top-k over logits + log p (with the
-# router's N(0, 0.905^2) logits) concentrates the load far beyond Zipf: only ~99 experts are
-# touched at M = 512.  The load the Zipf(1.1) config describes is that of drawing k distinct
-# experts per token from p (Gumbel-top-k: 464 experts touched, 48 empty, median group 3 at
-# M = 512, k = 10).  Scaling log p by 0.40 reproduces the touched and empty counts (464, 48;
-# median 4, largest group ~290 instead of ~470), found by simulating top-10 over i.i.d.
-# N(0, 0.905^2) logits.
+# Config 3's Zipf(1.1) load as a router bias.  Top-k over logits + log p (with the router's
+# N(0, 0.905^2) logits) concentrates the load far beyond Zipf: only ~99 experts are touched at
+# M = 512.  The load the config describes is drawing k distinct experts per token from p
+# (Plackett-Luce; at M = 512, k = 10: ~460 experts touched, ~50 empty, largest group ~465, median
+# 3).  zipf_bias_table.json holds the per-rank bias fitted to reproduce every rank's inclusion
+# probability (make_zipf_table.py); ZIPF_BIAS_SCALE * log p is the fallback for other (E, s),
+# which matches the touched and empty counts but not the largest group (~290).
 ZIPF_BIAS_SCALE = 0.40
+ZIPF_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "zipf_bias_table.json")
 
 
-def zipf_bias(seed: int, E: int, s: float = 1.1, scale: float = ZIPF_BIAS_SCALE, stream_id: int = 5):
-    """Router bias b_e = scale * log p_{pi(e)}, p_j ~ j^-s, over the permutation pi that sorts
-    rng_u64(seed, stream_id, e) (float32 numpy array of E)."""
+def zipf_rank_bias(E: int, s: float = 1.1):
+    """The fitted per-rank bias of zipf_bias_table.json (make_zipf_table.py) when it was fitted for
+    this E and s, else None."""
+    import json
+    import numpy as np
+    try:
+        with open(ZIPF_TABLE) as f:
+            t = json.load(f)
+    except OSError:
+        return None
+    if t["E"] != E or abs(t["s"] - s) > 1e-12:
+        return None
+    return np.array(t["bias"], np.float64)
+
+
+def zipf_bias(seed: int, E: int, s: float = 1.1, scale: float = None, stream_id: int = 5):
+    """Router bias for config 3's Zipf(s) load, over the permutation pi that sorts
+    rng_u64(seed, stream_id, e): the expert of rank j gets b_j (float32 numpy array of E).
+
+    b_j is the fitted per-rank bias of zipf_bias_table.json when one exists for (E, s): top-10
+    over the synthetic router's N(0, 0.905^2) logits plus b then includes each expert as often as
+    drawing 10 distinct experts per token from Zipf(s) does (make_zipf_table.py).  Otherwise, or
+    with an explicit scale, b_j = scale * log p_j with p_j ~ j^-s (scale 0.40 by default)."""
     import numpy as np
     keys = np.array([rng_u64(seed, stream_id, e) for e in range(E)], np.uint64)
     perm = np.argsort(keys, kind="stable")  # perm[j] = the expert of rank j
-    p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
-    p /= p.sum()
+    rank_b = zipf_rank_bias(E, s) if scale is None else None
+    if rank_b is None:
+        p = 1.0 / np.arange(1, E + 1, dtype=np.float64) ** s
+        p /= p.sum()
+        rank_b = (ZIPF_BIAS_SCALE if scale is None else scale) * np.log(p)
     b = np.zeros(E, np.float32)
-    b[perm] = (scale * np.log(p)).astype(np.float32)
+    b[perm] = rank_b.astype(np.float32)
     return b
