@@ -171,6 +171,22 @@ int trk_router_logits(const float *router, const float *bias, const float *shexp
                       uint32_t m, uint32_t n_expert, uint32_t hidden, int gemm_order, float *rlog,
                       float *sh, void *stream);
 
+/* The hyper-connection mix of the FFN input, part B (tr_model::exec::HcW {up}, exec.rs:49-55):
+ * up = the low-rank up projection [hc * hidden][lr] in a kb-32 TQ codec, hc streams (1..8), low
+ * rank lr (a multiple of 32, at most 1024). */
+typedef struct {
+    trk_mat up;
+    uint32_t hc, lr;
+} trk_hc_w;
+
+/* out[M][H] = MoE(mixed) where mixed is the MoE input the hyper-connection mix produces from the
+ * normed streams xn[M][hc][H] (hc_mix_a's output) and the low-rank projection lo[M][lr] summed
+ * over tiles: Model::hc_mix_b (exec.rs:1196-1234) + the S5 router + moe_block at M = 1 (two-level
+ * lo with hiprec), hc_b_batch (exec_batch.rs:929-1019) + moe_batch at M >= 2, on one tile.  The
+ * mix runs as the layer's input stage (one launch); the router then reads the mixed rows. */
+int trk_moe_forward_hc(trk_ctx *ctx, const trk_moe_w *w, const trk_hc_w *hc, const float *xn, const float *lo,
+                       uint32_t m, float *out, void *stream);
+
 /* Per-row routing: route_topk (router.rs:106-113) or, with a policy, route_mass
  * (router.rs:118-148).  ids/w: [m][32], n_sel: [m]. */
 int trk_route(const float *logits, uint32_t m, uint32_t n_expert, uint32_t k, const trk_moe_policy *policy,
@@ -264,7 +280,8 @@ enum {
     TRK_WS_ACTQ = 13,    /* activation rows of the down input, i8 */
     TRK_WS_ACTS = 14,    /* their folded scales, f32 */
     TRK_WS_SHLOGIT = 15, /* [M] f32: dot(shexp_gate, x) */
-    TRK_WS_BARRIER_ERR = 16 /* u32: nonzero if a one-launch decode layer ever timed out at a grid barrier */
+    TRK_WS_BARRIER_ERR = 16, /* u32: nonzero if a one-launch decode layer ever timed out at a grid barrier */
+    TRK_WS_MIXED = 17    /* [M][H] f32: the MoE input trk_moe_forward_hc mixed */
 };
 /* Ordered after the work queued on `stream` (synchronises that stream only). */
 int trk_debug_read(trk_ctx *ctx, int which, void *host_dst, size_t bytes, void *stream);

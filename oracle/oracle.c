@@ -839,6 +839,70 @@ int orc_moe_block(const orc_moe_w *W, const float *x, const float *rlog, int k,
     return k_used;
 }
 
+/* Hyper-connection mix, part B, on one tile (T = 1): the MoE input `mixed` of every row from the
+ * normed streams xn [m][hc][hh] and the low-rank projection lo [m][lr] (summed over tiles).
+ * up: the TQ matrix [hc * hh][lr] with (bits, 32).
+ *   decode (exec.rs:1196-1234, hc_mix_b): lo <- silu(lo / hc) with the scalar silu; quantised in
+ *     pairs when hiprec (CoreScratch::qz, exec.rs:284-290); gate = sigmoid(up . q) with the scalar
+ *     sigmoid; mixed[c] = (sum_s xn[s][c] * gate[s][c], accumulated from 0 with separate multiply
+ *     and add) * (1 / hc).
+ *   batch (exec_batch.rs:929-968, hc_b_batch): lo <- lo * (1 / hc), then silu_inplace (silu512 on
+ *     16-blocks, scalar tail); quant_rows per 32; gate = sigmoid_inplace(up . q) (sigmoid512 on
+ *     16-blocks); mixed = xn_0 * gate_0, then fma_inplace for s >= 1 (fused on 16-blocks, multiply
+ *     and add on the tail), then scale_inplace(1 / hc). */
+void orc_hc_mix(const uint8_t *up, int bits, int hc, int hh, int lr, const float *xn, const float *lo, int m,
+                int decode, int hiprec, float *mixed) {
+    const int nb = lr / 32, rows = hc * hh, mrows = decode && hiprec ? 2 : 1;
+    const float inv = 1.0f / (float)hc;
+    float *l2 = (float *)malloc(sizeof(float) * lr);
+    int8_t *q = (int8_t *)malloc((size_t)2 * lr);
+    float *qs = (float *)malloc(sizeof(float) * 2 * nb);
+    int32_t *qsu = (int32_t *)malloc(sizeof(int32_t) * 2 * nb);
+    float *gate = (float *)malloc(sizeof(float) * rows);
+    for (int mi = 0; mi < m; mi++) {
+        const float *lr_in = lo + (size_t)mi * lr;
+        if (decode) {
+            for (int j = 0; j < lr; j++) l2[j] = silu_scalar(lr_in[j] / (float)hc);
+            if (hiprec)
+                orc_quant_pair(l2, lr, 32, q, qs, qsu);
+            else
+                orc_quant_rows(l2, 1, lr, 32, q, qs, qsu);
+        } else {
+            const int body = lr / 16 * 16;
+            for (int j = 0; j < lr; j++) l2[j] = lr_in[j] * inv;
+            for (int j = 0; j < lr; j++) l2[j] = j < body ? orc_silu512(l2[j]) : silu_scalar(l2[j]);
+            orc_quant_rows(l2, 1, lr, 32, q, qs, qsu);
+        }
+        orc_qact qa = {mrows, lr, 32, q, qs, qsu, mrows == 2};
+        orc_gemv_tq_rows(up, lr, bits, 32, 0, rows / ORC_STRIP, &qa, gate, 0, NULL, 0);
+        const int gbody = rows / 16 * 16;
+        for (int i = 0; i < rows; i++)
+            gate[i] = decode ? orc_sigmoid(gate[i]) : (i < gbody ? orc_sigmoid512(gate[i]) : orc_sigmoid(gate[i]));
+        const float *x = xn + (size_t)mi * rows;
+        float *out = mixed + (size_t)mi * hh;
+        if (decode) {
+            for (int c = 0; c < hh; c++) {
+                float acc = 0.0f;
+                for (int sI = 0; sI < hc; sI++) acc += x[sI * hh + c] * gate[sI * hh + c];
+                out[c] = acc * inv;
+            }
+        } else {
+            const int body = hh / 16 * 16;
+            for (int c = 0; c < hh; c++) out[c] = x[c] * gate[c];
+            for (int sI = 1; sI < hc; sI++)
+                for (int c = 0; c < hh; c++)
+                    out[c] = c < body ? fmaf(x[sI * hh + c], gate[sI * hh + c], out[c])
+                                      : out[c] + x[sI * hh + c] * gate[sI * hh + c];
+            for (int c = 0; c < hh; c++) out[c] = out[c] * inv;
+        }
+    }
+    free(l2);
+    free(q);
+    free(qs);
+    free(qsu);
+    free(gate);
+}
+
 /* exec_batch.rs:1404-1580 (moe_batch) with the router of exec_batch.rs:989-1019 */
 int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, int k,
                   const orc_policy *policy, int router_dot_max_m, float *out, float *rlog_out,

@@ -142,6 +142,11 @@ typedef struct {
     uint64_t rows, experts; /* MoeStats::add (exec.rs:602-605) */
 } orc_moe_stats;
 
+/* Hyper-connection mix part B on one tile: mixed [m][hh] from xn [m][hc][hh] and lo [m][lr]
+ * (exec.rs:1196-1234 when decode, exec_batch.rs:929-968 otherwise); up: TQ [hc*hh][lr], kb 32. */
+void orc_hc_mix(const uint8_t *up, int bits, int hc, int hh, int lr, const float *xn, const float *lo, int m,
+                int decode, int hiprec, float *mixed);
+
 /* Decode path, one token (exec.rs:1540-1623 with the S5 router at exec.rs:1003-1011).
  * rlog: [E] logits or NULL (then computed with dot + optional bias into rlog_out).
  * ids/w: [32]; returns k_used (or -1 on error: untouched expert weights missing). */

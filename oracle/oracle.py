@@ -97,6 +97,7 @@ def _declare(L):
     L.orc_quant_pair.argtypes = [vp, i, i, vp, vp, vp]
     L.orc_gemv_tq_rows.argtypes = [vp, i, i, i, i, i, C.POINTER(QAct), vp, sz, vp, i]
     L.orc_gemm_tq_rows.argtypes = [vp, i, i, i, i, i, C.POINTER(QAct), vp, sz, vp, i]
+    L.orc_hc_mix.argtypes = [vp, i, i, i, i, vp, vp, i, i, i, vp]
     L.orc_dot.argtypes = [vp, vp, i]
     L.orc_dot.restype = f
     L.orc_gemm_f32_nt.argtypes = [vp, i, i, vp, i, i, i, vp, i]
@@ -263,6 +264,18 @@ def gemv_tq(w, k, bits, kb, rows_out, q, s, su, pair=False, y=None, rows=None, a
     fn = lib().orc_gemm_tq_rows if gemm else lib().orc_gemv_tq_rows
     fn(C.c_void_p(w.ctypes.data + off), k, bits, kb, s0, s1, C.byref(qa), _p(y), ldy, rp, int(accumulate))
     return y
+
+
+def hc_mix(up, bits, hc, lr, xn, lo, decode, hiprec=True):
+    """Hyper-connection mix part B (exec.rs:1196-1234 when decode, exec_batch.rs:929-968
+    otherwise): mixed [m][hh] from xn [m][hc][hh], lo [m][lr] and the TQ up matrix [hc*hh][lr]."""
+    xn = np.ascontiguousarray(xn, np.float32)
+    lo = np.ascontiguousarray(lo, np.float32)
+    m, hh = lo.shape[0], xn.shape[-1]
+    out = np.zeros((m, hh), np.float32)
+    lib().orc_hc_mix(_p(np.ascontiguousarray(up, np.uint8)), bits, hc, hh, lr, _p(xn), _p(lo), m, int(decode),
+                     int(hiprec), _p(out))
+    return out
 
 
 def dot(a, b):

@@ -583,3 +583,57 @@ def test_q6k_down_layer_runs(small_layer):
     sh = 1 / (1 + math.exp(-float(np.dot(L.shexp_gate.astype(np.float64), x))))
     want = f64_moe(L, x.astype(np.float64), r["ids"], r["w"].astype(np.float64), sh)
     assert np.abs(r["out"] - want).max() <= 3e-3 * np.abs(want).max()
+
+
+def _tq_from(q, d, m, bits):
+    return O.pack_tq(q.astype(np.uint8), d.astype(np.float16), m.astype(np.float16), bits, 32)
+
+
+def test_hc_mix_half_gate_when_up_is_zero():
+    """With every up block's d = m = 0 the gate is sigmoid(0) = 1/2 exactly, so mixed is the
+    stream sum times 1/hc in the reference's order: decode accumulates from 0 with a separate
+    multiply and add (exec.rs:1221-1227), batch multiplies stream 0 and fuses the rest
+    (exec_batch.rs:953-959); with a gate of 1/2 both are the same float32 sequence.  This fixes the
+    [hc][hh] stream layout, the 1/hc factor and sigmoid(0)."""
+    hc, hh, lr, M = 3, 64, 64, 4
+    rows = hc * hh
+    up = _tq_from(np.zeros((rows, lr)), np.zeros((rows, lr // 32)), np.zeros((rows, lr // 32)), 8)
+    rng = np.random.default_rng(5)
+    xn = rng.standard_normal((M, hc, hh)).astype(np.float32)
+    lo = rng.standard_normal((M, lr)).astype(np.float32)
+    inv = np.float32(1.0) / np.float32(hc)
+    want = np.zeros((M, hh), np.float32)
+    for mi in range(M):
+        acc = np.zeros(hh, np.float32)
+        for s in range(hc):
+            acc = (acc + xn[mi, s] * np.float32(0.5)).astype(np.float32)
+        want[mi] = acc * inv
+    got_dec = O.hc_mix(up, 8, hc, lr, xn[:1], lo[:1], True)
+    got_bat = O.hc_mix(up, 8, hc, lr, xn, lo, False)
+    assert np.array_equal(got_dec.view(np.uint32), want[:1].view(np.uint32))
+    assert np.array_equal(got_bat.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 5, 8])
+def test_hc_mix_against_f64(bits):
+    """mixed = sum_s xn_s * sigmoid(W_up . silu(lo / hc)) / hc in f64 on the dequantised up
+    matrix: the only differences are the int8 quantisation of silu(lo / hc) (per 32, two-level at
+    decode with hiprec) and f32 rounding."""
+    hc, hh, lr, M = 4, 96, 128, 3
+    rows = hc * hh
+    rng = np.random.default_rng(6 + bits)
+    q = rng.integers(0, 1 << bits, (rows, lr))
+    d = rng.uniform(5e-3, 2e-2, (rows, lr // 32)).astype(np.float16)
+    mm = (-d.astype(np.float32) * rng.uniform(0, 1 << (bits - 1), (rows, lr // 32))).astype(np.float16)
+    up = _tq_from(q, d, mm, bits)
+    W = q * np.repeat(d.astype(np.float64), 32, axis=1) + np.repeat(mm.astype(np.float64), 32, axis=1)
+    xn = rng.standard_normal((M, hc, hh)).astype(np.float32)
+    lo = (rng.standard_normal((M, lr)) * 3).astype(np.float32)
+    lsil = (lo / hc) / (1 + np.exp(-(lo.astype(np.float64) / hc)))
+    g = 1 / (1 + np.exp(-(lsil @ W.T)))                      # [M][hc*hh]
+    want = (xn.astype(np.float64) * g.reshape(M, hc, hh)).sum(axis=1) / hc
+    scale = np.abs(want).max()
+    for decode, hiprec, tol in ((True, True, 5e-5), (True, False, 3e-3), (False, False, 3e-3)):
+        got = O.hc_mix(up, bits, hc, lr, xn[:1] if decode else xn, lo[:1] if decode else lo, decode, hiprec)
+        err = np.abs(got - want[:got.shape[0]]).max()
+        assert err <= tol * scale, (decode, hiprec, err, scale)

@@ -445,6 +445,26 @@ extern "C" int trk_moe_forward(trk_ctx* c, const trk_moe_w* w, const float* x, c
     return forward(c, w, x, rlog, m, out, 0, (hipStream_t)stream);
 }
 
+extern "C" int trk_moe_forward_hc(trk_ctx* c, const trk_moe_w* w, const trk_hc_w* hc, const float* xn, const float* lo,
+                                  uint32_t m, float* out, void* stream) {
+    if (!c || !hc || !xn || !lo || !out) return fail(TRK_E_INVALID, "null argument");
+    if (hc->hc == 0 || hc->hc > 8) return fail(TRK_E_INVALID, "hc (%u) must be in 1..8", hc->hc);
+    if (hc->lr == 0 || hc->lr % 32 || hc->lr > 1024) return fail(TRK_E_INVALID, "lr (%u): a multiple of 32 up to 1024", hc->lr);
+    if (!fmt_is_tq(hc->up.fmt) || tq_kb(hc->up.fmt) != 32)
+        return fail(TRK_E_INVALID, "up: a kb-32 TQ codec (the low-rank row is quantised per 32)");
+    if (m == 0) return TRK_OK;
+    if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
+    const uint32_t H = c->cfg.hidden;
+    Mat up;
+    int rc = make_mat(hc->up, hc->hc * H, hc->lr, false, 1, "hc up", up);
+    if (rc) return rc;
+    Mats M;
+    if ((rc = check_weights(c, w, M))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    HIP_TRY(launch_hc_mix(up, hc->hc, H, hc->lr, xn, lo, m, c->cfg.hiprec, c->ws.xn, st));
+    return forward(c, w, c->ws.xn, nullptr, m, out, 0, st);
+}
+
 // ---- the layer without a context and without allocating ------------------------------------
 //
 // The workspace lives in one file-scope device array, `scratch`, of TRK_NOALLOC_SCRATCH_BYTES; every
@@ -643,6 +663,7 @@ extern "C" int trk_debug_read(trk_ctx* c, int which, void* host, size_t bytes, v
     case TRK_WS_ACTS: src = ws.acts; cap = ws.act_rows * (ws.F / 16) * 4; break;
     case TRK_WS_BARRIER_ERR: src = ws.counters + 2; cap = 4; break;
     case TRK_WS_SHLOGIT: src = ws.shl; cap = M * 4; break;
+    case TRK_WS_MIXED: src = ws.xn; cap = M * ws.H * 4; break;
     default: return fail(TRK_E_INVALID, "unknown workspace buffer %d", which);
     }
     if (bytes > cap) return fail(TRK_E_INVALID, "read of %zu bytes above the buffer's %zu", bytes, cap);

@@ -153,6 +153,9 @@ hipError_t launch_tq_act(const Workspace& ws, const float* h, uint32_t m, uint32
 hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                           hipStream_t st);
 hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st);
+// the hyper-connection mix part B (k_tq.hip): mixed [m][hh] from xn [m][hc][hh] and lo [m][lr]
+hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, const float* xn, const float* lo,
+                         uint32_t m, int pair, float* mixed, hipStream_t st);
 hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
                           hipStream_t st);

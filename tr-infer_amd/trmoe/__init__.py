@@ -22,7 +22,7 @@ TQ_FMTS = (FMT_TQ4_16, FMT_TQ4_32, FMT_TQ5_16, FMT_TQ5_32, FMT_TQ8_16, FMT_TQ8_3
 BASIS_ALL, BASIS_TOP = 0, 1
 K_MAX = 32
 (WS_RLOG, WS_IDS, WS_W, WS_NSEL, WS_ENT_TOK, WS_ENT_W, WS_ENT_EXP, WS_GRP_START, WS_GRP_EXP, WS_NGROUPS, WS_XQ,
- WS_XS, WS_ACTQ, WS_ACTS, WS_SHLOGIT, WS_BARRIER_ERR) = range(1, 17)
+ WS_XS, WS_ACTQ, WS_ACTS, WS_SHLOGIT, WS_BARRIER_ERR, WS_MIXED) = range(1, 18)
 
 
 class TrkError(RuntimeError):
@@ -32,6 +32,11 @@ class TrkError(RuntimeError):
 class Mat(C.Structure):
     _fields_ = [("ptr", C.c_void_p), ("rows", C.c_uint32), ("k", C.c_uint32), ("fmt", C.c_uint32),
                 ("count", C.c_uint32), ("stride", C.c_uint64)]
+
+
+class HcW(C.Structure):
+    """trk_hc_w: the hyper-connection up projection [hc * hidden][lr] (a kb-32 TQ codec)."""
+    _fields_ = [("up", Mat), ("hc", C.c_uint32), ("lr", C.c_uint32)]
 
 
 class MoeW(C.Structure):
@@ -70,6 +75,7 @@ def lib() -> C.CDLL:
         L.trk_set_moe.argtypes = [vp, C.POINTER(Policy)]
         L.trk_moe_forward.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, vp]
         L.trk_moe_residual.argtypes = [vp, C.POINTER(MoeW), vp, f, vp, u32, vp]
+        L.trk_moe_forward_hc.argtypes = [vp, C.POINTER(MoeW), C.POINTER(HcW), vp, vp, u32, vp, vp]
         L.trk_moe_forward_noalloc.argtypes = [C.POINTER(Cfg), C.POINTER(Policy), C.POINTER(MoeW), vp, vp, u32, vp,
                                               vp]
         L.trk_get_stats.argtypes = [vp, C.POINTER(Stats), i, vp]
@@ -166,6 +172,14 @@ class Context:
     def forward(self, w: "LayerWeights", x, out, rlog=None, stream=None):
         check(lib().trk_moe_forward(self.h, C.byref(w.moew), _ptr(x), _ptr(rlog), x.shape[0], _ptr(out),
                                     _stream(stream)))
+
+    def forward_hc(self, w: "LayerWeights", up, hc, lr, xn, lo, out, stream=None):
+        """trk_moe_forward_hc: out = MoE(the hyper-connection mix of xn [M][hc][H] and lo [M][lr]);
+        up: a uint8 tensor holding the TQ matrix [hc * H][lr] in `up_fmt` = (bits << 8) | 32."""
+        upt, fmt = up
+        hw = HcW(Mat(upt.data_ptr(), hc * w.H, lr, fmt, 1, matrix_bytes(fmt, hc * w.H, lr)), hc, lr)
+        check(lib().trk_moe_forward_hc(self.h, C.byref(w.moew), C.byref(hw), _ptr(xn), _ptr(lo), lo.shape[0],
+                                       _ptr(out), _stream(stream)))
 
     def launch_kernel(self, name: str, w: "LayerWeights", x, out, rlog=None, stream=None):
         """Launch one kernel of the forward sequence (timing in isolation; see trk_launch_kernel)."""
