@@ -29,15 +29,95 @@ struct TqArgs {
 
 constexpr uint32_t TQ_R = 16;  // rows per workgroup: one strip
 
+// gv_terms_tq with a runtime slice length S (dl [NA][S][16], dm [S][16], xq [NA][S * KB], xs [NA][S])
 template <int GK, int KB, int NA>
-__global__ __launch_bounds__(256) void tq_layer_kernel(TqArgs g) {
-    constexpr uint32_t R = TQ_R, S = (NA <= 2 ? 2048 : 1024) / R;
-    constexpr uint32_t UW = sizeof(GvTQ<GK, KB>) / 4, UB = UW * 8 <= 48 ? 8 : (48 / UW > 2 ? 48 / UW : 2);
+__device__ __forceinline__ void gv_terms_tq_rt(const GvTQ<GK, KB>& w, uint32_t l, uint32_t j, uint32_t na,
+                                               const int8_t* xq, const float4* xs, float* dl, float2* dm, uint32_t S) {
+    using T = GvTQ<GK, KB>;
+    const uint32_t cl = l / 4, rq = l % 4;
+    uint32_t lo[T::CPL][4], hi[T::CPL][4];
+#pragma unroll
+    for (uint32_t t = 0; t < T::CPL; t++) {
+        const uint32_t qw[4] = {w.q[t].x, w.q[t].y, w.q[t].z, w.q[t].w};
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            if constexpr (T::BITS == 8) {
+                lo[t][rr] = qw[rr] ^ 0x80808080u;  // q - 128
+                hi[t][rr] = 0;
+            } else {
+                lo[t][rr] = qw[rr] & 0x0f0f0f0fu;
+                hi[t][rr] = (qw[rr] >> 4) & 0x0f0f0f0fu;
+                if constexpr (T::BITS == 5) {
+                    const uint32_t r = 4 * rq + rr;
+                    const uint32_t pl = r < 8 ? w.p[t].x : w.p[t].y, ph = r < 8 ? w.p[t].z : w.p[t].w;
+                    lo[t][rr] |= q5_hi4((pl >> (4 * (r % 8))) & 0xfu);
+                    hi[t][rr] |= q5_hi4((ph >> (4 * (r % 8))) & 0xfu);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t a = 0; a < NA; a++) {
+        if (a >= na) break;
+        const int* x = reinterpret_cast<const int*>(xq + (size_t)a * S * KB + (size_t)j * KB);
+        int dot[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t t = 0; t < T::CPL; t++) {
+            const uint32_t c = cl + 4 * t;
+            if (T::NCH % 4 == 0 || c < T::NCH) {
+                const int xl = x[c];
+                const int xh = T::BITS == 8 ? 0 : x[T::NCH + c];
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++) {
+                    dot[rr] = sdot4((int)lo[t][rr], xl, dot[rr]);
+                    if constexpr (T::BITS != 8) dot[rr] = sdot4((int)hi[t][rr], xh, dot[rr]);
+                }
+            }
+        }
+        const int corr = T::BITS == 8 ? 128 * __float_as_int(xs[(size_t)a * S + j].z) : 0;
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const int v = dpp_ror8_add(dpp_ror4_add(dot[rr]));
+            if (cl == 0) dl[((size_t)a * S + j) * TQ_R + 4 * rq + rr] = (float)(v + corr);
+        }
+    }
+    if (cl == 0) {
+        const uint16_t dv[4] = {(uint16_t)(w.d.x & 0xffff), (uint16_t)(w.d.x >> 16), (uint16_t)(w.d.y & 0xffff),
+                                (uint16_t)(w.d.y >> 16)};
+        const uint16_t mv[4] = {(uint16_t)(w.m.x & 0xffff), (uint16_t)(w.m.x >> 16), (uint16_t)(w.m.y & 0xffff),
+                                (uint16_t)(w.m.y >> 16)};
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) dm[(size_t)j * TQ_R + 4 * rq + rr] = make_float2(h2f(dv[rr]), h2f(mv[rr]));
+    }
+}
+
+// LDS of a workgroup with K slices of S blocks: staged activations, their (scale, u, byte sum),
+// the block dots and the blocks' (d, m)
+template <int KB, int NA>
+constexpr size_t tq_lds_bytes(uint32_t S) {
+    return (size_t)NA * S * KB + (size_t)NA * S * 16 + (size_t)NA * S * TQ_R * 4 + (size_t)S * TQ_R * 8;
+}
+
+// S: blocks per K slice (a multiple of 8, set by the launch from K so that the LDS, and with it
+// the workgroups a CU holds, follows the shape)
+template <int GK, int KB, int NA>
+__global__ __launch_bounds__(256, 4) void tq_layer_kernel(TqArgs g, uint32_t S) {
+    constexpr uint32_t R = TQ_R;
+    // units whose loads a thread issues together: about 48 registers of weights (q chunks, the
+    // 5-bit plane, d and m)
+    using TW = GvTQ<GK, KB>;
+    constexpr uint32_t UW = 4 * TW::CPL + (TW::BITS == 5 ? 4 * TW::CPL : 0) + 4;
+    constexpr uint32_t UB = UW * 8 <= 32 ? 8 : (32 / UW > 2 ? 32 / UW : 2);
     constexpr bool XSUM = GK == GK_TQ8;
-    __shared__ __align__(16) int8_t xq[NA][S * KB];
-    __shared__ __align__(16) float4 xs[NA][S];
-    __shared__ float dl[NA][S][R];
-    __shared__ float2 dm[S][R];
+    extern __shared__ __align__(16) uint8_t tq_smem[];
+    int8_t* xq_ = reinterpret_cast<int8_t*>(tq_smem);                             // [NA][S * KB]
+    float4* xs_ = reinterpret_cast<float4*>(tq_smem + (size_t)NA * S * KB);       // [NA][S]
+    float* dl_ = reinterpret_cast<float*>(xs_ + (size_t)NA * S);                  // [NA][S][R]
+    float2* dm_ = reinterpret_cast<float2*>(dl_ + (size_t)NA * S * R);            // [S][R]
+    auto XQ = [&](uint32_t a, uint32_t o) -> int8_t* { return xq_ + (size_t)a * S * KB + o; };
+    auto XS = [&](uint32_t a, uint32_t j) -> float4& { return xs_[(size_t)a * S + j]; };
+    auto DL = [&](uint32_t a, uint32_t j, uint32_t r) -> float& { return dl_[((size_t)a * S + j) * R + r]; };
+    auto DM = [&](uint32_t j, uint32_t r) -> float2& { return dm_[(size_t)j * R + r]; };
     __shared__ uint32_t prow[2 * BR];  // physical activation rows of the unit
     __shared__ uint32_t orow[BR];      // output row of each logical row
     const Workspace& ws = g.ws;
@@ -117,7 +197,7 @@ __global__ __launch_bounds__(256) void tq_layer_kernel(TqArgs g) {
                 const uint32_t a = i / pr, o = (i % pr) * 16;
                 int4 v = make_int4(0, 0, 0, 0);
                 if (a < na) v = *reinterpret_cast<const int4*>(q + (size_t)prow[p0 + a] * K + (size_t)b0 * KB + o);
-                *reinterpret_cast<int4*>(&xq[a][o]) = v;
+                *reinterpret_cast<int4*>(XQ(a, o)) = v;
             }
             for (uint32_t i = tid; i < NA * S; i += 256) {
                 const uint32_t a = i / S, j = i % S;
@@ -139,7 +219,7 @@ __global__ __launch_bounds__(256) void tq_layer_kernel(TqArgs g) {
                         }
                     }
                 }
-                xs[a][j] = make_float4(sx, u, __int_as_float(xsum), 0.0f);
+                XS(a, j) = make_float4(sx, u, __int_as_float(xsum), 0.0f);
             }
             __syncthreads();
             const uint32_t n = n_items(sn);
@@ -147,46 +227,46 @@ __global__ __launch_bounds__(256) void tq_layer_kernel(TqArgs g) {
                 if (k0) load_batch(b0, sn, k0);
 #pragma unroll
                 for (uint32_t i = 0; i < UB; i++)
-                    if (k0 + i < n) gv_terms_tq<GK, KB, NA, R, S>(w[i], l, gi + 16 * (k0 + i), 0, na, xq, xs, dl, dm);
+                    if (k0 + i < n) gv_terms_tq_rt<GK, KB, NA>(w[i], l, gi + 16 * (k0 + i), na, XQ(0, 0), xs_, dl_, dm_, S);
             }
             const uint32_t b1 = b0 + sn, sn1 = nb - b1 < S ? nb - b1 : S;
             if (b1 < nb) load_batch(b1, sn1, 0);
             __syncthreads();
             if (ca < na) {
                 uint32_t j = 0;
-                for (; j + 8 <= sn; j += 8) {
-                    float2 tt[8];
-                    float4 x[8];
-                    float d[8];
+                for (; j + 4 <= sn; j += 4) {
+                    float2 tt[4];
+                    float4 x[4];
+                    float d[4];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        tt[i] = dm[j + i][cr];
-                        x[i] = xs[ca][j + i];
-                        d[i] = dl[ca][j + i][cr];
+                    for (int i = 0; i < 4; i++) {
+                        tt[i] = DM(j + i, cr);
+                        x[i] = XS(ca, j + i);
+                        d[i] = DL(ca, j + i, cr);
                     }
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
+                    for (int i = 0; i < 4; i++) {
                         acc = __builtin_fmaf(tt[i].y, x[i].y, acc);
                         acc = __builtin_fmaf(d[i], tt[i].x * x[i].x, acc);
                     }
                 }
                 for (; j < sn; j++) {
-                    const float2 tt = dm[j][cr];
-                    const float4 x = xs[ca][j];
+                    const float2 tt = DM(j, cr);
+                    const float4 x = XS(ca, j);
                     acc = __builtin_fmaf(tt.y, x.y, acc);
-                    acc = __builtin_fmaf(dl[ca][j][cr], tt.x * x.x, acc);
+                    acc = __builtin_fmaf(DL(ca, j, cr), tt.x * x.x, acc);
                 }
             }
             b0 = b1;
             sn = sn1;
         }
         __syncthreads();
-        if (ca < na) dl[ca][0][cr] = acc;
+        if (ca < na) DL(ca, 0, cr) = acc;
         __syncthreads();
         if (tid < R)
             for (uint32_t i = 0; i < na / P; i++) {
                 // two-level rows: coarse + residual (gemv.rs:150-160)
-                const float v = P == 2 ? dl[2 * i][0][tid] + dl[2 * i + 1][0][tid] : dl[i][0][tid];
+                const float v = P == 2 ? DL(2 * i, 0, tid) + DL(2 * i + 1, 0, tid) : DL(i, 0, tid);
                 out[(size_t)orow[p0 / P + i] * opitch + t * 16 + tid] = v;
             }
     }
@@ -418,12 +498,16 @@ hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, c
     return hipGetLastError();
 }
 
+// the K slice: all of K up to 128 blocks (64 with four activation rows per pass), rounded up to 8
 template <int KB, int NA>
-static hipError_t tq_go(const TqArgs& a, uint32_t fmt, dim3 grid, hipStream_t st) {
+static hipError_t tq_go(const TqArgs& a, uint32_t fmt, uint32_t K, dim3 grid, hipStream_t st) {
+    const uint32_t nb = K / KB, smax = NA <= 2 ? 128 : 64;
+    const uint32_t S = nb < smax ? (nb + 7) / 8 * 8 : smax;
+    const size_t lds = tq_lds_bytes<KB, NA>(S);
     switch (tq_bits(fmt)) {
-        case 4: tq_layer_kernel<GK_TQ4, KB, NA><<<grid, 256, 0, st>>>(a); break;
-        case 5: tq_layer_kernel<GK_TQ5, KB, NA><<<grid, 256, 0, st>>>(a); break;
-        case 8: tq_layer_kernel<GK_TQ8, KB, NA><<<grid, 256, 0, st>>>(a); break;
+        case 4: tq_layer_kernel<GK_TQ4, KB, NA><<<grid, 256, lds, st>>>(a, S); break;
+        case 5: tq_layer_kernel<GK_TQ5, KB, NA><<<grid, 256, lds, st>>>(a, S); break;
+        case 8: tq_layer_kernel<GK_TQ8, KB, NA><<<grid, 256, lds, st>>>(a, S); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -434,7 +518,7 @@ hipError_t launch_tq_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, 
     if (tq_kb(gate.fmt) != 32) return hipErrorInvalidValue;
     const TqArgs a{gate, up, sh_gate, sh_up, ws, h, m == 1 ? TQ_DEC_GU : TQ_BAT_GU, pair};
     const dim3 grid(2 * ws.F / 16, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
-    return m == 1 ? tq_go<32, 2>(a, gate.fmt, grid, st) : tq_go<32, 4>(a, gate.fmt, grid, st);
+    return m == 1 ? tq_go<32, 2>(a, gate.fmt, ws.H, grid, st) : tq_go<32, 4>(a, gate.fmt, ws.H, grid, st);
 }
 
 hipError_t launch_tq_act(const Workspace& ws, const float* h, uint32_t m, uint32_t kcap, int pair, hipStream_t st) {
@@ -449,7 +533,7 @@ hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& 
     if (tq_kb(down.fmt) != 16) return hipErrorInvalidValue;
     const TqArgs a{down, down, sh_down, sh_down, ws, nullptr, m == 1 ? TQ_DEC_DN : TQ_BAT_DN, pair};
     const dim3 grid(ws.H / 16, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
-    return m == 1 ? tq_go<16, 2>(a, down.fmt, grid, st) : tq_go<16, 4>(a, down.fmt, grid, st);
+    return m == 1 ? tq_go<16, 2>(a, down.fmt, ws.F, grid, st) : tq_go<16, 4>(a, down.fmt, ws.F, grid, st);
 }
 
 hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st) {

@@ -20,7 +20,7 @@ struct GvTQ {
     static constexpr uint32_t CPL = (NCH + 3) / 4;                 // chunks per lane
     static constexpr uint32_t BB = 64 + (BITS == 8 ? 16 * KB : 8 * KB) + (BITS == 5 ? 2 * KB : 0);
     uint4 q[CPL];
-    uint4 p[BITS == 5 ? CPL : 1];
+    uint4 p[BITS == 5 ? CPL : 0];  // the 5-bit plane's chunks (none for 4- and 8-bit codecs)
     uint2 d, m;
 };
 
