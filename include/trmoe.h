@@ -249,6 +249,11 @@ int trk_set_fusion(trk_ctx *ctx, int on);
  * counterpart in the reference, which runs one grouped kernel per expert matrix. */
 int trk_set_stream_rows(trk_ctx *ctx, int rows);
 
+/* Layers on TQ experts: the int8 MFMA kernels (on, the default, where H / 32 units of staged
+ * activations fit a workgroup's LDS) or the generic grouped TQ GEMV (off).  Both give the same
+ * bits; no counterpart in the reference. */
+int trk_set_tq_mfma(trk_ctx *ctx, int on);
+
 /* Per-kernel timing (the HIP counterpart of the reference's TR_PROFILE laps, exec.rs:344-430):
  * when on, every kernel a forward launches is bracketed by HIP events on the call's stream. */
 int trk_set_timing(trk_ctx *ctx, int on);

@@ -116,3 +116,26 @@ def test_tq_weights_rejected_when_mixed():
                                      C.c_void_p(out.data_ptr()), None)
     assert rc == -1 and b"formats" in trmoe.lib().trk_last_error()
     ctx.close()
+
+
+@pytest.mark.parametrize("key,kw,M,k,hiprec", [("real", REAL, 1, 8, True), ("real", REAL, 1, 8, False),
+                                               ("real", REAL, 16, 8, True), ("real", REAL, 64, 8, True),
+                                               ("c88", dict(seed=46, H=512, E=16, F=80, gate_bits=8, down_bits=8), 40, 4, True),
+                                               ("c54", dict(seed=39, H=512, E=16, F=80, gate_bits=5, down_bits=4), 1, 4, True),
+                                               ("c48", dict(seed=42, H=512, E=16, F=80, gate_bits=4, down_bits=8), 9, 4, True)])
+def test_tq_mfma_matches_generic(key, kw, M, k, hiprec):
+    """The int8 MFMA kernels (a TQ block per MFMA, SwiGLU in the gate/up launch) and the generic
+    grouped TQ GEMV give the same bits."""
+    say(f"tq mfma vs generic {key} M={M}")
+    import torch
+    L, orc, W = tq_layer(key, **kw)
+    x = dev(L.x(M, tid=300 + M))
+    outs = []
+    for mfma in (True, False):
+        ctx = trmoe.Context(L.H, L.E, L.F, k, max(M, 16), hiprec=hiprec)
+        ctx.set_tq_mfma(mfma)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, x, out)
+        outs.append(host(out).copy())
+        ctx.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), np.abs(outs[0] - outs[1]).max()

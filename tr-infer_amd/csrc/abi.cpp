@@ -80,6 +80,7 @@ struct trk_ctx {
     std::vector<hipEvent_t> spare;
     int fusion = 0;   // decode: one launch per layer (when the shape and the GPU allow it) if set
     int stream_rows = -1;  // batch: items of at most this many rows on the streaming GEMV (-1: automatic)
+    int tq_mfma = 1;       // TQ layers: the MFMA kernels where the shape fits (0: the generic TQ GEMV)
     int profile = 0;       // MoeStats::profile: add every routed row's mass profile to ws.prof
 };
 
@@ -368,9 +369,15 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
             TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
             TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         }
-        TIMED(K_TQ_GATEUP, launch_tq_gateup(M.gate, M.up, M.shg, M.shu, ws, ws.hgu, m, kcap, pair, st));
-        TIMED(K_TQ_ACT, launch_tq_act(ws, ws.hgu, m, kcap, pair, st));
-        TIMED(K_TQ_DOWN, launch_tq_down(M.down, M.shd, ws, m, kcap, pair, st));
+        if (c->tq_mfma && tqm_fits(H, ws.F)) {
+            // int8 MFMA per TQ block, SwiGLU + quantisation + fold in the gate/up launch
+            TIMED(K_TQ_GATEUP, launch_tqm_gateup(M.gate, M.up, M.shg, M.shu, ws, m, kcap, pair, st));
+            TIMED(K_TQ_DOWN, launch_tqm_down(M.down, M.shd, ws, m, kcap, pair, st));
+        } else {
+            TIMED(K_TQ_GATEUP, launch_tq_gateup(M.gate, M.up, M.shg, M.shu, ws, ws.hgu, m, kcap, pair, st));
+            TIMED(K_TQ_ACT, launch_tq_act(ws, ws.hgu, m, kcap, pair, st));
+            TIMED(K_TQ_DOWN, launch_tq_down(M.down, M.shd, ws, m, kcap, pair, st));
+        }
         if (m == 1)
             TIMED(K_TQ_COMBINE, launch_tq_combine(ws, out, residual, st));
         else
@@ -597,6 +604,12 @@ extern "C" int trk_profile_report(trk_ctx* c, double* cum, uint64_t* rows, void*
 extern "C" int trk_set_fusion(trk_ctx* c, int on) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     c->fusion = on ? 1 : 0;
+    return TRK_OK;
+}
+
+extern "C" int trk_set_tq_mfma(trk_ctx* c, int on) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    c->tq_mfma = on ? 1 : 0;
     return TRK_OK;
 }
 

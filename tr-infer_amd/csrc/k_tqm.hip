@@ -1,0 +1,421 @@
+// The MoE layer's expert products on the reference's packed TQ strips (codec.rs:1-46) with int8
+// MFMA.  A TQ block is 16 weight rows x kb values, the shape of a v_mfma_i32_16x16x32_i8 operand:
+// B[k 8g .. 8g+7][col r] for lane (g = l / 16, r = l % 16) is two 4-byte words of row r (chunks
+// 2 (g % 2) and 2 (g % 2) + 1 at kb 32, low or high nibbles by g / 2), and A[row][k ..] holds up
+// to 16 activation rows (a decode slot's one or two levels, or a batch item's entries).  One MFMA
+// per block gives every (activation row, weight row) dot exactly; a kb-16 block pair shares one
+// MFMA shape with the other block's activation lanes zeroed, so each 16-block's dot stays its own.
+// Lane l then holds D[activation row 4 g + v][weight row r] and runs the reference's per-block
+// f32 chain (gemv.rs:141-148) on its four outputs in block order.
+//
+//   tqm_gateup_kernel  a wave per (matrix, strip): waves 2 i and 2 i + 1 are the gate and up
+//                      strips of strip pair i; then SwiGLU (elem.rs:173), the per-16 quantisation
+//                      of the strip (two levels for a decode slot with TR_HIPREC, quant.rs:96-108)
+//                      and the routing-weight fold (exec.rs:1584-1606, exec_batch.rs:1528-1536)
+//   tqm_down_kernel    a wave per strip of H, the unit's down rows into yent
+#include "tq.hpp"
+
+namespace trk {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i tqm_mfma(long a, long b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+// B operand of lane (g, r) for the 32-wide unit at block b of a strip (kb 32: block b; kb 16:
+// blocks 2b and 2b + 1, lanes g < 2 the first), plus the d / m of row r for the unit's block(s).
+// The loads keep the raw words (no arithmetic on them), so a batch of units' loads stays in
+// flight; tqm_operand decodes them when the unit is used.
+template <int GK, int KB>
+struct TqmB {
+    static constexpr uint32_t NBL = KB == 16 ? 2 : 1;
+    static constexpr uint32_t P5 = GvTQ<GK, KB>::BITS == 5 ? 1 : 0;
+    static constexpr uint32_t REGS = 2 + 2 * P5 + 2 * NBL;  // VGPRs a unit holds
+    uint32_t w0, w1;
+    uint32_t p0[P5], p1[P5];
+    uint32_t d[NBL], m[NBL];  // f16 bits, zero-extended by the loads (no packing, no wait)
+};
+
+template <int GK, int KB>
+__device__ __forceinline__ void tqm_load(TqmB<GK, KB>& w, const uint8_t* __restrict__ strip, uint32_t b, uint32_t l) {
+    using T = GvTQ<GK, KB>;
+    const uint32_t g = l / 16, r = l % 16;
+    auto ld32 = [](const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); };
+    auto ld16 = [](const uint8_t* p) { return (uint32_t)*reinterpret_cast<const uint16_t*>(p); };
+    if constexpr (KB == 32) {
+        const uint8_t* blk = strip + (size_t)b * T::BB;
+        // 8-bit: chunks 2g, 2g + 1 (k = 8g ..); 4/5-bit: chunks 2 (g % 2), +1 (nibble g / 2)
+        const uint32_t c0 = T::BITS == 8 ? 2 * g : 2 * (g % 2);
+        w.w0 = ld32(blk + 64 + 64 * c0 + 4 * r);
+        w.w1 = ld32(blk + 64 + 64 * c0 + 64 + 4 * r);
+        if constexpr (T::BITS == 5) {  // plane of chunk c: 8 bytes (low nibbles) then 8 (high)
+            const uint8_t* pl = blk + 64 + 256 + 8 * (g / 2) + 4 * (r / 8);
+            w.p0[0] = ld32(pl + 16 * c0);
+            w.p1[0] = ld32(pl + 16 * (c0 + 1));
+        }
+        w.d[0] = ld16(blk + 2 * r);
+        w.m[0] = ld16(blk + 32 + 2 * r);
+    } else {
+        // kb 16: lanes g < 2 take block 2b, g >= 2 block 2b + 1; within a block k 8 (g % 2) ..
+        const uint8_t* blk = strip + (size_t)(2 * b + g / 2) * T::BB;
+        const uint32_t gg = g % 2;
+        if constexpr (T::BITS == 8) {  // 4 chunks: k = 4c ..; chunks 2gg, 2gg + 1
+            w.w0 = ld32(blk + 64 + 128 * gg + 4 * r);
+            w.w1 = ld32(blk + 64 + 128 * gg + 64 + 4 * r);
+        } else {  // 2 chunks: low nibbles k = 4c .., high k = 8 + 4c ..; nibble gg
+            w.w0 = ld32(blk + 64 + 4 * r);
+            w.w1 = ld32(blk + 128 + 4 * r);
+            if constexpr (T::BITS == 5) {
+                const uint8_t* pl = blk + 64 + 128 + 8 * gg + 4 * (r / 8);
+                w.p0[0] = ld32(pl);
+                w.p1[0] = ld32(pl + 16);
+            }
+        }
+        const uint8_t* b0 = strip + (size_t)(2 * b) * T::BB;
+        w.d[0] = ld16(b0 + 2 * r);
+        w.m[0] = ld16(b0 + 32 + 2 * r);
+        w.d[1] = ld16(b0 + T::BB + 2 * r);
+        w.m[1] = ld16(b0 + T::BB + 32 + 2 * r);
+    }
+}
+
+// The 8 int8 B values of lane (g, r) from the raw words.
+template <int GK, int KB>
+__device__ __forceinline__ long tqm_operand(const TqmB<GK, KB>& w, uint32_t l) {
+    using T = GvTQ<GK, KB>;
+    const uint32_t g = l / 16, r = l % 16;
+    uint32_t w0, w1;
+    if constexpr (T::BITS == 8) {  // stored q + 128 unsigned
+        w0 = w.w0 ^ 0x80808080u;
+        w1 = w.w1 ^ 0x80808080u;
+    } else {
+        const uint32_t h = KB == 32 ? g / 2 : g % 2;  // the nibble
+        w0 = (w.w0 >> (4 * h)) & 0x0f0f0f0fu;
+        w1 = (w.w1 >> (4 * h)) & 0x0f0f0f0fu;
+        if constexpr (T::BITS == 5) {
+            w0 |= q5_hi4((w.p0[0] >> (4 * (r % 8))) & 0xfu);
+            w1 |= q5_hi4((w.p1[0] >> (4 * (r % 8))) & 0xfu);
+        }
+    }
+    return (long)(((unsigned long long)w1 << 32) | w0);
+}
+
+// The activation rows of a work unit: a decode slot's one or two levels (x at gate/up, the slot's
+// SwiGLU rows at down) or a batch item's entry rows, staged in LDS once per workgroup in operand
+// order with their per-block (scale, u, byte sum).
+struct TqmArgs {
+    Mat a, b, sha, shb;  // gate/up: gate, up, shared gate, shared up; down: down, -, shared down, -
+    Workspace ws;
+    int decode, pair;
+};
+
+constexpr uint32_t TQM_RA = 16;   // activation rows of a unit at most (an item; a decode slot uses 1 or 2)
+constexpr uint32_t TQM_COLS = 4;  // batch: workgroups per item, each over a share of the strips
+
+// The unit of workgroup row y: returns false when there is none.  prow: physical activation rows;
+// orow: output row of each logical row; nr logical rows, P physical per logical.
+__device__ __forceinline__ bool tqm_unit(const Workspace& ws, bool gu, int decode, int pair, uint32_t y, bool& shared,
+                                         uint32_t& e, uint32_t& nr, uint32_t& P, uint32_t* prow, uint32_t* orow,
+                                         uint32_t tid) {
+    Item item{};
+    if (decode) {
+        const uint32_t ns = ws.n_sel[0];
+        if (y > ns) return false;
+        shared = y == ns;
+        e = shared ? 0u : ws.ids[y];
+        nr = 1;
+        P = pair ? 2u : 1u;
+    } else {
+        if (y >= ws.n_groups[2]) return false;
+        item = ws.items[y];
+        shared = item.expert == NO_EXPERT;
+        e = shared ? 0u : item.expert;
+        nr = item.nrows;
+        P = 1;
+    }
+    const uint32_t n_ent = ws.n_groups[1];
+    if (tid < nr * P) {
+        const uint32_t i = tid / P, lv = tid % P;
+        if (decode) {
+            prow[tid] = gu ? lv : 2 * y + lv;
+            if (lv == 0) orow[i] = y;
+        } else {
+            const uint32_t arow = shared ? n_ent + item.row0 + i : item.row0 + i;
+            prow[tid] = gu ? item_token(ws, item, shared, i) : arow;
+            orow[i] = arow;
+        }
+    }
+    return true;
+}
+
+// Stage the unit's activation rows (K bytes each, int8) in operand order As[unit b][lane] (8 bytes:
+// row l % 16, k 32b + 8 (l / 16) ..), zero for rows past np, and their per-block (scale, u, byte
+// sum) in Sc[block][row] (blocks of kbs values).
+template <int KBS, bool XSUM>
+__device__ __forceinline__ void tqm_stage(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                          const float* __restrict__ u, const uint32_t* prow, uint32_t np, uint32_t K,
+                                          long* As, float4* Sc, uint32_t tid, uint32_t nthr) {
+    const uint32_t nu = K / 32, nbs = K / KBS;
+    // rows past np are zero in the operand (LDS stores only)
+    if (np < 16)
+        for (uint32_t i = tid; i < nu * 64; i += nthr)
+            if (i % 16 >= np) As[i] = 0;
+    // the live rows: 8-byte pieces (unit b, k-group g, row), 8 loads in flight per thread before
+    // any is stored
+    const uint32_t n = nu * 4 * np;
+    for (uint32_t i0 = 0; i0 < n; i0 += 8 * nthr) {
+        long v[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + nthr * c, ic = i < n ? i : n - 1;
+            const uint32_t row = ic % np, bg = ic / np;  // bg = 4 b + g
+            v[c] = *reinterpret_cast<const long*>(q + (size_t)prow[row] * K + 8 * bg);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const uint32_t i = i0 + tid + nthr * c;
+            if (i < n) As[(i / np) * 16 + i % np] = v[c];  // As[b * 64 + g * 16 + row]
+        }
+    }
+    // (scale, u, byte sum) per (block, row): zero rows past np, 4 blocks in flight per thread
+    const uint32_t ns = nbs * 16;
+    for (uint32_t i0 = 0; i0 < ns; i0 += 4 * nthr) {
+        float4 v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = i0 + tid + nthr * c, ic = i < ns ? i : ns - 1;
+            const uint32_t b = ic / 16, row = ic % 16;
+            v[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (row < np) {
+                const size_t bi = (size_t)prow[row] * nbs + b;
+                int xs = 0;
+                if constexpr (XSUM) {  // 8-bit codecs: the block's byte sum corrects the q + 128 offset
+                    const int4* xp = reinterpret_cast<const int4*>(q + (size_t)prow[row] * K + (size_t)KBS * b);
+#pragma unroll
+                    for (int t = 0; t < KBS / 16; t++) {
+                        const int4 w = xp[t];
+                        xs = sdot4(w.x, 0x01010101, xs);
+                        xs = sdot4(w.y, 0x01010101, xs);
+                        xs = sdot4(w.z, 0x01010101, xs);
+                        xs = sdot4(w.w, 0x01010101, xs);
+                    }
+                }
+                v[c] = make_float4(s[bi], u[bi], __int_as_float(xs), 0.0f);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = i0 + tid + nthr * c;
+            if (i < ns) Sc[i] = v[c];
+        }
+    }
+}
+
+// The chain of one strip for lane l over all units: acc[v] for activation row 4 (l / 16) + v and
+// weight row l % 16.  Loads run UB units ahead.
+template <int GK, int KB>
+__device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uint32_t K, const long* As,
+                                          const float4* Sc, uint32_t l, float (&acc)[4]) {
+    // the walk over K is sequential per wave (the chain), so the loads run UB units ahead (about
+    // 64 VGPRs of raw words)
+    constexpr uint32_t UB = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
+    constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
+    const uint32_t nu = K / 32, g = l / 16;
+    for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    TqmB<GK, KB> w[UB];
+#pragma unroll
+    for (uint32_t i = 0; i < UB; i++)
+        if (i < nu) tqm_load<GK, KB>(w[i], strip, i, l);
+    for (uint32_t b0 = 0; b0 < nu; b0 += UB) {
+#pragma unroll
+        for (uint32_t i = 0; i < UB; i++) {
+            const uint32_t b = b0 + i;
+            if (b >= nu) break;
+            const TqmB<GK, KB> cw = w[i];
+            if (b + UB < nu) tqm_load<GK, KB>(w[i], strip, b + UB, l);  // the load UB units ahead
+            const long a = As[b * 64 + l];
+            const long bq = tqm_operand<GK, KB>(cw, l);
+            constexpr uint32_t NBL = TqmB<GK, KB>::NBL;  // blocks of the unit
+#pragma unroll
+            for (uint32_t hb = 0; hb < NBL; hb++) {
+                // kb 16: the activation lanes of the other block zeroed
+                const long am = KB == 16 ? ((g / 2 == hb) ? a : 0) : a;
+                const v4i d4 = tqm_mfma(am, bq);
+                const uint32_t blk = NBL * b + hb;
+                const float dd = h2f((uint16_t)cw.d[hb]), mm = h2f((uint16_t)cw.m[hb]);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const float4 sx = Sc[blk * 16 + 4 * g + v];
+                    const int dot = U8 ? d4[v] + 128 * __float_as_int(sx.z) : d4[v];
+                    acc[v] = __builtin_fmaf(mm, sx.y, acc[v]);
+                    acc[v] = __builtin_fmaf((float)dot, dd * sx.x, acc[v]);
+                }
+            }
+        }
+    }
+}
+
+// SwiGLU and the per-16 quantisation of one strip's rows: the 16 lanes of lane group gq hold one
+// activation row's 16 values (rows r of the strip); decode: levels 0 and 1 of the one logical
+// row in lane group 0 (two-level quantisation with pair); batch: rows 4 gq + i of the item.
+__device__ __forceinline__ void tqm_swiglu_store(const Workspace& ws, int decode, int pair, uint32_t P, uint32_t nr,
+                                                 const uint32_t* orow, uint32_t n_ent, uint32_t F, uint32_t nbf,
+                                                 uint32_t strip, uint32_t gq, uint32_t r, const float (&acc)[4],
+                                                 const float* hu) {
+    auto quant16 = [&](float x, float& s, int32_t& sum, int8_t& q, float& res) {
+        const float amax = row16_allreduce(__builtin_fabsf(x), [](float a, float b) { return mx_ps(a, b); });
+        s = amax / 127.0f;
+        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        const int32_t qi = cvt_rne(x * inv);
+        sum = row16_allreduce(qi, [](int32_t a, int32_t b) { return a + b; });
+        q = sat_i8(qi);
+        res = __builtin_fmaf(-(float)qi, s, x);
+    };
+    auto store = [&](uint32_t arow, int8_t q, float s, int32_t sum, float wgt) {
+        ws.actq[(size_t)arow * F + strip * 16 + r] = q;
+        if (r == 0) {
+            const float sf = s * wgt;
+            ws.acts[(size_t)arow * nbf + strip] = sf;
+            ws.actsum[(size_t)arow * nbf + strip] = sum;
+            ws.actu[(size_t)arow * nbf + strip] = sf * (float)sum;
+        }
+    };
+    if (decode) {
+        if (gq != 0) return;
+        const float hg = P == 2 ? acc[0] + acc[1] : acc[0], hv = P == 2 ? hu[0] + hu[1] : hu[0];
+        const float x = silu512(hg) * hv;
+        const uint32_t y = orow[0], ns = ws.n_sel[0];
+        const float wgt = y < ns ? ws.w[y] : sigmoid_libm(ws.shl[0]);
+        float s, res, s2, res2;
+        int32_t sum, sum2;
+        int8_t q, q2;
+        quant16(x, s, sum, q, res);
+        store(2 * y, q, s, sum, wgt);
+        if (pair) {
+            quant16(res, s2, sum2, q2, res2);
+            store(2 * y + 1, q2, s2, sum2, wgt);
+        }
+        return;
+    }
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = 4 * gq + i;
+        const float x = silu512(acc[i]) * hu[i];
+        float s, res;
+        int32_t sum;
+        int8_t q;
+        quant16(x, s, sum, q, res);
+        if (row < nr) {
+            const uint32_t arow = orow[row];
+            const float wgt = arow < n_ent ? ws.ent_w[arow] : sigmoid_libm(ws.shl[arow - n_ent]);
+            store(arow, q, s, sum, wgt);
+        }
+    }
+}
+
+// Grid (ceil(F / 16 / 2), units), 256 threads: waves 2i, 2i + 1 = gate and up of strip
+// 2 blockIdx.x + i.
+template <int GK>
+__global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t prow[2 * BR], orow[BR];
+    __shared__ float hu[2][64][4];  // up accumulators of the two strips, by lane
+    const Workspace& ws = g.ws;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
+    bool shared;
+    uint32_t e, nr, P;
+    if (!tqm_unit(ws, true, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid)) return;
+    long* As = reinterpret_cast<long*>(smem);                     // [H / 32][64]
+    float4* Sc = reinterpret_cast<float4*>(As + (size_t)(H / 32) * 64);  // [H / 32][16]
+    __syncthreads();
+    tqm_stage<32, GK == GK_TQ8>(ws.xq, ws.xs, ws.xu, prow, nr * P, H, As, Sc, tid, 256);
+    __syncthreads();
+    const uint32_t gq = l / 16, r = l % 16, n_ent = ws.n_groups[1];
+    const bool up = wv % 2 == 1;
+    // strip pairs blockIdx.x, + gridDim.x, ...: the staged activations serve them all
+    for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += gridDim.x) {
+        const uint32_t strip = 2 * sp + wv / 2;
+        const bool live = strip < F / 16;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) {
+            const Mat& M = up ? (shared ? g.shb : g.b) : (shared ? g.sha : g.a);
+            tqm_strip<GK, 32>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, H, As, Sc, l, acc);
+        }
+        if (up)
+            for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
+        __syncthreads();
+        if (!up && live) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
+                                          hu[wv / 2][l]);
+        __syncthreads();  // hu read before the next pair writes it
+    }
+}
+
+// Grid (H / 64, units), 256 threads: wave w takes strip 4 blockIdx.x + w of H.
+template <int GK>
+__global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t prow[2 * BR], orow[BR];
+    const Workspace& ws = g.ws;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F;
+    bool shared;
+    uint32_t e, nr, P;
+    if (!tqm_unit(ws, false, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid)) return;
+    long* As = reinterpret_cast<long*>(smem);                        // [F / 32][64]
+    float4* Sc = reinterpret_cast<float4*>(As + (size_t)(F / 32) * 64);  // [F / 16][16]
+    __syncthreads();
+    tqm_stage<16, GK == GK_TQ8>(ws.actq, ws.acts, ws.actu, prow, nr * P, F, As, Sc, tid, 256);
+    __syncthreads();
+    const Mat& M = shared ? g.sha : g.a;
+    const uint32_t gq = l / 16, r = l % 16;
+    // strip groups blockIdx.x, + gridDim.x, ...: the staged activations serve them all
+    for (uint32_t sg = blockIdx.x; 4 * sg < H / 16; sg += gridDim.x) {
+        const uint32_t strip = 4 * sg + wv;
+        float acc[4];
+        tqm_strip<GK, 16>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, F, As, Sc, l, acc);
+        if (g.decode) {
+            if (gq == 0) ws.yent[(size_t)orow[0] * H + strip * 16 + r] = P == 2 ? acc[0] + acc[1] : acc[0];
+            continue;
+        }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t row = 4 * gq + i;
+            if (row < nr) ws.yent[(size_t)orow[row] * H + strip * 16 + r] = acc[i];
+        }
+    }
+}
+
+hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
+                             uint32_t m, uint32_t kcap, int pair, hipStream_t st) {
+    if (tq_kb(gate.fmt) != 32 || ws.H % 32) return hipErrorInvalidValue;
+    const TqmArgs a{gate, up, sh_gate, sh_up, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0};
+    // decode: a workgroup per strip pair; batch: TQM_COLS workgroups per item, each looping over
+    // strip pairs with the item's activations staged once
+    const uint32_t pairs = (ws.F / 16 + 1) / 2;
+    const dim3 grid(m == 1 ? pairs : (pairs < TQM_COLS ? pairs : TQM_COLS), m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
+    const size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * 16;
+    switch (tq_bits(gate.fmt)) {
+        case 4: tqm_gateup_kernel<GK_TQ4><<<grid, 256, lds, st>>>(a); break;
+        case 5: tqm_gateup_kernel<GK_TQ5><<<grid, 256, lds, st>>>(a); break;
+        case 8: tqm_gateup_kernel<GK_TQ8><<<grid, 256, lds, st>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
+                           hipStream_t st) {
+    if (tq_kb(down.fmt) != 16 || ws.F % 32 || ws.H % 64) return hipErrorInvalidValue;
+    const TqmArgs a{down, down, sh_down, sh_down, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0};
+    // a workgroup per strip group (the activations of K = F are cheap to stage)
+    const dim3 grid(ws.H / 64, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
+    const size_t lds = (size_t)(ws.F / 32) * 64 * 8 + (size_t)(ws.F / 16) * 16 * 16;
+    switch (tq_bits(down.fmt)) {
+        case 4: tqm_down_kernel<GK_TQ4><<<grid, 256, lds, st>>>(a); break;
+        case 5: tqm_down_kernel<GK_TQ5><<<grid, 256, lds, st>>>(a); break;
+        case 8: tqm_down_kernel<GK_TQ8><<<grid, 256, lds, st>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace trk

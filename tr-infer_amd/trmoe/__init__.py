@@ -96,6 +96,7 @@ def lib() -> C.CDLL:
         L.trk_set_timing.argtypes = [vp, i]
         L.trk_set_fusion.argtypes = [vp, i]
         L.trk_set_stream_rows.argtypes = [vp, i]
+        L.trk_set_tq_mfma.argtypes = [vp, i]
         L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
         _lib = L
     return _lib
@@ -210,6 +211,10 @@ class Context:
 
     def set_fusion(self, on: bool):
         check(lib().trk_set_fusion(self.h, int(on)))
+
+    def set_tq_mfma(self, on: bool):
+        """TQ layers on the int8 MFMA kernels (True) or the generic grouped TQ GEMV (False)."""
+        check(lib().trk_set_tq_mfma(self.h, int(bool(on))))
 
     def set_stream_rows(self, rows: int):
         """Batch items of at most `rows` rows on the streaming GEMV (-1 automatic, 0 none)."""
