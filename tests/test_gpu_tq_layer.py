@@ -64,6 +64,9 @@ def run_case(L, orc, W, M, k, hiprec=True, policy=None, tid=0):
     ctx.forward(W, dev(x), out)
     got = host(out).copy()
     exact = routing_exact(ctx, r, M, policy[1] if policy else k, L, x) if not policy else False
+    # MoeStats: rows and selected experts, counted by whichever launch routed
+    nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+    assert ctx.stats() == (M, int(nsel.sum()))
     ctx.close()
     return got, want, exact
 

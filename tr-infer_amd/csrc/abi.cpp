@@ -358,8 +358,10 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H,
                                                  m == 1 ? 0 : gemm_order, ws.rlog, ws.shl, st, &xq, norm));
+        const bool mfma = c->tq_mfma && tqm_fits(H, ws.F);
         if (m == 1) {
-            TIMED(K_ROUTE, launch_route(lg, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
+            // the MFMA gate/up launch routes for itself
+            if (!mfma) TIMED(K_ROUTE, launch_route(lg, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
         } else if (m <= 4 && m * kcap <= 1024) {
             TIMED(K_DISPATCH, launch_dispatch_small(ws, m, kcap, lg, k, c->pol, st));
         } else if (m <= 16 && m * kcap <= 1024) {
@@ -369,9 +371,10 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
             TIMED(K_ROUTE, launch_route(lg, m, E, k, c->pol, ws.ids, ws.w, ws.n_sel, nullptr, st));
             TIMED(K_DISPATCH, launch_dispatch(ws, m, kcap, st));
         }
-        if (c->tq_mfma && tqm_fits(H, ws.F)) {
+        if (mfma) {
             // int8 MFMA per TQ block, SwiGLU + quantisation + fold in the gate/up launch
-            TIMED(K_TQ_GATEUP, launch_tqm_gateup(M.gate, M.up, M.shg, M.shu, ws, m, kcap, pair, st));
+            TIMED(K_TQ_GATEUP, launch_tqm_gateup(M.gate, M.up, M.shg, M.shu, ws, m, kcap, pair, m == 1 ? lg : nullptr, k,
+                                                 c->pol, st));
             TIMED(K_TQ_DOWN, launch_tqm_down(M.down, M.shd, ws, m, kcap, pair, st));
         } else {
             TIMED(K_TQ_GATEUP, launch_tq_gateup(M.gate, M.up, M.shg, M.shu, ws, ws.hgu, m, kcap, pair, st));

@@ -13,6 +13,7 @@
 //                      of the strip (two levels for a decode slot with TR_HIPREC, quant.rs:96-108)
 //                      and the routing-weight fold (exec.rs:1584-1606, exec_batch.rs:1528-1536)
 //   tqm_down_kernel    a wave per strip of H, the unit's down rows into yent
+#include "route.hpp"
 #include "tq.hpp"
 
 namespace trk {
@@ -109,6 +110,12 @@ struct TqmArgs {
     Mat a, b, sha, shb;  // gate/up: gate, up, shared gate, shared up; down: down, -, shared down, -
     Workspace ws;
     int decode, pair;
+    // decode gate/up with the routing inside (NJ > 0): every workgroup routes the logits row lg
+    // itself (route_topk / route_mass, router.rs:106-148) and workgroup (0, 0) publishes the ids,
+    // weights and count for the down and combine launches
+    const float* lg;
+    uint32_t k;
+    Policy pol;
 };
 
 constexpr uint32_t TQM_RA = 16;   // activation rows of a unit at most (an item; a decode slot uses 1 or 2)
@@ -118,13 +125,12 @@ constexpr uint32_t TQM_COLS = 4;  // batch: workgroups per item, each over a sha
 // orow: output row of each logical row; nr logical rows, P physical per logical.
 __device__ __forceinline__ bool tqm_unit(const Workspace& ws, bool gu, int decode, int pair, uint32_t y, bool& shared,
                                          uint32_t& e, uint32_t& nr, uint32_t& P, uint32_t* prow, uint32_t* orow,
-                                         uint32_t tid) {
+                                         uint32_t tid, uint32_t ns, const uint32_t* ids) {
     Item item{};
     if (decode) {
-        const uint32_t ns = ws.n_sel[0];
         if (y > ns) return false;
         shared = y == ns;
-        e = shared ? 0u : ws.ids[y];
+        e = shared ? 0u : ids[y];
         nr = 1;
         P = pair ? 2u : 1u;
     } else {
@@ -263,7 +269,7 @@ __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uin
 __device__ __forceinline__ void tqm_swiglu_store(const Workspace& ws, int decode, int pair, uint32_t P, uint32_t nr,
                                                  const uint32_t* orow, uint32_t n_ent, uint32_t F, uint32_t nbf,
                                                  uint32_t strip, uint32_t gq, uint32_t r, const float (&acc)[4],
-                                                 const float* hu) {
+                                                 const float* hu, uint32_t ns, const float* wsel) {
     auto quant16 = [&](float x, float& s, int32_t& sum, int8_t& q, float& res) {
         const float amax = row16_allreduce(__builtin_fabsf(x), [](float a, float b) { return mx_ps(a, b); });
         s = amax / 127.0f;
@@ -286,8 +292,8 @@ __device__ __forceinline__ void tqm_swiglu_store(const Workspace& ws, int decode
         if (gq != 0) return;
         const float hg = P == 2 ? acc[0] + acc[1] : acc[0], hv = P == 2 ? hu[0] + hu[1] : hu[0];
         const float x = silu512(hg) * hv;
-        const uint32_t y = orow[0], ns = ws.n_sel[0];
-        const float wgt = y < ns ? ws.w[y] : sigmoid_libm(ws.shl[0]);
+        const uint32_t y = orow[0];
+        const float wgt = y < ns ? wsel[y] : sigmoid_libm(ws.shl[0]);
         float s, res, s2, res2;
         int32_t sum, sum2;
         int8_t q, q2;
@@ -316,18 +322,53 @@ __device__ __forceinline__ void tqm_swiglu_store(const Workspace& ws, int decode
 
 // Grid (ceil(F / 16 / 2), units), 256 threads: waves 2i, 2i + 1 = gate and up of strip
 // 2 blockIdx.x + i.
-template <int GK>
+template <int GK, int NJ>
 __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t prow[2 * BR], orow[BR];
     __shared__ float hu[2][64][4];  // up accumulators of the two strips, by lane
     const Workspace& ws = g.ws;
     const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
-    bool shared;
-    uint32_t e, nr, P;
-    if (!tqm_unit(ws, true, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid)) return;
     long* As = reinterpret_cast<long*>(smem);                     // [H / 32][64]
     float4* Sc = reinterpret_cast<float4*>(As + (size_t)(H / 32) * 64);  // [H / 32][16]
+    uint32_t ns = 0;
+    const uint32_t* ids = ws.ids;
+    const float* wsel = ws.w;
+    if constexpr (NJ > 0) {
+        // the decode routing on wave 0 (the others wait at the barrier); MassBasis::All's
+        // exponentials in the LDS behind the staged activations
+        __shared__ uint2 cand[ROUTE_CAND];
+        __shared__ uint32_t r_ids[K_MAX];
+        __shared__ float r_w[K_MAX];
+        __shared__ uint32_t r_n;
+        float* ex = reinterpret_cast<float*>(Sc + (size_t)(H / 32) * 16);
+        if (wv == 0) {
+            const uint32_t n = route_row<NJ>(g.lg, ws.E, g.k, g.pol, l, cand, ex, r_ids, r_w);
+            if (l == 0) r_n = n;
+        }
+        __syncthreads();
+        ns = r_n;
+        ids = r_ids;
+        wsel = r_w;
+        if (blockIdx.x == 0 && blockIdx.y == 0) {  // for the down and combine launches, MoeStats
+            if (tid < ns) {
+                ws.ids[tid] = r_ids[tid];
+                ws.w[tid] = r_w[tid];
+            }
+            if (tid == 0) {
+                ws.n_sel[0] = ns;
+                if (ws.stats) {
+                    atomicAdd(&ws.stats[0], 1ull);
+                    atomicAdd(&ws.stats[1], (unsigned long long)ns);
+                }
+            }
+        }
+    } else if (g.decode) {
+        ns = ws.n_sel[0];
+    }
+    bool shared;
+    uint32_t e, nr, P;
+    if (!tqm_unit(ws, true, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid, ns, ids)) return;
     __syncthreads();
     tqm_stage<32, GK == GK_TQ8>(ws.xq, ws.xs, ws.xu, prow, nr * P, H, As, Sc, tid, 256);
     __syncthreads();
@@ -346,7 +387,7 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
             for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
         __syncthreads();
         if (!up && live) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
-                                          hu[wv / 2][l]);
+                                          hu[wv / 2][l], ns, wsel);
         __syncthreads();  // hu read before the next pair writes it
     }
 }
@@ -360,7 +401,9 @@ __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
     const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F;
     bool shared;
     uint32_t e, nr, P;
-    if (!tqm_unit(ws, false, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid)) return;
+    if (!tqm_unit(ws, false, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid,
+                  g.decode ? ws.n_sel[0] : 0u, ws.ids))
+        return;
     long* As = reinterpret_cast<long*>(smem);                        // [F / 32][64]
     float4* Sc = reinterpret_cast<float4*>(As + (size_t)(F / 32) * 64);  // [F / 16][16]
     __syncthreads();
@@ -385,18 +428,24 @@ __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
 }
 
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
-                             uint32_t m, uint32_t kcap, int pair, hipStream_t st) {
+                             uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
+                             hipStream_t st) {
     if (tq_kb(gate.fmt) != 32 || ws.H % 32) return hipErrorInvalidValue;
-    const TqmArgs a{gate, up, sh_gate, sh_up, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0};
+    const TqmArgs a{gate, up, sh_gate, sh_up, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0, lg, k, pol};
+    const int nj = m == 1 && lg ? (int)route_nj(ws.E) : 0;  // decode: routing inside
     // decode: a workgroup per strip pair; batch: TQM_COLS workgroups per item, each looping over
     // strip pairs with the item's activations staged once
     const uint32_t pairs = (ws.F / 16 + 1) / 2;
     const dim3 grid(m == 1 ? pairs : (pairs < TQM_COLS ? pairs : TQM_COLS), m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
-    const size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * 16;
-    switch (tq_bits(gate.fmt)) {
-        case 4: tqm_gateup_kernel<GK_TQ4><<<grid, 256, lds, st>>>(a); break;
-        case 5: tqm_gateup_kernel<GK_TQ5><<<grid, 256, lds, st>>>(a); break;
-        case 8: tqm_gateup_kernel<GK_TQ8><<<grid, 256, lds, st>>>(a); break;
+    size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * 16;
+    if (nj && pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;  // route_row's exponentials
+    switch (tq_bits(gate.fmt) * 100 + nj) {
+#define TQM_GU(b, gk)                                                                 \
+    case b * 100: tqm_gateup_kernel<gk, 0><<<grid, 256, lds, st>>>(a); break;         \
+    case b * 100 + 8: tqm_gateup_kernel<gk, 8><<<grid, 256, lds, st>>>(a); break;     \
+    case b * 100 + 16: tqm_gateup_kernel<gk, 16><<<grid, 256, lds, st>>>(a); break;
+        TQM_GU(4, GK_TQ4) TQM_GU(5, GK_TQ5) TQM_GU(8, GK_TQ8)
+#undef TQM_GU
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -405,7 +454,7 @@ hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate,
 hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                            hipStream_t st) {
     if (tq_kb(down.fmt) != 16 || ws.F % 32 || ws.H % 64) return hipErrorInvalidValue;
-    const TqmArgs a{down, down, sh_down, sh_down, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0};
+    const TqmArgs a{down, down, sh_down, sh_down, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0, nullptr, 0, Policy{}};
     // a workgroup per strip group (the activations of K = F are cheap to stage)
     const dim3 grid(ws.H / 64, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
     const size_t lds = (size_t)(ws.F / 32) * 64 * 8 + (size_t)(ws.F / 16) * 16 * 16;

@@ -75,6 +75,23 @@ __device__ __forceinline__ void dot_rows(const float* __restrict__ wr, const flo
             for (int u = 0; u < U; u++) acc[r] = __builtin_fmaf(a[u], b[u], acc[r]);
         }
     }
+    // the rest of the 64-wide steps, 8 at a time with their loads issued together (H = 2560 leaves
+    // 8 steps after the 32 above); the chain order is the same step order
+    constexpr int U2 = 8;
+    for (; i + 64 * U2 <= H; i += 64 * U2) {
+        float a[U2];
+#pragma unroll
+        for (int u = 0; u < U2; u++) a[u] = wr[i + 64 * u + lane];
+#pragma unroll
+        for (int r = 0; r < DOT_MR; r++) {
+            if ((uint32_t)r >= mr) break;
+            float b[U2];
+#pragma unroll
+            for (int u = 0; u < U2; u++) b[u] = xat<NORM>(x, m0 + r, H, i + 64 * u + lane, rinv, r, nw);
+#pragma unroll
+            for (int u = 0; u < U2; u++) acc[r] = __builtin_fmaf(a[u], b[u], acc[r]);
+        }
+    }
     for (; i + 64 <= H; i += 64) {
         const float a = wr[i + lane];
 #pragma unroll

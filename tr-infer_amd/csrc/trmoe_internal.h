@@ -155,14 +155,16 @@ hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& 
 hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st);
 // the TQ layer's expert products on int8 MFMA (k_tqm.hip): gate/up + SwiGLU + quantisation + fold,
 // and down into yent; tqm_fits: the shapes whose staged activations fit a workgroup's LDS
+// lg != null at m = 1: the decode routing (top-k or mass policy) runs inside the launch
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
-                             uint32_t m, uint32_t kcap, int pair, hipStream_t st);
+                             uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
+                             hipStream_t st);
 hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                            hipStream_t st);
 inline bool tqm_fits(uint32_t H, uint32_t F) {
     const size_t gu = (size_t)(H / 32) * 64 * 8 + (size_t)(H / 32) * 16 * 16;
     const size_t dn = (size_t)(F / 32) * 64 * 8 + (size_t)(F / 16) * 16 * 16;
-    return H % 64 == 0 && F % 32 == 0 && gu <= 64 * 1024 && dn <= 64 * 1024;
+    return H % 64 == 0 && F % 32 == 0 && gu + 1024 * 4 <= 64 * 1024 && dn <= 64 * 1024;
 }
 // the hyper-connection mix part B (k_tq.hip): mixed [m][hh] from xn [m][hc][hh] and lo [m][lr]
 hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, const float* xn, const float* lo,
