@@ -296,13 +296,40 @@ def bench_config4(args, layers, dev, stream, trmoe, torch, np):
     dn = H * (F // 256 * 210)  # Q6_K down bytes per expert
     nbytes = float(np.mean(touched) + 1) * (2 * F * Q4K_ROW_H + dn) + E * H * 4 + H * 4 + M * H * 4 * 2
     nops = (float(np.mean(ents)) + M) * 3 * 2 * H * F
+    # per-kernel times (each kernel alone over the rotation) and the dominant kernel's roofline
+    ctx.set_timing(True)
+    ctx.forward(lw[0], x, out)
+    names = list(ctx.timing())
+    ctx.set_timing(False)
+    kern = {}
+    for name in names:
+        ctx.forward(lw[0], x, out)
+
+        def kbody():
+            for i in range(steps):
+                ctx.launch_kernel(name, lw[i % len(lw)], x, out)
+
+        kern[name] = timed_graph(torch, stream, kbody, 1) / steps
     ctx.close()
     del lw
+    dom = max(kern, key=kern.get)
+    nent, tch = float(np.mean(ents)), float(np.mean(touched)) + 1
+    act = (nent + M) * (F + F // 16 * 12)
+    alg = {"batch_gateup": tch * 2 * F * Q4K_ROW_H + M * (H + H // 32 * 12) + act,
+           "batch_down": tch * dn + act + (nent + M) * H * 4}.get(dom)
+    roof = None
+    if alg:
+        ach = alg / (kern[dom] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, M),
+                "alg_bytes_per_launch": int(alg), "avg_launch_us": round(kern[dom] * 1e3, 2)}
+    log(f"config 4: {per * 1e3:.1f} us/layer, kernels {({k: round(v * 1e3, 2) for k, v in kern.items()})}")
     return {"tokens_per_s": round(M / (per * 1e-3), 1), "us_per_layer": round(per * 1e3, 2),
             "layer_GBps": round(nbytes / (per * 1e-3) / 1e9, 1),
             "hbm_frac": round(nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "int8_TOPS": round(nops / (per * 1e-3) / 1e12, 3), "mean_k": round(float(np.mean(ents)) / M, 3),
-            "experts_touched": round(float(np.mean(touched)), 1), "layers": len(layers), "steps": steps}
+            "experts_touched": round(float(np.mean(touched)), 1), "layers": len(layers), "steps": steps,
+            "kernels_us": {k: round(v * 1e3, 2) for k, v in kern.items()}, "roofline": roof}
 
 
 def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
