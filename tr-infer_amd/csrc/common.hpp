@@ -199,6 +199,20 @@ __device__ __forceinline__ void q4k_dm(float d, float dmin, int sc, int mn, floa
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// ---- rank-1 f32 terms on the matrix cores ---------------------------------------------------------
+// v_mfma_f32_4x4x1f32 (16 blocks of 4x4x1): lane l = 16g + r returns, for v = 0..3,
+//   c[v] + a_{16g + 4(r / 4) + v} * b_l
+// with one rounding: v_fma_f32's result bit for bit, and with c = -0 the rounded product,
+// v_mul_f32's result, signed zeros included (checked on gfx950 over random bit patterns,
+// denormals and infinities).  With a_l taken from token 4g + (l % 4) and b_l from output r this is
+// the per-block fma(m, u, acc) / d * sx of the MFMA epilogues, in the layout of a 16x16 MFMA's
+// output (lane (g, r) holds rows 4g .. 4g + 3 of column r).
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4f rank1(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f neg_zero4() { return v4f{-0.0f, -0.0f, -0.0f, -0.0f}; }
+
 // Device-coherent word access for data exchanged between workgroups inside one launch:
 // agent-scope atomic loads and stores go to memory directly, past the per-XCD L2, so neither
 // side needs a whole-cache write-back or invalidate.

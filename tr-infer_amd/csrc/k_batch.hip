@@ -434,31 +434,7 @@ __device__ __forceinline__ void load_q4sb(const uint8_t* __restrict__ rowp, uint
     for (int c = 0; c < 4; c++) w.qs[c] = *reinterpret_cast<const uint2*>(p + 16 + 32 * c + 8 * g);
 }
 
-// Stage an item's activation rows (int8, one block = 32 bytes per row) in MFMA operand order.
-__device__ __forceinline__ void stage_a(const int8_t* __restrict__ src_rows, const uint32_t* rowoff, uint32_t K,
-                                        long* As, uint32_t tid) {
-    // K is a multiple of 256, so 16 rows are a multiple of 256 pieces: every thread loads the same
-    // number, all requested before any is stored
-    const uint32_t pieces = K / 16;  // 16-byte pieces per row
-    for (uint32_t i0 = 0; i0 < 16 * pieces; i0 += 2048) {
-        uint4 v[8];
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * pieces ? i : 16 * pieces - 1;
-            v[c] = *reinterpret_cast<const uint4*>(src_rows + (size_t)rowoff[ic / pieces] + (ic % pieces) * 16);
-        }
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const uint32_t i = i0 + tid + 256 * c;
-            if (i < 16 * pieces) {
-                const uint32_t t = i / pieces, o = i % pieces;
-                const uint32_t b = o / 2, g0 = (o % 2) * 2;  // 16 bytes = k-groups g0, g0+1 of block b
-                As[b * 64 + g0 * 16 + t] = (long)(((unsigned long long)v[c].y << 32) | v[c].x);
-                As[b * 64 + (g0 + 1) * 16 + t] = (long)(((unsigned long long)v[c].w << 32) | v[c].z);
-            }
-        }
-    }
-}
+__device__ __forceinline__ const Q4Sb& settle(const Q4Sb& w) { return w; }
 
 // ---- gate/up on v_mfma_i32_16x16x64_i8 ------------------------------------------------------
 //
@@ -506,9 +482,25 @@ __device__ __forceinline__ void stage_a16(const int8_t* __restrict__ src_rows, c
 }
 
 constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table (16 + 1 against bank conflicts)
+constexpr uint32_t DM_GU = 9;       // the same for gate/up's 8 sub-blocks per row
 
 __device__ __forceinline__ v4i mfma_i8_64_acc(v4i_t a, v4i_t b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// The f32 epilogue of one 32-block of gate and up (gemv.rs:141-148 per output, blocks in order):
+// acc = fma(mm, u, acc), then acc = fma(dot, dd * sx, acc).  The fma with mm and the products
+// dd * sx run as rank-1 MFMAs (the same bits as the VALU forms); sx, su are this lane's row's.
+__device__ __forceinline__ void gateup_block(v4f& accg, v4f& accu, const v4i& dg, const v4i& du, float2 mg, float2 mu,
+                                             float sx, float su) {
+    const v4f dsg = rank1(sx, mg.x, neg_zero4()), dsu = rank1(sx, mu.x, neg_zero4());
+    accg = rank1(su, mg.y, accg);
+    accu = rank1(su, mu.y, accu);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        accg[i] = __builtin_fmaf((float)dg[i], dsg[i], accg[i]);
+        accu[i] = __builtin_fmaf((float)du[i], dsu[i], accu[i]);
+    }
 }
 
 // gate/up for items of at most 16 / S rows, S strips per MFMA output: the activation rows split
@@ -556,10 +548,11 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
     };
     W cw;
     load(0, cw);
-    float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f accg = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
     const v4i_t zero4 = {0, 0, 0, 0};
     const v4i z = {0, 0, 0, 0};
     const bool first = g < 2;
+    const uint32_t tl = orow + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
         W nw = cw;
@@ -592,16 +585,7 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
                 const uint32_t B = sb * 8 + j;
                 const v4i dg = dgv[jj], du = duv[jj];
                 const float2 mg = q4k_dm_rt(cw.hg, j), mu = q4k_dm_rt(cw.hu, j);
-                const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + orow);
-                const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + orow);
-                const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
-                    accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
-                    accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
-                    accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
-                    accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
-                }
+                gateup_block(accg, accu, dg, du, mg, mu, Sx[B * 16 + tl], Su[B * 16 + tl]);
             }
         }
         cw = nw;
@@ -635,10 +619,12 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
 }
 
 // gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
-// Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.
+// Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.  Registers are
+// held to three waves per SIMD (the LDS fits three workgroups per CU): at config 4 that took the
+// kernel from 540 to 487 us against two waves, the few spilled words being on the small-item path.
 template <int NSB>
-__global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat shg, Mat shu, Workspace ws,
-                                                          uint32_t skip_rows) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void batch_gateup_kernel(
+        Mat gate, Mat up, Mat shg, Mat shu, Workspace ws, uint32_t skip_rows) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8;
     const uint32_t F = gate.rows, nbf = F / 16;
     const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
@@ -656,8 +642,8 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     v4i_t* As = reinterpret_cast<v4i_t*>(smem);                      // [nb][2 halves][16 rows]
     float* Sx = reinterpret_cast<float*>(smem + nb * 64 * 8);        // [nb][16] activation scales
     float* Su = Sx + nb * 16;                                        // [nb][16] scale * sum
-    float2* Dm = reinterpret_cast<float2*>(Su + nb * 16);            // [4 waves][2][16][DM_STRIDE]
-    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Dm + 4 * 2 * 16 * DM_STRIDE);  // [16]
+    float2* Dm = reinterpret_cast<float2*>(Su + nb * 16);            // [4 waves][2][16][DM_GU]
+    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Dm + 4 * 2 * 16 * DM_GU);  // [16]
     uint32_t* tokv = rowoff + 16;                                    // [16]
 
     if (tid < 16) {
@@ -700,48 +686,62 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
     }
     __syncthreads();
 
-    float2* dmw = Dm + wv * 2 * 16 * DM_STRIDE;
+    float2* dmw = Dm + wv * 2 * 16 * DM_GU;
     const uint32_t nstep = (strips / 4) * NSB;   // (strip, superblock) steps of this wave
+    // Loads go out in row order: lane l reads row l / 4, 16-byte piece l % 4, so each four
+    // consecutive lanes read 64 contiguous bytes (the vector L1 serves that about 3x faster from L2
+    // than the MFMA order, where consecutive lanes read different rows).  ds_bpermute then moves
+    // each piece to MFMA lane (g, r) = (piece, row), from lane 4r + g.
+    const uint32_t lrow = lane / 4, lpc = lane % 4;
+    const int paddr = (int)(4 * r + g) * 4;
     auto rows_of = [&](uint32_t step, const uint8_t*& rg, const uint8_t*& ru) {
         const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
-        rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + r) * G.row_bytes;
-        ru = U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + r) * U.row_bytes;
+        rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + lrow) * G.row_bytes;
+        ru = U.ptr + (size_t)e * U.stride + (size_t)(strip * 16 + lrow) * U.row_bytes;
+    };
+    auto to_mfma = [&](const v4i_t& v) -> v4i_t {
+        v4i_t o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_ds_bpermute(paddr, v[i]);
+        return o;
     };
     Q4Sb16 cg, cu;
     {
         const uint8_t *rg, *ru;
         rows_of(0, rg, ru);
-        load_q4sb16(rg, 0, g, cg);
-        load_q4sb16(ru, 0, g, cu);
+        load_q4sb16(rg, 0, lpc, cg);
+        load_q4sb16(ru, 0, lpc, cu);
     }
-    float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f accg = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
     const v4i_t zero4 = {0, 0, 0, 0};
     const bool first = g < 2;  // this lane's bytes are of the pair's first chunk
+    const uint32_t tl = 4 * g + (r & 3);  // the token whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
         Q4Sb16 ng = cg, nu = cu;
         if (step + 1 < nstep) {  // the next superblock's loads go out before this one's math
             const uint8_t *rg, *ru;
             rows_of(step + 1, rg, ru);
-            load_q4sb16(rg, (step + 1) % NSB, g, ng);
-            load_q4sb16(ru, (step + 1) % NSB, g, nu);
+            load_q4sb16(rg, (step + 1) % NSB, lpc, ng);
+            load_q4sb16(ru, (step + 1) % NSB, lpc, nu);
         }
-        // (dd, mm) of sub-blocks 2g, 2g+1 of row r, gate then up
+        // (dd, mm) of sub-blocks 2 lpc, 2 lpc + 1 of the loaded row, gate then up
         wave_sync();
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
-            const uint32_t j = 2 * g + jj;
-            dmw[r * DM_STRIDE + j] = q4k_dm_rt(cg.hdr, j);
-            dmw[(16 + r) * DM_STRIDE + j] = q4k_dm_rt(cu.hdr, j);
+            const uint32_t j = 2 * lpc + jj;
+            dmw[lrow * DM_GU + j] = q4k_dm_rt(cg.hdr, j);
+            dmw[(16 + lrow) * DM_GU + j] = q4k_dm_rt(cu.hdr, j);
         }
+        const v4i_t qg[2] = {to_mfma(cg.q[0]), to_mfma(cg.q[1])}, qu[2] = {to_mfma(cu.q[0]), to_mfma(cu.q[1])};
         wave_sync();
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             // this lane's activation halves: sub-blocks 4pp + 2 (g / 2) (low nibbles) and the next
             const uint32_t bl = sb * 8 + 4 * pp + (first ? 0u : 2u);
             const v4i_t al = As[(bl * 2 + g % 2) * 16 + r], ah = As[((bl + 1) * 2 + g % 2) * 16 + r];
-            const v4i_t wgl = cg.q[pp] & 0x0f0f0f0f, wgh = (cg.q[pp] >> 4) & 0x0f0f0f0f;
-            const v4i_t wul = cu.q[pp] & 0x0f0f0f0f, wuh = (cu.q[pp] >> 4) & 0x0f0f0f0f;
+            const v4i_t wgl = qg[pp] & 0x0f0f0f0f, wgh = (qg[pp] >> 4) & 0x0f0f0f0f;
+            const v4i_t wul = qu[pp] & 0x0f0f0f0f, wuh = (qu[pp] >> 4) & 0x0f0f0f0f;
             v4i dgv[4], duv[4];  // sub-blocks 4pp + 0..3
             {
                 const v4i_t a0 = first ? al : zero4, a2 = first ? zero4 : al;
@@ -760,17 +760,8 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
                 const int j = 4 * pp + jj;
                 const uint32_t B = sb * 8 + j;
                 const v4i dg = dgv[jj], du = duv[jj];
-                const float2 mg = dmw[r * DM_STRIDE + j], mu = dmw[(16 + r) * DM_STRIDE + j];
-                const float4 sx = *reinterpret_cast<const float4*>(Sx + B * 16 + 4 * g);
-                const float4 su = *reinterpret_cast<const float4*>(Su + B * 16 + 4 * g);
-                const float sxa[4] = {sx.x, sx.y, sx.z, sx.w}, sua[4] = {su.x, su.y, su.z, su.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {  // gemv.rs:141-148 per output, blocks in order
-                    accg[i] = __builtin_fmaf(mg.y, sua[i], accg[i]);
-                    accg[i] = __builtin_fmaf((float)dg[i], mg.x * sxa[i], accg[i]);
-                    accu[i] = __builtin_fmaf(mu.y, sua[i], accu[i]);
-                    accu[i] = __builtin_fmaf((float)du[i], mu.x * sxa[i], accu[i]);
-                }
+                const float2 mg = dmw[r * DM_GU + j], mu = dmw[(16 + r) * DM_GU + j];
+                gateup_block(accg, accu, dg, du, mg, mu, Sx[B * 16 + tl], Su[B * 16 + tl]);
             }
         }
         cg = ng;
@@ -809,7 +800,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(Mat gate, Mat up, Mat
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
                                const Workspace& ws, uint32_t m, uint32_t skip_rows, hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32;
-    const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_STRIDE * 8 + 32 * 4;
+    const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_GU * 8 + 32 * 4;
     // a workgroup per (item, 16 strips) once the items fill the GPU; otherwise per (item, 4 strips)
     // so that a wave's chain of dependent weight loads stays short
     const dim3 grid(geo::mfma_gateup_cols(m, F), grouped_item_rows(ws, m));
@@ -833,32 +824,49 @@ hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gat
 // Q6_K operands of one superblock for lane (g, r) (superblocks are only 2-byte aligned, so each
 // piece comes from an aligned load and byte alignment): ql bytes 64n + 32s + 8g (n, s in {0, 1}),
 // qh bytes 128 + 32n + 8g, the scales of blocks 4g .. 4g+3 (this lane decodes them) and d.
+// Q6Raw holds the loaded words as they arrive; q6_settle aligns them when the superblock's math
+// starts, so that the next superblock's loads, issued before, stay in flight meanwhile (work on
+// a loaded value at load time would make the wave wait for it there).
+typedef uint32_t v3u __attribute__((ext_vector_type(3)));
+struct Q6Raw {
+    v3u ql[4], qh[2];  // 12-byte loads at the 4-byte boundary at or below each 8-byte piece
+    uint2 sv;          // the 8 bytes holding the 4 scale bytes 192 + 4g
+    uint32_t sh;       // the superblock's misalignment in bytes (0 or 2)
+    uint16_t d;
+};
 struct Q6Sb {
     uint2 ql[4], qh[2];
     uint32_t sc;  // int8 scales of blocks 4g .. 4g+3
     uint16_t d;
 };
-// 8 bytes at p + o (p 2-byte aligned) from one 12-byte load at the 4-byte boundary below, shifted
-// by the superblock's misalignment (0 or 2 bytes; the load stays inside the superblock when
-// 2 <= o + 12 - shift <= 210 and o >= shift, as for every ql / qh piece)
-__device__ __forceinline__ uint2 ld64_sh(const uint8_t* pa, uint32_t o, uint32_t sh) {
-    typedef uint32_t v3u __attribute__((ext_vector_type(3)));
-    const v3u v = *reinterpret_cast<const v3u*>(pa + o);
-    return make_uint2(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh));
-}
-__device__ __forceinline__ void load_q6sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q6Sb& w) {
+// The 12-byte load for the 8 bytes at p + o (p 2-byte aligned) stays inside the superblock when
+// 2 <= o + 12 - shift <= 210 and o >= shift, as for every ql / qh piece.
+__device__ __forceinline__ void load_q6sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q6Raw& w) {
     const uint8_t* p = rowp + sb * 210;
     const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;  // 0 or 2
     const uint8_t* pa = p - sh;
 #pragma unroll
-    for (int i = 0; i < 4; i++) w.ql[i] = ld64_sh(pa, 64 * (i / 2) + 32 * (i % 2) + 8 * g, sh);
+    for (int i = 0; i < 4; i++) w.ql[i] = *reinterpret_cast<const v3u*>(pa + 64 * (i / 2) + 32 * (i % 2) + 8 * g);
 #pragma unroll
-    for (int n = 0; n < 2; n++) w.qh[n] = ld64_sh(pa, 128 + 32 * n + 8 * g, sh);
+    for (int n = 0; n < 2; n++) w.qh[n] = *reinterpret_cast<const v3u*>(pa + 128 + 32 * n + 8 * g);
     // the 4 scale bytes 192 + 4g: one 8-byte load that stays inside the superblock (at 188 + 4g
-    // when p is 4-byte aligned, else at the 4-byte boundary 2 below 192 + 4g), then the bytes
-    const uint2 sv = *reinterpret_cast<const uint2*>(sh ? pa + 192 + 4 * g : p + 188 + 4 * g);
-    w.sc = sh ? __builtin_amdgcn_alignbyte(sv.y, sv.x, 2) : sv.y;
+    // when p is 4-byte aligned, else at the 4-byte boundary 2 below 192 + 4g)
+    w.sv = *reinterpret_cast<const uint2*>(sh ? pa + 192 + 4 * g : p + 188 + 4 * g);
+    w.sh = sh;
     w.d = *reinterpret_cast<const uint16_t*>(p + 208);
+}
+__device__ __forceinline__ uint2 align64(const v3u& v, uint32_t sh) {
+    return make_uint2(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh));
+}
+__device__ __forceinline__ Q6Sb settle(const Q6Raw& r) {
+    Q6Sb w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w.ql[i] = align64(r.ql[i], r.sh);
+#pragma unroll
+    for (int n = 0; n < 2; n++) w.qh[n] = align64(r.qh[n], r.sh);
+    w.sc = r.sh ? __builtin_amdgcn_alignbyte(r.sv.y, r.sv.x, 2) : r.sv.y;
+    w.d = r.d;
+    return w;
 }
 // 8 consecutive 6-bit values e = 32*q8 + 8g .. +7 of the superblock (q8 compile-time)
 __device__ __forceinline__ long q6_operand(const Q6Sb& w, int q8) {
@@ -872,6 +880,43 @@ __device__ __forceinline__ long q6_operand(const Q6Sb& w, int q8) {
 
 __device__ __forceinline__ v4i mfma_i8_acc(long a, long b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// The f32 epilogue of one 32-wide chunk of the down input = two 16-blocks (gemv.rs:141-148, blocks in
+// order): acc = fma(mm, u, acc), then acc = fma(dot, dd * sx, acc), per block.  The products
+// dd * sx run as rank-1 MFMAs off the accumulation chain (the same bits as v_mul_f32); the chain
+// stays on the VALU, since one chain per lane would otherwise wait on an MFMA every block.  sx
+// points at this lane's row of the first block's scales, su4 at the four rows 4g .. of its u; the
+// second block's are 16 floats on.
+__device__ __forceinline__ void down_blocks(v4f& acc, const v4i& c0, const v4i& c1, float2 d0, float2 d1,
+                                            const float* sx, const float* su4) {
+    const v4f ds0 = rank1(sx[0], d0.x, neg_zero4()), ds1 = rank1(sx[16], d1.x, neg_zero4());
+    const float4 u0 = *reinterpret_cast<const float4*>(su4), u1 = *reinterpret_cast<const float4*>(su4 + 16);
+    const float u0a[4] = {u0.x, u0.y, u0.z, u0.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        acc[i] = __builtin_fmaf(d0.y, u0a[i], acc[i]);
+        acc[i] = __builtin_fmaf((float)c0[i], ds0[i], acc[i]);
+        acc[i] = __builtin_fmaf(d1.y, u1a[i], acc[i]);
+        acc[i] = __builtin_fmaf((float)c1[i], ds1[i], acc[i]);
+    }
+}
+
+// The same chain with the products on the VALU too (fewer registers, for the small-item paths
+// whose register count sets the kernel's)
+__device__ __forceinline__ void down_blocks_valu(v4f& acc, const v4i& c0, const v4i& c1, float2 dm, const float* sx4,
+                                                 const float* su4) {
+    const float4 s0 = *reinterpret_cast<const float4*>(sx4), s1 = *reinterpret_cast<const float4*>(sx4 + 16);
+    const float4 u0 = *reinterpret_cast<const float4*>(su4), u1 = *reinterpret_cast<const float4*>(su4 + 16);
+    const float s0a[4] = {s0.x, s0.y, s0.z, s0.w}, u0a[4] = {u0.x, u0.y, u0.z, u0.w};
+    const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        acc[i] = __builtin_fmaf(dm.y, u0a[i], acc[i]);
+        acc[i] = __builtin_fmaf((float)c0[i], dm.x * s0a[i], acc[i]);
+        acc[i] = __builtin_fmaf(dm.y, u1a[i], acc[i]);
+        acc[i] = __builtin_fmaf((float)c1[i], dm.x * s1a[i], acc[i]);
+    }
 }
 
 // Q4_K down for items of at most 16 / S rows: S strips share one 16x16 MFMA output.  The rows of
@@ -911,7 +956,7 @@ __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const I
     };
     W cw;
     load(0, cw);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const v4i z = {0, 0, 0, 0};
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
@@ -930,19 +975,7 @@ __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const I
                 c1 = mfma_i8_acc(sel == (uint32_t)s ? ahi : 0l, bw, c1);
             }
             const float2 dm = q4k_dm_rt(cw.hdr, q8);  // sub-block q8 = 16-blocks 2 q8, 2 q8 + 1
-            const float4 s0 = *reinterpret_cast<const float4*>(Sx + (2 * q) * 16 + orow);
-            const float4 u0 = *reinterpret_cast<const float4*>(Su + (2 * q) * 16 + orow);
-            const float4 s1 = *reinterpret_cast<const float4*>(Sx + (2 * q + 1) * 16 + orow);
-            const float4 u1 = *reinterpret_cast<const float4*>(Su + (2 * q + 1) * 16 + orow);
-            const float s0a[4] = {s0.x, s0.y, s0.z, s0.w}, u0a[4] = {u0.x, u0.y, u0.z, u0.w};
-            const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc[i] = __builtin_fmaf(dm.y, u0a[i], acc[i]);
-                acc[i] = __builtin_fmaf((float)c0[i], dm.x * s0a[i], acc[i]);
-                acc[i] = __builtin_fmaf(dm.y, u1a[i], acc[i]);
-                acc[i] = __builtin_fmaf((float)c1[i], dm.x * s1a[i], acc[i]);
-            }
+            down_blocks_valu(acc, c0, c1, dm, Sx + (2 * q) * 16 + orow, Su + (2 * q) * 16 + orow);
         }
         cw = nw;
         if (sb == NSB - 1) {
@@ -961,24 +994,35 @@ __device__ __forceinline__ void down_strips_q4(const Mat& D, uint32_t e, const I
 // the 8 value bytes 8g .. 8g + 7 (unit bytes 34c + 2 + 8g: 4-byte aligned for odd c, 2 past it for
 // even c, read by an aligned 12-byte load and alignbyte), and the words holding d of blocks 2g
 // (low half of the word at 68g) and 2g + 1 (high half of the word at 68g + 32).
+struct Q8Raw {
+    v3u ev[4];   // even blocks c = 2i: 12 bytes at the 4-byte boundary 2 below the 8 value bytes
+    uint2 od[4];  // odd blocks c = 2i + 1: the 8 value bytes
+    uint32_t d0, d1;
+};
 struct Q8Sb {
     uint2 q[8];
     uint32_t d0, d1;
 };
-__device__ __forceinline__ void load_q8sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q8Sb& w) {
+__device__ __forceinline__ void load_q8sb(const uint8_t* __restrict__ rowp, uint32_t sb, uint32_t g, Q8Raw& w) {
     const uint8_t* p = rowp + sb * 272;
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-        if (c % 2) {
-            w.q[c] = *reinterpret_cast<const uint2*>(p + 34 * c + 2 + 8 * g);
-        } else {
-            typedef uint32_t v3u __attribute__((ext_vector_type(3)));
-            const v3u v = *reinterpret_cast<const v3u*>(p + 34 * c + 8 * g);
-            w.q[c] = make_uint2(__builtin_amdgcn_alignbyte(v.y, v.x, 2), __builtin_amdgcn_alignbyte(v.z, v.y, 2));
-        }
+    for (int i = 0; i < 4; i++) {
+        w.ev[i] = *reinterpret_cast<const v3u*>(p + 34 * (2 * i) + 8 * g);
+        w.od[i] = *reinterpret_cast<const uint2*>(p + 34 * (2 * i + 1) + 2 + 8 * g);
     }
     w.d0 = *reinterpret_cast<const uint32_t*>(p + 68 * g);
     w.d1 = *reinterpret_cast<const uint32_t*>(p + 68 * g + 32);
+}
+__device__ __forceinline__ Q8Sb settle(const Q8Raw& r) {
+    Q8Sb w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        w.q[2 * i] = align64(r.ev[i], 2);
+        w.q[2 * i + 1] = r.od[i];
+    }
+    w.d0 = r.d0;
+    w.d1 = r.d1;
+    return w;
 }
 
 // Q5_1 operands of one unit of 8 blocks (192 bytes, 16-byte aligned) for lane (g, r): per block c
@@ -997,6 +1041,7 @@ __device__ __forceinline__ void load_q51sb(const uint8_t* __restrict__ rowp, uin
     w.dm0 = *reinterpret_cast<const uint32_t*>(p + 48 * g);
     w.dm1 = *reinterpret_cast<const uint32_t*>(p + 48 * g + 24);
 }
+__device__ __forceinline__ const Q51Sb& settle(const Q51Sb& w) { return w; }
 // elements 8g .. 8g + 7 of block q8 as 8 bytes (q5_1_rows, blocks.py:57-68); q5_hi4 puts four qh
 // bits at bit 4 of four bytes.  The swap pairs lane groups 0/1 and 2/3 and leaves, in an odd
 // group's lanes, their own first word in one result and the partner's (qh) in the other: the
@@ -1016,8 +1061,13 @@ __device__ __forceinline__ long q51_operand(const Q51Sb& w, int q8, uint32_t g) 
 
 // FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
 // q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
+//
+// Q6_K's registers are held to four waves per SIMD (config 4's down 461 -> 450 us); the other
+// formats keep the compiler's allocation (held to four, the Q4_K small-item paths spill and the
+// M = 512 down slows from 125.7 to 128-130 us).
 template <int NSB, int FK>
-__global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4 : 1))) void batch_down_kernel(
+        Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
     constexpr bool Q6 = FK == 1;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
     const uint32_t H = down.rows;
@@ -1038,56 +1088,20 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
     float* Su = Sx + nbf * 16;                                       // [nbf][16] scale * sum
     float2* Dm = reinterpret_cast<float2*>(Su + nbf * 16);           // [4 waves][16][DM_STRIDE]
     int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [nbf][16] sums (Q8_0)
-    uint32_t* rowoff = reinterpret_cast<uint32_t*>(Ss + nbf * 16);   // [16]
-
-    if (tid < 16) rowoff[tid] = (arow0 + (tid < item.nrows ? tid : 0u)) * F;
-    __syncthreads();
-    stage_a(ws.actq, rowoff, F, As, tid);
-    for (uint32_t i0 = 0; i0 < 16 * nbf; i0 += 1024) {
-        float a[4], c2[4];
-        int32_t c3[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nbf ? i : 16 * nbf - 1;
-            const size_t row = rowoff[ic / nbf] / F;
-            a[c] = ws.acts[row * nbf + ic % nbf];
-            c2[c] = ws.actu[row * nbf + ic % nbf];
-            if constexpr (FK == 2) c3[c] = ws.actsum[row * nbf + ic % nbf];
-        }
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t i = i0 + tid + 256 * c;
-            if (i < 16 * nbf) {
-                Sx[(i % nbf) * 16 + i / nbf] = a[c];
-                Su[(i % nbf) * 16 + i / nbf] = c2[c];
-                if constexpr (FK == 2) Ss[(i % nbf) * 16 + i / nbf] = c3[c];
-            }
-        }
-    }
-    __syncthreads();
 
     const uint32_t strips = H / 16 / gridDim.x;
-    if constexpr (FK == 0) {
-        // small items: several strips per MFMA output (a wave owns strips / 4 strips)
-        if (item.nrows <= 4 && strips % 16 == 0) {
-            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
-            return;
-        }
-        if (item.nrows <= 8 && strips % 8 == 0) {
-            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
-            return;
-        }
-    }
+    // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
+    const uint32_t small = FK != 0 ? 0u : (item.nrows <= 4 && strips % 16 == 0) ? 4u
+                                        : (item.nrows <= 8 && strips % 8 == 0) ? 2u : 0u;
     const uint32_t g = lane / 16, r = lane % 16;
-    float2* dmw = Dm + wv * 16 * DM_STRIDE;
     const uint32_t nstep = (strips / 4) * NSB;
     auto row_of = [&](uint32_t step) -> const uint8_t* {
         const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
         return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
     };
     using W = typename std::conditional<
-            Q6, Q6Sb,
-            typename std::conditional<FK == 2, Q8Sb, typename std::conditional<FK == 3, Q51Sb, Q4Sb>::type>::type>::type;
+            Q6, Q6Raw,
+            typename std::conditional<FK == 2, Q8Raw, typename std::conditional<FK == 3, Q51Sb, Q4Sb>::type>::type>::type;
     auto load = [&](uint32_t step, W& w) {
         if constexpr (Q6)
             load_q6sb(row_of(step), step % NSB, g, w);
@@ -1098,13 +1112,52 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
         else
             load_q4sb(row_of(step), step % NSB, g, w);
     };
-    W cw;
-    load(0, cw);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // The item's activation rows and their scales go out together.  Entry rows are consecutive
+    // from arow0; rows past the item repeat its first row.  Thread j takes row j % 16, so
+    // consecutive threads fill consecutive LDS words (no bank conflicts on the stores).
+    uint4 av[NSB];  // 16 rows x F / 16 pieces = 256 NSB pieces of 16 bytes
+    float sv[NSB], uv[NSB];
+    int32_t tv[NSB];
+#pragma unroll
+    for (int c = 0; c < NSB; c++) {
+        const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
+        const size_t row = arow0 + (t < item.nrows ? t : 0u);
+        av[c] = *reinterpret_cast<const uint4*>(ws.actq + row * F + o * 16);
+        sv[c] = ws.acts[row * nbf + o];  // o < nbf = 16 NSB: block o of row t
+        uv[c] = ws.actu[row * nbf + o];
+        if constexpr (FK == 2) tv[c] = ws.actsum[row * nbf + o];
+    }
+#pragma unroll
+    for (int c = 0; c < NSB; c++) {
+        const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
+        // piece o = k-groups 2 (o % 2), +1 of 32-wide chunk o / 2 (MFMA operand order, stage_a)
+        As[(o / 2) * 64 + (o % 2) * 32 + t] = (long)(((unsigned long long)av[c].y << 32) | av[c].x);
+        As[(o / 2) * 64 + (o % 2) * 32 + 16 + t] = (long)(((unsigned long long)av[c].w << 32) | av[c].z);
+        Sx[o * 16 + t] = sv[c];
+        Su[o * 16 + t] = uv[c];
+        if constexpr (FK == 2) Ss[o * 16 + t] = tv[c];
+    }
+    __syncthreads();
+
+    if constexpr (FK == 0) {
+        if (small == 4) {
+            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
+            return;
+        }
+        if (small == 2) {
+            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
+            return;
+        }
+    }
+    W lw;  // issued here rather than before the staging: held across it, it cost the Q4_K kernel a wave per SIMD
+    load(0, lw);
+    float2* dmw = Dm + wv * 16 * DM_STRIDE;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t tl = 4 * g + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
-        W nw = cw;
-        if (step + 1 < nstep) load(step + 1, nw);
+        const auto cw = settle(lw);  // this superblock's words (loaded during the previous step)
+        if (step + 1 < nstep) load(step + 1, lw);  // the next superblock's loads go out before this one's math
         // (dd, mm) of the superblock's 16 blocks of row r: this lane decodes blocks 4g .. 4g+3
         wave_sync();
         if constexpr (Q6) {
@@ -1161,21 +1214,8 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
                 c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
             }
             const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
-            const float4 s0 = *reinterpret_cast<const float4*>(Sx + (2 * q) * 16 + 4 * g);
-            const float4 u0 = *reinterpret_cast<const float4*>(Su + (2 * q) * 16 + 4 * g);
-            const float4 s1 = *reinterpret_cast<const float4*>(Sx + (2 * q + 1) * 16 + 4 * g);
-            const float4 u1 = *reinterpret_cast<const float4*>(Su + (2 * q + 1) * 16 + 4 * g);
-            const float s0a[4] = {s0.x, s0.y, s0.z, s0.w}, u0a[4] = {u0.x, u0.y, u0.z, u0.w};
-            const float s1a[4] = {s1.x, s1.y, s1.z, s1.w}, u1a[4] = {u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc[i] = __builtin_fmaf(d0.y, u0a[i], acc[i]);
-                acc[i] = __builtin_fmaf((float)c0[i], d0.x * s0a[i], acc[i]);
-                acc[i] = __builtin_fmaf(d1.y, u1a[i], acc[i]);
-                acc[i] = __builtin_fmaf((float)c1[i], d1.x * s1a[i], acc[i]);
-            }
+            down_blocks(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + 4 * g);
         }
-        cw = nw;
         if (sb == NSB - 1) {
             const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
 #pragma unroll
@@ -1192,7 +1232,7 @@ __global__ __launch_bounds__(256) void batch_down_kernel(Mat down, Mat shd, Work
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t skip_rows,
                              hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
-    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8 + 16 * 4;
+    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8;
     const dim3 grid(geo::mfma_down_cols(m, H), grouped_item_rows(ws, m));
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
     const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
