@@ -111,6 +111,20 @@ def test_router_gemm_tiles_bit_exact(m):
     assert np.array_equal(host(lg).view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,E,H", [(1024, 512, 2048), (1100, 80, 512), (1057, 96, 2560), (3072, 512, 2048)])
+def test_router_mfma_bit_exact(m, E, H):
+    """The matrix-core router gemm (m >= 1024): the same bits as gemm_f32_nt's chains and halving
+    tree, with ragged token and expert tiles, a bias, and config 4's full shape."""
+    say(f"router mfma m={m} E={E} H={H}")
+    router = O.gen_normal(2, 1, E * H, 0.02).reshape(E, H)
+    x = O.gen_normal(2, 5, m * H, 1.0).reshape(m, H)
+    bias = O.gen_normal(2, 6, E, 1.0).astype(np.float32)
+    lg, _ = trmoe.router_logits(to_dev(router), to_dev(x), bias=to_dev(bias), gemm_order=True)
+    want = (O.gemm_f32_nt(x, router) + bias[None, :]).astype(np.float32)
+    got = host(lg)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.abs(got - want).max()
+
+
 def routing_cases(E=512):
     rng = np.random.default_rng(5)
     lg = [rng.standard_normal((8, E)).astype(np.float32),

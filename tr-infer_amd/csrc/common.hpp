@@ -301,6 +301,15 @@ __device__ __forceinline__ bool xcd_order(uint32_t n_items, uint32_t& col, uint3
     return true;
 }
 
+// The same for a 1-D grid whose first n workgroups are live: id -> its place in XCD order.
+__device__ __forceinline__ bool xcd_order_1d(uint32_t n, uint32_t& idx) {
+    const uint32_t id = blockIdx.x;
+    if (id >= n) return false;
+    const uint32_t x = id % 8, slot = id / 8, base = n / 8, rem = n % 8;
+    idx = x * base + (x < rem ? x : rem) + slot;
+    return true;
+}
+
 __device__ __forceinline__ uint32_t item_token(const Workspace& ws, const Item& it, bool shared, uint32_t row) {
     const uint32_t r = row < it.nrows ? row : 0u;
     return shared ? it.row0 + r : ws.ent_tok[it.row0 + r];

@@ -168,6 +168,22 @@ __host__ __device__ constexpr int gemm_pad(int d, int kc) {  // floats of paddin
 // The first n_aux workgroups of the grid do the launch's other work, so that it needs no launch of
 // its own: workgroups < n_dot compute the shared gate's logit (always in dot order,
 // exec_batch.rs:1520), a wave per DOT_MR rows; the rest quantise x for the grouped kernels.
+__device__ __forceinline__ void router_aux(const float* __restrict__ x, uint32_t m, uint32_t H,
+                                           const float* __restrict__ shg, float* __restrict__ sh, const XQuant& xquant,
+                                           uint32_t n_dot, uint32_t aux) {
+    if (aux < n_dot) {
+        const uint32_t lane = threadIdx.x % WAVE, m0 = (aux * 4 + threadIdx.x / WAVE) * DOT_MR;
+        if (m0 < m) {
+            const uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
+            float res[DOT_MR];
+            dot_rows(shg, x, m0, mr, H, lane, res);
+            if (lane == 0)
+                for (uint32_t r = 0; r < mr; r++) sh[m0 + r] = res[r];
+        }
+    } else {
+        quantize_x_rows(x, m, H, xquant, aux - n_dot);
+    }
+}
 template <int RM, int RE, int QM, int KC, bool DB>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restrict__ router,
                                                          const float* __restrict__ bias,
@@ -177,18 +193,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
                                                          XQuant xquant, uint32_t n_dot, uint32_t n_aux) {
     constexpr int QE = 16 / QM, TM = QM * RM, TE = QE * RE;
     if (blockIdx.x < n_aux) {  // workgroup-uniform
-        if (blockIdx.x < n_dot) {
-            const uint32_t lane = threadIdx.x % WAVE, m0 = (blockIdx.x * 4 + threadIdx.x / WAVE) * DOT_MR;
-            if (m0 < m) {
-                const uint32_t mr = m - m0 < (uint32_t)DOT_MR ? m - m0 : (uint32_t)DOT_MR;
-                float res[DOT_MR];
-                dot_rows(shg, x, m0, mr, H, lane, res);
-                if (lane == 0)
-                    for (uint32_t r = 0; r < mr; r++) sh[m0 + r] = res[r];
-            }
-        } else {
-            quantize_x_rows(x, m, H, xquant, blockIdx.x - n_dot);
-        }
+        router_aux(x, m, H, shg, sh, xquant, n_dot, blockIdx.x);
         return;
     }
     // rows between the 16-lane groups of one wave (q = 0..3): x rows differ when qm does
@@ -304,6 +309,140 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const float* __restric
         }
 }
 
+// The same gemm_f32_nt order on the matrix cores.  v_mfma_f32_4x4x1f32 is 16 independent 4x4 outer
+// products with accumulate, each element one fma rounded once (the same bits as v_fma_f32): block
+// j of the instruction is chain j of a 4-token x 4-expert tile, its k = 16s + j.  Lane l = 4j + u
+// gives the A value x[token u][k] and the B value w[expert u][k], and gets back acc[token v][expert
+// u] of chain j, v = 0..3.  A wave holds a 16 x 16 tile as 4 x 4 such accumulators (64 VGPRs): per
+// 16-wide step it reads 8 floats from LDS for 16 instructions = 4096 fmas, twice the VALU's fma
+// rate with a quarter of the register tile's LDS reads per fma.  The chains are reduced at the end
+// by the same halving tree (chain j ^ 8, ^ 4, ^ 2, ^ 1: lanes 32, 16, 8, 4 apart).
+// Workgroup tile TM x TE = 32 x 32 (waves 2 x 2), x and router staged in LDS row-major in KC-wide
+// chunks, double-buffered, the global loads two chunks ahead (as in router_gemm_kernel).
+__device__ __forceinline__ float chains_sum(float v) {  // lanes 4j + u, over j: the halving tree
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // chains j, j ^ 8
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(b[0]) + __uint_as_float(b[1]);  // j ^ 4
+    v = v + dpp_f<0x128>(v);                            // row_ror:8: j ^ 2
+    v = v + dpp_f<0x124>(v);                            // row_ror:4: j +- 1, equal after the step before
+    return v;
+}
+template <int KC>
+__global__ __launch_bounds__(256) void router_mfma_kernel(const float* __restrict__ router,
+                                                         const float* __restrict__ bias,
+                                                         const float* __restrict__ x, uint32_t m, uint32_t E,
+                                                         uint32_t H, float* __restrict__ rlog,
+                                                         const float* __restrict__ shg, float* __restrict__ sh,
+                                                         XQuant xquant, uint32_t n_dot) {
+    // row pitch 8 mod 32 words: the 4 rows x 8 columns each half-wave reads fall in 32 distinct banks
+    constexpr int TM = 32, TE = 32, XK = KC + 8;
+    // tiles first, the aux workgroups after them; the tiles in XCD order (xcd_order): an XCD takes
+    // a contiguous run of tiles, so the expert tiles of one token tile share its L2's copy of x
+    const uint32_t tiles_e = (E + TE - 1) / TE, tiles = tiles_e * ((m + TM - 1) / TM);
+    if (blockIdx.x >= tiles) {  // workgroup-uniform
+        router_aux(x, m, H, shg, sh, xquant, n_dot, blockIdx.x - tiles);
+        return;
+    }
+    uint32_t bx;
+    if (!xcd_order_1d(tiles, bx)) return;
+    __shared__ __align__(16) float xs[2][TM][XK];
+    __shared__ __align__(16) float wsm[2][TE][XK];
+    const uint32_t tid = threadIdx.x, wv = tid / WAVE, lane = tid % WAVE, j = lane / 4, u = lane % 4;
+    const uint32_t wm = wv / 2, we = wv % 2;  // the wave's 16 x 16 quadrant
+    const uint32_t m0 = (bx / tiles_e) * TM, e0 = (bx % tiles_e) * TE;
+
+    constexpr int XV = TM * KC / 4, WV = TE * KC / 4;  // float4 per chunk
+    constexpr int NV = (XV + WV) / 256;
+    static_assert((XV + WV) % 256 == 0, "every thread stages the same number of float4");
+    float4 sa[NV], sb[NV];
+    auto fetch = [&](uint32_t ck, float4 (&st)[NV]) {
+        const uint32_t k0 = ck * KC;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const uint32_t v = tid + 256 * i;
+            if (v < (uint32_t)XV) {
+                const uint32_t r = v / (KC / 4), c4 = v % (KC / 4);
+                const uint32_t row = m0 + r < m ? m0 + r : m - 1;
+                st[i] = *reinterpret_cast<const float4*>(x + (size_t)row * H + k0 + 4 * c4);
+            } else {
+                const uint32_t w = v - XV, r = w / (KC / 4), c4 = w % (KC / 4);
+                const uint32_t ex = e0 + r < E ? e0 + r : E - 1;
+                st[i] = *reinterpret_cast<const float4*>(router + (size_t)ex * H + k0 + 4 * c4);
+            }
+        }
+    };
+    auto store = [&](int buf, const float4 (&st)[NV]) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const uint32_t v = tid + 256 * i;
+            float* dst = v < (uint32_t)XV ? &xs[buf][v / (KC / 4)][4 * (v % (KC / 4))]
+                                          : &wsm[buf][(v - XV) / (KC / 4)][4 * ((v - XV) % (KC / 4))];
+            reinterpret_cast<float2*>(dst)[0] = make_float2(st[i].x, st[i].y);
+            reinterpret_cast<float2*>(dst)[1] = make_float2(st[i].z, st[i].w);
+        }
+    };
+    v4f acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int s = 0; s < KC / 16; s++) {
+            const uint32_t c = 16 * s + j;
+            float xv[4], wvv[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) xv[a] = xs[buf][16 * wm + 4 * a + u][c];
+#pragma unroll
+            for (int b = 0; b < 4; b++) wvv[b] = wsm[buf][16 * we + 4 * b + u][c];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[a][b] = rank1(xv[a], wvv[b], acc[a][b]);
+        }
+    };
+    const uint32_t nchunk = H / KC;
+    fetch(0, sa);
+    if (nchunk > 1) fetch(1, sb);
+    store(0, sa);
+    __syncthreads();
+    for (uint32_t ck = 0; ck < nchunk; ck += 2) {
+        if (ck + 2 < nchunk) fetch(ck + 2, sa);
+        if (ck + 1 < nchunk) store(1, sb);  // the other buffer: nobody reads it now
+        compute(0);
+        __syncthreads();
+        if (ck + 1 >= nchunk) break;
+        if (ck + 3 < nchunk) fetch(ck + 3, sb);
+        if (ck + 2 < nchunk) store(0, sa);
+        compute(1);
+        __syncthreads();
+    }
+    // every lane ends with all 16 (a, b) sums; lane (j, u) stores tile (a, b) = (j / 4, j % 4):
+    // tokens 4a + v, expert 4b + u
+    float outv[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) outv[v] = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float t = chains_sum(acc[a][b][v]);
+                outv[v] = j == (uint32_t)(4 * a + b) ? t : outv[v];
+            }
+    const uint32_t ex = e0 + 16 * we + 4 * (j % 4) + u;
+    if (ex < E) {
+        const float bb = bias ? bias[ex] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const uint32_t row = m0 + 16 * wm + 4 * (j / 4) + v;
+            if (row < m) rlog[(size_t)row * E + ex] = bias ? outv[v] + bb : outv[v];
+        }
+    }
+}
+
 // workgroup tiles of the router gemm by batch size (the first entry whose min_m <= m and whose
 // chunk divides H)
 struct GemmCfg {
@@ -350,6 +489,15 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         const uint32_t n_dot = shexp_gate ? (chunks + 3) / 4 : 0u;
         const uint32_t n_aux = n_dot + (xquant ? (m * (H / 32) * 4 + 255) / 256 : 0u);
         const XQuant& xq = xquant ? *xquant : none;
+        // the matrix-core gemm from 1024 rows (config 4: 160 -> 91 us); at 512 its 256 workgroups
+        // (one per CU) ran 36.5 us against the VALU tiles' 35.4.  64-wide chunks: 32 and 128 were
+        // no faster
+        if (m >= 1024 && H % 64 == 0) {
+            const uint32_t tiles = ((E + 31) / 32) * ((m + 31) / 32);
+            router_mfma_kernel<64><<<tiles + n_aux, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shexp_gate, sh, xq,
+                                                                  n_dot);
+            return hipGetLastError();
+        }
         switch (id) {
 #define GEMM_ARGS router, bias, x, m, E, H, rlog, shexp_gate, sh, xq, n_dot, n_aux, st
             case 1: launch_gemm_cfg<4, 4, 4, 128, true>(GEMM_ARGS); break;

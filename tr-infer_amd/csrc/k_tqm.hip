@@ -118,7 +118,6 @@ struct TqmArgs {
     Policy pol;
 };
 
-constexpr uint32_t TQM_RA = 16;   // activation rows of a unit at most (an item; a decode slot uses 1 or 2)
 constexpr uint32_t TQM_COLS = 4;  // batch: workgroups per item, each over a share of the strips
 
 // The unit of workgroup row y: returns false when there is none.  prow: physical activation rows;
