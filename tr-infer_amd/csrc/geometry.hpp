@@ -42,8 +42,14 @@ inline uint32_t chunks(uint32_t m) { return (m + CHUNK - 1) / CHUNK; }
 inline uint64_t doff_elems(uint32_t m, uint32_t E) { return (uint64_t)chunks(m) * E; }
 inline bool dispatch_split(uint32_t m) { return m >= 256; }
 
-// MFMA gate/up: grid.x column blocks of F / 16 / grid.x strips, four waves taking every fourth
-inline uint32_t mfma_gateup_cols(uint32_t m, uint32_t F) { return m >= 64 ? F / 256 : F / 64; }
+// MFMA gate/up: grid.x column blocks of F / 16 / grid.x strips, four waves taking every fourth.
+// A wave's strips run one after another, so with few items (one or two rounds of workgroups on
+// the GPU) the kernel time is a wave's chain of strips: 128-wide blocks below 2048 rows (M = 512:
+// gate/up 210 -> 197 us), 256-wide from 2048 (config 4: 507 against 512 us with 128), 64-wide for
+// small batches.
+inline uint32_t mfma_gateup_cols(uint32_t m, uint32_t F) {
+    return m >= 2048 && F % 256 == 0 ? F / 256 : m >= 64 && F % 128 == 0 ? F / 128 : F / 64;
+}
 inline uint32_t mfma_gateup_strips(uint32_t m, uint32_t F) { return F / 16 / mfma_gateup_cols(m, F); }
 // MFMA down: grid.x blocks of 256 or 64 output rows, four waves of 16-row strips
 inline uint32_t mfma_down_cols(uint32_t m, uint32_t H) { return m >= 64 ? H / 256 : H / 64; }
