@@ -219,16 +219,22 @@ __device__ __forceinline__ void tqm_stage(const int8_t* __restrict__ q, const fl
 }
 
 // The chain of one strip for lane l over all units: acc[v] for activation row 4 (l / 16) + v and
-// weight row l % 16.  Loads run UB units ahead.
-template <int GK, int KB>
+// weight row l % 16.  Loads run UB units ahead.  R1: the block's fma with mm and its products
+// dd * sx as rank-1 MFMAs (rank1, the same bits), each lane reading only its own row's (s, u), with
+// a quarter of the units in flight (the full window went to scratch memory).  The batch down takes
+// it (real shape M = 512: 381 -> 347 us); the gate/up, whose waves each chain 5 strips, doubled in
+// time with it (the MFMA latency on every block of the chain), and decode keeps the VALU form too.
+template <int GK, int KB, bool R1>
 __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uint32_t K, const long* As,
                                           const float4* Sc, uint32_t l, float (&acc)[4]) {
     // the walk over K is sequential per wave (the chain), so the loads run UB units ahead (about
     // 64 VGPRs of raw words)
-    constexpr uint32_t UB = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
+    constexpr uint32_t UB0 = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
+    constexpr uint32_t UB = R1 ? (UB0 / 4 > 0 ? UB0 / 4 : 1u) : UB0;
     constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
-    const uint32_t nu = K / 32, g = l / 16;
+    const uint32_t nu = K / 32, g = l / 16, tl = 4 * g + (l & 3);
     for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    v4f a4 = {0.0f, 0.0f, 0.0f, 0.0f};
     TqmB<GK, KB> w[UB];
 #pragma unroll
     for (uint32_t i = 0; i < UB; i++)
@@ -250,16 +256,29 @@ __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uin
                 const v4i d4 = tqm_mfma(am, bq);
                 const uint32_t blk = NBL * b + hb;
                 const float dd = h2f((uint16_t)cw.d[hb]), mm = h2f((uint16_t)cw.m[hb]);
+                if constexpr (R1) {
+                    const float2 su = *reinterpret_cast<const float2*>(&Sc[blk * 16 + tl]);
+                    a4 = rank1(su.y, mm, a4);
+                    const v4f ds = rank1(su.x, dd, neg_zero4());
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const float4 sx = Sc[blk * 16 + 4 * g + v];
-                    const int dot = U8 ? d4[v] + 128 * __float_as_int(sx.z) : d4[v];
-                    acc[v] = __builtin_fmaf(mm, sx.y, acc[v]);
-                    acc[v] = __builtin_fmaf((float)dot, dd * sx.x, acc[v]);
+                    for (int v = 0; v < 4; v++) {
+                        const int dot = U8 ? d4[v] + 128 * __float_as_int(Sc[blk * 16 + 4 * g + v].z) : d4[v];
+                        a4[v] = __builtin_fmaf((float)dot, ds[v], a4[v]);
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const float4 sx = Sc[blk * 16 + 4 * g + v];
+                        const int dot = U8 ? d4[v] + 128 * __float_as_int(sx.z) : d4[v];
+                        acc[v] = __builtin_fmaf(mm, sx.y, acc[v]);
+                        acc[v] = __builtin_fmaf((float)dot, dd * sx.x, acc[v]);
+                    }
                 }
             }
         }
     }
+    if constexpr (R1)
+        for (int v = 0; v < 4; v++) acc[v] = a4[v];
 }
 
 // SwiGLU and the per-16 quantisation of one strip's rows: the 16 lanes of lane group gq hold one
@@ -380,7 +399,7 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
             const Mat& M = up ? (shared ? g.shb : g.b) : (shared ? g.sha : g.a);
-            tqm_strip<GK, 32>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, H, As, Sc, l, acc);
+            tqm_strip<GK, 32, false>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, H, As, Sc, l, acc);
         }
         if (up)
             for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
@@ -392,7 +411,7 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
 }
 
 // Grid (H / 64, units), 256 threads: wave w takes strip 4 blockIdx.x + w of H.
-template <int GK>
+template <int GK, bool R1>
 __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t prow[2 * BR], orow[BR];
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
     for (uint32_t sg = blockIdx.x; 4 * sg < H / 16; sg += gridDim.x) {
         const uint32_t strip = 4 * sg + wv;
         float acc[4];
-        tqm_strip<GK, 16>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, F, As, Sc, l, acc);
+        tqm_strip<GK, 16, R1>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, F, As, Sc, l, acc);
         if (g.decode) {
             if (gq == 0) ws.yent[(size_t)orow[0] * H + strip * 16 + r] = P == 2 ? acc[0] + acc[1] : acc[0];
             continue;
@@ -457,10 +476,14 @@ hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace&
     // a workgroup per strip group (the activations of K = F are cheap to stage)
     const dim3 grid(ws.H / 64, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
     const size_t lds = (size_t)(ws.F / 32) * 64 * 8 + (size_t)(ws.F / 16) * 16 * 16;
-    switch (tq_bits(down.fmt)) {
-        case 4: tqm_down_kernel<GK_TQ4><<<grid, 256, lds, st>>>(a); break;
-        case 5: tqm_down_kernel<GK_TQ5><<<grid, 256, lds, st>>>(a); break;
-        case 8: tqm_down_kernel<GK_TQ8><<<grid, 256, lds, st>>>(a); break;
+    // the batch kernels with the rank-1 MFMA epilogue, decode with the VALU one
+    switch (tq_bits(down.fmt) * 2 + (m == 1 ? 0 : 1)) {
+        case 8: tqm_down_kernel<GK_TQ4, false><<<grid, 256, lds, st>>>(a); break;
+        case 9: tqm_down_kernel<GK_TQ4, true><<<grid, 256, lds, st>>>(a); break;
+        case 10: tqm_down_kernel<GK_TQ5, false><<<grid, 256, lds, st>>>(a); break;
+        case 11: tqm_down_kernel<GK_TQ5, true><<<grid, 256, lds, st>>>(a); break;
+        case 16: tqm_down_kernel<GK_TQ8, false><<<grid, 256, lds, st>>>(a); break;
+        case 17: tqm_down_kernel<GK_TQ8, true><<<grid, 256, lds, st>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
