@@ -902,6 +902,19 @@ __device__ __forceinline__ void down_blocks(v4f& acc, const v4i& c0, const v4i& 
     }
 }
 
+// The whole block on the matrix cores but the dot's fma: acc = fma(mm, u, acc) as a rank-1 MFMA
+// too (su: this lane's row's u), so the chain alternates MFMA and VALU
+__device__ __forceinline__ void down_blocks_mc(v4f& acc, const v4i& c0, const v4i& c1, float2 d0, float2 d1,
+                                               const float* sx, const float* su) {
+    const v4f ds0 = rank1(sx[0], d0.x, neg_zero4()), ds1 = rank1(sx[16], d1.x, neg_zero4());
+    acc = rank1(su[0], d0.y, acc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf((float)c0[i], ds0[i], acc[i]);
+    acc = rank1(su[16], d1.y, acc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf((float)c1[i], ds1[i], acc[i]);
+}
+
 // The same chain with the products on the VALU too (fewer registers, for the small-item paths
 // whose register count sets the kernel's)
 __device__ __forceinline__ void down_blocks_valu(v4f& acc, const v4i& c0, const v4i& c1, float2 dm, const float* sx4,
@@ -1214,7 +1227,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
                 c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
             }
             const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
-            down_blocks(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + 4 * g);
+            // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
+            // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
+            if constexpr (Q6)
+                down_blocks_mc(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + tl);
+            else
+                down_blocks(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + 4 * g);
         }
         if (sb == NSB - 1) {
             const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
