@@ -1072,40 +1072,25 @@ __device__ __forceinline__ long q51_operand(const Q51Sb& w, int q8, uint32_t g) 
     return (long)(((unsigned long long)hi << 32) | lo);
 }
 
-// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
-// q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
-//
-// Q6_K's registers are held to four waves per SIMD (config 4's down 461 -> 450 us); the other
-// formats keep the compiler's allocation (held to four, the Q4_K small-item paths spill and the
-// M = 512 down slows from 125.7 to 128-130 us).
-template <int NSB, int FK>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4 : 1))) void batch_down_kernel(
-        Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
+// One or two items of one expert (NI): their activation rows staged side by side, every weight
+// load, unpack and (dd, mm) decode shared by both (at config 4 an expert's ~60 rows make ~4 items,
+// each of which otherwise re-reads and re-unpacks the expert's weights).
+template <int NSB, int FK, int NI>
+__device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item (&its)[NI], const uint32_t (&arow0)[NI],
+                                           const Workspace& ws, uint32_t H, uint32_t strips, uint32_t bx,
+                                           uint8_t* smem) {
     constexpr bool Q6 = FK == 1;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, NQ = NSB * 8;  // NQ 32-wide chunks
-    const uint32_t H = down.rows;
     const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-    uint32_t bx, itn;  // column block and item, in XCD order
-    if (!xcd_order(ws.n_groups[2], bx, itn)) return;
-    const Item item = ws.items[itn];
-    if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
-    const bool shared = item.expert == NO_EXPERT;
-    const uint32_t n_ent = ws.n_groups[1];
-    const Mat& D = shared ? shd : down;
-    const uint32_t e = shared ? 0u : item.expert;
-    const uint32_t arow0 = shared ? n_ent + item.row0 : item.row0;
+    long* As = reinterpret_cast<long*>(smem);                          // [NI][NQ][64]
+    float* Sx = reinterpret_cast<float*>(smem + NI * NQ * 64 * 8);     // [NI][nbf][16] folded scales
+    float* Su = Sx + NI * nbf * 16;                                    // [NI][nbf][16] scale * sum
+    float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][16][DM_STRIDE]
+    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
 
-    extern __shared__ __align__(16) uint8_t smem[];
-    long* As = reinterpret_cast<long*>(smem);                        // [NQ][64]
-    float* Sx = reinterpret_cast<float*>(smem + NQ * 64 * 8);        // [nbf][16] folded scales
-    float* Su = Sx + nbf * 16;                                       // [nbf][16] scale * sum
-    float2* Dm = reinterpret_cast<float2*>(Su + nbf * 16);           // [4 waves][16][DM_STRIDE]
-    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [nbf][16] sums (Q8_0)
-
-    const uint32_t strips = H / 16 / gridDim.x;
     // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
-    const uint32_t small = FK != 0 ? 0u : (item.nrows <= 4 && strips % 16 == 0) ? 4u
-                                        : (item.nrows <= 8 && strips % 8 == 0) ? 2u : 0u;
+    const uint32_t small = FK != 0 || NI != 1 ? 0u : (its[0].nrows <= 4 && strips % 16 == 0) ? 4u
+                                                   : (its[0].nrows <= 8 && strips % 8 == 0) ? 2u : 0u;
     const uint32_t g = lane / 16, r = lane % 16;
     const uint32_t nstep = (strips / 4) * NSB;
     auto row_of = [&](uint32_t step) -> const uint8_t* {
@@ -1125,47 +1110,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
         else
             load_q4sb(row_of(step), step % NSB, g, w);
     };
-    // The item's activation rows and their scales go out together.  Entry rows are consecutive
-    // from arow0; rows past the item repeat its first row.  Thread j takes row j % 16, so
+    // The items' activation rows and their scales go out together.  Entry rows are consecutive
+    // from arow0; rows past an item repeat its first row.  Thread j takes row j % 16, so
     // consecutive threads fill consecutive LDS words (no bank conflicts on the stores).
-    uint4 av[NSB];  // 16 rows x F / 16 pieces = 256 NSB pieces of 16 bytes
-    float sv[NSB], uv[NSB];
-    int32_t tv[NSB];
 #pragma unroll
-    for (int c = 0; c < NSB; c++) {
-        const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
-        const size_t row = arow0 + (t < item.nrows ? t : 0u);
-        av[c] = *reinterpret_cast<const uint4*>(ws.actq + row * F + o * 16);
-        sv[c] = ws.acts[row * nbf + o];  // o < nbf = 16 NSB: block o of row t
-        uv[c] = ws.actu[row * nbf + o];
-        if constexpr (FK == 2) tv[c] = ws.actsum[row * nbf + o];
-    }
+    for (int it = 0; it < NI; it++) {
+        uint4 av[NSB];  // 16 rows x F / 16 pieces = 256 NSB pieces of 16 bytes
+        float sv[NSB], uv[NSB];
+        int32_t tv[NSB];
 #pragma unroll
-    for (int c = 0; c < NSB; c++) {
-        const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
-        // piece o = k-groups 2 (o % 2), +1 of 32-wide chunk o / 2 (MFMA operand order, stage_a)
-        As[(o / 2) * 64 + (o % 2) * 32 + t] = (long)(((unsigned long long)av[c].y << 32) | av[c].x);
-        As[(o / 2) * 64 + (o % 2) * 32 + 16 + t] = (long)(((unsigned long long)av[c].w << 32) | av[c].z);
-        Sx[o * 16 + t] = sv[c];
-        Su[o * 16 + t] = uv[c];
-        if constexpr (FK == 2) Ss[o * 16 + t] = tv[c];
+        for (int c = 0; c < NSB; c++) {
+            const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
+            const size_t row = arow0[it] + (t < its[it].nrows ? t : 0u);
+            av[c] = *reinterpret_cast<const uint4*>(ws.actq + row * F + o * 16);
+            sv[c] = ws.acts[row * nbf + o];  // o < nbf = 16 NSB: block o of row t
+            uv[c] = ws.actu[row * nbf + o];
+            if constexpr (FK == 2) tv[c] = ws.actsum[row * nbf + o];
+        }
+        long* A = As + it * NQ * 64;
+#pragma unroll
+        for (int c = 0; c < NSB; c++) {
+            const uint32_t j = tid + 256 * c, t = j % 16, o = j / 16;
+            // piece o = k-groups 2 (o % 2), +1 of 32-wide chunk o / 2 (MFMA operand order)
+            A[(o / 2) * 64 + (o % 2) * 32 + t] = (long)(((unsigned long long)av[c].y << 32) | av[c].x);
+            A[(o / 2) * 64 + (o % 2) * 32 + 16 + t] = (long)(((unsigned long long)av[c].w << 32) | av[c].z);
+            Sx[(it * nbf + o) * 16 + t] = sv[c];
+            Su[(it * nbf + o) * 16 + t] = uv[c];
+            if constexpr (FK == 2) Ss[(it * nbf + o) * 16 + t] = tv[c];
+        }
     }
     __syncthreads();
 
-    if constexpr (FK == 0) {
+    if constexpr (FK == 0 && NI == 1) {
         if (small == 4) {
-            down_strips_q4<NSB, 4>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
+            down_strips_q4<NSB, 4>(D, e, its[0], arow0[0], H, As, Sx, Su, ws, wv, lane, strips, bx);
             return;
         }
         if (small == 2) {
-            down_strips_q4<NSB, 2>(D, e, item, arow0, H, As, Sx, Su, ws, wv, lane, strips, bx);
+            down_strips_q4<NSB, 2>(D, e, its[0], arow0[0], H, As, Sx, Su, ws, wv, lane, strips, bx);
             return;
         }
     }
     W lw;  // issued here rather than before the staging: held across it, it cost the Q4_K kernel a wave per SIMD
     load(0, lw);
     float2* dmw = Dm + wv * 16 * DM_STRIDE;
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f acc[NI];
+#pragma unroll
+    for (int it = 0; it < NI; it++) acc[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t tl = 4 * g + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
@@ -1208,8 +1199,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
 #pragma unroll
         for (int q8 = 0; q8 < 8; q8++) {  // 32-wide chunks of the superblock = block pairs
             const uint32_t q = sb * 8 + q8;
-            const long af = As[q * 64 + lane];
-            const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
             long bw;
             if constexpr (Q6)
                 bw = q6_operand(cw, q8);
@@ -1219,48 +1208,112 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
                 bw = q51_operand(cw, q8, g);
             else
                 bw = unpack8(cw.qs[q8 / 2], q8 % 2);
-            v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
-            if constexpr (FK == 2) {
-                const int4 t0 = *reinterpret_cast<const int4*>(Ss + (2 * q) * 16 + 4 * g);
-                const int4 t1 = *reinterpret_cast<const int4*>(Ss + (2 * q + 1) * 16 + 4 * g);
-                c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
-                c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
-            }
             const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
-            // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
-            // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
-            if constexpr (Q6)
-                down_blocks_mc(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + tl);
-            else
-                down_blocks(acc, c0, c1, d0, d1, Sx + (2 * q) * 16 + tl, Su + (2 * q) * 16 + 4 * g);
+#pragma unroll
+            for (int it = 0; it < NI; it++) {
+                const long af = As[(it * NQ + q) * 64 + lane];
+                const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
+                v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+                const float* sx = Sx + (it * nbf + 2 * q) * 16;
+                const float* su = Su + (it * nbf + 2 * q) * 16;
+                if constexpr (FK == 2) {
+                    const int4 t0 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q) * 16 + 4 * g);
+                    const int4 t1 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q + 1) * 16 + 4 * g);
+                    c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
+                    c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
+                }
+                // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
+                // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
+                if constexpr (Q6)
+                    down_blocks_mc(acc[it], c0, c1, d0, d1, sx + tl, su + tl);
+                else
+                    down_blocks(acc[it], c0, c1, d0, d1, sx + tl, su + 4 * g);
+            }
         }
         if (sb == NSB - 1) {
             const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t row = 4 * g + i;
-                if (row < item.nrows) ws.yent[(size_t)(arow0 + row) * H + strip * 16 + r] = acc[i];
-                acc[i] = 0.0f;
+            for (int it = 0; it < NI; it++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t row = 4 * g + i;
+                    if (row < its[it].nrows) ws.yent[(size_t)(arow0[it] + row) * H + strip * 16 + r] = acc[it][i];
+                    acc[it][i] = 0.0f;
+                }
+        }
+    }
+}
+
+// FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
+// q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
+// PR = 2 (large batches): a workgroup per item pair (2p, 2p + 1) in XCD order; a pair of one
+// expert runs as one group sharing the weights, other pairs one item after the other.
+//
+// Q6_K's registers are held to four waves per SIMD (config 4's down 461 -> 450 us); the other
+// formats keep the compiler's allocation (held to four, the Q4_K small-item paths spill and the
+// M = 512 down slows from 125.7 to 128-130 us).
+template <int NSB, int FK, int PR>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4 : 1))) void batch_down_kernel(
+        Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
+    const uint32_t H = down.rows, n_items = ws.n_groups[2], n_ent = ws.n_groups[1];
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t strips = H / 16 / gridDim.x;
+    uint32_t bx, grp;  // column block and item (pair), in XCD order
+    if (!xcd_order(PR == 2 ? (n_items + 1) / 2 : n_items, bx, grp)) return;
+    auto item_args = [&](const Item& it, uint32_t& e, uint32_t& arow0) -> const Mat& {
+        const bool shared = it.expert == NO_EXPERT;
+        e = shared ? 0u : it.expert;
+        arow0 = shared ? n_ent + it.row0 : it.row0;
+        return shared ? shd : down;
+    };
+    auto one = [&](uint32_t itn) {
+        const Item its[1] = {ws.items[itn]};
+        if (its[0].nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
+        uint32_t e, a0[1];
+        const Mat& D = item_args(its[0], e, a0[0]);
+        down_items<NSB, FK, 1>(D, e, its, a0, ws, H, strips, bx, smem);
+    };
+    if constexpr (PR == 1) {
+        one(grp);
+    } else {
+        const uint32_t i0 = 2 * grp, i1 = i0 + 1;
+        const Item it0 = ws.items[i0];
+        const Item it1 = i1 < n_items ? ws.items[i1] : it0;
+        const bool paired = i1 < n_items && it1.expert == it0.expert && it0.nrows > skip_rows &&
+                            it1.nrows > skip_rows && (FK != 0 || (it0.nrows > 8 && it1.nrows > 8));
+        if (paired) {
+            const Item its[2] = {it0, it1};
+            uint32_t e, a0[2], e1;
+            const Mat& D = item_args(it0, e, a0[0]);
+            item_args(it1, e1, a0[1]);
+            down_items<NSB, FK, 2>(D, e, its, a0, ws, H, strips, bx, smem);
+        } else {
+            one(i0);
+            if (i1 < n_items) {
+                __syncthreads();  // the first item's LDS reads are done before the second stages
+                one(i1);
             }
         }
     }
-    (void)NQ;
 }
 
 hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t skip_rows,
                              hipStream_t st) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
-    const size_t lds = (size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12 + 4 * 16 * DM_STRIDE * 8;
-    const dim3 grid(geo::mfma_down_cols(m, H), grouped_item_rows(ws, m));
+    // item pairs sharing the weights where an expert has several items (config 4: ~4 per expert)
+    const int pr = geo::down_pairs(m) ? 2 : 1;
+    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 16 * DM_STRIDE * 8;
+    const uint32_t rows = grouped_item_rows(ws, m);
+    const dim3 grid(geo::mfma_down_cols(m, H), pr == 2 ? (rows + 1) / 2 : rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
     const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
-    switch (F / 256 * 4 + fk) {
-#define DN_CASE(n)                                                                                    \
-    case n * 4: batch_down_kernel<n, 0><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;     \
-    case n * 4 + 1: batch_down_kernel<n, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
-    case n * 4 + 2: batch_down_kernel<n, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
-    case n * 4 + 3: batch_down_kernel<n, 3><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
-        DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
+    switch ((F / 256 * 4 + fk) * 2 + pr - 1) {
+#define DN_CASE(n, f)                                                                                          \
+    case (n * 4 + f) * 2: batch_down_kernel<n, f, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
+    case (n * 4 + f) * 2 + 1: batch_down_kernel<n, f, 2><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break;
+#define DN_F(n) DN_CASE(n, 0) DN_CASE(n, 1) DN_CASE(n, 2) DN_CASE(n, 3)
+        DN_F(1) DN_F(2) DN_F(3) DN_F(4) DN_F(5) DN_F(6) DN_F(7) DN_F(8)
+#undef DN_F
 #undef DN_CASE
         default: return hipErrorInvalidValue;
     }
