@@ -524,9 +524,19 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
         const uint32_t row = orow + i < item.nrows ? orow + i : 0u;
         wgt[i] = shared ? sigmoid_libm(ws.shl[item.row0 + row]) : ws.ent_w[item.row0 + row];
     }
-    auto rowp = [&](const Mat& M, uint32_t step, uint32_t s) -> const uint8_t* {
+    // the qs pieces load in row order (lane l: row l / 4, piece l % 4; each four lanes 64 contiguous
+    // bytes) and move to MFMA lane (g, r) by ds_bpermute from lane 4r + g; the headers load per row
+    const uint32_t lrow = lane / 4, lpc = lane % 4;
+    const int paddr = (int)(4 * r + g) * 4;
+    auto rowp = [&](const Mat& M, uint32_t step, uint32_t s, uint32_t row) -> const uint8_t* {
         const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + s);
-        return M.ptr + (size_t)e * M.stride + (size_t)(strip * 16 + r) * M.row_bytes + (step % NSB) * 144;
+        return M.ptr + (size_t)e * M.stride + (size_t)(strip * 16 + row) * M.row_bytes + (step % NSB) * 144;
+    };
+    auto to_mfma = [&](const v4i_t& v) -> v4i_t {
+        v4i_t o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_ds_bpermute(paddr, v[i]);
+        return o;
     };
     struct W {
         uint4 hg, hu;
@@ -535,16 +545,16 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
     auto load = [&](uint32_t step, W& w) {
 #pragma unroll
         for (int s = 0; s < S; s++) {
-            const uint8_t* pg = rowp(G, step, s);
-            const uint8_t* pu = rowp(U, step, s);
+            const uint8_t* pg = rowp(G, step, s, lrow);
+            const uint8_t* pu = rowp(U, step, s, lrow);
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                w.qg[s][c] = *reinterpret_cast<const v4i_t*>(pg + 16 + 64 * c + 16 * g);
-                w.qu[s][c] = *reinterpret_cast<const v4i_t*>(pu + 16 + 64 * c + 16 * g);
+                w.qg[s][c] = *reinterpret_cast<const v4i_t*>(pg + 16 + 64 * c + 16 * lpc);
+                w.qu[s][c] = *reinterpret_cast<const v4i_t*>(pu + 16 + 64 * c + 16 * lpc);
             }
         }
-        w.hg = *reinterpret_cast<const uint4*>(rowp(G, step, own));
-        w.hu = *reinterpret_cast<const uint4*>(rowp(U, step, own));
+        w.hg = *reinterpret_cast<const uint4*>(rowp(G, step, own, r));
+        w.hu = *reinterpret_cast<const uint4*>(rowp(U, step, own, r));
     };
     W cw;
     load(0, cw);
@@ -568,8 +578,9 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
             for (int s = 0; s < S; s++) {
                 const bool m = sel == (uint32_t)s;
                 const v4i_t b0 = m ? a0 : zero4, b1 = m ? a1 : zero4, b2 = m ? a2 : zero4, b3 = m ? a3 : zero4;
-                const v4i_t wgl = cw.qg[s][pp] & 0x0f0f0f0f, wgh = (cw.qg[s][pp] >> 4) & 0x0f0f0f0f;
-                const v4i_t wul = cw.qu[s][pp] & 0x0f0f0f0f, wuh = (cw.qu[s][pp] >> 4) & 0x0f0f0f0f;
+                const v4i_t qgs = to_mfma(cw.qg[s][pp]), qus = to_mfma(cw.qu[s][pp]);
+                const v4i_t wgl = qgs & 0x0f0f0f0f, wgh = (qgs >> 4) & 0x0f0f0f0f;
+                const v4i_t wul = qus & 0x0f0f0f0f, wuh = (qus >> 4) & 0x0f0f0f0f;
                 dgv[0] = mfma_i8_64_acc(b0, wgl, dgv[0]);
                 duv[0] = mfma_i8_64_acc(b0, wul, duv[0]);
                 dgv[1] = mfma_i8_64_acc(b1, wgh, dgv[1]);
