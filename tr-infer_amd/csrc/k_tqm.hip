@@ -281,6 +281,59 @@ __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uin
         for (int v = 0; v < 4; v++) acc[v] = a4[v];
 }
 
+// Two strips' chains in one wave (the batch gate/up): the same walk as tqm_strip's VALU form, with
+// half the unit window per strip and each unit's activations and scales read once for both.  The
+// waves of that kernel chain several strips each; two independent chains fill the latency of one.
+template <int GK, int KB>
+__device__ __forceinline__ void tqm_strip2(const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, uint32_t K,
+                                           const long* As, const float4* Sc, uint32_t l, float (&acc0)[4],
+                                           float (&acc1)[4]) {
+    constexpr uint32_t UB0 = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
+    constexpr uint32_t UB = UB0 / 2 > 0 ? UB0 / 2 : 1u;
+    constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
+    const uint32_t nu = K / 32, g = l / 16;
+    for (int v = 0; v < 4; v++) acc0[v] = acc1[v] = 0.0f;
+    TqmB<GK, KB> w0[UB], w1[UB];
+#pragma unroll
+    for (uint32_t i = 0; i < UB; i++)
+        if (i < nu) {
+            tqm_load<GK, KB>(w0[i], s0, i, l);
+            tqm_load<GK, KB>(w1[i], s1, i, l);
+        }
+    for (uint32_t b0 = 0; b0 < nu; b0 += UB) {
+#pragma unroll
+        for (uint32_t i = 0; i < UB; i++) {
+            const uint32_t b = b0 + i;
+            if (b >= nu) break;
+            const TqmB<GK, KB> c0 = w0[i], c1 = w1[i];
+            if (b + UB < nu) {  // the loads UB units ahead
+                tqm_load<GK, KB>(w0[i], s0, b + UB, l);
+                tqm_load<GK, KB>(w1[i], s1, b + UB, l);
+            }
+            const long a = As[b * 64 + l];
+            const long bq0 = tqm_operand<GK, KB>(c0, l), bq1 = tqm_operand<GK, KB>(c1, l);
+            constexpr uint32_t NBL = TqmB<GK, KB>::NBL;  // blocks of the unit
+#pragma unroll
+            for (uint32_t hb = 0; hb < NBL; hb++) {
+                const long am = KB == 16 ? ((g / 2 == hb) ? a : 0) : a;
+                const v4i d40 = tqm_mfma(am, bq0), d41 = tqm_mfma(am, bq1);
+                const uint32_t blk = NBL * b + hb;
+                const float dd0 = h2f((uint16_t)c0.d[hb]), mm0 = h2f((uint16_t)c0.m[hb]);
+                const float dd1 = h2f((uint16_t)c1.d[hb]), mm1 = h2f((uint16_t)c1.m[hb]);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const float4 sx = Sc[blk * 16 + 4 * g + v];
+                    const int xs = U8 ? 128 * __float_as_int(sx.z) : 0;
+                    acc0[v] = __builtin_fmaf(mm0, sx.y, acc0[v]);
+                    acc0[v] = __builtin_fmaf((float)(d40[v] + xs), dd0 * sx.x, acc0[v]);
+                    acc1[v] = __builtin_fmaf(mm1, sx.y, acc1[v]);
+                    acc1[v] = __builtin_fmaf((float)(d41[v] + xs), dd1 * sx.x, acc1[v]);
+                }
+            }
+        }
+    }
+}
+
 // SwiGLU and the per-16 quantisation of one strip's rows: the 16 lanes of lane group gq hold one
 // activation row's 16 values (rows r of the strip); decode: levels 0 and 1 of the one logical
 // row in lane group 0 (two-level quantisation with pair); batch: rows 4 gq + i of the item.
@@ -344,7 +397,7 @@ template <int GK, int NJ>
 __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t prow[2 * BR], orow[BR];
-    __shared__ float hu[2][64][4];  // up accumulators of the two strips, by lane
+    __shared__ float hu[2][2][64][4];  // up accumulators of two strip pairs x two strips, by lane
     const Workspace& ws = g.ws;
     const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
     long* As = reinterpret_cast<long*>(smem);                     // [H / 32][64]
@@ -392,21 +445,38 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     __syncthreads();
     const uint32_t gq = l / 16, r = l % 16, n_ent = ws.n_groups[1];
     const bool up = wv % 2 == 1;
-    // strip pairs blockIdx.x, + gridDim.x, ...: the staged activations serve them all
-    for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += gridDim.x) {
-        const uint32_t strip = 2 * sp + wv / 2;
-        const bool live = strip < F / 16;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // strip pairs blockIdx.x, + gridDim.x, ...: the staged activations serve them all.  Batch: two
+    // pairs per pass, a wave walking its strip of each as two chains (tqm_strip2)
+    const uint32_t per = NJ == 0 && !g.decode ? 2u : 1u;  // (NJ > 0: decode, its registers untouched)
+    for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += per * gridDim.x) {
+        const uint32_t strip = 2 * sp + wv / 2, strip1 = 2 * (sp + gridDim.x) + wv / 2;
+        const bool live = strip < F / 16, two = per == 2 && 2 * (sp + gridDim.x) < F / 16;  // two: uniform
+        const bool live1 = two && strip1 < F / 16;  // implies live
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
             const Mat& M = up ? (shared ? g.shb : g.b) : (shared ? g.sha : g.a);
-            tqm_strip<GK, 32, false>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, H, As, Sc, l, acc);
+            const uint8_t* p0 = M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes;
+            if constexpr (NJ == 0) {
+                if (two)  // a strip past F repeats the first one's walk; its result is dropped
+                    tqm_strip2<GK, 32>(p0, live1 ? M.ptr + (size_t)e * M.stride + (size_t)strip1 * M.row_bytes : p0,
+                                       H, As, Sc, l, acc, acc1);
+                else
+                    tqm_strip<GK, 32, false>(p0, H, As, Sc, l, acc);
+            } else {
+                tqm_strip<GK, 32, false>(p0, H, As, Sc, l, acc);
+            }
         }
         if (up)
-            for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
+            for (int v = 0; v < 4; v++) {
+                hu[0][wv / 2][l][v] = acc[v];
+                hu[1][wv / 2][l][v] = acc1[v];
+            }
         __syncthreads();
         if (!up && live) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
-                                          hu[wv / 2][l], ns, wsel);
-        __syncthreads();  // hu read before the next pair writes it
+                                          hu[0][wv / 2][l], ns, wsel);
+        if (!up && live1) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip1, gq, r, acc1,
+                                           hu[1][wv / 2][l], ns, wsel);
+        __syncthreads();  // hu read before the next pass writes it
     }
 }
 
