@@ -118,7 +118,7 @@ struct TqmArgs {
     Policy pol;
 };
 
-constexpr uint32_t TQM_COLS = 4;  // batch: workgroups per item, each over a share of the strips
+constexpr uint32_t TQM_PAIRS = 4;  // batch: strip pairs per workgroup (two passes of two; real shape: 5 per item)
 
 // The unit of workgroup row y: returns false when there is none.  prow: physical activation rows;
 // orow: output row of each logical row; nr logical rows, P physical per logical.
@@ -521,10 +521,11 @@ hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate,
     if (tq_kb(gate.fmt) != 32 || ws.H % 32) return hipErrorInvalidValue;
     const TqmArgs a{gate, up, sh_gate, sh_up, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0, lg, k, pol};
     const int nj = m == 1 && lg ? (int)route_nj(ws.E) : 0;  // decode: routing inside
-    // decode: a workgroup per strip pair; batch: TQM_COLS workgroups per item, each looping over
-    // strip pairs with the item's activations staged once
+    // decode: a workgroup per strip pair; batch: a workgroup per TQM_PAIRS strip pairs of an item,
+    // looping over them with the item's activations staged once (5 or 2 pairs per workgroup at the
+    // real shape: 478 / 484 us against 460 for 4)
     const uint32_t pairs = (ws.F / 16 + 1) / 2;
-    const dim3 grid(m == 1 ? pairs : (pairs < TQM_COLS ? pairs : TQM_COLS), m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
+    const dim3 grid(m == 1 ? pairs : (pairs + TQM_PAIRS - 1) / TQM_PAIRS, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
     size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * 16;
     if (nj && pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;  // route_row's exponentials
     switch (tq_bits(gate.fmt) * 100 + nj) {
