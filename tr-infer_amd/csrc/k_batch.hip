@@ -1086,7 +1086,7 @@ __device__ __forceinline__ long q51_operand(const Q51Sb& w, int q8, uint32_t g) 
 // One or two items of one expert (NI): their activation rows staged side by side, every weight
 // load, unpack and (dd, mm) decode shared by both (at config 4 an expert's ~60 rows make ~4 items,
 // each of which otherwise re-reads and re-unpacks the expert's weights).
-template <int NSB, int FK, int NI>
+template <int NSB, int FK, int NI, int NS = 1>
 __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item (&its)[NI], const uint32_t (&arow0)[NI],
                                            const Workspace& ws, uint32_t H, uint32_t strips, uint32_t bx,
                                            uint8_t* smem) {
@@ -1096,30 +1096,31 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     long* As = reinterpret_cast<long*>(smem);                          // [NI][NQ][64]
     float* Sx = reinterpret_cast<float*>(smem + NI * NQ * 64 * 8);     // [NI][nbf][16] folded scales
     float* Su = Sx + NI * nbf * 16;                                    // [NI][nbf][16] scale * sum
-    float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][16][DM_STRIDE]
-    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
+    static_assert(NS == 1 || NI == 1, "two strips per wave for one item");
+    float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][NS][16][DM_STRIDE]
+    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * NS * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
 
     // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
-    const uint32_t small = FK != 0 || NI != 1 ? 0u : (its[0].nrows <= 4 && strips % 16 == 0) ? 4u
+    const uint32_t small = FK != 0 || NI != 1 || NS != 1 ? 0u : (its[0].nrows <= 4 && strips % 16 == 0) ? 4u
                                                    : (its[0].nrows <= 8 && strips % 8 == 0) ? 2u : 0u;
     const uint32_t g = lane / 16, r = lane % 16;
-    const uint32_t nstep = (strips / 4) * NSB;
-    auto row_of = [&](uint32_t step) -> const uint8_t* {
-        const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
-        return D.ptr + (size_t)e * D.stride + (size_t)(strip * 16 + r) * D.row_bytes;
+    const uint32_t nstep = (strips / 4 / NS) * NSB;
+    auto strip_of = [&](uint32_t step, int s) { return bx * strips + wv + 4 * ((step / NSB) * NS + s); };
+    auto row_of = [&](uint32_t step, int s) -> const uint8_t* {
+        return D.ptr + (size_t)e * D.stride + (size_t)(strip_of(step, s) * 16 + r) * D.row_bytes;
     };
     using W = typename std::conditional<
             Q6, Q6Raw,
             typename std::conditional<FK == 2, Q8Raw, typename std::conditional<FK == 3, Q51Sb, Q4Sb>::type>::type>::type;
-    auto load = [&](uint32_t step, W& w) {
+    auto load = [&](uint32_t step, int s, W& w) {
         if constexpr (Q6)
-            load_q6sb(row_of(step), step % NSB, g, w);
+            load_q6sb(row_of(step, s), step % NSB, g, w);
         else if constexpr (FK == 2)
-            load_q8sb(row_of(step), step % NSB, g, w);
+            load_q8sb(row_of(step, s), step % NSB, g, w);
         else if constexpr (FK == 3)
-            load_q51sb(row_of(step), step % NSB, g, w);
+            load_q51sb(row_of(step, s), step % NSB, g, w);
         else
-            load_q4sb(row_of(step), step % NSB, g, w);
+            load_q4sb(row_of(step, s), step % NSB, g, w);
     };
     // The items' activation rows and their scales go out together.  Entry rows are consecutive
     // from arow0; rows past an item repeat its first row.  Thread j takes row j % 16, so
@@ -1162,95 +1163,114 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
             return;
         }
     }
-    W lw;  // issued here rather than before the staging: held across it, it cost the Q4_K kernel a wave per SIMD
-    load(0, lw);
-    float2* dmw = Dm + wv * 16 * DM_STRIDE;
-    v4f acc[NI];
+    W lw[NS];  // issued here rather than before the staging: held across it, it cost the Q4_K kernel a wave per SIMD
 #pragma unroll
-    for (int it = 0; it < NI; it++) acc[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < NS; s++) load(0, s, lw[s]);
+    float2* dmw = Dm + wv * NS * 16 * DM_STRIDE;
+    v4f acc[NI * NS];
+#pragma unroll
+    for (int it = 0; it < NI * NS; it++) acc[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t tl = 4 * g + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
-        const auto cw = settle(lw);  // this superblock's words (loaded during the previous step)
-        if (step + 1 < nstep) load(step + 1, lw);  // the next superblock's loads go out before this one's math
+        typename std::decay<decltype(settle(lw[0]))>::type cws[NS];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            cws[s] = settle(lw[s]);  // this superblock's words (loaded during the previous step)
+            if (step + 1 < nstep) load(step + 1, s, lw[s]);  // the next superblock's loads go out now
+        }
         // (dd, mm) of the superblock's 16 blocks of row r: this lane decodes blocks 4g .. 4g+3
         wave_sync();
-        if constexpr (Q6) {
-            const float d = h2f(cw.d);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
-                dmw[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
-            }
-        } else if constexpr (FK == 3) {
+        for (int s = 0; s < NS; s++) {
+            const auto& cw = cws[s];
+            float2* dm_s = dmw + s * 16 * DM_STRIDE;
+            if constexpr (Q6) {
+                const float d = h2f(cw.d);
 #pragma unroll
-            for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
-                const uint32_t dm = jj ? cw.dm1 : cw.dm0;
-                const float2 v = make_float2(h2f((uint16_t)(dm & 0xffffu)), h2f((uint16_t)(dm >> 16)));
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
-            }
-        } else if constexpr (FK == 2) {
+                for (int i = 0; i < 4; i++) {
+                    const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
+                    dm_s[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
+                }
+            } else if constexpr (FK == 3) {
 #pragma unroll
-            for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
-                const float dd = h2f((uint16_t)(jj ? cw.d1 >> 16 : cw.d0 & 0xffffu));
-                const float2 v = make_float2(dd, f16_round(-128.0f * dd));
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
-            }
-        } else {
+                for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
+                    const uint32_t dm = jj ? cw.dm1 : cw.dm0;
+                    const float2 v = make_float2(h2f((uint16_t)(dm & 0xffffu)), h2f((uint16_t)(dm >> 16)));
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                }
+            } else if constexpr (FK == 2) {
 #pragma unroll
-            for (int jj = 0; jj < 2; jj++) {  // sub-block 2g + jj covers blocks 4g + 2jj, +1
-                const float2 v = q4k_dm_rt(cw.hdr, 2 * g + jj);
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                dmw[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
+                    const float dd = h2f((uint16_t)(jj ? cw.d1 >> 16 : cw.d0 & 0xffffu));
+                    const float2 v = make_float2(dd, f16_round(-128.0f * dd));
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                }
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {  // sub-block 2g + jj covers blocks 4g + 2jj, +1
+                    const float2 v = q4k_dm_rt(cw.hdr, 2 * g + jj);
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
+                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                }
             }
         }
         wave_sync();
 #pragma unroll
         for (int q8 = 0; q8 < 8; q8++) {  // 32-wide chunks of the superblock = block pairs
             const uint32_t q = sb * 8 + q8;
-            long bw;
-            if constexpr (Q6)
-                bw = q6_operand(cw, q8);
-            else if constexpr (FK == 2)
-                bw = (long)(((unsigned long long)cw.q[q8].y << 32) | cw.q[q8].x);
-            else if constexpr (FK == 3)
-                bw = q51_operand(cw, q8, g);
-            else
-                bw = unpack8(cw.qs[q8 / 2], q8 % 2);
-            const float2 d0 = dmw[r * DM_STRIDE + 2 * q8], d1 = dmw[r * DM_STRIDE + 2 * q8 + 1];
 #pragma unroll
-            for (int it = 0; it < NI; it++) {
-                const long af = As[(it * NQ + q) * 64 + lane];
-                const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
-                v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
-                const float* sx = Sx + (it * nbf + 2 * q) * 16;
-                const float* su = Su + (it * nbf + 2 * q) * 16;
-                if constexpr (FK == 2) {
-                    const int4 t0 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q) * 16 + 4 * g);
-                    const int4 t1 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q + 1) * 16 + 4 * g);
-                    c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
-                    c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
-                }
-                // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
-                // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
+            for (int s = 0; s < NS; s++) {
+                const auto& cw = cws[s];
+                long bw;
                 if constexpr (Q6)
-                    down_blocks_mc(acc[it], c0, c1, d0, d1, sx + tl, su + tl);
+                    bw = q6_operand(cw, q8);
+                else if constexpr (FK == 2)
+                    bw = (long)(((unsigned long long)cw.q[q8].y << 32) | cw.q[q8].x);
+                else if constexpr (FK == 3)
+                    bw = q51_operand(cw, q8, g);
                 else
-                    down_blocks(acc[it], c0, c1, d0, d1, sx + tl, su + 4 * g);
+                    bw = unpack8(cw.qs[q8 / 2], q8 % 2);
+                const float2* dm_s = dmw + s * 16 * DM_STRIDE;
+                const float2 d0 = dm_s[r * DM_STRIDE + 2 * q8], d1 = dm_s[r * DM_STRIDE + 2 * q8 + 1];
+#pragma unroll
+                for (int it = 0; it < NI; it++) {
+                    const long af = As[(it * NQ + q) * 64 + lane];
+                    const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
+                    v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+                    const float* sx = Sx + (it * nbf + 2 * q) * 16;
+                    const float* su = Su + (it * nbf + 2 * q) * 16;
+                    if constexpr (FK == 2) {
+                        const int4 t0 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q) * 16 + 4 * g);
+                        const int4 t1 = *reinterpret_cast<const int4*>(Ss + (it * nbf + 2 * q + 1) * 16 + 4 * g);
+                        c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
+                        c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
+                    }
+                    // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
+                    // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
+                    if constexpr (Q6)
+                        down_blocks_mc(acc[s * NI + it], c0, c1, d0, d1, sx + tl, su + tl);
+                    else
+                        down_blocks(acc[s * NI + it], c0, c1, d0, d1, sx + tl, su + 4 * g);
+                }
             }
         }
         if (sb == NSB - 1) {
-            const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
 #pragma unroll
-            for (int it = 0; it < NI; it++)
+            for (int s = 0; s < NS; s++) {
+                const uint32_t strip = strip_of(step, s);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t row = 4 * g + i;
-                    if (row < its[it].nrows) ws.yent[(size_t)(arow0[it] + row) * H + strip * 16 + r] = acc[it][i];
-                    acc[it][i] = 0.0f;
-                }
+                for (int it = 0; it < NI; it++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t row = 4 * g + i;
+                        if (row < its[it].nrows)
+                            ws.yent[(size_t)(arow0[it] + row) * H + strip * 16 + r] = acc[s * NI + it][i];
+                        acc[s * NI + it][i] = 0.0f;
+                    }
+            }
         }
     }
 }
@@ -1277,12 +1297,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
         arow0 = shared ? n_ent + it.row0 : it.row0;
         return shared ? shd : down;
     };
+#ifndef TRK_DN_NS
+#define TRK_DN_NS 2
+#endif
     auto one = [&](uint32_t itn) {
         const Item its[1] = {ws.items[itn]};
         if (its[0].nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
         uint32_t e, a0[1];
         const Mat& D = item_args(its[0], e, a0[0]);
-        down_items<NSB, FK, 1>(D, e, its, a0, ws, H, strips, bx, smem);
+        // a wave walks two of its strips at once (two chains) unless the item takes a small-item
+        // path (Q4_K, <= 8 rows); Q6_K stays at one: its four waves per SIMD leave no registers
+        // for a second chain
+        const bool small = FK == 0 && its[0].nrows <= 8;
+        if constexpr (TRK_DN_NS == 2 && FK != 1) {
+            if (!small && strips % 8 == 0) {
+                down_items<NSB, FK, 1, 2>(D, e, its, a0, ws, H, strips, bx, smem);
+                return;
+            }
+        }
+        down_items<NSB, FK, 1, 1>(D, e, its, a0, ws, H, strips, bx, smem);
     };
     if constexpr (PR == 1) {
         one(grp);
@@ -1313,7 +1346,7 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
     // item pairs sharing the weights where an expert has several items (config 4: ~4 per expert)
     const int pr = geo::down_pairs(m) ? 2 : 1;
-    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 16 * DM_STRIDE * 8;
+    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 2 * 16 * DM_STRIDE * 8;
     const uint32_t rows = grouped_item_rows(ws, m);
     const dim3 grid(geo::mfma_down_cols(m, H), pr == 2 ? (rows + 1) / 2 : rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
