@@ -150,11 +150,13 @@ def test_decode_one_launch_matches_three(policy):
 
 
 @pytest.mark.parametrize("shape,M,k", [("small", 4, 4), ("small", 16, 4), ("small", 37, 6), ("full", 4, 10),
-                                       ("full", 8, 10), ("full", 16, 10), ("small", 700, 3), ("small", 2200, 2)])
+                                       ("full", 8, 10), ("full", 16, 10), ("small", 700, 3), ("small", 2200, 2),
+                                       ("odd", 2100, 5)])
 def test_batch_layer_and_dispatch(shape, M, k):
-    # M = 700: the split (parallel) scatter; M = 2200: three rounds of 1024 tokens, 35 chunks
+    # M = 700: the split (parallel) scatter; M = 2200: three rounds of 1024 tokens, 35 chunks;
+    # from M = 2048 the gate/up runs item pairs of one expert as 32-row tiles (odd: 3 superblocks)
     say(f"batch layer {shape} M={M} k={k}")
-    L, orc, W = layer(shape, **(SMALL if shape == "small" else FULL))
+    L, orc, W = layer(shape, **{"small": SMALL, "full": FULL, "odd": ODD}[shape])
     ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))
     import torch
     x = L.x(M, tid=200 + M)

@@ -154,9 +154,11 @@ static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max
         {(void**)&ws.ent_of, M * TRK_MOE_K_MAX * 4},
         {(void**)&ws.grp_start, (E + 2) * 4},
         {(void**)&ws.grp_exp, (E + 1) * 4},
-        {(void**)&ws.n_groups, 16},
+        {(void**)&ws.n_groups, 32},
         {(void**)&ws.doff, geo::doff_elems(m_max, E) * 4},  // [ceil(m / 64)][E] per-chunk offsets
         {(void**)&ws.items, (size_t)ws.item_cap * sizeof(Item)},
+        {(void**)&ws.pairs, ((size_t)ws.item_cap / 2 + 1) * 4},
+        {(void**)&ws.single, (size_t)ws.item_cap * 4},
         {(void**)&ws.actq, ws.act_rows * F},
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.actsum, ws.act_rows * (F / 16) * 4},

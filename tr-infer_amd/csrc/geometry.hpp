@@ -51,6 +51,13 @@ inline uint32_t mfma_gateup_cols(uint32_t m, uint32_t F) {
     return m >= 2048 && F % 256 == 0 ? F / 256 : m >= 64 && F % 128 == 0 ? F / 128 : F / 64;
 }
 inline uint32_t mfma_gateup_strips(uint32_t m, uint32_t F) { return F / 16 / mfma_gateup_cols(m, F); }
+// MFMA gate/up over item pairs from 2048 rows: two items of one expert run as one 32-row tile
+// (v_mfma_i32_32x32x32_i8) in a workgroup of eight waves, each taking every eighth strip of the
+// column block.  The pair's activations and scales take 40 H bytes of LDS, which leaves room for
+// two workgroups per CU up to H = 2048.
+inline bool gateup_pairs(uint32_t m, uint32_t H) { return m >= 2048 && H <= 2048; }
+inline uint64_t gateup_pair_lds(uint32_t H) { return (uint64_t)H * 40; }
+inline uint32_t gateup_pair_strips(uint32_t m, uint32_t F) { return mfma_gateup_strips(m, F); }
 // MFMA down: grid.x blocks of 256 or 64 output rows, four waves of 16-row strips
 inline uint32_t mfma_down_cols(uint32_t m, uint32_t H) { return m >= 64 ? H / 256 : H / 64; }
 inline uint32_t mfma_down_rows(uint32_t m, uint32_t H) { return H / mfma_down_cols(m, H); }
@@ -94,6 +101,10 @@ inline const char* check_call(const Caps& c, uint32_t m, uint32_t kcap, bool tq 
     {  // MFMA gate/up: the column blocks tile F's strips exactly, four waves each
         const uint32_t cols = mfma_gateup_cols(m, c.F), s = mfma_gateup_strips(m, c.F);
         if (cols == 0 || cols * s * 16 != c.F || s % 4) return "MFMA gate/up grid does not tile F";
+        // the pairs' workgroups: eight waves over the block's strips (the launcher runs every item
+        // on the 16-row path otherwise), and two workgroups' LDS per CU
+        if (gateup_pairs(m, c.H) && gateup_pair_strips(m, c.F) % 8 == 0 && 2 * gateup_pair_lds(c.H) > 160 * 1024)
+            return "MFMA gate/up pair LDS above 80 KiB";
     }
     {  // MFMA down: the row blocks tile H exactly, 16-row strips over four waves
         const uint32_t cols = mfma_down_cols(m, c.H), r = mfma_down_rows(m, c.H);

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     uint32_t* cnt = reinterpret_cast<uint32_t*>(masks + DISPATCH_WAVES * E);  // [E]
     uint32_t* run = cnt + E;                                                  // [E]
     uint32_t* off = run + E;                                                  // [W][E]
-    uint32_t* wtot = off + DISPATCH_WAVES * E;                                // [W][3]
+    uint32_t* wtot = off + DISPATCH_WAVES * E;                                // [W][5]
     const uint32_t rounds = (m + DT - 1) / DT, nchunks = (m + 63) / 64;
     const uint32_t ept = (E + DT - 1) / DT;  // experts per thread in the scans (contiguous)
 
@@ -103,33 +103,37 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     }
     __syncthreads();
 
-    // block-wide exclusive scans of (entries, non-empty, items) over the experts
-    uint32_t loc[3] = {0, 0, 0};
+    // block-wide exclusive scans of (entries, non-empty, items, item pairs, unpaired items) over the
+    // experts
+    uint32_t loc[5] = {0, 0, 0, 0, 0};
     for (uint32_t i = 0; i < ept; i++) {
         const uint32_t e = tid * ept + i;
-        const uint32_t c = e < E ? cnt[e] : 0u;
+        const uint32_t c = e < E ? cnt[e] : 0u, nc = (c + BR - 1) / BR;
         loc[0] += c;
         loc[1] += c ? 1u : 0u;
-        loc[2] += (c + BR - 1) / BR;
+        loc[2] += nc;
+        loc[3] += nc / 2;
+        loc[4] += nc % 2;
     }
-    uint32_t inc[3];
+    uint32_t inc[5];
 #pragma unroll
-    for (int v = 0; v < 3; v++) {
+    for (int v = 0; v < 5; v++) {
         inc[v] = wave_incl_scan_u32(loc[v]);
-        if (lane == 63) wtot[wv * 3 + v] = inc[v];
+        if (lane == 63) wtot[wv * 5 + v] = inc[v];
     }
     __syncthreads();
-    uint32_t base[3] = {0, 0, 0}, tot[3] = {0, 0, 0};
+    uint32_t base[5] = {0, 0, 0, 0, 0}, tot[5] = {0, 0, 0, 0, 0};
     for (uint32_t w = 0; w < DISPATCH_WAVES; w++)
 #pragma unroll
-        for (int v = 0; v < 3; v++) {
-            const uint32_t x = wtot[w * 3 + v];
+        for (int v = 0; v < 5; v++) {
+            const uint32_t x = wtot[w * 5 + v];
             if (w < wv) base[v] += x;
             tot[v] += x;
         }
     const uint32_t n_ent = tot[0], ng = tot[1], n_routed_items = tot[2];
     {
         uint32_t st = base[0] + inc[0] - loc[0], gi = base[1] + inc[1] - loc[1], it = base[2] + inc[2] - loc[2];
+        uint32_t pi = base[3] + inc[3] - loc[3], si = base[4] + inc[4] - loc[4];
         for (uint32_t i = 0; i < ept; i++) {
             const uint32_t e = tid * ept + i;
             if (e >= E) break;
@@ -140,18 +144,24 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
                 ws.grp_exp[gi] = e;
                 for (uint32_t q = 0; q < nc; q++) {
                     const uint32_t nr = c - q * BR < BR ? c - q * BR : BR;
-                    ws.items[it + q] = Item{e, st + q * BR, nr, 0};
+                    ws.items[it + q] = Item{e, st + q * BR, nr, q};
                 }
+                for (uint32_t q = 0; q < nc / 2; q++) ws.pairs[pi + q] = it + 2 * q;
+                if (nc % 2) ws.single[si] = it + nc - 1;
             }
             st += c;
             gi += c ? 1u : 0u;
             it += nc;
+            pi += nc / 2;
+            si += nc % 2;
         }
     }
     const uint32_t n_sh = (m + BR - 1) / BR;  // the shared expert over the tokens, last
     for (uint32_t q = tid; q < n_sh; q += DT) {
         const uint32_t r0 = q * BR;
-        ws.items[n_routed_items + q] = Item{NO_EXPERT, r0, m - r0 < BR ? m - r0 : BR, 0};
+        ws.items[n_routed_items + q] = Item{NO_EXPERT, r0, m - r0 < BR ? m - r0 : BR, q};
+        if (q % 2 == 0 && q + 1 < n_sh) ws.pairs[tot[3] + q / 2] = n_routed_items + q;
+        if (q % 2 == 0 && q + 1 == n_sh) ws.single[tot[4]] = n_routed_items + q;
     }
     if (tid == 0) {
         if (ws.stats) {  // MoeStats: rows and selected experts of this call
@@ -162,6 +172,8 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
         ws.n_groups[0] = ng;
         ws.n_groups[1] = n_ent;
         ws.n_groups[2] = n_routed_items + n_sh;
+        ws.n_groups[4] = tot[3] + n_sh / 2;
+        ws.n_groups[5] = tot[4] + n_sh % 2;
     }
     __syncthreads();
 
@@ -370,7 +382,7 @@ hipError_t launch_dispatch_small(const Workspace& ws, uint32_t m, uint32_t kcap,
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st) {
     const size_t E = ws.E;
     if (E > 2 * DT) return hipErrorInvalidValue;
-    const size_t lds = DISPATCH_WAVES * E * 8 + (2 * E + DISPATCH_WAVES * E + DISPATCH_WAVES * 3) * 4;
+    const size_t lds = DISPATCH_WAVES * E * 8 + (2 * E + DISPATCH_WAVES * E + DISPATCH_WAVES * 5) * 4;
     // from a few hundred tokens on, one workgroup's scattered stores dominate: spread them
     const int split = geo::dispatch_split(m) ? 1 : 0;
     if (split && geo::doff_elems(m, ws.E) > geo::doff_elems(ws.m_max, ws.E)) return hipErrorInvalidValue;
@@ -629,18 +641,15 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
     }
 }
 
-// gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
-// Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.  Registers are
-// held to three waves per SIMD (the LDS fits three workgroups per CU): at config 4 that took the
-// kernel from 540 to 487 us against two waves, the few spilled words being on the small-item path.
+// gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch) of one
+// item over column block bx: the block's strips of 16 rows, each wave every fourth of them.
 template <int NSB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void batch_gateup_kernel(
-        Mat gate, Mat up, Mat shg, Mat shu, Workspace ws, uint32_t skip_rows) {
+__device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, const Mat& shg, const Mat& shu,
+                                            const Workspace& ws, uint32_t skip_rows, uint32_t bx, uint32_t itn,
+                                            uint8_t* smem) {
     constexpr uint32_t H = NSB * 256, nb = NSB * 8;
     const uint32_t F = gate.rows, nbf = F / 16;
     const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
-    uint32_t bx, itn;  // column block and item, in XCD order
-    if (!xcd_order(ws.n_groups[2], bx, itn)) return;
     const Item item = ws.items[itn];
     if (item.nrows <= skip_rows) return;  // a streaming-GEMV item (k_stream.hip)
     const bool shared = item.expert == NO_EXPERT;
@@ -649,7 +658,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     const Mat& U = shared ? shu : up;
     const uint32_t e = shared ? 0u : item.expert;
 
-    extern __shared__ __align__(16) uint8_t smem[];
     v4i_t* As = reinterpret_cast<v4i_t*>(smem);                      // [nb][2 halves][16 rows]
     float* Sx = reinterpret_cast<float*>(smem + nb * 64 * 8);        // [nb][16] activation scales
     float* Su = Sx + nb * 16;                                        // [nb][16] scale * sum
@@ -808,18 +816,262 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
     }
 }
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16i mfma_i8_32x32(v4i_t a, v4i_t b) {
+    const v16i z = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+}
+
+// The f32 epilogue of one 32-block on a 32 x 32 tile (gemv.rs:141-148 per output, blocks in
+// order): lane (h, c) holds weight row c at tile rows 8q + 4h + u, u = 0 .. 3, in element u of
+// acc[q].  sx4 / su4 hold the scales of tile rows 8q + 4h + (lane % 4), q = 0 .. 3: the rank-1
+// MFMA's a operand for output u of this lane comes from lane 4 (lane / 4) + u.
+__device__ __forceinline__ void block32(v4f (&acc)[4], const v16i& d, float2 dm, float4 sx4, float4 su4) {
+    const float sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w}, su[4] = {su4.x, su4.y, su4.z, su4.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const v4f ds = rank1(sx[q], dm.x, neg_zero4());
+        acc[q] = rank1(su[q], dm.y, acc[q]);
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[q][u] = __builtin_fmaf((float)d[4 * q + u], ds[u], acc[q][u]);
+    }
+}
+
+// (dd, mm) of sub-blocks 2 ch and 2 ch + 1 of this lane's row: lane (h, c) decodes sub-block
+// 2 ch + h and permlane32_swap hands each half the other's (result 0 holds lanes 0-31's value in
+// both halves, result 1 lanes 32-63's).
+__device__ __forceinline__ void q4k_dm_pair(uint4 hdr, uint32_t ch, uint32_t h, float2& d0, float2& d1) {
+    const float2 v = q4k_dm_rt(hdr, 2 * ch + h);
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v.x), __float_as_uint(v.x), false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v.y), __float_as_uint(v.y), false, false);
+    d0 = make_float2(__uint_as_float(x[0]), __uint_as_float(y[0]));
+    d1 = make_float2(__uint_as_float(x[1]), __uint_as_float(y[1]));
+}
+
+// gate/up of item pairs (large batches: an expert with more than 16 rows has several items; the
+// dispatch lists its items as pairs of parts 2j, 2j + 1 in ws.pairs).  A pair is one 32-row tile of
+// activation rows on v_mfma_i32_32x32x32_i8: rows 0-15 the first item's, 16-31 the second's.  A wave
+// takes a strip of 16 features at a time with its 16 gate rows and 16 up rows as the 32 B-operand
+// rows: lane (h, c) = (lane / 32, lane % 32) feeds A = tile row c's activations and B = gate row c
+// (c < 16) or up row c - 16 of the strip, k = 16h .. 16h + 15 of a 32-block, and gets back that
+// weight row at tile rows 8q + 4h + u in element 4q + u.  A 16-byte qs piece holds 16 values of
+// sub-block 2ch in its low nibbles and of 2ch + 1 in its high ones, so each nibble half is one
+// MFMA with nothing masked, and every weight load, unpack and (dd, mm) decode serves 32 activation
+// rows.  Eight waves share the staged activations (32 rows: 40 H bytes of LDS, two workgroups per
+// CU) and hold few registers (four waves per SIMD).  The per-block f32 chain, SwiGLU, quantisation
+// and fold are those of the 16-row path, output by output.
+template <int NSB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void batch_gateup_pairs_kernel(
+        Mat gate, Mat up, Mat shg, Mat shu, Workspace ws) {
+    constexpr uint32_t H = NSB * 256, nb = NSB * 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint32_t bx, pu;  // column block and pair, in XCD order
+    if (!xcd_order(ws.n_groups[4], bx, pu)) return;
+    const uint32_t i0 = ws.pairs[pu];
+    const Item it0 = ws.items[i0], it1 = ws.items[i0 + 1];
+    const bool shared = it0.expert == NO_EXPERT;
+    const Mat& G = shared ? shg : gate;
+    const Mat& U = shared ? shu : up;
+    const uint32_t e = shared ? 0u : it0.expert;
+    const uint32_t F = G.rows, nbf = F / 16, n_ent = ws.n_groups[1];
+    const uint32_t tid = threadIdx.x, wv = tid / 64, lane = tid % 64;
+    const uint32_t h = lane / 32, c = lane % 32;
+    v4i_t* As = reinterpret_cast<v4i_t*>(smem);                   // [nb][2 halves][32 rows]
+    float4* SxT = reinterpret_cast<float4*>(smem + nb * 1024);     // [nb][8 (h, u)]: rows 8q + 4h + u
+    float4* SuT = SxT + nb * 8;
+
+    // tile row c's token and routing weight (exec_batch.rs:1533-1535; shared: the gate)
+    const Item& itc = c < 16 ? it0 : it1;
+    const uint32_t rc = c % 16 < itc.nrows ? c % 16 : 0u;
+    const uint32_t tok = item_token(ws, itc, shared, c % 16);
+    const float wgt_c = shared ? sigmoid_libm(ws.shl[itc.row0 + rc]) : ws.ent_w[itc.row0 + rc];
+
+    // activations: 16-byte piece p of tile row r at As[p * 32 + r]; four lanes read 64 contiguous
+    // bytes of one row, and a wave's stores fill whole 256-byte bank rows
+    {
+        constexpr uint32_t lim = 32 * 2 * nb;
+        for (uint32_t i0 = 0; i0 < lim; i0 += 4096) {
+            v4i_t v[8];
+            uint32_t dst[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t idx = i0 + tid + 512 * k, ic = idx < lim ? idx : lim - 1;
+                const uint32_t row = (ic / 4) % 32, pc = 4 * (ic / 128) + ic % 4;
+                const uint32_t t = (uint32_t)__shfl((int)tok, (int)row);
+                v[k] = *reinterpret_cast<const v4i_t*>(ws.xq + (size_t)t * H + pc * 16);
+                dst[k] = pc * 32 + row;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (i0 + tid + 512 * k < lim) As[dst[k]] = v[k];
+        }
+        constexpr uint32_t lims = 32 * nb;
+        float* sx = reinterpret_cast<float*>(SxT);
+        float* su = reinterpret_cast<float*>(SuT);
+        for (uint32_t i0 = 0; i0 < lims; i0 += 2048) {
+            float a[4], b[4];
+            uint32_t dst[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t idx = i0 + tid + 512 * k, ic = idx < lims ? idx : lims - 1;
+                const uint32_t row = (ic / 4) % 32, B = 4 * (ic / 128) + ic % 4;
+                const uint32_t t = (uint32_t)__shfl((int)tok, (int)row);
+                a[k] = ws.xs[(size_t)t * nb + B];
+                b[k] = ws.xu[(size_t)t * nb + B];
+                dst[k] = B * 32 + (row % 8) * 4 + row / 8;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (i0 + tid + 512 * k < lims) {
+                    sx[dst[k]] = a[k];
+                    su[dst[k]] = b[k];
+                }
+        }
+    }
+    __syncthreads();
+
+    // Weight rows: lane (h, c) loads the header of B-operand row c; lane l loads the 16-byte qs
+    // pieces 2 ch + l % 2 (ch = 0 .. 3) of B-operand row l / 2 (gate rows in lanes 0-31, up rows in
+    // 32-63; two lanes read one 32-byte chunk), and MFMA lane (h, c) takes its piece from lane 2c + h.
+    // Gate and up have one shape and format, so one stride and row size serve both.
+    const uint32_t strips = F / 16 / gridDim.x;  // of this workgroup; wave wv takes wv, wv + 8, ..
+    const uint32_t nstep = (strips / 8) * NSB;   // (strip, superblock) steps of this wave
+    const size_t rb = G.row_bytes;
+    const uint8_t* hbase = (c < 16 ? G.ptr : U.ptr) + (size_t)e * G.stride + (size_t)(c % 16) * rb;
+    const uint8_t* qbase =
+            (lane < 32 ? G.ptr : U.ptr) + (size_t)e * G.stride + (size_t)((lane / 2) % 16) * rb + 16 + 16 * (lane % 2);
+    const int paddr = (int)(2 * c + h) * 4;
+    auto strip_of = [&](uint32_t step) { return bx * strips + wv + 8 * (step / NSB); };
+    struct Raw {
+        uint4 hdr;
+        v4i_t q[4];
+    };
+    auto load = [&](uint32_t step, Raw& w) {
+        const size_t off = (size_t)strip_of(step) * 16 * rb + (step % NSB) * 144;
+        w.hdr = *reinterpret_cast<const uint4*>(hbase + off);
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) w.q[ch] = *reinterpret_cast<const v4i_t*>(qbase + off + 32 * ch);
+    };
+    auto to_mfma = [&](const v4i_t& v) -> v4i_t {
+        v4i_t o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = __builtin_amdgcn_ds_bpermute(paddr, v[i]);
+        return o;
+    };
+    v4f acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t sl = 4 * h + (lane & 3);  // this lane's (h, u) slot of the scale tables
+    const bool odd = c >= 16;                // this lane's row of the strip: up (odd DPP row) or gate
+    // one (strip, superblock) step on the words in cur, the next step's loads going out into nxt first
+    auto step_on = [&](uint32_t step, const Raw& cur, Raw& nxt) {
+        const uint32_t sb = step % NSB;
+        if (step + 1 < nstep) load(step + 1, nxt);
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+            const v4i_t qv = to_mfma(cur.q[ch]);
+            float2 dm[2];
+            q4k_dm_pair(cur.hdr, ch, h, dm[0], dm[1]);
+#pragma unroll
+            for (int nib = 0; nib < 2; nib++) {
+                const uint32_t B = sb * 8 + 2 * ch + nib;
+                const v4i_t a = As[(B * 2 + h) * 32 + c];
+                const v4i_t w = nib ? (qv >> 4) & 0x0f0f0f0f : qv & 0x0f0f0f0f;
+                block32(acc, mfma_i8_32x32(a, w), dm[nib], SxT[B * 8 + sl], SuT[B * 8 + sl]);
+            }
+        }
+        if (sb != NSB - 1) return;
+        // SwiGLU (elem.rs:173) and per-16 quantisation.  Gate rows sit in DPP rows 0 and 2 of the
+        // wave, up rows in 1 and 3; one permlane16_swap per two outputs gives a gate lane the up
+        // value of its tile row 8q + 4h + u (q = 0, 1) and an up lane the gate value of tile row
+        // 8(q + 2) + 4h + u, so each lane finishes one output and the 16 lanes of a DPP row
+        // quantise one tile row's strip.
+        const uint32_t strip = strip_of(step);
+        const Item& it = odd ? it1 : it0;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float send = odd ? acc[qq][u] : acc[qq + 2][u];
+                const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(send), __float_as_uint(send), false,
+                                                                false);
+                const float g = odd ? __uint_as_float(x[0]) : acc[qq][u];
+                const float up_v = odd ? acc[qq + 2][u] : __uint_as_float(x[1]);
+                const uint32_t row = 8 * qq + 4 * h + u, t = odd ? 16 + row : row;
+                const float v = silu512(g) * up_v;
+                const float amax = row16_allreduce(__builtin_fabsf(v), [](float x, float y) { return mx_ps(x, y); });
+                const float s = amax / 127.0f;
+                const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+                const int32_t qi = cvt_rne(v * inv);
+                const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
+                const float w = __shfl(wgt_c, (int)t);
+                if (row < it.nrows) {
+                    const uint32_t arow = shared ? n_ent + it.row0 + row : it.row0 + row;
+                    ws.actq[(size_t)arow * F + strip * 16 + c % 16] = sat_i8(qi);
+                    if (c % 16 == 0) {
+                        const float sf = s * w;  // exec_batch.rs:1533-1535
+                        ws.acts[(size_t)arow * nbf + strip] = sf;
+                        ws.actsum[(size_t)arow * nbf + strip] = sum;
+                        ws.actu[(size_t)arow * nbf + strip] = sf * (float)sum;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    // two buffers of raw words, alternating (the loop runs two steps per turn, so no copies)
+    Raw ra, rb2;
+    load(0, ra);
+    for (uint32_t step = 0; step < nstep; step += 2) {
+        step_on(step, ra, rb2);
+        if (step + 1 < nstep) step_on(step + 1, rb2, ra);
+    }
+}
+
+// gate/up + SwiGLU + per-16 requantisation + weight fold (tasks A and B of moe_batch).
+// Grid (F / 256, items): a workgroup covers 16 strips of F, each wave 4 of them.  Registers are
+// held to three waves per SIMD (the LDS fits three workgroups per CU): at config 4 that took the
+// kernel from 540 to 487 us against two waves, the few spilled words being on the small-item path.
+// LIST: the items in no pair (ws.single), after batch_gateup_pairs_kernel has run the pairs.
+template <int NSB, int LIST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void batch_gateup_kernel(
+        Mat gate, Mat up, Mat shg, Mat shu, Workspace ws, uint32_t skip_rows) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint32_t bx, itn;  // column block and item, in XCD order
+    if (!xcd_order(ws.n_groups[LIST ? 5 : 2], bx, itn)) return;
+    if (LIST) itn = ws.single[itn];
+    gateup_item<NSB>(gate, up, shg, shu, ws, skip_rows, bx, itn, smem);
+}
+
 hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up,
                                const Workspace& ws, uint32_t m, uint32_t skip_rows, hipStream_t st) {
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32;
     const size_t lds = (size_t)nb * 64 * 8 + (size_t)nb * 16 * 8 + 4 * 2 * 16 * DM_GU * 8 + 32 * 4;
     // a workgroup per (item, 16 strips) once the items fill the GPU; otherwise per (item, 4 strips)
     // so that a wave's chain of dependent weight loads stays short
-    const dim3 grid(geo::mfma_gateup_cols(m, F), grouped_item_rows(ws, m));
-    switch (H / 256) {
+    const uint32_t cols = geo::mfma_gateup_cols(m, F), rows = grouped_item_rows(ws, m);
+    // item pairs of one expert as 32-row tiles where experts have several items (config 4: ~4
+    // each), when no item streams and gate and up share one layout
+    const bool pairs = geo::gateup_pairs(m, H) && skip_rows == 0 && geo::gateup_pair_strips(m, F) % 8 == 0 &&
+                       gate.stride == up.stride && gate.row_bytes == up.row_bytes &&
+                       sh_gate.row_bytes == gate.row_bytes && sh_up.row_bytes == gate.row_bytes;
+    // the unpaired items (an expert's last when its count is odd) are one round of workgroups: a
+    // strip per wave keeps their chains short
+    const dim3 grid(cols, rows), pgrid(cols, rows / 2 + 1), sgrid(F % 64 == 0 ? F / 64 : cols, rows);
+    const size_t plds = (size_t)geo::gateup_pair_lds(H);
+    switch (H / 256 * 2 + (pairs ? 1 : 0)) {
 #define GU_CASE(n) \
-    case n: batch_gateup_kernel<n><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws, skip_rows); break;
-        GU_CASE(1) GU_CASE(2) GU_CASE(3) GU_CASE(4) GU_CASE(5) GU_CASE(6) GU_CASE(7) GU_CASE(8) GU_CASE(9)
+    case n * 2: batch_gateup_kernel<n, 0><<<grid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws, skip_rows); break;
+#define GU_CASE2(n)                                                                                     \
+    GU_CASE(n)                                                                                          \
+    case n * 2 + 1:                                                                                     \
+        batch_gateup_pairs_kernel<n><<<pgrid, 512, plds, st>>>(gate, up, sh_gate, sh_up, ws);           \
+        batch_gateup_kernel<n, 1><<<sgrid, 256, lds, st>>>(gate, up, sh_gate, sh_up, ws, skip_rows);     \
+        break;
+        GU_CASE2(1) GU_CASE2(2) GU_CASE2(3) GU_CASE2(4) GU_CASE2(5) GU_CASE2(6) GU_CASE2(7) GU_CASE2(8) GU_CASE(9)
         GU_CASE(10) GU_CASE(11) GU_CASE(12) GU_CASE(13) GU_CASE(14) GU_CASE(15) GU_CASE(16)
+#undef GU_CASE2
 #undef GU_CASE
         default: return hipErrorInvalidValue;
     }
@@ -1277,8 +1529,9 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
 
 // FK: 0 Q4_K, 1 Q6_K, 2 Q8_0, 3 Q5_1.  Q8_0's MFMA runs on the signed bytes; the unsigned dot of
 // q8_0_rows' form (blocks.py:71-78) adds 128 times the activation block's sum, in int32.
-// PR = 2 (large batches): a workgroup per item pair (2p, 2p + 1) in XCD order; a pair of one
-// expert runs as one group sharing the weights, other pairs one item after the other.
+// PR = 2 (large batches): the items of one expert pair up as (part 2j, 2j + 1); a pair runs in the
+// first item's workgroup as one group sharing the weights (the second's exits at once), other
+// items alone.  Config 4's Q6_K down 416 -> 400 us against pairs by item index (2p, 2p + 1).
 //
 // Q6_K's registers are held to four waves per SIMD (config 4's down 461 -> 450 us); the other
 // formats keep the compiler's allocation (held to four, the Q4_K small-item paths spill and the
@@ -1289,8 +1542,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
     const uint32_t H = down.rows, n_items = ws.n_groups[2], n_ent = ws.n_groups[1];
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t strips = H / 16 / gridDim.x;
-    uint32_t bx, grp;  // column block and item (pair), in XCD order
-    if (!xcd_order(PR == 2 ? (n_items + 1) / 2 : n_items, bx, grp)) return;
+    uint32_t bx, grp;  // column block and item, in XCD order
+    if (!xcd_order(n_items, bx, grp)) return;
     auto item_args = [&](const Item& it, uint32_t& e, uint32_t& arow0) -> const Mat& {
         const bool shared = it.expert == NO_EXPERT;
         e = shared ? 0u : it.expert;
@@ -1317,27 +1570,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4
         }
         down_items<NSB, FK, 1, 1>(D, e, its, a0, ws, H, strips, bx, smem);
     };
+    auto pair = [&](const Item& a, const Item& b) {  // consecutive items a, b that run as a pair
+        return b.expert == a.expert && a.nrows > skip_rows && b.nrows > skip_rows &&
+               (FK != 0 || (a.nrows > 8 && b.nrows > 8));
+    };
     if constexpr (PR == 1) {
         one(grp);
     } else {
-        const uint32_t i0 = 2 * grp, i1 = i0 + 1;
-        const Item it0 = ws.items[i0];
-        const Item it1 = i1 < n_items ? ws.items[i1] : it0;
-        const bool paired = i1 < n_items && it1.expert == it0.expert && it0.nrows > skip_rows &&
-                            it1.nrows > skip_rows && (FK != 0 || (it0.nrows > 8 && it1.nrows > 8));
-        if (paired) {
-            const Item its[2] = {it0, it1};
-            uint32_t e, a0[2], e1;
-            const Mat& D = item_args(it0, e, a0[0]);
-            item_args(it1, e1, a0[1]);
-            down_items<NSB, FK, 2>(D, e, its, a0, ws, H, strips, bx, smem);
-        } else {
-            one(i0);
-            if (i1 < n_items) {
-                __syncthreads();  // the first item's LDS reads are done before the second stages
-                one(i1);
+        // the items of one expert pair up as (part 2j, 2j + 1), run by the first item's workgroup
+        const Item it = ws.items[grp];
+        if (it.part % 2) {
+            const Item pv = ws.items[grp - 1];
+            if (pv.part + 1 == it.part && pair(pv, it)) return;
+        } else if (grp + 1 < n_items) {
+            const Item nx = ws.items[grp + 1];
+            if (nx.part == it.part + 1 && pair(it, nx)) {
+                const Item its[2] = {it, nx};
+                uint32_t e, a0[2], e1;
+                const Mat& D = item_args(it, e, a0[0]);
+                item_args(nx, e1, a0[1]);
+                down_items<NSB, FK, 2>(D, e, its, a0, ws, H, strips, bx, smem);
+                return;
             }
         }
+        one(grp);
     }
 }
 
@@ -1348,7 +1604,7 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     const int pr = geo::down_pairs(m) ? 2 : 1;
     const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 2 * 16 * DM_STRIDE * 8;
     const uint32_t rows = grouped_item_rows(ws, m);
-    const dim3 grid(geo::mfma_down_cols(m, H), pr == 2 ? (rows + 1) / 2 : rows);
+    const dim3 grid(geo::mfma_down_cols(m, H), rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
     const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
     switch ((F / 256 * 4 + fk) * 2 + pr - 1) {

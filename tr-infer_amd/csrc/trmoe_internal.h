@@ -41,9 +41,10 @@ struct Mat {
 };
 
 // Grouped-GEMM work item: `nrows` entry rows starting at `row0` of the sorted entries, all of
-// expert `expert` (expert == 0xffffffff: the shared expert, rows are tokens).
+// expert `expert` (expert == 0xffffffff: the shared expert, rows are tokens); `part` is the item's
+// index among its expert's items (row0 = the expert's first entry + 16 part).
 struct Item {
-    uint32_t expert, row0, nrows, pad;
+    uint32_t expert, row0, nrows, part;
 };
 constexpr uint32_t BR = 16;                  // most entry rows of an item: one 16-row MFMA tile
 constexpr uint32_t NO_EXPERT = 0xffffffffu;  // Item::expert of the shared expert's items
@@ -72,9 +73,11 @@ struct Workspace {
     uint32_t* ent_of;     // [m_max][32]: entry index of (token, slot)
     uint32_t* grp_start;  // [E + 2]
     uint32_t* grp_exp;    // [E + 1]
-    uint32_t* n_groups;   // [4]: n_groups, n_ent, n_items, pad
+    uint32_t* n_groups;   // [8]: n_groups, n_ent, n_items, pad, n_pairs, n_single, pad, pad
     uint32_t* doff;       // dispatch: [ceil(m_max / 64)][E] first entry of each (64-token chunk, expert)
     Item* items;          // [item_cap]
+    uint32_t* pairs;      // [item_cap / 2 + 1]: first item of each pair (parts 2j, 2j + 1 of one expert)
+    uint32_t* single;     // [item_cap]: the items in no pair (an expert's last when its count is odd)
     int8_t* actq;         // [act_rows][F] (decode: [33][2][F])
     float* acts;          // [act_rows][F/16]
     int32_t* actsum;
