@@ -111,10 +111,11 @@ def test_router_gemm_tiles_bit_exact(m):
     assert np.array_equal(host(lg).view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,E,H", [(1024, 512, 2048), (1100, 80, 512), (1057, 96, 2560), (3072, 512, 2048)])
+@pytest.mark.parametrize("m,E,H", [(512, 512, 2048), (700, 96, 768), (1024, 512, 2048), (1100, 80, 512),
+                                   (1057, 96, 2560), (3072, 512, 2048)])
 def test_router_mfma_bit_exact(m, E, H):
-    """The matrix-core router gemm (m >= 1024): the same bits as gemm_f32_nt's chains and halving
-    tree, with ragged token and expert tiles, a bias, and config 4's full shape."""
+    """The matrix-core router gemm (m >= 512): the same bits as gemm_f32_nt's chains and halving
+    tree, with ragged token and expert tiles, a bias, and the full shapes of configs 3 and 4."""
     say(f"router mfma m={m} E={E} H={H}")
     router = O.gen_normal(2, 1, E * H, 0.02).reshape(E, H)
     x = O.gen_normal(2, 5, m * H, 1.0).reshape(m, H)

@@ -489,10 +489,10 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         const uint32_t n_dot = shexp_gate ? (chunks + 3) / 4 : 0u;
         const uint32_t n_aux = n_dot + (xquant ? (m * (H / 32) * 4 + 255) / 256 : 0u);
         const XQuant& xq = xquant ? *xquant : none;
-        // the matrix-core gemm from 1024 rows (config 4: 160 -> 91 us); at 512 its 256 workgroups
-        // (one per CU) ran 36.5 us against the VALU tiles' 35.4.  64-wide chunks: 32 and 128 were
-        // no faster
-        if (m >= 1024 && H % 64 == 0) {
+        // the matrix-core gemm from 512 rows (config 4: 160 -> 91 us; M = 512: 35 -> 31 us, its 256
+        // workgroups one per CU).  64-wide chunks: 32 and 128 were no faster, nor chunks stored
+        // transposed so that a lane reads its four steps as one float4
+        if (m >= 512 && H % 64 == 0) {
             const uint32_t tiles = ((E + 31) / 32) * ((m + 31) / 32);
             router_mfma_kernel<64><<<tiles + n_aux, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shexp_gate, sh, xq,
                                                                   n_dot);
