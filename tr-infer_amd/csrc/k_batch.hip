@@ -495,6 +495,7 @@ __device__ __forceinline__ void stage_a16(const int8_t* __restrict__ src_rows, c
 
 constexpr uint32_t DM_STRIDE = 17;  // float2 per row of a wave's (dd, mm) table (16 + 1 against bank conflicts)
 constexpr uint32_t DM_GU = 9;       // the same for gate/up's 8 sub-blocks per row
+constexpr uint32_t DN_ZERO = 512;   // longs of zeros in the down's LDS: 8 chunks of 64 lanes apart
 
 __device__ __forceinline__ v4i mfma_i8_64_acc(v4i_t a, v4i_t b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -1351,6 +1352,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     static_assert(NS == 1 || NI == 1, "two strips per wave for one item");
     float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][NS][16][DM_STRIDE]
     int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * NS * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
+    long* Zr = reinterpret_cast<long*>(Ss + NI * nbf * 16);            // [DN_ZERO] zeros
 
     // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
     const uint32_t small = FK != 0 || NI != 1 || NS != 1 ? 0u : (its[0].nrows <= 4 && strips % 16 == 0) ? 4u
@@ -1403,6 +1405,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
             if constexpr (FK == 2) Ss[(it * nbf + o) * 16 + t] = tv[c];
         }
     }
+    for (uint32_t i = tid; i < DN_ZERO; i += 256) Zr[i] = 0;
     __syncthreads();
 
     if constexpr (FK == 0 && NI == 1) {
@@ -1425,6 +1428,17 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     const uint32_t tl = 4 * g + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
+        // The two MFMAs of a 32-wide chunk take its activations with the other 16-block's k-groups
+        // zeroed: lanes of the other half read a zero region instead (one pointer choice per step
+        // and item rather than two selects per chunk and register).
+        const long* alo[NI];
+        const long* ahi[NI];
+#pragma unroll
+        for (int it = 0; it < NI; it++) {
+            const long* a = As + (it * NQ + sb * 8) * 64 + lane;
+            alo[it] = g < 2 ? a : Zr;
+            ahi[it] = g < 2 ? Zr : a;
+        }
         typename std::decay<decltype(settle(lw[0]))>::type cws[NS];
 #pragma unroll
         for (int s = 0; s < NS; s++) {
@@ -1489,9 +1503,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
                 const float2 d0 = dm_s[r * DM_STRIDE + 2 * q8], d1 = dm_s[r * DM_STRIDE + 2 * q8 + 1];
 #pragma unroll
                 for (int it = 0; it < NI; it++) {
-                    const long af = As[(it * NQ + q) * 64 + lane];
-                    const long alo = g < 2 ? af : 0l, ahi = g < 2 ? 0l : af;
-                    v4i c0 = mfma_i8(alo, bw), c1 = mfma_i8(ahi, bw);
+                    v4i c0 = mfma_i8(alo[it][q8 * 64], bw), c1 = mfma_i8(ahi[it][q8 * 64], bw);
                     const float* sx = Sx + (it * nbf + 2 * q) * 16;
                     const float* su = Su + (it * nbf + 2 * q) * 16;
                     if constexpr (FK == 2) {
@@ -1602,7 +1614,8 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
     // item pairs sharing the weights where an expert has several items (config 4: ~4 per expert)
     const int pr = geo::down_pairs(m) ? 2 : 1;
-    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 2 * 16 * DM_STRIDE * 8;
+    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 2 * 16 * DM_STRIDE * 8 +
+                       DN_ZERO * 8;
     const uint32_t rows = grouped_item_rows(ws, m);
     const dim3 grid(geo::mfma_down_cols(m, H), rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
