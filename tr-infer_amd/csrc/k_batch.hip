@@ -1352,7 +1352,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     static_assert(NS == 1 || NI == 1, "two strips per wave for one item");
     float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][NS][16][DM_STRIDE]
     int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * NS * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
-    long* Zr = reinterpret_cast<long*>(Ss + NI * nbf * 16);            // [DN_ZERO] zeros
+    long* Zr = reinterpret_cast<long*>(Ss + (FK == 2 ? NI * nbf * 16 : 0));  // [DN_ZERO] zeros
 
     // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
     const uint32_t small = FK != 0 || NI != 1 || NS != 1 ? 0u : (its[0].nrows <= 4 && strips % 16 == 0) ? 4u
@@ -1614,12 +1614,15 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     const uint32_t H = down.rows, F = down.k, nbf = F / 16, NQ = F / 32;
     // item pairs sharing the weights where an expert has several items (config 4: ~4 per expert)
     const int pr = geo::down_pairs(m) ? 2 : 1;
-    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * 12) + 4 * 2 * 16 * DM_STRIDE * 8 +
-                       DN_ZERO * 8;
+    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
+    // per item: activations, scales, scale * sum and (Q8_0) the sums; the (dd, mm) tables of four
+    // waves for two strips each (one for Q6_K, which walks one strip at a time); the zero region.
+    // Q6_K: 36.5 KB at F = 512, four workgroups per CU (the four waves per SIMD it is held to)
+    const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * (fk == 2 ? 12 : 8)) +
+                       4 * (fk == 1 ? 1 : 2) * 16 * DM_STRIDE * 8 + DN_ZERO * 8;
     const uint32_t rows = grouped_item_rows(ws, m);
     const dim3 grid(geo::mfma_down_cols(m, H), rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
-    const int fk = down.fmt == TRK_FMT_Q6_K ? 1 : down.fmt == TRK_FMT_Q8_0 ? 2 : down.fmt == TRK_FMT_Q5_1 ? 3 : 0;
     switch ((F / 256 * 4 + fk) * 2 + pr - 1) {
 #define DN_CASE(n, f)                                                                                          \
     case (n * 4 + f) * 2: batch_down_kernel<n, f, 1><<<grid, 256, lds, st>>>(down, sh_down, ws, skip_rows); break; \
