@@ -1350,8 +1350,10 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     float* Sx = reinterpret_cast<float*>(smem + NI * NQ * 64 * 8);     // [NI][nbf][16] folded scales
     float* Su = Sx + NI * nbf * 16;                                    // [NI][nbf][16] scale * sum
     static_assert(NS == 1 || NI == 1, "two strips per wave for one item");
-    float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][NS][16][DM_STRIDE]
-    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * NS * 16 * DM_STRIDE);  // [NI][nbf][16] sums (Q8_0)
+    // (dd, mm) per row: Q6_K's 16 blocks; the other formats' 8 (a 32-block's two 16-blocks share it)
+    constexpr uint32_t DS = Q6 ? DM_STRIDE : 9;
+    float2* Dm = reinterpret_cast<float2*>(Su + NI * nbf * 16);        // [4 waves][NS][16][DS]
+    int32_t* Ss = reinterpret_cast<int32_t*>(Dm + 4 * NS * 16 * DS);   // [NI][nbf][16] sums (Q8_0)
     long* Zr = reinterpret_cast<long*>(Ss + (FK == 2 ? NI * nbf * 16 : 0));  // [DN_ZERO] zeros
 
     // small Q4_K items: several strips per MFMA output (a wave owns strips / 4 strips)
@@ -1421,7 +1423,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
     W lw[NS];  // issued here rather than before the staging: held across it, it cost the Q4_K kernel a wave per SIMD
 #pragma unroll
     for (int s = 0; s < NS; s++) load(0, s, lw[s]);
-    float2* dmw = Dm + wv * NS * 16 * DM_STRIDE;
+    float2* dmw = Dm + wv * NS * 16 * DS;
     v4f acc[NI * NS];
 #pragma unroll
     for (int it = 0; it < NI * NS; it++) acc[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1450,37 +1452,30 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const auto& cw = cws[s];
-            float2* dm_s = dmw + s * 16 * DM_STRIDE;
+            float2* dm_s = dmw + s * 16 * DS;
             if constexpr (Q6) {
                 const float d = h2f(cw.d);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float dd = f16_round(d * (float)(int8_t)((cw.sc >> (8 * i)) & 0xffu));
-                    dm_s[r * DM_STRIDE + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
+                    dm_s[r * DS + 4 * g + i] = make_float2(dd, f16_round(-32.0f * dd));
                 }
             } else if constexpr (FK == 3) {
 #pragma unroll
                 for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
                     const uint32_t dm = jj ? cw.dm1 : cw.dm0;
-                    const float2 v = make_float2(h2f((uint16_t)(dm & 0xffffu)), h2f((uint16_t)(dm >> 16)));
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                    dm_s[r * DS + 2 * g + jj] = make_float2(h2f((uint16_t)(dm & 0xffffu)), h2f((uint16_t)(dm >> 16)));
                 }
             } else if constexpr (FK == 2) {
 #pragma unroll
                 for (int jj = 0; jj < 2; jj++) {  // block 2g + jj covers 16-blocks 4g + 2jj, +1
                     const float dd = h2f((uint16_t)(jj ? cw.d1 >> 16 : cw.d0 & 0xffffu));
-                    const float2 v = make_float2(dd, f16_round(-128.0f * dd));
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
+                    dm_s[r * DS + 2 * g + jj] = make_float2(dd, f16_round(-128.0f * dd));
                 }
             } else {
 #pragma unroll
-                for (int jj = 0; jj < 2; jj++) {  // sub-block 2g + jj covers blocks 4g + 2jj, +1
-                    const float2 v = q4k_dm_rt(cw.hdr, 2 * g + jj);
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj] = v;
-                    dm_s[r * DM_STRIDE + 4 * g + 2 * jj + 1] = v;
-                }
+                for (int jj = 0; jj < 2; jj++)  // sub-block 2g + jj covers blocks 4g + 2jj, +1
+                    dm_s[r * DS + 2 * g + jj] = q4k_dm_rt(cw.hdr, 2 * g + jj);
             }
         }
         wave_sync();
@@ -1499,8 +1494,9 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
                     bw = q51_operand(cw, q8, g);
                 else
                     bw = unpack8(cw.qs[q8 / 2], q8 % 2);
-                const float2* dm_s = dmw + s * 16 * DM_STRIDE;
-                const float2 d0 = dm_s[r * DM_STRIDE + 2 * q8], d1 = dm_s[r * DM_STRIDE + 2 * q8 + 1];
+                const float2* dm_s = dmw + s * 16 * DS;
+                const float2 d0 = Q6 ? dm_s[r * DS + 2 * q8] : dm_s[r * DS + q8];
+                const float2 d1 = Q6 ? dm_s[r * DS + 2 * q8 + 1] : d0;
 #pragma unroll
                 for (int it = 0; it < NI; it++) {
                     v4i c0 = mfma_i8(alo[it][q8 * 64], bw), c1 = mfma_i8(ahi[it][q8 * 64], bw);
@@ -1549,7 +1545,7 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
 // formats keep the compiler's allocation (held to four, the Q4_K small-item paths spill and the
 // M = 512 down slows from 125.7 to 128-130 us).
 template <int NSB, int FK, int PR>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK == 1 ? 4 : 1))) void batch_down_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FK <= 1 ? 4 : 1))) void batch_down_kernel(
         Mat down, Mat shd, Workspace ws, uint32_t skip_rows) {
     const uint32_t H = down.rows, n_items = ws.n_groups[2], n_ent = ws.n_groups[1];
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1619,7 +1615,7 @@ hipError_t launch_batch_down(const Mat& down, const Mat& sh_down, const Workspac
     // waves for two strips each (one for Q6_K, which walks one strip at a time); the zero region.
     // Q6_K: 36.5 KB at F = 512, four workgroups per CU (the four waves per SIMD it is held to)
     const size_t lds = (size_t)pr * ((size_t)NQ * 64 * 8 + (size_t)nbf * 16 * (fk == 2 ? 12 : 8)) +
-                       4 * (fk == 1 ? 1 : 2) * 16 * DM_STRIDE * 8 + DN_ZERO * 8;
+                       4 * (fk == 1 ? 1 : 2) * 16 * (fk == 1 ? DM_STRIDE : 9) * 8 + DN_ZERO * 8;
     const uint32_t rows = grouped_item_rows(ws, m);
     const dim3 grid(geo::mfma_down_cols(m, H), rows);
     if (down.fmt != sh_down.fmt) return hipErrorInvalidValue;  // one format per layer
