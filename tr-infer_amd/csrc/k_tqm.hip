@@ -156,12 +156,13 @@ __device__ __forceinline__ bool tqm_unit(const Workspace& ws, bool gu, int decod
 }
 
 // Stage the unit's activation rows (K bytes each, int8) in operand order As[unit b][lane] (8 bytes:
-// row l % 16, k 32b + 8 (l / 16) ..), zero for rows past np, and their per-block (scale, u, byte
-// sum) in Sc[block][row] (blocks of kbs values).
+// row l % 16, k 32b + 8 (l / 16) ..), zero for rows past np, and their per-block (scale, u) in
+// Sc[block][row] (blocks of kbs values), with the byte sum as a third word for the 8-bit codecs
+// (SC = 4 floats per entry; 2 otherwise).
 template <int KBS, bool XSUM>
 __device__ __forceinline__ void tqm_stage(const int8_t* __restrict__ q, const float* __restrict__ s,
                                           const float* __restrict__ u, const uint32_t* prow, uint32_t np, uint32_t K,
-                                          long* As, float4* Sc, uint32_t tid, uint32_t nthr) {
+                                          long* As, float* Sc, uint32_t tid, uint32_t nthr) {
     const uint32_t nu = K / 32, nbs = K / KBS;
     // rows past np are zero in the operand (LDS stores only)
     if (np < 16)
@@ -213,7 +214,12 @@ __device__ __forceinline__ void tqm_stage(const int8_t* __restrict__ q, const fl
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t i = i0 + tid + nthr * c;
-            if (i < ns) Sc[i] = v[c];
+            if (i < ns) {
+                if constexpr (XSUM)
+                    reinterpret_cast<float4*>(Sc)[i] = v[c];
+                else
+                    reinterpret_cast<float2*>(Sc)[i] = make_float2(v[c].x, v[c].y);
+            }
         }
     }
 }
@@ -226,12 +232,13 @@ __device__ __forceinline__ void tqm_stage(const int8_t* __restrict__ q, const fl
 // time with it (the MFMA latency on every block of the chain), and decode keeps the VALU form too.
 template <int GK, int KB, bool R1>
 __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uint32_t K, const long* As,
-                                          const float4* Sc, uint32_t l, float (&acc)[4]) {
+                                          const float* Sc, uint32_t l, float (&acc)[4]) {
     // the walk over K is sequential per wave (the chain), so the loads run UB units ahead (about
     // 64 VGPRs of raw words)
     constexpr uint32_t UB0 = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
     constexpr uint32_t UB = R1 ? (UB0 / 4 > 0 ? UB0 / 4 : 1u) : UB0;
     constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
+    constexpr uint32_t SC = U8 ? 4 : 2;  // floats per Sc entry
     const uint32_t nu = K / 32, g = l / 16, tl = 4 * g + (l & 3);
     for (int v = 0; v < 4; v++) acc[v] = 0.0f;
     v4f a4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -257,21 +264,21 @@ __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uin
                 const uint32_t blk = NBL * b + hb;
                 const float dd = h2f((uint16_t)cw.d[hb]), mm = h2f((uint16_t)cw.m[hb]);
                 if constexpr (R1) {
-                    const float2 su = *reinterpret_cast<const float2*>(&Sc[blk * 16 + tl]);
+                    const float2 su = *reinterpret_cast<const float2*>(&Sc[(blk * 16 + tl) * SC]);
                     a4 = rank1(su.y, mm, a4);
                     const v4f ds = rank1(su.x, dd, neg_zero4());
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        const int dot = U8 ? d4[v] + 128 * __float_as_int(Sc[blk * 16 + 4 * g + v].z) : d4[v];
+                        const int dot = U8 ? d4[v] + 128 * __float_as_int(Sc[(blk * 16 + 4 * g + v) * SC + 2]) : d4[v];
                         a4[v] = __builtin_fmaf((float)dot, ds[v], a4[v]);
                     }
                 } else {
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        const float4 sx = Sc[blk * 16 + 4 * g + v];
-                        const int dot = U8 ? d4[v] + 128 * __float_as_int(sx.z) : d4[v];
-                        acc[v] = __builtin_fmaf(mm, sx.y, acc[v]);
-                        acc[v] = __builtin_fmaf((float)dot, dd * sx.x, acc[v]);
+                        const float* sx = Sc + (blk * 16 + 4 * g + v) * SC;
+                        const int dot = U8 ? d4[v] + 128 * __float_as_int(sx[2]) : d4[v];
+                        acc[v] = __builtin_fmaf(mm, sx[1], acc[v]);
+                        acc[v] = __builtin_fmaf((float)dot, dd * sx[0], acc[v]);
                     }
                 }
             }
@@ -286,11 +293,12 @@ __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uin
 // waves of that kernel chain several strips each; two independent chains fill the latency of one.
 template <int GK, int KB>
 __device__ __forceinline__ void tqm_strip2(const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, uint32_t K,
-                                           const long* As, const float4* Sc, uint32_t l, float (&acc0)[4],
+                                           const long* As, const float* Sc, uint32_t l, float (&acc0)[4],
                                            float (&acc1)[4]) {
     constexpr uint32_t UB0 = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
     constexpr uint32_t UB = UB0 / 2 > 0 ? UB0 / 2 : 1u;
     constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
+    constexpr uint32_t SC = U8 ? 4 : 2;  // floats per Sc entry
     const uint32_t nu = K / 32, g = l / 16;
     for (int v = 0; v < 4; v++) acc0[v] = acc1[v] = 0.0f;
     TqmB<GK, KB> w0[UB], w1[UB];
@@ -322,12 +330,12 @@ __device__ __forceinline__ void tqm_strip2(const uint8_t* __restrict__ s0, const
                 const float dd1 = h2f((uint16_t)c1.d[hb]), mm1 = h2f((uint16_t)c1.m[hb]);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const float4 sx = Sc[blk * 16 + 4 * g + v];
-                    const int xs = U8 ? 128 * __float_as_int(sx.z) : 0;
-                    acc0[v] = __builtin_fmaf(mm0, sx.y, acc0[v]);
-                    acc0[v] = __builtin_fmaf((float)(d40[v] + xs), dd0 * sx.x, acc0[v]);
-                    acc1[v] = __builtin_fmaf(mm1, sx.y, acc1[v]);
-                    acc1[v] = __builtin_fmaf((float)(d41[v] + xs), dd1 * sx.x, acc1[v]);
+                    const float* sx = Sc + (blk * 16 + 4 * g + v) * SC;
+                    const int xs = U8 ? 128 * __float_as_int(sx[2]) : 0;
+                    acc0[v] = __builtin_fmaf(mm0, sx[1], acc0[v]);
+                    acc0[v] = __builtin_fmaf((float)(d40[v] + xs), dd0 * sx[0], acc0[v]);
+                    acc1[v] = __builtin_fmaf(mm1, sx[1], acc1[v]);
+                    acc1[v] = __builtin_fmaf((float)(d41[v] + xs), dd1 * sx[0], acc1[v]);
                 }
             }
         }
@@ -397,24 +405,24 @@ template <int GK, int NJ>
 __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t prow[2 * BR], orow[BR];
-    __shared__ float hu[2][2][64][4];  // up accumulators of two strip pairs x two strips, by lane
+    constexpr uint32_t SC = GK == GK_TQ8 ? 4 : 2;  // floats per Sc entry
     const Workspace& ws = g.ws;
     const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
     long* As = reinterpret_cast<long*>(smem);                     // [H / 32][64]
-    float4* Sc = reinterpret_cast<float4*>(As + (size_t)(H / 32) * 64);  // [H / 32][16]
+    float* Sc = reinterpret_cast<float*>(As + (size_t)(H / 32) * 64);  // [H / 32][16][SC]
+    // decode: MassBasis::All's exponentials during the routing, then the up accumulators
+    float* tail = Sc + (size_t)(H / 32) * 16 * SC;
     uint32_t ns = 0;
     const uint32_t* ids = ws.ids;
     const float* wsel = ws.w;
     if constexpr (NJ > 0) {
-        // the decode routing on wave 0 (the others wait at the barrier); MassBasis::All's
-        // exponentials in the LDS behind the staged activations
+        // the decode routing on wave 0 (the others wait at the barrier)
         __shared__ uint2 cand[ROUTE_CAND];
         __shared__ uint32_t r_ids[K_MAX];
         __shared__ float r_w[K_MAX];
         __shared__ uint32_t r_n;
-        float* ex = reinterpret_cast<float*>(Sc + (size_t)(H / 32) * 16);
         if (wv == 0) {
-            const uint32_t n = route_row<NJ>(g.lg, ws.E, g.k, g.pol, l, cand, ex, r_ids, r_w);
+            const uint32_t n = route_row<NJ>(g.lg, ws.E, g.k, g.pol, l, cand, tail, r_ids, r_w);
             if (l == 0) r_n = n;
         }
         __syncthreads();
@@ -444,38 +452,41 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     tqm_stage<32, GK == GK_TQ8>(ws.xq, ws.xs, ws.xu, prow, nr * P, H, As, Sc, tid, 256);
     __syncthreads();
     const uint32_t gq = l / 16, r = l % 16, n_ent = ws.n_groups[1];
+    const Mat& Ga = shared ? g.sha : g.a;
+    const Mat& Ub = shared ? g.shb : g.b;
+    if (NJ == 0 && !g.decode) {
+        // Batch: four strips per pass (strip pairs blockIdx.x and blockIdx.x + gridDim.x, then every
+        // 2 gridDim.x further); a wave takes one strip, its gate and up rows as two chains over the
+        // staged activations (tqm_strip2), and finishes it with SwiGLU itself, so no accumulators
+        // cross waves and the LDS holds only the activations (three workgroups per CU at the real
+        // shape)
+        for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += 2 * gridDim.x) {
+            const uint32_t strip = wv < 2 ? 2 * sp + wv : 2 * (sp + gridDim.x) + wv - 2;
+            if (strip >= F / 16) continue;  // wave-uniform
+            float acc[4], accu[4];
+            tqm_strip2<GK, 32>(Ga.ptr + (size_t)e * Ga.stride + (size_t)strip * Ga.row_bytes,
+                               Ub.ptr + (size_t)e * Ub.stride + (size_t)strip * Ub.row_bytes, H, As, Sc, l, acc, accu);
+            tqm_swiglu_store(ws, 0, 0, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc, accu, ns, wsel);
+        }
+        return;
+    }
+    // decode: waves 2i, 2i + 1 = gate and up of strip 2 blockIdx.x + i; the up wave hands its
+    // accumulators over in LDS
+    float (*hu)[64][4] = reinterpret_cast<float (*)[64][4]>(tail);  // [2 strips][64][4]
     const bool up = wv % 2 == 1;
-    // strip pairs blockIdx.x, + gridDim.x, ...: the staged activations serve them all.  Batch: two
-    // pairs per pass, a wave walking its strip of each as two chains (tqm_strip2)
-    const uint32_t per = NJ == 0 && !g.decode ? 2u : 1u;  // (NJ > 0: decode, its registers untouched)
-    for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += per * gridDim.x) {
-        const uint32_t strip = 2 * sp + wv / 2, strip1 = 2 * (sp + gridDim.x) + wv / 2;
-        const bool live = strip < F / 16, two = per == 2 && 2 * (sp + gridDim.x) < F / 16;  // two: uniform
-        const bool live1 = two && strip1 < F / 16;  // implies live
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t sp = blockIdx.x; 2 * sp < F / 16; sp += gridDim.x) {
+        const uint32_t strip = 2 * sp + wv / 2;
+        const bool live = strip < F / 16;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
-            const Mat& M = up ? (shared ? g.shb : g.b) : (shared ? g.sha : g.a);
-            const uint8_t* p0 = M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes;
-            if constexpr (NJ == 0) {
-                if (two)  // a strip past F repeats the first one's walk; its result is dropped
-                    tqm_strip2<GK, 32>(p0, live1 ? M.ptr + (size_t)e * M.stride + (size_t)strip1 * M.row_bytes : p0,
-                                       H, As, Sc, l, acc, acc1);
-                else
-                    tqm_strip<GK, 32, false>(p0, H, As, Sc, l, acc);
-            } else {
-                tqm_strip<GK, 32, false>(p0, H, As, Sc, l, acc);
-            }
+            const Mat& M = up ? Ub : Ga;
+            tqm_strip<GK, 32, false>(M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes, H, As, Sc, l, acc);
         }
         if (up)
-            for (int v = 0; v < 4; v++) {
-                hu[0][wv / 2][l][v] = acc[v];
-                hu[1][wv / 2][l][v] = acc1[v];
-            }
+            for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
         __syncthreads();
         if (!up && live) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
-                                          hu[0][wv / 2][l], ns, wsel);
-        if (!up && live1) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip1, gq, r, acc1,
-                                           hu[1][wv / 2][l], ns, wsel);
+                                          hu[wv / 2][l], ns, wsel);
         __syncthreads();  // hu read before the next pass writes it
     }
 }
@@ -493,7 +504,7 @@ __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
                   g.decode ? ws.n_sel[0] : 0u, ws.ids))
         return;
     long* As = reinterpret_cast<long*>(smem);                        // [F / 32][64]
-    float4* Sc = reinterpret_cast<float4*>(As + (size_t)(F / 32) * 64);  // [F / 16][16]
+    float* Sc = reinterpret_cast<float*>(As + (size_t)(F / 32) * 64);  // [F / 16][16][SC]
     __syncthreads();
     tqm_stage<16, GK == GK_TQ8>(ws.actq, ws.acts, ws.actu, prow, nr * P, F, As, Sc, tid, 256);
     __syncthreads();
@@ -526,8 +537,12 @@ hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate,
     // real shape: 478 / 484 us against 460 for 4)
     const uint32_t pairs = (ws.F / 16 + 1) / 2;
     const dim3 grid(m == 1 ? pairs : (pairs + TQM_PAIRS - 1) / TQM_PAIRS, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
-    size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * 16;
-    if (nj && pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;  // route_row's exponentials
+    const size_t sc = tq_bits(gate.fmt) == 8 ? 16 : 8;  // bytes per Sc entry
+    size_t lds = (size_t)(ws.H / 32) * 64 * 8 + (size_t)(ws.H / 32) * 16 * sc;
+    if (m == 1) {  // decode: the up accumulators of two strips; route_row's exponentials before them
+        const size_t ex = nj && pol.enabled && pol.basis == TRK_BASIS_ALL ? (size_t)ws.E * 4 : 0;
+        lds += ex > 2 * 64 * 4 * 4 ? ex : 2 * 64 * 4 * 4;
+    }
     switch (tq_bits(gate.fmt) * 100 + nj) {
 #define TQM_GU(b, gk)                                                                 \
     case b * 100: tqm_gateup_kernel<gk, 0><<<grid, 256, lds, st>>>(a); break;         \
