@@ -328,7 +328,7 @@ __device__ __forceinline__ float chains_sum(float v) {  // lanes 4j + u, over j:
     v = v + dpp_f<0x124>(v);                            // row_ror:4: j +- 1, equal after the step before
     return v;
 }
-template <int KC>
+template <int KC, int NB>
 __global__ __launch_bounds__(256) void router_mfma_kernel(const float* __restrict__ router,
                                                          const float* __restrict__ bias,
                                                          const float* __restrict__ x, uint32_t m, uint32_t E,
@@ -336,7 +336,9 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float* __restric
                                                          const float* __restrict__ shg, float* __restrict__ sh,
                                                          XQuant xquant, uint32_t n_dot) {
     // row pitch 8 mod 32 words: the 4 rows x 8 columns each half-wave reads fall in 32 distinct banks
-    constexpr int TM = 32, TE = 32, XK = KC + 8;
+    // NB = 4: a wave holds 16 tokens x 16 experts (32 x 32 per workgroup); NB = 2: 16 x 8 (twice
+    // the workgroups for the same rows, where one 32 x 32 tile per CU left a wave per SIMD)
+    constexpr int TM = 32, TE = 8 * NB, XK = KC + 8;
     // tiles first, the aux workgroups after them; the tiles in XCD order (xcd_order): an XCD takes
     // a contiguous run of tiles, so the expert tiles of one token tile share its L2's copy of x
     const uint32_t tiles_e = (E + TE - 1) / TE, tiles = tiles_e * ((m + TM - 1) / TM);
@@ -382,24 +384,24 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float* __restric
             reinterpret_cast<float2*>(dst)[1] = make_float2(st[i].z, st[i].w);
         }
     };
-    v4f acc[4][4];
+    v4f acc[4][NB];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < NB; b++) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
 #pragma unroll
         for (int s = 0; s < KC / 16; s++) {
             const uint32_t c = 16 * s + j;
-            float xv[4], wvv[4];
+            float xv[4], wvv[NB];
 #pragma unroll
             for (int a = 0; a < 4; a++) xv[a] = xs[buf][16 * wm + 4 * a + u][c];
 #pragma unroll
-            for (int b = 0; b < 4; b++) wvv[b] = wsm[buf][16 * we + 4 * b + u][c];
+            for (int b = 0; b < NB; b++) wvv[b] = wsm[buf][4 * NB * we + 4 * b + u][c];
 #pragma unroll
             for (int a = 0; a < 4; a++)
 #pragma unroll
-                for (int b = 0; b < 4; b++) acc[a][b] = rank1(xv[a], wvv[b], acc[a][b]);
+                for (int b = 0; b < NB; b++) acc[a][b] = rank1(xv[a], wvv[b], acc[a][b]);
         }
     };
     const uint32_t nchunk = H / KC;
@@ -418,26 +420,26 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float* __restric
         compute(1);
         __syncthreads();
     }
-    // every lane ends with all 16 (a, b) sums; lane (j, u) stores tile (a, b) = (j / 4, j % 4):
-    // tokens 4a + v, expert 4b + u
+    // every lane ends with all 4 NB (a, b) sums; lane (j, u), j < 4 NB, stores tile (a, b) =
+    // (j / NB, j % NB): tokens 4a + v, expert 4b + u
     float outv[4];
 #pragma unroll
     for (int v = 0; v < 4; v++) outv[v] = 0.0f;
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const float t = chains_sum(acc[a][b][v]);
-                outv[v] = j == (uint32_t)(4 * a + b) ? t : outv[v];
+                outv[v] = j == (uint32_t)(NB * a + b) ? t : outv[v];
             }
-    const uint32_t ex = e0 + 16 * we + 4 * (j % 4) + u;
-    if (ex < E) {
+    const uint32_t ex = e0 + 4 * NB * we + 4 * (j % NB) + u;
+    if (j < 4 * NB && ex < E) {
         const float bb = bias ? bias[ex] : 0.0f;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const uint32_t row = m0 + 16 * wm + 4 * (j / 4) + v;
+            const uint32_t row = m0 + 16 * wm + 4 * (j / NB) + v;
             if (row < m) rlog[(size_t)row * E + ex] = bias ? outv[v] + bb : outv[v];
         }
     }
@@ -492,9 +494,14 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
         // the matrix-core gemm from 512 rows (config 4: 160 -> 91 us; M = 512: 35 -> 31 us, its 256
         // workgroups one per CU).  64-wide chunks: 32 and 128 were no faster, nor chunks stored
         // transposed so that a lane reads its four steps as one float4
-        if (m >= 512 && H % 64 == 0) {
+        if (m >= 512 && H % 64 == 0 && m < 1024) {  // 16 x 8 per wave: two waves per SIMD at M = 512
+            const uint32_t tiles = ((E + 15) / 16) * ((m + 31) / 32);
+            router_mfma_kernel<64, 2><<<tiles + n_aux, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shexp_gate, sh, xq,
+                                                                    n_dot);
+            return hipGetLastError();
+        } else if (m >= 512 && H % 64 == 0) {
             const uint32_t tiles = ((E + 31) / 32) * ((m + 31) / 32);
-            router_mfma_kernel<64><<<tiles + n_aux, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shexp_gate, sh, xq,
+            router_mfma_kernel<64, 4><<<tiles + n_aux, 256, 0, st>>>(router, bias, x, m, E, H, rlog, shexp_gate, sh, xq,
                                                                   n_dot);
             return hipGetLastError();
         }
