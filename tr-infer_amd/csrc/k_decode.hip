@@ -409,7 +409,10 @@ __device__ __forceinline__ const uint8_t* down_unit_row(const Mat& down, const M
     const uint8_t* base = sh ? shd.ptr : down.ptr;
     const uint64_t stride = sh ? shd.stride : down.stride;
     const uint32_t rb = sh ? shd.row_bytes : down.row_bytes;
-    const uint32_t e = (sh || !live) ? 0u : ids[s];
+    // the id is requested with the count rather than after it (slots below kcap are inside the id
+    // row; a slot past the count is never used)
+    const uint32_t eid = s < kcap ? ids[s] : 0u;
+    const uint32_t e = (sh || !live) ? 0u : eid;
     return base + (size_t)e * stride + (size_t)(row0 + r) * rb;
 }
 
