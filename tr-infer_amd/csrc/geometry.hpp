@@ -57,7 +57,10 @@ inline uint32_t mfma_gateup_strips(uint32_t m, uint32_t F) { return F / 16 / mfm
 // two workgroups per CU up to H = 2048.
 inline bool gateup_pairs(uint32_t m, uint32_t H) { return m >= 2048 && H <= 2048; }
 inline uint64_t gateup_pair_lds(uint32_t H) { return (uint64_t)H * 40; }
-inline uint32_t gateup_pair_strips(uint32_t m, uint32_t F) { return mfma_gateup_strips(m, F); }
+// a pair's workgroup takes 32 strips (four per wave) where F allows: the 80 KB of staged
+// activations then serve twice the weights (config 4 gate/up 500 -> 483 us against 16 strips)
+inline uint32_t gateup_pair_cols(uint32_t m, uint32_t F) { return F % 512 == 0 ? F / 512 : mfma_gateup_cols(m, F); }
+inline uint32_t gateup_pair_strips(uint32_t m, uint32_t F) { return F / 16 / gateup_pair_cols(m, F); }
 // MFMA down: grid.x blocks of 256 or 64 output rows, four waves of 16-row strips
 inline uint32_t mfma_down_cols(uint32_t m, uint32_t H) { return m >= 64 ? H / 256 : H / 64; }
 inline uint32_t mfma_down_rows(uint32_t m, uint32_t H) { return H / mfma_down_cols(m, H); }

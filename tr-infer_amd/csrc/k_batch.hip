@@ -1059,7 +1059,7 @@ hipError_t launch_batch_gateup(const Mat& gate, const Mat& up, const Mat& sh_gat
                        sh_gate.row_bytes == gate.row_bytes && sh_up.row_bytes == gate.row_bytes;
     // the unpaired items (an expert's last when its count is odd) are one round of workgroups: a
     // strip per wave keeps their chains short
-    const dim3 grid(cols, rows), pgrid(cols, rows / 2 + 1), sgrid(F % 64 == 0 ? F / 64 : cols, rows);
+    const dim3 grid(cols, rows), pgrid(geo::gateup_pair_cols(m, F), rows / 2 + 1), sgrid(F % 64 == 0 ? F / 64 : cols, rows);
     const size_t plds = (size_t)geo::gateup_pair_lds(H);
     switch (H / 256 * 2 + (pairs ? 1 : 0)) {
 #define GU_CASE(n) \
