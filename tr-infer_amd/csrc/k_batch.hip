@@ -989,6 +989,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
         // quantise one tile row's strip.
         const uint32_t strip = strip_of(step);
         const Item& it = odd ? it1 : it0;
+        // the first output row of this lane's item, opaque to the compiler: otherwise it hoists the
+        // 16 row addresses below out of the strip loop and keeps them in scratch memory (spill
+        // traffic through HBM on every strip)
+        uint32_t arow0 = shared ? n_ent + it.row0 : it.row0;
+        asm volatile("" : "+v"(arow0));
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
 #pragma unroll
@@ -1007,7 +1012,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
                 const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
                 const float w = __shfl(wgt_c, (int)t);
                 if (row < it.nrows) {
-                    const uint32_t arow = shared ? n_ent + it.row0 + row : it.row0 + row;
+                    const uint32_t arow = arow0 + row;
                     ws.actq[(size_t)arow * F + strip * 16 + c % 16] = sat_i8(qi);
                     if (c % 16 == 0) {
                         const float sf = s * w;  // exec_batch.rs:1533-1535
