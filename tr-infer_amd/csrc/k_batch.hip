@@ -615,6 +615,10 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
         cw = nw;
         if (sb == NSB - 1) {
             const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + own);
+            // the item's first output row, opaque to the compiler so that it does not hoist the row
+            // addresses below out of the strip loop into scratch memory
+            uint32_t arow0 = shared ? n_ent + item.row0 : item.row0;
+            asm volatile("" : "+v"(arow0));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = orow + i;
@@ -626,7 +630,7 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
                 const int32_t qi = cvt_rne(v * inv);
                 const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
                 if (row < item.nrows) {
-                    const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
+                    const uint32_t arow = arow0 + row;
                     ws.actq[(size_t)arow * F + strip * 16 + r] = sat_i8(qi);
                     if (r == 0) {
                         const float sf = sc * wgt[i];  // exec_batch.rs:1533-1535
@@ -790,6 +794,9 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
             // SwiGLU (elem.rs:173) and per-16 quantisation across the 16 lanes holding one entry's
             // strip (lanes 16g .. 16g+15, one DPP row)
             const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
+            // the item's first output row, opaque to the compiler (as in gateup_strips)
+            uint32_t arow0 = shared ? n_ent + item.row0 : item.row0;
+            asm volatile("" : "+v"(arow0));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = 4 * g + i;
@@ -801,7 +808,7 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
                 const int32_t qi = cvt_rne(v * inv);
                 const int32_t sum = row16_allreduce(qi, [](int32_t x, int32_t y) { return x + y; });
                 if (row < item.nrows) {
-                    const uint32_t arow = shared ? n_ent + item.row0 + row : item.row0 + row;
+                    const uint32_t arow = arow0 + row;
                     ws.actq[(size_t)arow * F + strip * 16 + r] = sat_i8(qi);
                     if (r == 0) {
                         const float sf = s * wgt[i];  // exec_batch.rs:1533-1535
