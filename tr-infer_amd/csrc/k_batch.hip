@@ -474,21 +474,30 @@ __device__ __forceinline__ void load_q4sb16(const uint8_t* __restrict__ rowp, ui
     for (int c = 0; c < 2; c++) w.q[c] = *reinterpret_cast<const v4i_t*>(p + 16 + 64 * c + 16 * g);
 }
 // Activation rows staged as [block][half][row] 16-byte pieces: lane (g, r) reads half g % 2 of a
-// block of entry row r.
+// block of entry row r.  The row of piece p sits at slot r ^ a16_swz(p) of the piece's 16: each
+// four consecutive staging lanes read 64 contiguous bytes of one row (pieces 4j .. 4j + 3), and the
+// swizzle puts the 16 lanes of a quarter-wave (four rows, four pieces) in 16 different 16-byte
+// bank groups, also its two halves in 8; the plain [piece][row] order put them all in one.
+__device__ __forceinline__ uint32_t a16_swz(uint32_t p) {
+    const uint32_t b = p % 4;
+    return 4 * b + 2 * (b / 2);
+}
 __device__ __forceinline__ void stage_a16(const int8_t* __restrict__ src_rows, const uint32_t* rowoff, uint32_t K,
                                           v4i_t* As, uint32_t tid) {
-    const uint32_t pieces = K / 16;  // 16-byte pieces per row = (block, half)
+    const uint32_t pieces = K / 16;  // 16-byte pieces per row = (block, half); a multiple of 4
     for (uint32_t i0 = 0; i0 < 16 * pieces; i0 += 2048) {
         v4i_t v[8];
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * pieces ? i : 16 * pieces - 1;
-            v[c] = *reinterpret_cast<const v4i_t*>(src_rows + (size_t)rowoff[ic / pieces] + (ic % pieces) * 16);
+            const uint32_t row = (ic / 4) % 16, pc = 4 * (ic / 64) + ic % 4;
+            v[c] = *reinterpret_cast<const v4i_t*>(src_rows + (size_t)rowoff[row] + pc * 16);
         }
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const uint32_t i = i0 + tid + 256 * c;
-            if (i < 16 * pieces) As[(i % pieces) * 16 + i / pieces] = v[c];
+            const uint32_t row = (i / 4) % 16, pc = 4 * (i / 64) + i % 4;
+            if (i < 16 * pieces) As[pc * 16 + (row ^ a16_swz(pc))] = v[c];
         }
     }
 }
@@ -576,6 +585,8 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
     const v4i z = {0, 0, 0, 0};
     const bool first = g < 2;
     const uint32_t tl = orow + (r & 3);  // the row whose scales this lane feeds the rank-1 MFMAs
+    // staged slots of row arl in the pieces read below (block bl even: piece % 4 = g % 2, 2 + g % 2)
+    const uint32_t arl_l = arl ^ a16_swz(g % 2), arl_h = arl ^ a16_swz(2 + g % 2);
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
         W nw = cw;
@@ -583,7 +594,7 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const uint32_t bl = sb * 8 + 4 * pp + (first ? 0u : 2u);
-            const v4i_t al = As[(bl * 2 + g % 2) * 16 + arl], ah = As[((bl + 1) * 2 + g % 2) * 16 + arl];
+            const v4i_t al = As[(bl * 2 + g % 2) * 16 + arl_l], ah = As[((bl + 1) * 2 + g % 2) * 16 + arl_h];
             const v4i_t a0 = first ? al : zero4, a2 = first ? zero4 : al;
             const v4i_t a1 = first ? ah : zero4, a3 = first ? zero4 : ah;
             v4i dgv[4] = {z, z, z, z}, duv[4] = {z, z, z, z};
@@ -681,16 +692,16 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
         float a[4], c2[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nb ? i : 16 * nb - 1;
-            a[c] = ws.xs[(size_t)tokv[ic / nb] * nb + ic % nb];
-            c2[c] = ws.xu[(size_t)tokv[ic / nb] * nb + ic % nb];
+            const uint32_t i = i0 + tid + 256 * c, ic = i < 16 * nb ? i : 16 * nb - 1;  // row ic % 16, block ic / 16
+            a[c] = ws.xs[(size_t)tokv[ic % 16] * nb + ic / 16];
+            c2[c] = ws.xu[(size_t)tokv[ic % 16] * nb + ic / 16];
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t i = i0 + tid + 256 * c;
             if (i < 16 * nb) {
-                Sx[(i % nb) * 16 + i / nb] = a[c];
-                Su[(i % nb) * 16 + i / nb] = c2[c];
+                Sx[i] = a[c];
+                Su[i] = c2[c];
             }
         }
     }
@@ -740,6 +751,8 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
     const v4i_t zero4 = {0, 0, 0, 0};
     const bool first = g < 2;  // this lane's bytes are of the pair's first chunk
     const uint32_t tl = 4 * g + (r & 3);  // the token whose scales this lane feeds the rank-1 MFMAs
+    // staged slots of row r in the pieces read below (block bl even: piece % 4 = g % 2, 2 + g % 2)
+    const uint32_t r_l = r ^ a16_swz(g % 2), r_h = r ^ a16_swz(2 + g % 2);
     for (uint32_t step = 0; step < nstep; step++) {
         const uint32_t sb = step % NSB;
         Q4Sb16 ng = cg, nu = cu;
@@ -763,7 +776,7 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
         for (int pp = 0; pp < 2; pp++) {
             // this lane's activation halves: sub-blocks 4pp + 2 (g / 2) (low nibbles) and the next
             const uint32_t bl = sb * 8 + 4 * pp + (first ? 0u : 2u);
-            const v4i_t al = As[(bl * 2 + g % 2) * 16 + r], ah = As[((bl + 1) * 2 + g % 2) * 16 + r];
+            const v4i_t al = As[(bl * 2 + g % 2) * 16 + r_l], ah = As[((bl + 1) * 2 + g % 2) * 16 + r_h];
             const v4i_t wgl = qg[pp] & 0x0f0f0f0f, wgh = (qg[pp] >> 4) & 0x0f0f0f0f;
             const v4i_t wul = qu[pp] & 0x0f0f0f0f, wuh = (qu[pp] >> 4) & 0x0f0f0f0f;
             v4i dgv[4], duv[4];  // sub-blocks 4pp + 0..3
@@ -894,8 +907,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
     const uint32_t tok = item_token(ws, itc, shared, c % 16);
     const float wgt_c = shared ? sigmoid_libm(ws.shl[itc.row0 + rc]) : ws.ent_w[itc.row0 + rc];
 
-    // activations: 16-byte piece p of tile row r at As[p * 32 + r]; four lanes read 64 contiguous
-    // bytes of one row, and a wave's stores fill whole 256-byte bank rows
+    // activations: 16-byte piece p of tile row r at As[p * 32 + (r ^ a16_swz(p))]; four lanes read
+    // 64 contiguous bytes of one row, and the 16 lanes of a quarter-wave store to 16 bank groups
     {
         constexpr uint32_t lim = 32 * 2 * nb;
         for (uint32_t i0 = 0; i0 < lim; i0 += 4096) {
@@ -907,7 +920,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
                 const uint32_t row = (ic / 4) % 32, pc = 4 * (ic / 128) + ic % 4;
                 const uint32_t t = (uint32_t)__shfl((int)tok, (int)row);
                 v[k] = *reinterpret_cast<const v4i_t*>(ws.xq + (size_t)t * H + pc * 16);
-                dst[k] = pc * 32 + row;
+                dst[k] = pc * 32 + (row ^ a16_swz(pc));
             }
 #pragma unroll
             for (int k = 0; k < 8; k++)
@@ -971,6 +984,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
     for (int q = 0; q < 4; q++) acc[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t sl = 4 * h + (lane & 3);  // this lane's (h, u) slot of the scale tables
     const bool odd = c >= 16;                // this lane's row of the strip: up (odd DPP row) or gate
+    // tile row c's staged slot in piece 2B + h: B % 2 = nib, so piece % 4 = 2 nib + h
+    const uint32_t cs[2] = {c ^ a16_swz(h), c ^ a16_swz(2 + h)};
     // one (strip, superblock) step on the words in cur, the next step's loads going out into nxt first
     auto step_on = [&](uint32_t step, const Raw& cur, Raw& nxt) {
         const uint32_t sb = step % NSB;
@@ -983,7 +998,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
 #pragma unroll
             for (int nib = 0; nib < 2; nib++) {
                 const uint32_t B = sb * 8 + 2 * ch + nib;
-                const v4i_t a = As[(B * 2 + h) * 32 + c];
+                const v4i_t a = As[(B * 2 + h) * 32 + cs[nib]];
                 const v4i_t w = nib ? (qv >> 4) & 0x0f0f0f0f : qv & 0x0f0f0f0f;
                 block32(acc, mfma_i8_32x32(a, w), dm[nib], SxT[B * 8 + sl], SuT[B * 8 + sl]);
             }
