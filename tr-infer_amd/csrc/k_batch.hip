@@ -548,8 +548,11 @@ __device__ __forceinline__ void gateup_strips(const Mat& G, const Mat& U, uint32
     }
     // the qs pieces load in row order (lane l: row l / 4, piece l % 4; each four lanes 64 contiguous
     // bytes) and move to MFMA lane (g, r) by ds_bpermute from lane 4r + g; the headers load per row
-    const uint32_t lrow = lane / 4, lpc = lane % 4;
-    const int paddr = (int)(4 * r + g) * 4;
+    // piece lpc ^ 2 (lane / 32) (the four lanes of a row still read its 64 bytes): MFMA lane (g, r)
+    // then takes its piece from lane 4r + (g ^ 2 (r / 8)), and any 32 consecutive lanes read 32
+    // sources distinct modulo 32
+    const uint32_t lrow = lane / 4, lpc = (lane % 4) ^ (2 * (lane / 32));
+    const int paddr = (int)(4 * r + (g ^ (2 * (r / 8)))) * 4;
     auto rowp = [&](const Mat& M, uint32_t step, uint32_t s, uint32_t row) -> const uint8_t* {
         const uint32_t strip = bx * strips + wv + 4 * ((step / NSB) * S + s);
         return M.ptr + (size_t)e * M.stride + (size_t)(strip * 16 + row) * M.row_bytes + (step % NSB) * 144;
@@ -727,8 +730,8 @@ __device__ __forceinline__ void gateup_item(const Mat& gate, const Mat& up, cons
     // consecutive lanes read 64 contiguous bytes (the vector L1 serves that about 3x faster from L2
     // than the MFMA order, where consecutive lanes read different rows).  ds_bpermute then moves
     // each piece to MFMA lane (g, r) = (piece, row), from lane 4r + g.
-    const uint32_t lrow = lane / 4, lpc = lane % 4;
-    const int paddr = (int)(4 * r + g) * 4;
+    const uint32_t lrow = lane / 4, lpc = (lane % 4) ^ (2 * (lane / 32));  // as in gateup_strips
+    const int paddr = (int)(4 * r + (g ^ (2 * (r / 8)))) * 4;
     auto rows_of = [&](uint32_t step, const uint8_t*& rg, const uint8_t*& ru) {
         const uint32_t strip = bx * strips + wv + 4 * (step / NSB);
         rg = G.ptr + (size_t)e * G.stride + (size_t)(strip * 16 + lrow) * G.row_bytes;
@@ -952,16 +955,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void b
     __syncthreads();
 
     // Weight rows: lane (h, c) loads the header of B-operand row c; lane l loads the 16-byte qs
-    // pieces 2 ch + l % 2 (ch = 0 .. 3) of B-operand row l / 2 (gate rows in lanes 0-31, up rows in
-    // 32-63; two lanes read one 32-byte chunk), and MFMA lane (h, c) takes its piece from lane 2c + h.
+    // pieces 2 ch + ((l % 2) ^ (l / 32)) (ch = 0 .. 3) of B-operand row l / 2 (gate rows in lanes
+    // 0-31, up rows in 32-63; two lanes read one 32-byte chunk), and MFMA lane (h, c) takes its piece
+    // from lane 2c + (h ^ (c / 16)).
     // Gate and up have one shape and format, so one stride and row size serve both.
     const uint32_t strips = F / 16 / gridDim.x;  // of this workgroup; wave wv takes wv, wv + 8, ..
     const uint32_t nstep = (strips / 8) * NSB;   // (strip, superblock) steps of this wave
     const size_t rb = G.row_bytes;
     const uint8_t* hbase = (c < 16 ? G.ptr : U.ptr) + (size_t)e * G.stride + (size_t)(c % 16) * rb;
     const uint8_t* qbase =
-            (lane < 32 ? G.ptr : U.ptr) + (size_t)e * G.stride + (size_t)((lane / 2) % 16) * rb + 16 + 16 * (lane % 2);
-    const int paddr = (int)(2 * c + h) * 4;
+            (lane < 32 ? G.ptr : U.ptr) + (size_t)e * G.stride + (size_t)((lane / 2) % 16) * rb + 16 +
+            16 * ((lane % 2) ^ (lane / 32));
+    // lanes 32-63 hold the two pieces of a chunk the other way round, so that MFMA lane (h, c) takes
+    // its piece from lane 2c + (h ^ (c / 16)) and any 32 consecutive lanes read 32 sources distinct
+    // modulo 32
+    const int paddr = (int)(2 * c + (h ^ (c / 16))) * 4;
     auto strip_of = [&](uint32_t step) { return bx * strips + wv + 8 * (step / NSB); };
     struct Raw {
         uint4 hdr;
