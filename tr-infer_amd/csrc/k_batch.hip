@@ -94,7 +94,7 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
             for (uint32_t w = 0; w < DISPATCH_WAVES; w++) {
                 const uint32_t pc = popc64(masks[w * E + e]);
                 const uint32_t ch = r * DISPATCH_WAVES + w;  // 64-token chunk
-                if (split && ch < nchunks) ws.doff[(size_t)ch * E + e] = pc;  // its count, for now
+                if (split && rounds > 1 && ch < nchunks) ws.doff[(size_t)ch * E + e] = pc;  // its count, for now
                 c += pc;
             }
             cnt[e] = c;
@@ -177,6 +177,16 @@ __global__ __launch_bounds__(DISPATCH_WAVES * 64) void dispatch_kernel(Workspace
     }
     __syncthreads();
 
+    if (split && rounds == 1) {  // one round: the chunk counts are the masks still in LDS
+        for (uint32_t e = tid; e < E; e += DT) {
+            uint32_t o = run[e];
+            for (uint32_t w = 0; w < DISPATCH_WAVES && w < nchunks; w++) {
+                ws.doff[(size_t)w * E + e] = o;
+                o += popc64(masks[w * E + e]);
+            }
+        }
+        return;
+    }
     if (split) {  // the chunk counts become each chunk's first position per expert
         for (uint32_t e = tid; e < E; e += DT) {
             uint32_t o = run[e];
@@ -230,7 +240,7 @@ __global__ __launch_bounds__(64) void scatter_kernel(Workspace ws, uint32_t m, u
     const uint32_t E = ws.E, c = blockIdx.x, lane = threadIdx.x, t = c * 64 + lane;
     extern __shared__ __align__(16) uint8_t smem[];
     unsigned long long* masks = reinterpret_cast<unsigned long long*>(smem);  // [E]
-    for (uint32_t e = lane; e < E; e += 64) masks[e] = 0ull;
+    uint32_t* first = reinterpret_cast<uint32_t*>(masks + E);                // [E] the chunk's first positions
     uint32_t id[K_MAX];
     float wt[K_MAX];
     const uint32_t ns = t < m ? load_ids(ws, t, kc4, id) : 0u;
@@ -241,6 +251,23 @@ __global__ __launch_bounds__(64) void scatter_kernel(Workspace ws, uint32_t m, u
                 const float4 v = reinterpret_cast<const float4*>(ws.w + (size_t)t * K_MAX)[q];
                 wt[4 * q] = v.x; wt[4 * q + 1] = v.y; wt[4 * q + 2] = v.z; wt[4 * q + 3] = v.w;
             }
+    }
+    // the chunk's row of first positions, requested together with the ids (one round trip)
+    for (uint32_t e0 = 0; e0 < E; e0 += 512) {
+        uint32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t e = e0 + lane + 64 * j;
+            v[j] = e < E ? ws.doff[(size_t)c * E + e] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t e = e0 + lane + 64 * j;
+            if (e < E) {
+                first[e] = v[j];
+                masks[e] = 0ull;
+            }
+        }
     }
     wave_sync();
     uint32_t* mw = reinterpret_cast<uint32_t*>(masks);
@@ -253,7 +280,7 @@ __global__ __launch_bounds__(64) void scatter_kernel(Workspace ws, uint32_t m, u
     for (uint32_t s = 0; s < K_MAX; s++)
         if (s < ns) {
             const uint32_t e = id[s];
-            const uint32_t pos = ws.doff[(size_t)c * E + e] + popc64(masks[e] & below);
+            const uint32_t pos = first[e] + popc64(masks[e] & below);
             ws.ent_tok[pos] = t;
             ws.ent_w[pos] = wt[s];
             ws.ent_exp[pos] = e;
@@ -387,7 +414,7 @@ hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipSt
     const int split = geo::dispatch_split(m) ? 1 : 0;
     if (split && geo::doff_elems(m, ws.E) > geo::doff_elems(ws.m_max, ws.E)) return hipErrorInvalidValue;
     dispatch_kernel<<<1, DT, lds, st>>>(ws, m, (kcap + 3) / 4, split);
-    if (split) scatter_kernel<<<geo::chunks(m), 64, E * 8, st>>>(ws, m, (kcap + 3) / 4);
+    if (split) scatter_kernel<<<geo::chunks(m), 64, E * 12, st>>>(ws, m, (kcap + 3) / 4);
     return hipGetLastError();
 }
 
