@@ -291,11 +291,13 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_reduc
 // contiguous run of the live ids [0, gridDim.x * n_items) in dispatch order, so the consecutive
 // items of one expert (each re-reads that expert's weights) run on one XCD close in time and
 // share its L2.  A bijection on the live ids; false for the ids past them.
-__device__ __forceinline__ bool xcd_order(uint32_t n_items, uint32_t& col, uint32_t& itn) {
+// reverse: each XCD walks its run from the end (the last items first).
+__device__ __forceinline__ bool xcd_order(uint32_t n_items, uint32_t& col, uint32_t& itn, bool reverse = false) {
     const uint32_t gx = gridDim.x, id = blockIdx.x + gx * blockIdx.y, T = gx * n_items;
     if (id >= T) return false;
     const uint32_t x = id % 8, slot = id / 8, base = T / 8, rem = T % 8;
-    const uint32_t nid = x * base + (x < rem ? x : rem) + slot;
+    const uint32_t cnt = base + (x < rem ? 1u : 0u);  // ids of this XCD: slot < cnt
+    const uint32_t nid = x * base + (x < rem ? x : rem) + (reverse ? cnt - 1 - slot : slot);
     col = nid % gx;
     itn = nid / gx;
     return true;

@@ -1102,7 +1102,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         Mat gate, Mat up, Mat shg, Mat shu, Workspace ws, uint32_t skip_rows) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint32_t bx, itn;  // column block and item, in XCD order
-    if (!xcd_order(ws.n_groups[LIST ? 5 : 2], bx, itn)) return;
+    // the unpaired items walk each XCD's run backwards: its first items then belong to the experts
+    // the pairs launch read last on that XCD, whose weights may still sit in the caches
+    if (!xcd_order(ws.n_groups[LIST ? 5 : 2], bx, itn, LIST != 0)) return;
     if (LIST) itn = ws.single[itn];
     gateup_item<NSB>(gate, up, shg, shu, ws, skip_rows, bx, itn, smem);
 }
