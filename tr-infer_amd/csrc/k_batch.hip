@@ -1572,9 +1572,10 @@ __device__ __forceinline__ void down_items(const Mat& D, uint32_t e, const Item 
                         c0 += v4i{t0.x, t0.y, t0.z, t0.w} * 128;
                         c1 += v4i{t1.x, t1.y, t1.z, t1.w} * 128;
                     }
-                    // Q6_K (VALU-bound at config 4): the chain's fma with mm on the matrix cores too (down
-                    // 465 -> 456 us); the other formats keep it on the VALU (M = 512 Q4_K: 121.6 against 124)
-                    if constexpr (Q6)
+                    // Q6_K and Q4_K: the chain's fma with mm on the matrix cores too, where other waves'
+                    // VALU work overlaps it (config 4 Q6_K down 379-386 -> 371-372 us, M = 512 Q4_K
+                    // 114.5 -> 112.5 us at four waves per SIMD); Q8_0 / Q5_1 keep it on the VALU
+                    if constexpr (Q6 || FK == 0)
                         down_blocks_mc(acc[s * NI + it], c0, c1, d0, d1, sx + tl, su + tl);
                     else
                         down_blocks(acc[s * NI + it], c0, c1, d0, d1, sx + tl, su + 4 * g);
