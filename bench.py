@@ -362,21 +362,6 @@ def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
     return out_res
 
 
-def gen_tq_stack(torch, trmoe, count, rows, k, fmt, dev, gen):
-    """A stack of `count` packed TQ matrices on the GPU (codec.rs:1-46): uniform q bytes (and
-    5-bit planes), each block's f16 d in [5e-4, 3e-3] and m = -d * U(0, 2^(bits-1)), the sign
-    pattern of converted GGUF weights."""
-    mb = trmoe.matrix_bytes(fmt, rows, k)
-    bb, bits = trmoe.tq_block_bytes(fmt), fmt >> 8
-    t = torch.randint(0, 256, (count, mb), dtype=torch.uint8, device=dev, generator=gen)
-    blocks = t.view(count, mb // bb, bb)
-    d = torch.empty((count, mb // bb, 16), device=dev).uniform_(5e-4, 3e-3, generator=gen)
-    m = -d * torch.empty_like(d).uniform_(0, float(1 << (bits - 1)), generator=gen)
-    blocks[:, :, 0:32] = d.half().view(torch.uint8)
-    blocks[:, :, 32:64] = m.half().view(torch.uint8)
-    return t
-
-
 def bench_tq(args, dev, stream, trmoe, torch, np):
     """The layer on the reference's own packed TQ experts at the real expert shape: H = 2560,
     F = 640, E = 512, top-10, gate/up TQ4_32 and down TQ5_16 (python/tests/test_blocks_real.py:
@@ -389,13 +374,7 @@ def bench_tq(args, dev, stream, trmoe, torch, np):
     t0 = time.time()
     lw = []
     for _ in range(args.tq_layers):
-        router = torch.randn((Et, Ht), device=dev, generator=gen) * 0.02
-        shg = torch.randn(Ht, device=dev, generator=gen) * 0.02
-        gate, up = (gen_tq_stack(torch, trmoe, Et, Ft, Ht, gf, dev, gen) for _ in range(2))
-        down = gen_tq_stack(torch, trmoe, Et, Ht, Ft, df, dev, gen)
-        sg, su = (gen_tq_stack(torch, trmoe, 1, Ft, Ht, gf, dev, gen)[0] for _ in range(2))
-        sd = gen_tq_stack(torch, trmoe, 1, Ht, Ft, df, dev, gen)[0]
-        lw.append(trmoe.LayerWeights(Ht, Et, Ft, router, shg, gate, up, down, sg, su, sd, gf, df))
+        lw.append(trmoe.LayerWeights.generate_tq(gen, Ht, Et, Ft, gf, df, device=dev))
     torch.cuda.synchronize()
     per_expert = 2 * trmoe.matrix_bytes(gf, Ft, Ht) + trmoe.matrix_bytes(df, Ht, Ft)
     log(f"TQ layers: {len(lw)} x {Et} experts ({len(lw) * Et * per_expert / 1e9:.1f} GB) in {time.time() - t0:.1f}s")

@@ -55,7 +55,7 @@ enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
  * (crates/tr-model/src/weights.rs:14-35): `fmt` names the GGUF block format read directly on
  * the GPU where the CPU path reads its TQ re-layout.  Gate/up: Q4_K.  Down (routed and shared
  * alike): Q4_K, Q6_K, Q8_0 or Q5_1 (blocks.py:57-78).  Q4_K, Q8_0 and Q5_1 stacks are 16-byte aligned,
- * Q6_K 2-byte aligned.  trk_gemv also takes a TQ codec (TRK_FMT_TQ*, 4-byte aligned): then the
+ * Q6_K 2-byte aligned.  trk_gemv also takes a TQ codec (TRK_FMT_TQ*, 16-byte aligned): then the
  * matrix is the reference's packed strips, exactly as trpack writes them. */
 typedef struct {
     const void *ptr;
@@ -123,6 +123,12 @@ int trk_set_moe(trk_ctx *ctx, const trk_moe_policy *policy);
 int trk_moe_forward(trk_ctx *ctx, const trk_moe_w *w, const float *x, const float *rlog, uint32_t m,
                     float *out, void *stream);
 
+/* The device workspace, in bytes, that the layer needs for m rows of this configuration: what
+ * trk_create allocates for m_max = m, and what trk_moe_forward_noalloc needs of its static scratch.
+ * Host-only (no GPU call); errors as for trk_create.  Sizing helper for callers that preallocate,
+ * as Model::load_with sizes its arenas (exec.rs:733-779, exec_batch.rs:127-211). */
+int trk_workspace_bytes(const trk_cfg *cfg, uint32_t m, size_t *bytes);
+
 /* Config-5 layer: h[M][H] += MoE(rmsnorm(h; rms_w, eps)).  Composes elem::rmsnorm
  * (elem.rs:255-262), the MoE block and elem::add_inplace (elem.rs:104-118).  Below the router
  * GEMM threshold (and with the one-launch decode layer off) the logits launch normalises h as it
@@ -136,7 +142,8 @@ int trk_moe_residual(trk_ctx *ctx, const trk_moe_w *w, const float *rms_w, float
  * ignored: the workspace is laid out for this call's m), policy the routing (NULL = top
  * n_expert_used).  The workspace lives in a static device array of TRK_NOALLOC_SCRATCH_BYTES per
  * GPU, held until the process ends; a call whose workspace does not fit returns TRK_E_CAPACITY (at
- * H = 2048, E = 512, F = 512, k = 10 that is M above 64).  Every call on one GPU shares that array:
+ * H = 2048, E = 512, F = 512, k = 10 that is M above 100; trk_workspace_bytes gives the need of any
+ * shape).  Every call on one GPU shares that array:
  * calls that overlap on one GPU (several host threads or streams) race.  MoeStats are not counted
  * and the one-launch decode layer is not used.  Results are those of trk_moe_forward. */
 #define TRK_NOALLOC_SCRATCH_BYTES (16u << 20)

@@ -80,6 +80,14 @@ def test_noalloc_rejects_a_workspace_above_the_scratch():
     assert rc == -3 and b"scratch" in L.trk_last_error()
     bad = trmoe.Cfg(2000, 512, 512, 10, 0, 0, 16, 1)
     assert L.trk_moe_forward_noalloc(C.byref(bad), None, None, C.c_void_p(256), None, 1, C.c_void_p(256), None) == -1
+    # the boundary at BASELINE's shape: trk_workspace_bytes is the layout noalloc checks
+    m_max = trmoe.noalloc_max_m(2048, 512, 512, 10)
+    assert m_max == 100
+    assert trmoe.workspace_bytes(2048, 512, 512, 10, m_max) <= trmoe.NOALLOC_SCRATCH_BYTES
+    assert trmoe.workspace_bytes(2048, 512, 512, 10, m_max + 1) > trmoe.NOALLOC_SCRATCH_BYTES
+    rc = L.trk_moe_forward_noalloc(C.byref(cfg), None, None, C.c_void_p(256), None, m_max + 1, C.c_void_p(256), None)
+    assert rc == -3 and b"scratch" in L.trk_last_error()
+    assert L.trk_workspace_bytes(None, 1, None) == -1
 
 
 def test_gemv_rejects_bad_codecs_and_ranges():
@@ -87,8 +95,8 @@ def test_gemv_rejects_bad_codecs_and_ranges():
     inside the matrix; GGUF formats with the kb their TQ conversion has."""
     L = trmoe.lib()
 
-    def call(fmt, rows, k, kb, s0=0, s1=1, m=1, pair=0, q=64, ldy=4096):
-        mat = trmoe.Mat(C.c_void_p(256), rows, k, fmt, 1, 0)
+    def call(fmt, rows, k, kb, s0=0, s1=1, m=1, pair=0, q=64, ldy=4096, ptr=256):
+        mat = trmoe.Mat(C.c_void_p(ptr), rows, k, fmt, 1, 0)
         return L.trk_gemv(C.byref(mat), 0, s0, s1, kb, C.c_void_p(q), C.c_void_p(64), C.c_void_p(64), m, pair,
                           C.c_void_p(64), ldy, None, 0, None)
 
@@ -99,6 +107,8 @@ def test_gemv_rejects_bad_codecs_and_ranges():
     assert call(trmoe.FMT_Q6_K, 64, 512, 32) == -1 and b"unsupported" in L.trk_last_error()
     assert call(trmoe.FMT_Q8_0, 64, 640, 32) == -1 and b"256" in L.trk_last_error()
     assert call(trmoe.FMT_Q5_1, 64, 512, 16, q=72) == -1 and b"aligned" in L.trk_last_error()
+    # TQ strips are read in 16-byte pieces: a pointer 4-byte but not 16-byte aligned is refused
+    assert call(trmoe.FMT_TQ4_32, 64, 2560, 32, ptr=260) == -1 and b"16-byte" in L.trk_last_error()
     assert call(trmoe.FMT_TQ4_16, 64, 640, 16, m=3, pair=1) == -1 and b"twos" in L.trk_last_error()
     assert call(trmoe.FMT_TQ4_16, 64, 640, 16, s1=4, m=2, ldy=63) == -1 and b"ldy" in L.trk_last_error()
     # within the contract and with nothing to do: no device work, status OK

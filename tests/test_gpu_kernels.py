@@ -258,6 +258,39 @@ def test_gemv_tq_bit_exact(bits, kb, rows, K, pair, m, strips):
     gemv_check(to_dev(tq), tq, rows, K, fmt, bits, kb, x, pair, strips)
 
 
+@pytest.mark.parametrize("m", [1, 70, 300, 512])
+def test_designed_rounding_orders(m):
+    """The designed cases that pin the oracle's f32 orders (test_oracle.py: test_gemv_epilogue_order,
+    test_gemm_f32_nt_lane_map, test_rmsnorm_product_order) through the GPU kernels: the GEMV's
+    two-FMA epilogue (gemv.rs:141-148), the router GEMM's lane / chain map on each of its tile paths
+    (smallgemm.rs:8-59; m = 1 and 70 VALU tiles of two sizes, 300 the 16 x 16 tiles, 512 the matrix
+    cores) and RMSNorm's (x r) w (elem.rs:255-262), each against the literal the case was built
+    for."""
+    from test_oracle import epilogue_order_case, rmsnorm_order_case
+    say(f"designed rounding orders m={m}")
+    w, k, bits, kb, xq, s, su = epilogue_order_case()
+    y = host(trmoe.gemv(to_dev(w), 16, k, (bits << 8) | kb, 0, 1, kb, to_dev(xq), to_dev(s), to_dev(su)))
+    assert y[0, 0] == np.float32(2.0 ** -10) and np.all(y[0, 1:] == 0)
+    a = np.float32(1 + 2.0 ** -12)
+    H, E = 256, 8
+    router = np.zeros((E, H), np.float32)
+    router[0, 0], router[0, 16] = a, a
+    router[1, 0], router[1, 16], router[1, 1] = 1e8, -1e8, 1.0
+    router[2, 0], router[2, 8], router[2, 1] = 1e8, 1.0, -1e8
+    x = np.ones((m, H), np.float32)
+    x[:, 0], x[:, 16] = a, -a
+    # row 0: the fused chain of lane 0 leaves -2^-24; rows 1 and 2 see x = a at k = 0 and -a at
+    # k = 16, so their designed sums are taken on rows of ones
+    lg, _ = trmoe.router_logits(to_dev(router), to_dev(x), gemm_order=True)
+    assert np.all(host(lg)[:, 0] == np.float32(-(2.0 ** -24)))
+    lg, _ = trmoe.router_logits(to_dev(router), to_dev(np.ones((m, H), np.float32)), gemm_order=True)
+    got = host(lg)
+    assert np.all(got[:, 1] == 1.0) and np.all(got[:, 2] == 0.0)
+    xr, wr, want = rmsnorm_order_case()
+    yr = host(trmoe.rmsnorm(to_dev(np.tile(xr, (2, 1))), to_dev(wr), 0.0))
+    assert np.array_equal(yr.view(np.uint32), np.tile(want, (2, 1)).view(np.uint32))
+
+
 def test_swiglu_and_rmsnorm_bit_exact():
     say("swiglu / rmsnorm")
     rng = np.random.default_rng(2)

@@ -413,13 +413,29 @@ def test_prefill_zipf_full_size_sampled():
     assert np.isfinite(got).all()
     orc = L.oracle()
     rlog_gpu = ctx.read(trmoe.WS_RLOG, M * E * 4, np.float32).reshape(M, E)
-    for t in (0, 1, 77, 300, 511):
+    w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :10]
+    # 32 tokens: 8 of the largest group's (the 16-row MFMA tiles and item pairs of the most popular
+    # expert), the others spread over the batch
+    big = int(np.argmax(sizes))
+    big_toks = ent_tok[ent_exp == big]
+    chosen = set(big_toks[np.linspace(0, len(big_toks) - 1, 8).astype(int)].tolist())
+    for t in np.linspace(0, M - 1, 40).astype(int).tolist():
+        if len(chosen) < 32:
+            chosen.add(t)
+    sample = sorted(chosen)
+    assert len(sample) == 32 and sum(t in big_toks for t in sample) >= 8
+    n_exact = 0
+    for t in sample:
         xt = x[t:t + 1]
         want_lg = orc.logits(xt, dot_rows=False)
         assert np.array_equal(rlog_gpu[t].view(np.uint32), want_lg[0].view(np.uint32))
         r = orc.moe_batch(xt, k=10, router_dot_max_m=0)
         assert np.array_equal(r["ids"][0, :10], ids[t])
-        compare_out(got[t], r["out"][0], False, f"token {t}")
+        exact = np.array_equal(w[t], r["w"][0, :10]) and shared_gate_exact(L, xt)
+        n_exact += exact
+        compare_out(got[t], r["out"][0], exact, f"token {t}")
+    say(f"config 3: {len(sample)} tokens, {n_exact} with bit-identical routing weights and gate")
+    assert n_exact >= len(sample) // 2
     ctx.close()
 
 
@@ -530,6 +546,38 @@ def test_config5_residual_full_m512():
             want = (h_in[t] + r["out"][0]).astype(np.float32)
             exact = np.array_equal(r["w"][0, :k], w[t]) and shared_gate_exact(L, xn)
             compare_out(h_out[t], want, exact, f"C5 layer {l} row {t}")
+    ctx.close()
+
+
+def test_config5_residual_full_m1():
+    """BASELINE config 5 at decode, M = 1, over two full-size layers (H 2048, E 512, F 512, top-10)
+    through trk_moe_residual: the RMSNorm runs inside the dot-order logits launch, the decode down
+    adds into h.  After each layer: the quantised normalised row (two levels) bit-exact against
+    orc_rmsnorm + quant_pair, the routing against moe_block's, and h against h + moe_block(rmsnorm(h))
+    (elem.rs:255-262, exec.rs:1540-1623), bit-identical where the routing weights agree."""
+    say("config 5 M=1, two full layers")
+    import torch
+    k = 10
+    ctx = trmoe.Context(2048, 512, 512, k, 16)
+    h = dev(Layer(seed=1, H=2048, E=4, F=256, lazy=True).x(1, tid=661))
+    for l in range(2):
+        L, W = full_layer_on_gpu(1, l)
+        rms = O.gen_uniform(1, (l << 32) | 4, 2048, 0.9, 1.1)
+        h_in = host(h).copy()
+        ctx.residual(W, dev(rms), 1e-6, h)
+        torch.cuda.synchronize()
+        h_out = host(h)
+        xn = O.rmsnorm(h_in[0], rms, 1e-6)
+        oq, _, _ = O.quant_pair(xn, 32)
+        assert np.array_equal(ctx.read(trmoe.WS_XQ, 2 * 2048, np.int8)[:oq.size], oq.reshape(-1)), f"layer {l} xq"
+        r = L.oracle().moe_block(xn, k=k, hiprec=True)
+        ids = ctx.read(trmoe.WS_IDS, 4 * 32, np.uint32)[:k]
+        w = ctx.read(trmoe.WS_W, 4 * 32, np.float32)[:k]
+        assert np.array_equal(ids, r["ids"]), f"layer {l} ids"
+        want = (h_in[0] + r["out"]).astype(np.float32)
+        exact = np.array_equal(w, r["w"]) and shared_gate_exact(L, xn[None])
+        say(f"config 5 M=1: layer {l} exact={exact}")
+        compare_out(h_out[0], want, exact, f"C5 M=1 layer {l}")
     ctx.close()
 
 

@@ -7,6 +7,8 @@ multiples of 256; every gate/down bit width.  Bar as for the GGUF layer: bit-ide
 routing weights and the shared gate agree bit for bit, else within 1e-5 of the output scale."""
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import numpy as np
 import pytest
 
@@ -53,7 +55,10 @@ def reference(orc, x, k, policy=None, hiprec=True):
     return r, r["out"]
 
 
-def run_case(L, orc, W, M, k, hiprec=True, policy=None, tid=0):
+def run_case(L, orc, W, M, k, hiprec=True, policy=None, tid=0, mfma=None):
+    """The layer on L's TQ experts at M rows against the oracle.  mfma: require (True) or rule out
+    (False) the int8 MFMA kernels, read from the launches the call made (the generic path runs a
+    separate SwiGLU launch, tq_act)."""
     import torch
     x = L.x(M, tid=tid)
     r, want = reference(orc, x, k, policy, hiprec)
@@ -61,7 +66,13 @@ def run_case(L, orc, W, M, k, hiprec=True, policy=None, tid=0):
     if policy:
         ctx.set_moe(policy)
     out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+    if mfma is not None:
+        ctx.set_timing(True)
     ctx.forward(W, dev(x), out)
+    if mfma is not None:
+        launched = ctx.timing()
+        ctx.set_timing(False)
+        assert "tq_gateup" in launched and ("tq_act" not in launched) == mfma, launched
     got = host(out).copy()
     exact = routing_exact(ctx, r, M, policy[1] if policy else k, L, x) if not policy else False
     # MoeStats: rows and selected experts, counted by whichever launch routed
@@ -79,14 +90,18 @@ def test_tq_layer_real_shape(M, hiprec):
     compare_out(got, want, exact, f"tq real M={M}")
 
 
-@pytest.mark.parametrize("gate_bits,down_bits", [(5, 4), (8, 8), (4, 8)])
+@pytest.mark.parametrize("gate_bits,down_bits,F", [(5, 4, 96), (8, 8, 96), (4, 8, 96), (5, 5, 96), (8, 4, 160),
+                                                   (5, 4, 80), (8, 8, 80)])
 @pytest.mark.parametrize("M", [1, 9, 40])
-def test_tq_layer_codecs(gate_bits, down_bits, M):
-    say(f"tq layer codecs gate={gate_bits} down={down_bits} M={M}")
-    L, orc, W = tq_layer(f"c{gate_bits}{down_bits}", seed=30 + gate_bits + down_bits, H=512, E=16, F=80,
+def test_tq_layer_codecs(gate_bits, down_bits, F, M):
+    """Every gate/up and down bit width.  F a multiple of 32 runs the int8 MFMA kernels (every
+    instantiation of k_tqm.hip: the 8-bit codecs' byte-sum correction, TQ5_32 gate/up, TQ4_16 and
+    TQ8_16 downs); F = 80 the generic grouped TQ GEMV."""
+    say(f"tq layer codecs gate={gate_bits} down={down_bits} F={F} M={M}")
+    L, orc, W = tq_layer(f"c{gate_bits}{down_bits}F{F}", seed=30 + gate_bits + down_bits + F, H=512, E=16, F=F,
                          gate_bits=gate_bits, down_bits=down_bits)
-    got, want, exact = run_case(L, orc, W, M, 4, tid=100 + M)
-    compare_out(got, want, exact, f"tq codecs {gate_bits}/{down_bits} M={M}")
+    got, want, exact = run_case(L, orc, W, M, 4, tid=100 + M, mfma=F % 32 == 0)
+    compare_out(got, want, exact, f"tq codecs {gate_bits}/{down_bits} F={F} M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 24])
@@ -123,9 +138,12 @@ def test_tq_weights_rejected_when_mixed():
 
 @pytest.mark.parametrize("key,kw,M,k,hiprec", [("real", REAL, 1, 8, True), ("real", REAL, 1, 8, False),
                                                ("real", REAL, 16, 8, True), ("real", REAL, 64, 8, True),
-                                               ("c88", dict(seed=46, H=512, E=16, F=80, gate_bits=8, down_bits=8), 40, 4, True),
-                                               ("c54", dict(seed=39, H=512, E=16, F=80, gate_bits=5, down_bits=4), 1, 4, True),
-                                               ("c48", dict(seed=42, H=512, E=16, F=80, gate_bits=4, down_bits=8), 9, 4, True)])
+                                               ("m88", dict(seed=46, H=512, E=16, F=96, gate_bits=8, down_bits=8), 40, 4, True),
+                                               ("m88", dict(seed=46, H=512, E=16, F=96, gate_bits=8, down_bits=8), 1, 4, True),
+                                               ("m54", dict(seed=39, H=512, E=16, F=96, gate_bits=5, down_bits=4), 1, 4, True),
+                                               ("m54", dict(seed=39, H=512, E=16, F=96, gate_bits=5, down_bits=4), 300, 4, True),
+                                               ("m48", dict(seed=42, H=512, E=16, F=160, gate_bits=4, down_bits=8), 9, 4, True),
+                                               ("m48", dict(seed=42, H=512, E=16, F=160, gate_bits=4, down_bits=8), 300, 4, True)])
 def test_tq_mfma_matches_generic(key, kw, M, k, hiprec):
     """The int8 MFMA kernels (a TQ block per MFMA, SwiGLU in the gate/up launch) and the generic
     grouped TQ GEMV give the same bits."""
@@ -138,7 +156,89 @@ def test_tq_mfma_matches_generic(key, kw, M, k, hiprec):
         ctx = trmoe.Context(L.H, L.E, L.F, k, max(M, 16), hiprec=hiprec)
         ctx.set_tq_mfma(mfma)
         out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.set_timing(True)
         ctx.forward(W, x, out)
+        launched = ctx.timing()
+        assert ("tq_act" not in launched) == mfma, launched  # the path asked for is the one that ran
         outs.append(host(out).copy())
         ctx.close()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), np.abs(outs[0] - outs[1]).max()
+
+
+_full = {}
+
+
+def tq_full_layer():
+    """The real expert shape at the real expert count: H 2560, F 640, E 512, TQ4_32 gate/up and
+    TQ5_16 down (1.78 GB of experts), generated on the GPU and copied back for the oracle."""
+    if not _full:
+        import torch
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(23)
+        H, E, F = 2560, 512, 640
+        bias = trmoe.zipf_bias(1, E)
+        W = trmoe.LayerWeights.generate_tq(gen, H, E, F, router_bias=dev(bias))
+        t = {k: host(v) for k, v in W.tensors.items() if k != "router_bias"}
+        orc = O.TQOracleLayer(H, E, F, t["router"], t["shexp_gate"], t["gate"], t["up"], t["down"], t["sh_gate"],
+                              t["sh_up"], t["sh_down"], 4, 5, bias)
+        x = host(torch.randn((512, H), device="cuda", generator=gen))
+        _full.update(W=W, orc=orc, x=x, H=H, E=E, F=F, shexp_gate=t["shexp_gate"])
+    return _full
+
+
+@pytest.mark.parametrize("policy", [None, (1, 10, 0.9, O.BASIS_TOP)])
+def test_tq_full_shape_m512_sampled(policy):
+    """The TQ layer at the bench's own configuration: E = 512, M = 512, Zipf(1.1)-biased router,
+    top-10 or dynamic k.  The split dispatch, the MFMA batch gate/up over TQM_PAIRS strip pairs and
+    the four-strip-group down all run.  Every token's ids against the oracle's route on the GPU's
+    logits, and 16 sampled tokens (4 from the largest group) against moe_batch, bit-identical where
+    the routing weights and the shared gate agree."""
+    say(f"tq full shape M=512 policy={policy}")
+    import torch
+    from test_gpu_layer import shared_gate_exact, ulp
+    d = tq_full_layer()
+    W, orc, x, H, E, F = d["W"], d["orc"], d["x"], d["H"], d["E"], d["F"]
+    M, k = 512, 10
+    ctx = trmoe.Context(H, E, F, k, M, k_cap=policy[1] if policy else 0)
+    if policy:
+        ctx.set_moe(policy)
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    ctx.set_timing(True)
+    ctx.forward(W, dev(x), out)
+    launched = ctx.timing()
+    ctx.set_timing(False)
+    assert "tq_act" not in launched and "tq_gateup" in launched, launched
+    got = host(out)
+    assert np.isfinite(got).all()
+    rlog = ctx.read(trmoe.WS_RLOG, M * E * 4, np.float32).reshape(M, E)
+    ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+    w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+    nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+    w_exact = np.zeros(M, bool)
+    for t in range(M):
+        oi, ow = O.route_mass(rlog[t], *policy) if policy else O.route_topk(rlog[t], k)
+        assert nsel[t] == len(oi) and np.array_equal(ids[t, :nsel[t]], oi), t
+        assert ulp(w[t, :nsel[t]], ow).max() <= 3, t
+        w_exact[t] = np.array_equal(w[t, :nsel[t]], ow)
+    n_ent = int(nsel.sum())
+    ent_tok = ctx.read(trmoe.WS_ENT_TOK, 4 * n_ent, np.uint32)
+    ent_exp = ctx.read(trmoe.WS_ENT_EXP, 4 * n_ent, np.uint32)
+    sizes = np.bincount(ent_exp, minlength=E)
+    assert sizes.max() > 100  # the skewed load of the Zipf bias
+    big_toks = ent_tok[ent_exp == int(np.argmax(sizes))]
+    chosen = set(big_toks[np.linspace(0, len(big_toks) - 1, 4).astype(int)].tolist())
+    for t in np.linspace(0, M - 1, 20).astype(int).tolist():
+        if len(chosen) < 16:
+            chosen.add(t)
+    n_exact = 0
+    for t in sorted(chosen):
+        xt = x[t:t + 1]
+        assert np.array_equal(rlog[t].view(np.uint32), orc.logits(xt, False)[0].view(np.uint32)), t
+        r = orc.moe_batch(xt, k=k, policy=policy, router_dot_max_m=0)
+        assert np.array_equal(r["ids"][0, :nsel[t]], ids[t, :nsel[t]])
+        exact = bool(w_exact[t]) and shared_gate_exact(SimpleNamespace(shexp_gate=d["shexp_gate"]), xt)
+        n_exact += exact
+        compare_out(got[t], r["out"][0], exact, f"tq full M=512 token {t}")
+    say(f"tq full shape: {len(chosen)} tokens, {n_exact} bit-identical")
+    ctx.close()
+

@@ -500,6 +500,88 @@ def test_dot_chain_order():
     assert O.dot(a, b) == 0.0
 
 
+def epilogue_order_case():
+    """One TQ8_32 strip whose row 0 makes the order of gemv.rs:141-148 observable (the other rows
+    are zero).  Activation scale sx = 1, so u = sx * sum = sum and t = d * sx = d exactly.
+    d = 1 + 2^-10 (f16 0x3C01), dot = 127 * 7 + 104 * 149 = 16385, so dot * d = 16401 + 2^-10:
+    between the floats 16401 and 16401 + 2^-9, a tie that rounds to even, 16401.  m = -71 and
+    sum = 127 + 104 = 231 give m * u = -16401 exactly.  The reference's order, fma(m, u, 0) =
+    -16401 then fma(dot, t, acc) = 2^-10 exactly (the fused product keeps the half-ulp).  Plain
+    mul + add gives round(dot * d) - 16401 = 0; the terms swapped give round(dot * d) then
+    fma(m, u, 16401) = 0."""
+    k, kb, bits = 32, 32, 8
+    q = np.zeros((16, k), np.uint8)
+    q[0, 0], q[0, 1] = 7, 149
+    d = np.full((16, 1), 0x3C00, np.uint16)
+    d[0, 0] = 0x3C01
+    m = np.zeros((16, 1), np.uint16)
+    m[0, 0] = O.f32_to_f16(-71.0)
+    assert O.f16_to_f32(m[0, 0]) == -71.0 and O.f16_to_f32(d[0, 0]) == 1 + 2.0 ** -10
+    w = O.pack_tq(q, d, m, bits, kb)
+    xq = np.zeros((1, k), np.int8)
+    xq[0, 0], xq[0, 1] = 127, 104
+    return w, k, bits, kb, xq, np.ones((1, 1), np.float32), np.array([[231]], np.int32)
+
+
+def test_gemv_epilogue_order():
+    """The two-FMA epilogue of gemv.rs:141-148, pinned by a designed case (epilogue_order_case):
+    acc = fma(m, sx * sum, acc) first, then fma(cvt(dot), d * sx, acc), both fused."""
+    w, k, bits, kb, xq, s, su = epilogue_order_case()
+    y = O.gemv_tq(w, k, bits, kb, 16, xq, s, su)
+    assert y[0, 0] == np.float32(2.0 ** -10)
+    assert np.all(y[0, 1:] == 0)
+
+
+def test_gemm_f32_nt_lane_map():
+    """smallgemm.rs:8-59: output (i, j) accumulates k = 16 s + l in lane l with one fused
+    multiply-add per step, then _mm512_reduce_add_ps's halving tree (lanes l and l + 8, then
+    + 4, + 2, + 1).  Designed cases:
+    - (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 rounds (a tie, to even) to 1 + 2^-11; the same product
+      negated at k = 16, in the same lane, leaves -2^-24 with a fused chain and 0 with mul + add;
+    - 1e8 at k = 0 and -1e8 at k = 16 cancel inside lane 0, so the 1 at k = 1 survives: 1;
+    - 1e8 (lane 0) and 1 (lane 8) meet first in the tree (1e8 + 1 rounds to 1e8), and -1e8
+      (lane 1) only at the last step: 0."""
+    a = np.float32(1 + 2.0 ** -12)
+    x = np.ones((1, 32), np.float32)
+    x[0, 0], x[0, 16] = a, -a
+    w = np.zeros((4, 32), np.float32)
+    w[0, 0], w[0, 16] = a, a
+    y = O.gemm_f32_nt(x, w)
+    assert y[0, 0] == np.float32(-(2.0 ** -24)) and y[0, 1] == 0.0
+    w = np.zeros((4, 32), np.float32)
+    w[0, 0], w[0, 16], w[0, 1] = 1e8, -1e8, 1.0
+    w[1, 0], w[1, 8], w[1, 1] = 1e8, 1.0, -1e8
+    y = O.gemm_f32_nt(np.ones((1, 32), np.float32), w)
+    assert y[0, 0] == 1.0 and y[0, 1] == 0.0
+
+
+def rmsnorm_order_case():
+    """n = 64; sixteen entries 2^-30 make sumsq = 2^-56 exactly, the mean 2^-62, r = 1 / sqrt(2^-62)
+    = 2^31 (eps = 0).  Two probes p = 2^-90 (1 + 2^-23), whose squares vanish below the sum's ulp:
+    with w = 2^-60 the reference's (x r) w gives 2^-119 (1 + 2^-23), while (x w) r underflows
+    through the subnormals (2^-150 (1 + 2^-23) -> 2^-149) to 2^-118; with w = 2^100, (x r) w gives
+    2^41 (1 + 2^-23), while x (r w) overflows (2^131 -> inf)."""
+    x = np.zeros(64, np.float32)
+    w = np.ones(64, np.float32)
+    x[::4] = np.float32(2.0 ** -30)
+    p = np.float32(2.0 ** -90 * (1 + 2.0 ** -23))
+    x[1], w[1] = p, np.float32(2.0 ** -60)
+    x[2], w[2] = p, np.float32(2.0 ** 100)
+    want = np.zeros(64, np.float32)
+    want[::4] = 2.0
+    want[1] = np.float32(2.0 ** -119 * (1 + 2.0 ** -23))
+    want[2] = np.float32(2.0 ** 41 * (1 + 2.0 ** -23))
+    return x, w, want
+
+
+def test_rmsnorm_product_order():
+    """elem.rs:255-262: y = (x * r) * w with r = 1 / sqrt(sumsq / n + eps), pinned by a designed
+    case (rmsnorm_order_case) that (x w) r and x (r w) both miss."""
+    x, w, want = rmsnorm_order_case()
+    y = O.rmsnorm(x, w, 0.0)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
 # ---- the MoE block -----------------------------------------------------------------------
 
 def f64_moe(layer, x, ids, w, sh_scale):

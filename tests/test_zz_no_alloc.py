@@ -35,6 +35,7 @@ SHAPES = {"small": dict(seed=11, H=512, E=32, F=256), "full": dict(seed=1, H=204
 
 
 @pytest.mark.parametrize("shape,k,sizes,policy", [("full", 10, (40, 3), None), ("full", 10, (16, 1), None),
+                                                  ("full", 10, (100, 7), None),  # 100: the largest M that fits
                                                   ("small", 4, (64, 5), None),
                                                   ("small", 4, (37, 1), (1, 8, 0.6, O.BASIS_TOP))])
 def test_noalloc_matches_forward(shape, k, sizes, policy):

@@ -178,6 +178,16 @@ static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max
     return off;
 }
 
+extern "C" int trk_workspace_bytes(const trk_cfg* cfg, uint32_t m, size_t* bytes) {
+    if (!cfg || !bytes) return fail(TRK_E_INVALID, "trk_workspace_bytes: null argument");
+    uint32_t k_cap = 0;
+    const int rc = check_cfg(cfg, m, k_cap);
+    if (rc) return rc;
+    Workspace ws{};
+    *bytes = layout_workspace(ws, *cfg, m, k_cap, nullptr);
+    return TRK_OK;
+}
+
 extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
     if (!cfg || !out) return fail(TRK_E_INVALID, "trk_create: null argument");
     uint32_t k_cap = 0;
@@ -748,7 +758,9 @@ extern "C" int trk_gemv(const trk_mat* w, uint32_t item, uint32_t s0, uint32_t s
         // gemv_tq_rows asserts xq.kb == c.kb (gemv.rs:27); blocks never straddle k
         if (kb != tq_kb(w->fmt)) return fail(TRK_E_INVALID, "kb %u differs from the codec's %u", kb, tq_kb(w->fmt));
         if (w->k % kb) return fail(TRK_E_INVALID, "k %u is not a multiple of kb %u", w->k, kb);
-        if ((uintptr_t)w->ptr % 4 || (w->count > 1 && w->stride % 4)) return fail(TRK_E_INVALID, "TQ matrix must be 4-byte aligned");
+        // the block readers take 16-byte pieces; every codec's block is a multiple of 16 bytes
+        if ((uintptr_t)w->ptr % 16 || (w->count > 1 && w->stride % 16))
+            return fail(TRK_E_INVALID, "TQ matrix pointer/stride must be 16-byte aligned");
         pitch = (uint64_t)(w->k / kb) * tq_block_bytes(w->fmt);
         mbytes = pitch * ((w->rows + 15) / 16);
     } else {

@@ -71,6 +71,7 @@ def lib() -> C.CDLL:
         vp, u32, u64, i, f, sz = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_size_t
         L.trk_last_error.restype = C.c_char_p
         L.trk_create.argtypes = [C.POINTER(Cfg), C.POINTER(vp)]
+        L.trk_workspace_bytes.argtypes = [C.POINTER(Cfg), u32, C.POINTER(sz)]
         L.trk_destroy.argtypes = [vp]
         L.trk_set_moe.argtypes = [vp, C.POINTER(Policy)]
         L.trk_moe_forward.argtypes = [vp, C.POINTER(MoeW), vp, vp, u32, vp, vp]
@@ -319,6 +320,21 @@ class LayerWeights:
         return cls(H, E, F, router, shg, gate, up, down, sh_gate, sh_up, sh_down, FMT_Q4_K, down_fmt, router_bias)
 
 
+    @classmethod
+    def generate_tq(cls, gen, H, E, F, gate_fmt=None, down_fmt=None, router_bias=None, device="cuda"):
+        """A synthetic layer of packed TQ experts generated on the GPU from a torch Generator:
+        router and shared-gate vector ~ N(0, 0.02), every TQ matrix as `gen_tq_stack`."""
+        import torch
+        gf = FMT_TQ4_32 if gate_fmt is None else gate_fmt
+        df = FMT_TQ5_16 if down_fmt is None else down_fmt
+        router = torch.randn((E, H), device=device, generator=gen) * 0.02
+        shg = torch.randn(H, device=device, generator=gen) * 0.02
+        gate, up = (gen_tq_stack(gen, E, F, H, gf, device) for _ in range(2))
+        down = gen_tq_stack(gen, E, H, F, df, device)
+        sg, su = (gen_tq_stack(gen, 1, F, H, gf, device)[0] for _ in range(2))
+        sd = gen_tq_stack(gen, 1, H, F, df, device)[0]
+        return cls(H, E, F, router, shg, gate, up, down, sg, su, sd, gf, df, router_bias)
+
     def with_down(self, down_fmt, seed, layer, device="cuda", stream=None):
         """The same layer with its routed and shared down projections regenerated in `down_fmt`
         (config 4: Q4_K gate/up, Q6_K down); every other tensor is shared with this one."""
@@ -337,7 +353,46 @@ class LayerWeights:
                             t["sh_up"], sh_down, FMT_Q4_K, down_fmt, t["router_bias"])
 
 
+def gen_tq_stack(gen, count, rows, k, fmt, device="cuda"):
+    """A stack of `count` packed TQ matrices [rows][k] on the GPU (codec.rs:1-46): uniform q bytes
+    (and 5-bit planes), each block's f16 d in [5e-4, 3e-3] and m = -d * U(0, 2^(bits-1)), the sign
+    pattern of converted GGUF weights.  `gen` is a torch Generator on `device`."""
+    import torch
+    mb = matrix_bytes(fmt, rows, k)
+    bb, bits = tq_block_bytes(fmt), fmt >> 8
+    t = torch.randint(0, 256, (count, mb), dtype=torch.uint8, device=device, generator=gen)
+    blocks = t.view(count, mb // bb, bb)
+    d = torch.empty((count, mb // bb, 16), device=device).uniform_(5e-4, 3e-3, generator=gen)
+    m = -d * torch.empty_like(d).uniform_(0, float(1 << (bits - 1)), generator=gen)
+    blocks[:, :, 0:32] = d.half().view(torch.uint8)
+    blocks[:, :, 32:64] = m.half().view(torch.uint8)
+    return t
+
+
 NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def workspace_bytes(hidden, n_expert, n_ff, k, m, k_cap=0):
+    """trk_workspace_bytes: the device workspace of the layer for m rows (host-side sizing)."""
+    out = C.c_size_t()
+    cfg = Cfg(hidden, n_expert, n_ff, k, m, k_cap, 16, 1)
+    check(lib().trk_workspace_bytes(C.byref(cfg), m, C.byref(out)))
+    return out.value
+
+
+def noalloc_max_m(hidden, n_expert, n_ff, k, k_cap=0):
+    """The largest M whose workspace fits trk_moe_forward_noalloc's static scratch (the need grows
+    with M)."""
+    lo, hi = 0, 1
+    while workspace_bytes(hidden, n_expert, n_ff, k, hi, k_cap) <= NOALLOC_SCRATCH_BYTES:
+        lo, hi = hi, 2 * hi
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        if workspace_bytes(hidden, n_expert, n_ff, k, mid, k_cap) <= NOALLOC_SCRATCH_BYTES:
+            lo = mid
+        else:
+            hi = mid
+    return lo
 
 
 def forward_noalloc(hidden, n_expert, n_ff, k, w: "LayerWeights", x, out, policy=None, k_cap=0, router_dot_max_m=16,
