@@ -296,6 +296,7 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
         int8_t* dq = ws.actq + (size_t)aslot * P * F + strip * 16;
         float* ds = ws.acts + (size_t)aslot * P * nbf + strip;
         int32_t* dsu = ws.actsum + (size_t)aslot * P * nbf + strip;
+        float* dsx = ws.actu + (size_t)aslot * P * nbf + strip;  // folded scale * sum (gemv.rs:144)
         float v = av;
 #pragma unroll
         for (int p = 0; p < P; p++) {
@@ -314,12 +315,14 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
                 if (tid == 0) {
                     st_devf(ds + p * nbf, sc * wgt);
                     st_dev(reinterpret_cast<uint32_t*>(dsu + p * nbf), (uint32_t)sum);
+                    st_devf(dsx + p * nbf, (sc * wgt) * (float)sum);
                 }
             } else {
                 dq[p * F + tid] = sat_i8(qi);
                 if (tid == 0) {
                     ds[p * nbf] = sc * wgt;
                     dsu[p * nbf] = sum;
+                    dsx[p * nbf] = (sc * wgt) * (float)sum;
                 }
             }
             v = __builtin_fmaf(-(float)qi, sc, v);  // residual for the second level (quant.rs:132)
@@ -399,7 +402,7 @@ struct DownFirst {
 
 template <int NSB>
 __device__ __forceinline__ const uint8_t* down_unit_row(const Mat& down, const Mat& shd, uint32_t kcap, uint32_t n,
-                                                        const uint32_t* ids, uint32_t row0, uint32_t u, bool& live) {
+                                                        uint32_t eid, uint32_t row0, uint32_t u, bool& live) {
     using DL = DownLanes<NSB>;
     const uint32_t ln = threadIdx.x % 64;
     const uint32_t s = u / DN_R, r = u % DN_R;
@@ -409,30 +412,94 @@ __device__ __forceinline__ const uint8_t* down_unit_row(const Mat& down, const M
     const uint8_t* base = sh ? shd.ptr : down.ptr;
     const uint64_t stride = sh ? shd.stride : down.stride;
     const uint32_t rb = sh ? shd.row_bytes : down.row_bytes;
-    // the id is requested with the count rather than after it (slots below kcap are inside the id
-    // row; a slot past the count is never used)
-    const uint32_t eid = s < kcap ? ids[s] : 0u;
     const uint32_t e = (sh || !live) ? 0u : eid;
     return base + (size_t)e * stride + (size_t)(row0 + r) * rb;
 }
 
+// The slot id a lane's first unit reads (requested ahead of the activations, so that the weight
+// requests wait only for it).
 template <int NSB>
+__device__ __forceinline__ uint32_t down_first_id(const uint32_t* ids, uint32_t kcap) {
+    using DL = DownLanes<NSB>;
+    const uint32_t s = (threadIdx.x / 64 * DL::UPW + threadIdx.x % 64 / DL::L) / DN_R;
+    return ids[s < kcap ? s : 0u];
+}
+
+// Q4: 1 the down format is Q4_K, 0 another, -1 known only at run time.  Known at compile time the
+// requests need no branch around them (a branch makes the wait before the activation stores cover
+// the weights too).
+template <int NSB, int Q4 = -1>
 __device__ __forceinline__ void down_first(const Mat& down, const Mat& shd, uint32_t kcap, uint32_t n,
-                                           const uint32_t* ids, uint32_t row0, DownFirst& f) {
+                                           uint32_t eid0, uint32_t row0, DownFirst& f) {
     using DL = DownLanes<NSB>;
     const uint32_t wv = threadIdx.x / 64, ln = threadIdx.x % 64, q = ln % DL::L;
     const uint32_t u0 = wv * DL::UPW + ln / DL::L;
-    f.rowp = down_unit_row<NSB>(down, shd, kcap, n, ids, row0, u0, f.live);
+    f.rowp = down_unit_row<NSB>(down, shd, kcap, n, eid0, row0, u0, f.live);
     f.hdr = make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) f.qs[i] = f.hdr;
-    if (f.live && down.fmt == TRK_FMT_Q4_K) load_half_q4k(f.rowp, q / 2, q % 2, f.hdr, f.qs);
+    // lanes without a unit read expert 0 (a valid row): no per-lane branch around the requests
+    if (Q4 == 1 || (Q4 < 0 && down.fmt == TRK_FMT_Q4_K)) load_half_q4k(f.rowp, q / 2, q % 2, f.hdr, f.qs);
 }
 
+// The slots' activation rows, scales and sums, staged in LDS: one piece (16 bytes of a row, its
+// 16-block's scale and sum) per entry, a round of 4 entries per thread (1024 per round).
+typedef int v4i32 __attribute__((ext_vector_type(4)));  // (HIP's int4 arrays went to scratch here)
+struct DownStage {
+    v4i32 t[4];
+    float sc[4], u[4];  // folded scale, scale * sum (written by the gate/up launch)
+};
+
 template <int P, int NSB, bool COH>
+__device__ __forceinline__ void down_stage_load(const Workspace& ws, uint32_t kcap, uint32_t i0, DownStage& st) {
+    constexpr uint32_t F = NSB * 256, QP = P * F / 16;  // int4 pieces of a slot = its scales = its sums
+    const uint32_t tid = threadIdx.x, nq = (kcap + 1) * QP;
+    // clamped indices, so no per-lane branch separates the loads
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
+        const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
+        const int4* src = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F) + ic % QP;
+        const size_t o = (size_t)a * QP + ic % QP;
+        if constexpr (COH) {
+            const unsigned long long* w2 = reinterpret_cast<const unsigned long long*>(src);
+            const unsigned long long lo = ld_dev(w2), hi = ld_dev(w2 + 1);
+            st.t[c] = v4i32{(int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi, (int)(uint32_t)(hi >> 32)};
+            st.sc[c] = ld_devf(ws.acts + o);
+            st.u[c] = ld_devf(ws.actu + o);
+        } else {
+            st.t[c] = *reinterpret_cast<const v4i32*>(src);
+            st.sc[c] = ws.acts[o];
+            st.u[c] = ws.actu[o];
+        }
+    }
+}
+
+template <int P, int NSB>
+__device__ __forceinline__ void down_stage_store(uint8_t* smem, uint32_t kcap, uint32_t i0, const DownStage& st) {
+    constexpr uint32_t F = NSB * 256, nbf = NSB * 16, SQ = P * F + 16, QP = P * F / 16;
+    static_assert(QP == P * nbf, "a 16-byte piece per 16-block");
+    const uint32_t slots = kcap + 1, nq = slots * QP, tid = threadIdx.x;
+    int8_t* aq = (int8_t*)smem;                       // [slots][SQ]
+    float* as = (float*)(smem + (size_t)slots * SQ);  // [slots][P][nbf] folded scale
+    float* au = as + slots * P * nbf;                 // [slots][P][nbf] scale * sum
+    // every thread stores (entries past the end repeat the last one with its own value): a
+    // conditional store would let the compiler sink the loads behind the weight requests
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
+        *reinterpret_cast<v4i32*>(aq + (size_t)(ic / QP) * SQ + (ic % QP) * 16) = st.t[c];
+        as[ic] = st.sc[c];
+        au[ic] = st.u[c];
+    }
+}
+
+// PRE: st holds the first staging round, already requested (the standalone kernel requests it ahead
+// of the weights, so the activations' round trip overlaps the weights'); otherwise requested here
+template <int P, int NSB, bool COH, bool PRE>
 __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const Workspace& ws, uint32_t kcap,
                                           uint32_t n, const uint32_t* ids, float* __restrict__ out, int residual,
-                                          uint32_t row0, uint8_t* smem, const DownFirst& first) {
+                                          uint32_t row0, uint8_t* smem, const DownFirst& first, DownStage& st) {
     using DL = DownLanes<NSB>;
     constexpr uint32_t F = NSB * 256, nbf = NSB * 16, SQ = P * F + 16;
     const uint32_t tid = threadIdx.x;
@@ -447,43 +514,14 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
     float* vres = au + slots * P * nbf;                        // [slots][DN_R]
 
     {
-        // loads first (clamped indices, so no per-lane branch separates them), then the stores:
-        // one memory round trip per chunk of 4 (int4 piece, scale, sum) per thread
-        constexpr uint32_t QP = P * F / 16;  // int4 pieces of a slot = its scales = its sums
-        static_assert(QP == P * nbf, "a 16-byte piece per 16-block");
-        const uint32_t nq = slots * QP;
-        for (uint32_t i0 = 0; i0 < nq; i0 += 1024) {
-            int4 t[4];
-            float sc[4];
-            int32_t su[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
-                const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
-                const int4* src = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F) + ic % QP;
-                const size_t o = (size_t)a * QP + ic % QP;
-                if constexpr (COH) {
-                    const unsigned long long* w2 = reinterpret_cast<const unsigned long long*>(src);
-                    const unsigned long long lo = ld_dev(w2), hi = ld_dev(w2 + 1);
-                    t[c] = make_int4((int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
-                                     (int)(uint32_t)(hi >> 32));
-                    sc[c] = ld_devf(ws.acts + o);
-                    su[c] = (int32_t)ld_dev(reinterpret_cast<const uint32_t*>(ws.actsum + o));
-                } else {
-                    t[c] = *src;
-                    sc[c] = ws.acts[o];
-                    su[c] = ws.actsum[o];
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint32_t i = i0 + tid + 256 * c;
-                if (i < nq) {
-                    *reinterpret_cast<int4*>(aq + (size_t)(i / QP) * SQ + (i % QP) * 16) = t[c];
-                    as[i] = sc[c];
-                    au[i] = sc[c] * (float)su[c];
-                }
-            }
+        // one memory round trip per round of 4 (int4 piece, scale, sum) per thread
+        const uint32_t nq = slots * (P * F / 16);
+        if (!PRE) down_stage_load<P, NSB, COH>(ws, kcap, 0, st);
+        down_stage_store<P, NSB>(smem, kcap, 0, st);
+        for (uint32_t i0 = 1024; i0 < nq; i0 += 1024) {
+            DownStage sn;
+            down_stage_load<P, NSB, COH>(ws, kcap, i0, sn);
+            down_stage_store<P, NSB>(smem, kcap, i0, sn);
         }
     }
     __syncthreads();
@@ -494,7 +532,8 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
         bool live = first.live;
         const uint8_t* rowp = first.rowp;
         if (pass > 0) {
-            rowp = down_unit_row<NSB>(down, shd, kcap, n, ids, row0, u, live);
+            const uint32_t su = u / DN_R;
+            rowp = down_unit_row<NSB>(down, shd, kcap, n, su < kcap ? ids[su] : 0u, row0, u, live);
             if (live && q4) load_half_q4k(rowp, sb, h2, hdr, qs);
         }
         const uint32_t s = live ? u / DN_R : 0u;
@@ -548,14 +587,20 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
     }
 }
 
-template <int P, int NSB>
+template <int P, int NSB, int Q4>
 __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t kcap,
                                                          float* __restrict__ out, int residual) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t row0 = blockIdx.x * DN_R, n = ws.n_sel[0];
+    // the count and the first unit's expert id are requested together (slots below kcap are inside
+    // the id row; a slot past the count is never used), then the activations, whose round trip runs
+    // beside the weights' once the id is in
+    const uint32_t row0 = blockIdx.x * DN_R, n = ws.n_sel[0], eid0 = down_first_id<NSB>(ws.ids, kcap);
+    DownStage st;
+    down_stage_load<P, NSB, false>(ws, kcap, 0, st);
+    __builtin_amdgcn_sched_barrier(0);  // keep those requests ahead of the weights'
     DownFirst first;
-    down_first<NSB>(down, shd, kcap, n, ws.ids, row0, first);
-    down_unit<P, NSB, false>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first);
+    down_first<NSB, Q4>(down, shd, kcap, n, eid0, row0, first);
+    down_unit<P, NSB, false, true>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first, st);
 }
 
 // ---- the whole decode layer in one launch ----------------------------------------------------
@@ -651,9 +696,10 @@ __global__ __launch_bounds__(256) void decode_pipe_kernel(const float* __restric
         __syncthreads();
         const uint32_t n = r_ids[K_MAX];
         DownFirst first;
-        down_first<NSBF>(down, shd, kcap, n, r_ids, row0, first);  // in flight during the wait
+        down_first<NSBF>(down, shd, kcap, n, down_first_id<NSBF>(r_ids, kcap), row0, first);  // in flight during the wait
         pipe_wait(cw, PIPE_B, gu);
-        down_unit<P, NSBF, true>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first);
+        DownStage st;
+        down_unit<P, NSBF, true, false>(down, shd, ws, kcap, n, r_ids, out, residual, row0, usm, first, st);
     }
     __syncthreads();
     if (tid == 0) {  // the last workgroup out zeroes the counters for the next launch
@@ -744,12 +790,15 @@ hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspa
     const int P = pair ? 2 : 1;
     const size_t slots = kcap + 1;
     const size_t lds = slots * ((size_t)P * F + 16) + slots * P * nbf * 8 + slots * DN_R * 4 + 64;
-    switch (F / 256 * 2 + (pair ? 1 : 0)) {
-#define DN_CASE(ns) \
-    case ns * 2: decode_down_kernel<1, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break; \
-    case ns * 2 + 1: decode_down_kernel<2, ns><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break;
+    const bool q4 = down.fmt == TRK_FMT_Q4_K;
+    switch ((F / 256 * 2 + (pair ? 1 : 0)) * 2 + (q4 ? 1 : 0)) {
+#define DN_CASE2(ns, p, q)                                                                                          \
+    case (ns * 2 + p - 1) * 2 + q:                                                                                  \
+        decode_down_kernel<p, ns, q><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break;
+#define DN_CASE(ns) DN_CASE2(ns, 1, 0) DN_CASE2(ns, 1, 1) DN_CASE2(ns, 2, 0) DN_CASE2(ns, 2, 1)
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE
+#undef DN_CASE2
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -16,9 +16,9 @@ namespace trk {
 // order-preserving key of a logit (-0 and +0 share one key, as they compare equal); 0 for values
 // that never enter the top-k (nan, -inf: router.rs:75-76)
 __device__ __forceinline__ uint32_t fkey(float v) {
-    if (!(v > -__builtin_inff())) return 0u;
     const uint32_t u = __float_as_uint(v + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return v > -__builtin_inff() ? k : 0u;  // selects, no branch
 }
 __device__ __forceinline__ float fkey_inv(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
@@ -80,6 +80,8 @@ __device__ __forceinline__ uint32_t route_select_rounds(const float* __restrict_
     return ksel;
 }
 
+constexpr uint32_t ROUTE_CAND_DUMMY = 95;  // the candidate slot lanes without a candidate write
+
 // One token on one whole wave.  Lanes < count write ids_out[lane] / w_out[lane]; returns count.
 // `cand` is 96 entries of LDS for this wave; `ex` (E floats of LDS) is used only for
 // MassBasis::All.
@@ -105,7 +107,10 @@ __device__ uint32_t route_select(const float* __restrict__ lg, uint32_t E, uint3
     }
     uint32_t key[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) key[j] = lane + 64u * j < E ? fkey(v[j]) : 0u;
+    for (int j = 0; j < NJ; j++) {
+        const uint32_t kf = fkey(v[j]);
+        key[j] = lane + 64u * j < E ? kf : 0u;
+    }
     const uint32_t kk = pol.enabled ? pol.max : k;
     uint32_t lmax = key[0];
 #pragma unroll
@@ -123,16 +128,16 @@ __device__ uint32_t route_select(const float* __restrict__ lg, uint32_t E, uint3
         T = c3 >= kk ? t3 : (c2 >= kk ? t2 : (c1 >= kk ? t1 : T));
     }
     const uint32_t L = T > 1u ? T : 1u;  // key 0 (nan, -inf) is never selectable
+    // every lane writes (those without a candidate to slot 95, which the ranking below rewrites
+    // before it is read): no branch per j
     uint32_t C = 0;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const bool c = key[j] >= L;
         const uint64_t m = __ballot(c);
-        if (c) {
-            const uint32_t pos =
-                    C + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (pos < 64u) cand[pos] = make_uint2(key[j], lane + 64u * j);
-        }
+        const uint32_t pos =
+                C + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        cand[c && pos < 64u ? pos : ROUTE_CAND_DUMMY] = make_uint2(key[j], lane + 64u * j);
         C += (uint32_t)__popcll(m);
     }
     my_key = 0;
