@@ -737,21 +737,107 @@ void orc_mass_profile(const float *logits, int n, float *cum) {
     }
 }
 
-/* exec.rs:630-639 (Model::route) */
-static int route(const float *logits, int n, int k, const orc_policy *p, uint32_t *ids, float *w) {
-    if (p) return orc_route_mass(logits, n, p, ids, w);
-    orc_route_topk(logits, n, k, ids, w);
-    return k;
+/* exec_batch.rs:214-225 (fold_ids): subset packs map the routed ids onto the packed experts,
+ * keeping them distinct within the token */
+int orc_fold_ids(uint32_t *ids, int n, uint32_t packed) {
+    if (n > (int)packed) return -1; /* exec_batch.rs:217: more routed experts than packed experts */
+    for (int i = 0; i < n; i++) {
+        uint32_t id = ids[i] % packed;
+        for (;;) {
+            int taken = 0;
+            for (int j = 0; j < i; j++) taken |= ids[j] == id;
+            if (!taken) break;
+            id = (id + 1) % packed;
+        }
+        ids[i] = id;
+    }
+    return 0;
+}
+
+/* exec.rs:630-639 (Model::route), then the subset-pack fold of exec.rs:1545-1549 /
+ * exec_batch.rs:1418-1420 */
+static int route_w(const orc_moe_w *W, const float *logits, int k, const orc_policy *p, uint32_t *ids, float *w) {
+    int n = W->E, used;
+    if (p)
+        used = orc_route_mass(logits, n, p, ids, w);
+    else {
+        orc_route_topk(logits, n, k, ids, w);
+        used = k;
+    }
+    if (W->packed > 0 && W->packed < W->E && orc_fold_ids(ids, used, (uint32_t)W->packed) != 0) return -1;
+    return used;
+}
+
+static int tiles_of(const orc_moe_w *W) { return W->tiles > 1 ? W->tiles : 1; }
+
+/* bytes of one tile's gate/up [F/T][H] and down [H][F/T] matrices */
+static size_t gu_tile_bytes(const orc_moe_w *W, int bits) {
+    return orc_tq_matrix_bytes(W->F / tiles_of(W), W->H, bits, 32);
+}
+static size_t dn_tile_bytes(const orc_moe_w *W, int bits) {
+    return orc_tq_matrix_bytes(W->H, W->F / tiles_of(W), bits, 16);
 }
 
 /* ========================================================================================== */
 /* MoE block                                                                                  */
 /* ========================================================================================== */
 
+/* Router logits of one row in dot order (exec.rs:1003-1011): with T tiles, tile t's partial is
+ * dot(router_t[e], x[H/T t ..]) over its H/T columns, and the partials are summed in tile order
+ * (Mailboxes::reduce, exchange.rs:122-136: the first copied, the others added). */
 static void router_logits_dot(const orc_moe_w *W, const float *x, float *rlog) {
+    const int T = tiles_of(W), hl = W->H / T;
     for (int e = 0; e < W->E; e++) {
-        rlog[e] = orc_dot(W->router + (size_t)e * W->H, x, W->H);
-        if (W->router_bias) rlog[e] = rlog[e] + W->router_bias[e];
+        float v = 0.0f;
+        for (int t = 0; t < T; t++) {
+            const float p = orc_dot(W->router + ((size_t)t * W->E + e) * hl, x + (size_t)t * hl, hl);
+            v = t == 0 ? p : v + p;
+        }
+        rlog[e] = W->router_bias ? v + W->router_bias[e] : v;
+    }
+}
+
+/* The batch router (exec_batch.rs:1008-1016): per tile gemm_f32_nt over the tile's H/T columns,
+ * the partials summed in tile order.  (The reference's batch all-reduce starts each row's sum at a
+ * tile that depends on which core handles the row, exec_batch.rs:741-747; tile order 0..T-1 is its
+ * sum where that is core 0 of a single-socket pack.) */
+static void router_logits_gemm(const orc_moe_w *W, const float *x, int M, float *lg) {
+    const int T = tiles_of(W), hl = W->H / T, E = W->E;
+    if (T == 1) {
+        orc_gemm_f32_nt(x, W->H, M, W->router, W->H, E, W->H, lg, E);
+    } else {
+        float *p = (float *)malloc(sizeof(float) * (size_t)M * E);
+        for (int t = 0; t < T; t++) {
+            orc_gemm_f32_nt(x + (size_t)t * hl, W->H, M, W->router + (size_t)t * E * hl, hl, E, hl,
+                            t == 0 ? lg : p, E);
+            if (t > 0)
+                for (size_t i = 0; i < (size_t)M * E; i++) lg[i] = lg[i] + p[i];
+        }
+        free(p);
+    }
+    if (W->router_bias)
+        for (int mi = 0; mi < M; mi++)
+            for (int e = 0; e < E; e++) lg[(size_t)mi * E + e] = lg[(size_t)mi * E + e] + W->router_bias[e];
+}
+
+/* Router logits of M rows as the decode path (dot_rows: per-row dot) or the batch gemm computes
+ * them, tiles and bias included. */
+void orc_moe_logits(const orc_moe_w *W, const float *x, int M, int dot_rows, float *out) {
+    if (dot_rows)
+        for (int mi = 0; mi < M; mi++) router_logits_dot(W, x + (size_t)mi * W->H, out + (size_t)mi * W->E);
+    else
+        router_logits_gemm(W, x, M, out);
+}
+
+/* Tile t's slice [F/T t, F/T (t+1)) of `rows` activation rows of length F (with their per-16
+ * scales and sums), copied out contiguously. */
+static void act_slice(const int8_t *q, const float *s, const int32_t *su, int rows, int F, int T, int t, int8_t *tq,
+                      float *ts, int32_t *tsu) {
+    const int per = F / T, nbf = F / 16, nbt = per / 16;
+    for (int r = 0; r < rows; r++) {
+        memcpy(tq + (size_t)r * per, q + (size_t)r * F + (size_t)per * t, per);
+        memcpy(ts + (size_t)r * nbt, s + (size_t)r * nbf + (size_t)nbt * t, sizeof(float) * nbt);
+        memcpy(tsu + (size_t)r * nbt, su + (size_t)r * nbf + (size_t)nbt * t, sizeof(int32_t) * nbt);
     }
 }
 
@@ -768,7 +854,11 @@ int orc_moe_block(const orc_moe_w *W, const float *x, const float *rlog, int k,
     else
         router_logits_dot(W, x, lg);
     if (rlog_out) memcpy(rlog_out, lg, sizeof(float) * E);
-    int k_used = route(lg, E, k, policy, ids, w);
+    int k_used = route_w(W, lg, k, policy, ids, w);
+    if (k_used < 0) {
+        free(lg);
+        return -1;
+    }
     int slots = k_used + 1;
     for (int s = 0; s < k_used; s++)
         if (!W->gate[ids[s]] || !W->up[ids[s]] || !W->down[ids[s]]) {
@@ -792,13 +882,19 @@ int orc_moe_block(const orc_moe_w *W, const float *x, const float *rlog, int k,
     orc_qact qa = {mrows, H, 32, xq, xs, xsu, hiprec};
     float *hg = (float *)malloc(sizeof(float) * (size_t)slots * F);
     float *hu = (float *)malloc(sizeof(float) * (size_t)slots * F);
-    /* tasks A (exec.rs:1563-1577) */
+    /* tasks A (exec.rs:1563-1577); tile t computes rows [F/T t, F/T (t+1)) */
+    const int T = tiles_of(W), per = F / T;
     for (int slot = 0; slot < slots; slot++) {
         const uint8_t *g = slot < k_used ? W->gate[ids[slot]] : W->sh_gate;
         const uint8_t *u = slot < k_used ? W->up[ids[slot]] : W->sh_up;
         int gb = slot < k_used ? W->gate_bits : W->sh_gate_bits;
-        orc_gemv_tq_rows(g, H, gb, 32, 0, F / ORC_STRIP, &qa, hg + (size_t)slot * F, 0, NULL, 0);
-        orc_gemv_tq_rows(u, H, gb, 32, 0, F / ORC_STRIP, &qa, hu + (size_t)slot * F, 0, NULL, 0);
+        const size_t tb = gu_tile_bytes(W, gb);
+        for (int t = 0; t < T; t++) {
+            orc_gemv_tq_rows(g + t * tb, H, gb, 32, 0, per / ORC_STRIP, &qa, hg + (size_t)slot * F + (size_t)per * t, 0,
+                             NULL, 0);
+            orc_gemv_tq_rows(u + t * tb, H, gb, 32, 0, per / ORC_STRIP, &qa, hu + (size_t)slot * F + (size_t)per * t, 0,
+                             NULL, 0);
+        }
     }
     /* tasks B (exec.rs:1584-1606): kb = down.kb = 16 */
     int kb = 16, nb = F / kb;
@@ -818,14 +914,29 @@ int orc_moe_block(const orc_moe_w *W, const float *x, const float *rlog, int k,
             orc_quant_rows(act, 1, F, kb, q, sc, su);
         for (int i = 0; i < mrows * nb; i++) sc[i] *= wgt;
     }
-    /* tasks C (exec.rs:1610-1621) */
-    for (int slot = 0; slot < slots; slot++) {
-        const uint8_t *dm = slot < k_used ? W->down[ids[slot]] : W->sh_down;
-        int db = slot < k_used ? W->down_bits : W->sh_down_bits;
-        orc_qact da = {mrows, F, kb, aq + (size_t)2 * slot * F, as + (size_t)2 * slot * nb,
-                       asu + (size_t)2 * slot * nb, hiprec};
-        orc_gemv_tq_rows(dm, F, db, kb, 0, H / ORC_STRIP, &da, out, 0, NULL, slot > 0);
+    /* tasks C (exec.rs:1610-1621): each tile's partial over its columns of F, slot 0 stored and
+     * later slots added, the shared expert last; then the tiles' partials in tile order
+     * (exec.rs:1035-1038, Mailboxes::reduce) */
+    int8_t *tq = (int8_t *)malloc((size_t)2 * per);
+    float *ts = (float *)malloc(sizeof(float) * 2 * (per / kb));
+    int32_t *tsu = (int32_t *)malloc(sizeof(int32_t) * 2 * (per / kb));
+    float *part = T > 1 ? (float *)malloc(sizeof(float) * H) : out;
+    for (int t = 0; t < T; t++) {
+        for (int slot = 0; slot < slots; slot++) {
+            const uint8_t *dm = slot < k_used ? W->down[ids[slot]] : W->sh_down;
+            int db = slot < k_used ? W->down_bits : W->sh_down_bits;
+            act_slice(aq + (size_t)2 * slot * F, as + (size_t)2 * slot * nb, asu + (size_t)2 * slot * nb, mrows, F, T, t,
+                      tq, ts, tsu);
+            orc_qact da = {mrows, per, kb, tq, ts, tsu, hiprec};
+            orc_gemv_tq_rows(dm + t * dn_tile_bytes(W, db), per, db, kb, 0, H / ORC_STRIP, &da, part, 0, NULL, slot > 0);
+        }
+        if (T > 1)
+            for (int h = 0; h < H; h++) out[h] = t == 0 ? part[h] : out[h] + part[h];
     }
+    if (T > 1) free(part);
+    free(tq);
+    free(ts);
+    free(tsu);
     free(lg);
     free(xq);
     free(xs);
@@ -916,10 +1027,7 @@ int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, 
     } else if (M < router_dot_max_m) {
         for (int mi = 0; mi < M; mi++) router_logits_dot(W, x + (size_t)mi * H, lg + (size_t)mi * E);
     } else {
-        orc_gemm_f32_nt(x, H, M, W->router, H, E, H, lg, E);
-        if (W->router_bias)
-            for (int mi = 0; mi < M; mi++)
-                for (int e = 0; e < E; e++) lg[(size_t)mi * E + e] = lg[(size_t)mi * E + e] + W->router_bias[e];
+        router_logits_gemm(W, x, M, lg);
     }
     if (rlog_out) memcpy(rlog_out, lg, sizeof(float) * (size_t)M * E);
     /* routing + quant_rows per token (exec_batch.rs:1415-1425) */
@@ -928,7 +1036,12 @@ int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, 
     float *xs = (float *)malloc(sizeof(float) * (size_t)M * nbx);
     int32_t *xsu = (int32_t *)malloc(sizeof(int32_t) * (size_t)M * nbx);
     for (int mi = 0; mi < M; mi++) {
-        n_sel[mi] = (uint32_t)route(lg + (size_t)mi * E, E, k, policy, ids + (size_t)mi * ka, w + (size_t)mi * ka);
+        const int used = route_w(W, lg + (size_t)mi * E, k, policy, ids + (size_t)mi * ka, w + (size_t)mi * ka);
+        if (used < 0) {
+            free(lg); free(xq); free(xs); free(xsu);
+            return -1;
+        }
+        n_sel[mi] = (uint32_t)used;
     }
     orc_quant_rows(x, M, H, 32, xq, xs, xsu);
     /* grouping (exec_batch.rs:1428-1462): stable sort of token-major (token, slot) by expert */
@@ -981,7 +1094,9 @@ int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, 
             return -1;
         }
     }
-    /* tasks A (exec_batch.rs:1481-1509): gate/up per group on the gathered rows, shared on all */
+    /* tasks A (exec_batch.rs:1481-1509): gate/up per group on the gathered rows, shared on all;
+     * tile t computes rows [F/T t, F/T (t+1)) */
+    const int T = tiles_of(W), per = F / T;
     int rows_all = n_ent + M;
     float *hg = (float *)malloc(sizeof(float) * (size_t)rows_all * F);
     float *hu = (float *)malloc(sizeof(float) * (size_t)rows_all * F);
@@ -998,12 +1113,24 @@ int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, 
             memcpy(gsu + (size_t)i * nbx, xsu + (size_t)tok * nbx, sizeof(int32_t) * nbx);
         }
         orc_qact ga = {r1 - r0, H, 32, gq, gs, gsu, 0};
-        orc_gemm_tq_rows(W->gate[e], H, W->gate_bits, 32, 0, F / ORC_STRIP, &ga, hg + (size_t)r0 * F, F, NULL, 0);
-        orc_gemm_tq_rows(W->up[e], H, W->gate_bits, 32, 0, F / ORC_STRIP, &ga, hu + (size_t)r0 * F, F, NULL, 0);
+        const size_t tb = gu_tile_bytes(W, W->gate_bits);
+        for (int t = 0; t < T; t++) {
+            orc_gemm_tq_rows(W->gate[e] + t * tb, H, W->gate_bits, 32, 0, per / ORC_STRIP, &ga,
+                             hg + (size_t)r0 * F + (size_t)per * t, F, NULL, 0);
+            orc_gemm_tq_rows(W->up[e] + t * tb, H, W->gate_bits, 32, 0, per / ORC_STRIP, &ga,
+                             hu + (size_t)r0 * F + (size_t)per * t, F, NULL, 0);
+        }
     }
     orc_qact all = {M, H, 32, xq, xs, xsu, 0};
-    orc_gemm_tq_rows(W->sh_gate, H, W->sh_gate_bits, 32, 0, F / ORC_STRIP, &all, hg + (size_t)n_ent * F, F, NULL, 0);
-    orc_gemm_tq_rows(W->sh_up, H, W->sh_gate_bits, 32, 0, F / ORC_STRIP, &all, hu + (size_t)n_ent * F, F, NULL, 0);
+    {
+        const size_t tb = gu_tile_bytes(W, W->sh_gate_bits);
+        for (int t = 0; t < T; t++) {
+            orc_gemm_tq_rows(W->sh_gate + t * tb, H, W->sh_gate_bits, 32, 0, per / ORC_STRIP, &all,
+                             hg + (size_t)n_ent * F + (size_t)per * t, F, NULL, 0);
+            orc_gemm_tq_rows(W->sh_up + t * tb, H, W->sh_gate_bits, 32, 0, per / ORC_STRIP, &all,
+                             hu + (size_t)n_ent * F + (size_t)per * t, F, NULL, 0);
+        }
+    }
     /* tasks B (exec_batch.rs:1513-1536) */
     int kb = 16, nbd = F / kb;
     int8_t *aq = (int8_t *)malloc((size_t)rows_all * F);
@@ -1016,16 +1143,31 @@ int orc_moe_batch(const orc_moe_w *W, const float *x, const float *rlog, int M, 
         orc_quant_rows(act, 1, F, kb, aq + (size_t)r * F, as + (size_t)r * nbd, asu + (size_t)r * nbd);
         for (int i = 0; i < nbd; i++) as[(size_t)r * nbd + i] *= wgt;
     }
-    /* tasks C (exec_batch.rs:1539-1561): shared first (overwrite), then groups ascending by
-     * expert, each group's rows accumulated into their tokens' rows */
-    orc_qact sa = {M, F, kb, aq + (size_t)n_ent * F, as + (size_t)n_ent * nbd, asu + (size_t)n_ent * nbd, 0};
-    orc_gemm_tq_rows(W->sh_down, F, W->sh_down_bits, kb, 0, H / ORC_STRIP, &sa, out, H, NULL, 0);
-    for (int g = 0; g < ng; g++) {
-        int r0 = (int)grp_start[g], r1 = (int)grp_start[g + 1];
-        uint32_t e = grp_expert[g];
-        orc_qact da = {r1 - r0, F, kb, aq + (size_t)r0 * F, as + (size_t)r0 * nbd, asu + (size_t)r0 * nbd, 0};
-        orc_gemm_tq_rows(W->down[e], F, W->down_bits, kb, 0, H / ORC_STRIP, &da, out, H, ent_tok + r0, 1);
+    /* tasks C (exec_batch.rs:1539-1561), per tile over its columns of F: shared first
+     * (overwrite), then groups ascending by expert, each group's rows accumulated into their
+     * tokens' rows; then the tiles' partials in tile order (exec_batch.rs:821-849) */
+    int8_t *tq = (int8_t *)malloc((size_t)rows_all * per);
+    float *ts = (float *)malloc(sizeof(float) * (size_t)rows_all * (per / kb));
+    int32_t *tsu = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows_all * (per / kb));
+    float *part = T > 1 ? (float *)malloc(sizeof(float) * (size_t)M * H) : out;
+    const int nbt = per / kb;
+    for (int t = 0; t < T; t++) {
+        act_slice(aq, as, asu, rows_all, F, T, t, tq, ts, tsu);
+        orc_qact sa = {M, per, kb, tq + (size_t)n_ent * per, ts + (size_t)n_ent * nbt, tsu + (size_t)n_ent * nbt, 0};
+        orc_gemm_tq_rows(W->sh_down + t * dn_tile_bytes(W, W->sh_down_bits), per, W->sh_down_bits, kb, 0, H / ORC_STRIP,
+                         &sa, part, H, NULL, 0);
+        for (int g = 0; g < ng; g++) {
+            int r0 = (int)grp_start[g], r1 = (int)grp_start[g + 1];
+            uint32_t e = grp_expert[g];
+            orc_qact da = {r1 - r0, per, kb, tq + (size_t)r0 * per, ts + (size_t)r0 * nbt, tsu + (size_t)r0 * nbt, 0};
+            orc_gemm_tq_rows(W->down[e] + t * dn_tile_bytes(W, W->down_bits), per, W->down_bits, kb, 0, H / ORC_STRIP, &da,
+                             part, H, ent_tok + r0, 1);
+        }
+        if (T > 1)
+            for (size_t i = 0; i < (size_t)M * H; i++) out[i] = t == 0 ? part[i] : out[i] + part[i];
     }
+    if (T > 1) free(part);
+    free(tq); free(ts); free(tsu);
     free(lg); free(xq); free(xs); free(xsu); free(cnt);
     free(hg); free(hu); free(gq); free(gs); free(gsu);
     free(aq); free(as); free(asu); free(act);

@@ -136,7 +136,24 @@ typedef struct {
     const uint8_t *const *down; /* [E] [H][F] */
     int sh_gate_bits, sh_down_bits;
     const uint8_t *sh_gate, *sh_up, *sh_down;
+    /* T tiles (python/trpack/plan.py:106-118,174-181): 0 or 1 = one tile.  With T > 1 the
+     * router is [T][E][H/T] (tile t: columns [H/T t, H/T (t+1)) of every expert's row), each
+     * gate/up pointer holds the T tiles' [F/T][H] matrices back to back (tile t: rows
+     * [F/T t, F/T (t+1))), each down pointer the T tiles' [H][F/T] matrices (tile t: columns
+     * [F/T t, F/T (t+1))), and the shared expert's likewise. */
+    int tiles;
+    /* n_expert_packed of a subset pack (exec.rs:1545-1549): routed ids are folded onto the first
+     * `packed` experts by fold_ids (exec_batch.rs:214-225); 0 = E (no folding). */
+    int packed;
 } orc_moe_w;
+
+/* fold_ids (exec_batch.rs:214-225): ids[i] <- the first of ids[i] % packed, +1, +2, ... (mod
+ * packed) not among ids[0..i).  Returns -1 (the reference asserts) when n > packed. */
+int orc_fold_ids(uint32_t *ids, int n, uint32_t packed);
+
+/* Router logits of M rows x [M][H] into out [M][E]: per-row dot order (dot_rows) or the batch gemm
+ * order, with the layer's tiles and bias. */
+void orc_moe_logits(const orc_moe_w *W, const float *x, int M, int dot_rows, float *out);
 
 typedef struct {
     uint64_t rows, experts; /* MoeStats::add (exec.rs:602-605) */

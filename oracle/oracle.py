@@ -63,7 +63,7 @@ class MoeW(C.Structure):
                 ("router_bias", C.c_void_p), ("shexp_gate", C.c_void_p), ("gate_bits", C.c_int),
                 ("down_bits", C.c_int), ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
                 ("sh_gate_bits", C.c_int), ("sh_down_bits", C.c_int), ("sh_gate", C.c_void_p),
-                ("sh_up", C.c_void_p), ("sh_down", C.c_void_p)]
+                ("sh_up", C.c_void_p), ("sh_down", C.c_void_p), ("tiles", C.c_int), ("packed", C.c_int)]
 
 
 class Stats(C.Structure):
@@ -116,6 +116,8 @@ def _declare(L):
     L.orc_route_mass.restype = i
     L.orc_mass_profile.argtypes = [vp, i, vp]
     L.orc_moe_block.argtypes = [C.POINTER(MoeW), vp, vp, i, C.POINTER(Policy), i, vp, vp, vp, vp, C.POINTER(Stats)]
+    L.orc_moe_logits.argtypes = [C.POINTER(MoeW), vp, i, i, vp]
+    L.orc_fold_ids.argtypes = [vp, i, C.c_uint32]
     L.orc_moe_block.restype = i
     L.orc_moe_batch.argtypes = [C.POINTER(MoeW), vp, vp, i, i, C.POINTER(Policy), i, vp, vp, vp, vp, vp,
                                 vp, vp, vp, vp, vp, vp, vp, C.POINTER(Stats)]
@@ -318,6 +320,14 @@ def route_topk(logits, k):
     return ids[:k].copy(), w[:k].copy()
 
 
+def fold_ids(ids, packed):
+    """fold_ids (exec_batch.rs:214-225) on a copy of ids."""
+    out = np.ascontiguousarray(ids, np.uint32).copy()
+    if lib().orc_fold_ids(_p(out), out.size, packed) != 0:
+        raise ValueError("more routed experts than packed experts")
+    return out
+
+
 def route_mass(logits, mn, mx, mass, basis=BASIS_TOP):
     lg = np.ascontiguousarray(logits, np.float32)
     ids = np.zeros(MOE_K_MAX, np.uint32)
@@ -401,32 +411,40 @@ class OracleLayer:
             self._up_ptrs[e] = u.ctypes.data
             self._down_ptrs[e] = d.ctypes.data
 
+    tiles = 1   # the reference's T tiles (plan.py:106-118): see TQOracleLayer
+    packed = 0  # n_expert_packed of a subset pack (fold_ids); 0: all E experts packed
+
     def _w(self):
         return MoeW(self.H, self.E, self.F, self.router.ctypes.data,
                     None if self.router_bias is None else self.router_bias.ctypes.data,
                     self.shexp_gate.ctypes.data, self.gate_bits, self.down_bits,
                     C.cast(self._gate_ptrs, C.c_void_p), C.cast(self._up_ptrs, C.c_void_p),
                     C.cast(self._down_ptrs, C.c_void_p), self.gate_bits, self.sh_down_bits,
-                    self.sh_gate.ctypes.data, self.sh_up.ctypes.data, self.sh_down.ctypes.data)
+                    self.sh_gate.ctypes.data, self.sh_up.ctypes.data, self.sh_down.ctypes.data, self.tiles,
+                    self.packed)
 
     def logits(self, x, dot_rows=True):
-        """Router logits as the decode path (dot) or batch gemm path computes them."""
+        """Router logits as the decode path (dot) or batch gemm path computes them (tiles: the
+        tiles' partials in tile order)."""
         x = np.ascontiguousarray(x, np.float32).reshape(-1, self.H)
-        if dot_rows:
-            lg = np.array([[dot(self.router[e], xi) for e in range(self.E)] for xi in x], np.float32)
-        else:
-            lg = gemm_f32_nt(x, self.router)
-        if self.router_bias is not None:
-            lg = (lg + self.router_bias[None, :]).astype(np.float32)
+        lg = np.zeros((x.shape[0], self.E), np.float32)
+        W = self._w()
+        lib().orc_moe_logits(C.byref(W), _p(x), x.shape[0], int(bool(dot_rows)), _p(lg))
         return lg
+
+    def _routed(self, lg, k, policy):
+        """The experts a row's routing uses (folded onto the packed experts of a subset pack)."""
+        ids, _ = (route_mass(lg, *policy) if policy else route_topk(lg, k))
+        if self.packed and self.packed < self.E:
+            ids = fold_ids(ids, self.packed)
+        return ids
 
     def moe_block(self, x, k=10, policy=None, hiprec=True, rlog=None):
         x = np.ascontiguousarray(x, np.float32)
         if rlog is None:
             rlog = self.logits(x, True)[0]
         rlog = np.ascontiguousarray(rlog, np.float32)
-        ids, _ = (route_mass(rlog, *policy) if policy else route_topk(rlog, k))
-        self.ensure(ids)
+        self.ensure(self._routed(rlog, k, policy))
         out = np.zeros(self.H, np.float32)
         ids_o = np.zeros(MOE_K_MAX, np.uint32)
         w_o = np.zeros(MOE_K_MAX, np.float32)
@@ -448,8 +466,7 @@ class OracleLayer:
         ids = np.zeros((M, MOE_K_MAX), np.uint32)
         w = np.zeros((M, MOE_K_MAX), np.float32)
         for mi in range(M):
-            ii, _ = (route_mass(rlog[mi], *policy) if policy else route_topk(rlog[mi], k))
-            self.ensure(ii)
+            self.ensure(self._routed(rlog[mi], k, policy))
         E = self.E
         out = np.zeros((M, self.H), np.float32)
         n_sel = np.zeros(M, np.uint32)
@@ -513,8 +530,13 @@ class TQOracleLayer(OracleLayer):
     gate / up [E] arrays of a kb-32 codec, down [E] of a kb-16 codec, used as they are."""
 
     def __init__(self, H, E, F, router, shexp_gate, gate_tq, up_tq, down_tq, sh_gate, sh_up, sh_down, gate_bits,
-                 down_bits, router_bias=None):
+                 down_bits, router_bias=None, tiles=1, packed=0):
+        """tiles = T > 1: a pack written for T tiles (plan.py:106-118,174-181).  router is then
+        [T][E][H/T] (tile t: columns [H/T t, H/T (t+1))); each expert's gate / up array holds its T
+        tiles' [F/T][H] matrices back to back and its down array the T tiles' [H][F/T] matrices;
+        the shared expert's likewise.  packed: n_expert_packed of a subset pack (fold_ids)."""
         self.H, self.E, self.F = H, E, F
+        self.tiles, self.packed = tiles, packed
         self.router = np.ascontiguousarray(router, np.float32)
         self.router_bias = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
         self.shexp_gate = np.ascontiguousarray(shexp_gate, np.float32)
@@ -525,7 +547,7 @@ class TQOracleLayer(OracleLayer):
         self._up_ptrs = (C.c_void_p * E)()
         self._down_ptrs = (C.c_void_p * E)()
         self._tq = {}
-        for e in range(E):
+        for e in range(min(E, len(gate_tq))):  # a subset pack holds only its first experts
             g, u, d = (np.ascontiguousarray(a[e], np.uint8) for a in (gate_tq, up_tq, down_tq))
             self._tq[e] = (g, u, d)
             self._gate_ptrs[e] = g.ctypes.data

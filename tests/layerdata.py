@@ -120,3 +120,62 @@ class TQLayer:
 
     def x(self, M, tid=0, sigma=1.0):
         return O.gen_normal(self.seed, stream(0, 900 + tid), M * self.H, sigma).reshape(M, self.H)
+
+
+class TiledTQLayer:
+    """A layer as a pack written for T tiles stores it (python/trpack/plan.py:106-118,174-181):
+    the router K-split into [T][E][H/T], every expert's gate / up split by rows into T [F/T][H]
+    TQ matrices and its down split by columns into T [H][F/T] matrices, the shared expert alike.
+    Tile arrays are tile-major, [T][E][bytes] (how the GPU takes them: tile t at t * tile_stride);
+    the oracle takes each expert's tiles back to back.  packed: a subset pack of the first
+    `packed` experts (the router still scores all E)."""
+
+    def __init__(self, seed=1, H=2560, E=32, F=640, T=2, gate_bits=4, down_bits=5, packed=0):
+        rng = np.random.default_rng(seed)
+        assert F % (16 * T) == 0 and H % T == 0
+        self.H, self.E, self.F, self.T, self.seed, self.packed = H, E, F, T, seed, packed
+        self.gate_bits, self.down_bits = gate_bits, down_bits
+        self.gate_fmt, self.down_fmt = (gate_bits << 8) | 32, (down_bits << 8) | 16
+        per, hl = F // T, H // T
+        Ep = packed or E
+        self.router_full = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        self.router = np.ascontiguousarray(self.router_full.reshape(E, T, hl).transpose(1, 0, 2))  # [T][E][hl]
+        self.shexp_gate = (rng.standard_normal(H) * 0.02).astype(np.float32)
+        self.gate = np.stack([np.stack([random_tq(rng, per, H, gate_bits, 32) for _ in range(Ep)]) for _ in range(T)])
+        self.up = np.stack([np.stack([random_tq(rng, per, H, gate_bits, 32) for _ in range(Ep)]) for _ in range(T)])
+        self.down = np.stack([np.stack([random_tq(rng, H, per, down_bits, 16) for _ in range(Ep)]) for _ in range(T)])
+        self.sh_gate = np.stack([random_tq(rng, per, H, gate_bits, 32) for _ in range(T)])
+        self.sh_up = np.stack([random_tq(rng, per, H, gate_bits, 32) for _ in range(T)])
+        self.sh_down = np.stack([random_tq(rng, H, per, down_bits, 16) for _ in range(T)])
+
+    def oracle(self):
+        def per_expert(a):  # [T][E][bytes] -> [E][T * bytes]
+            return np.ascontiguousarray(a.transpose(1, 0, 2)).reshape(a.shape[1], -1)
+        return O.TQOracleLayer(self.H, self.E, self.F, self.router, self.shexp_gate, per_expert(self.gate),
+                               per_expert(self.up), per_expert(self.down), self.sh_gate.reshape(-1),
+                               self.sh_up.reshape(-1), self.sh_down.reshape(-1), self.gate_bits, self.down_bits,
+                               tiles=self.T, packed=self.packed)
+
+    def x(self, M, tid=0, sigma=1.0):
+        return O.gen_normal(self.seed, stream(0, 950 + tid), M * self.H, sigma).reshape(M, self.H)
+
+
+def untile(L):
+    """The untiled layer holding the same weights as TiledTQLayer L: gate / up tiles concatenated
+    by rows (a TQ strip is a self-contained 16-row unit), each down strip's blocks concatenated
+    over the tiles in column order (a TQ block is self-contained), the router rows rejoined."""
+    T, E, H, F = L.T, L.packed or L.E, L.H, L.F
+    per = F // T
+    bb = O.tq_matrix_bytes(16, 16, L.down_bits, 16)  # one block
+    sb = per // 16 * bb  # one strip of a down tile
+
+    def down_full(tiles):  # [T][bytes of [H][per]] -> bytes of [H][F]
+        strips = [t.reshape(H // 16, sb) for t in tiles]
+        return np.concatenate(strips, axis=1).reshape(-1)
+
+    gate = np.stack([np.concatenate([L.gate[t][e] for t in range(T)]) for e in range(E)])
+    up = np.stack([np.concatenate([L.up[t][e] for t in range(T)]) for e in range(E)])
+    down = np.stack([down_full([L.down[t][e] for t in range(T)]) for e in range(E)])
+    return O.TQOracleLayer(H, L.E, F, L.router_full, L.shexp_gate, gate, up, down, L.sh_gate.reshape(-1),
+                           L.sh_up.reshape(-1), down_full(list(L.sh_down)), L.gate_bits, L.down_bits,
+                           packed=L.packed)

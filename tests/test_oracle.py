@@ -719,3 +719,79 @@ def test_hc_mix_against_f64(bits):
         got = O.hc_mix(up, bits, hc, lr, xn[:1] if decode else xn, lo[:1] if decode else lo, decode, hiprec)
         err = np.abs(got - want[:got.shape[0]]).max()
         assert err <= tol * scale, (decode, hiprec, err, scale)
+
+
+# ---- subset packs and packs written for T tiles --------------------------------------------
+
+def test_fold_ids():
+    """exec_batch.rs:214-225, designed cases: each id taken mod packed, then stepped (mod packed)
+    past the ids already folded; more ids than packed experts is refused (the reference asserts)."""
+    assert O.fold_ids([3, 19, 35], 16).tolist() == [3, 4, 5]
+    assert O.fold_ids([15, 31, 0], 16).tolist() == [15, 0, 1]
+    assert O.fold_ids([7, 2, 9, 40], 8).tolist() == [7, 2, 1, 0]
+    assert O.fold_ids([5], 16).tolist() == [5]
+    with pytest.raises(ValueError):
+        O.fold_ids(list(range(9)), 8)
+    rng = np.random.default_rng(3)
+    for _ in range(50):  # distinct, inside the pack, and unchanged where nothing collides
+        ids = rng.choice(512, 10, replace=False).astype(np.uint32)
+        f = O.fold_ids(ids, 16)
+        assert len(set(f.tolist())) == 10 and f.max() < 16 and f[0] == ids[0] % 16
+
+
+def test_tiled_router_tile_order():
+    """exec.rs:1003-1011 + exchange.rs:122-136: with T tiles each logit is the tiles' partial dots
+    over their H/T columns, summed in tile order.  Designed partials 1e8, 1, -1e8 (one nonzero per
+    tile slice against x = 1) give (1e8 + 1) - 1e8 = 0; 1e8, -1e8, 1 give 1."""
+    from layerdata import TiledTQLayer
+    L = TiledTQLayer(seed=5, H=192, E=16, F=96, T=3)
+    L.router[:] = 0
+    L.router[0, 0, 0], L.router[1, 0, 5], L.router[2, 0, 63] = 1e8, 1.0, -1e8
+    L.router[0, 1, 1], L.router[1, 1, 2], L.router[2, 1, 3] = 1e8, -1e8, 1.0
+    orc = L.oracle()
+    x = np.ones((2, 192), np.float32)
+    for dot_rows in (True, False):
+        lg = orc.logits(x, dot_rows)
+        assert lg[0, 0] == 0.0 and lg[0, 1] == 1.0 and np.all(lg[:, 2:] == 0), dot_rows
+
+
+@pytest.mark.parametrize("T", [2, 4])
+def test_tiled_layer_against_untiled(T):
+    """A pack written for T tiles computes the same layer as the untiled pack of the same bytes,
+    up to the order of the f32 sums (the router's and the down's partials per tile): ids equal,
+    outputs within 2e-6 of the output scale, decode and batch.  A tile reading another tile's rows
+    or columns would be off by the whole term."""
+    from layerdata import TiledTQLayer, untile
+    L = TiledTQLayer(seed=7, H=512, E=16, F=256, T=T)
+    tiled, flat = L.oracle(), untile(L)
+    x = L.x(6, tid=3)
+    a, b = tiled.moe_block(x[0], k=4), flat.moe_block(x[0], k=4)
+    assert np.array_equal(a["ids"], b["ids"])
+    assert np.abs(a["out"] - b["out"]).max() <= 2e-6 * np.abs(b["out"]).max()
+    a, b = tiled.moe_batch(x, k=4), flat.moe_batch(x, k=4)
+    assert np.array_equal(a["ids"], b["ids"])
+    assert np.abs(a["out"] - b["out"]).max() <= 2e-6 * np.abs(b["out"]).max()
+    # and the tiles are not interchangeable: swapping two down tiles changes the output
+    before = tiled.moe_block(x[0], k=4)["out"]
+    L.down[[0, 1]] = L.down[[1, 0]]
+    after = L.oracle().moe_block(x[0], k=4)["out"]
+    assert np.abs(after - before).max() > 1e-2 * np.abs(before).max()
+
+
+def test_subset_pack_folds_ids():
+    """A subset pack (n_expert_packed < E): the layer routes on all E logits, then folds the ids
+    onto the packed experts (exec.rs:1545-1549, exec_batch.rs:1418-1420); the result equals the
+    full pack's layer with the folded ids' experts."""
+    from layerdata import TiledTQLayer
+    L = TiledTQLayer(seed=9, H=512, E=64, F=128, T=1, packed=16)
+    orc = L.oracle()
+    x = L.x(3, tid=4)
+    r = orc.moe_block(x[0], k=6)
+    lg = orc.logits(x[:1], True)[0]
+    ids, w = O.route_topk(lg, 6)
+    assert np.array_equal(r["ids"], O.fold_ids(ids, 16)) and np.array_equal(r["w"], w)
+    rb = orc.moe_batch(x, k=6)
+    lgb = orc.logits(x, False)
+    for t in range(3):
+        assert np.array_equal(rb["ids"][t, :6], O.fold_ids(O.route_topk(lgb[t], 6)[0], 16))
+    assert rb["ent_expert"].max() < 16
