@@ -50,24 +50,34 @@ enum {
 };
 enum { TRK_BASIS_ALL = 0, TRK_BASIS_TOP = 1 }; /* MassBasis (router.rs:9-16) */
 
-/* A stack of `count` weight matrices [rows][k] in GGUF superblocks, row-major, `stride` bytes
- * apart.  Replaces tr_model::weights::TqMat {ptr, rows, k, codec, count, stride}
- * (crates/tr-model/src/weights.rs:14-35): `fmt` names the GGUF block format read directly on
- * the GPU where the CPU path reads its TQ re-layout.  Gate/up: Q4_K.  Down (routed and shared
- * alike): Q4_K, Q6_K, Q8_0 or Q5_1 (blocks.py:57-78).  Q4_K, Q8_0 and Q5_1 stacks are 16-byte aligned,
- * Q6_K 2-byte aligned.  trk_gemv also takes a TQ codec (TRK_FMT_TQ*, 16-byte aligned): then the
- * matrix is the reference's packed strips, exactly as trpack writes them. */
+/* A stack of `count` weight matrices [rows][k], `stride` bytes apart.  Replaces
+ * tr_model::weights::TqMat {ptr, rows, k, codec, count, stride} (crates/tr-model/src/weights.rs:
+ * 14-35); `fmt` says how the bytes are laid out:
+ *   - a TQ codec (TRK_FMT_TQ*): the reference's packed strips exactly as trpack writes them, a
+ *     pack's TensorKind::Tq entry uploaded unchanged.  register() (weights.rs:207-210) fills
+ *     rows, k, codec, count and stride from the manifest entry (manifest.rs:65-94): pass the same
+ *     values, with fmt = bits << 8 | kb.  Gate/up take a kb-32 codec, downs a kb-16 codec (the
+ *     activations' block sizes).  16-byte aligned (every TQ block is a multiple of 16 bytes).
+ *   - a GGUF block format read in place on the GPU (the CPU path reads its TQ re-layout):
+ *     gate/up Q4_K; down (routed and shared alike) Q4_K, Q6_K, Q8_0 or Q5_1 (blocks.py:57-78);
+ *     row-major rows of superblocks.  Q4_K, Q8_0 and Q5_1 stacks are 16-byte aligned, Q6_K 2-byte.
+ * tile_stride: bytes from one tile's tensor to the next in a layer packed for n_tiles > 1 tiles
+ * (trk_cfg): tile t's tensor (the pack's entry for tile t) starts at ptr + t * tile_stride, and
+ * rows / k give ONE tile's shape (gate/up [n_ff / T][H], down [H][n_ff / T], python/trpack/
+ * plan.py:106-118).  Ignored with one tile. */
 typedef struct {
     const void *ptr;
     uint32_t rows, k;
     uint32_t fmt;
     uint32_t count;
     uint64_t stride;
+    uint64_t tile_stride;
 } trk_mat;
 
 /* One layer's MoE weights. Replaces tr_model::exec::MoeW (crates/tr-model/src/exec.rs:86-96). */
 typedef struct {
-    const float *router;      /* [E][H] f32 (ffn_gate_inp) */
+    const float *router;      /* [E][H] f32 (ffn_gate_inp); packed for T > 1 tiles: the tiles'
+                                 K-split slices back to back, [T][E][H / T] (plan.py:174-181) */
     const float *router_bias; /* [E] f32 or NULL: additive logit bias for synthetic load skew;
                                  the reference has no bias (pass NULL for its semantics) */
     const float *shexp_gate;  /* [H] f32 (ffn_gate_inp_shexp) */
@@ -86,7 +96,8 @@ typedef struct {
 typedef struct {
     uint32_t hidden;           /* H (multiple of 256) */
     uint32_t n_expert;         /* E (<= 1024) */
-    uint32_t n_ff;             /* F, per routed and shared expert (multiple of 256) */
+    uint32_t n_ff;             /* F, per routed and shared expert (a multiple of 256 for GGUF
+                                  experts, of 16 per tile for TQ experts) */
     uint32_t n_expert_used;    /* k of the fixed top-k routing (<= 32) */
     uint32_t m_max;            /* most rows one call may carry (the reference's batch_max) */
     uint32_t k_cap;            /* most experts one token may select, sizes the entry buffers
@@ -95,6 +106,15 @@ typedef struct {
                                   gemm_f32_nt order (exec_batch.rs:989-1019: the reference
                                   switches at its tile's core count); 0 = 16 */
     int32_t hiprec;            /* M == 1: two-level activations (TR_HIPREC, exec.rs:782) */
+    uint32_t n_tiles;          /* T, the tiles the pack was written for (ModelConfig::n_tiles,
+                                  plan.py:88): 0 or 1 = one.  With T > 1 (TQ experts only) the
+                                  router is K-split and every expert is split by n_ff into T
+                                  tiles, as trpack shards them; the layer then sums the tiles'
+                                  router partials and down partials in tile order (exchange.rs:
+                                  122-136), as the reference's tiles do */
+    uint32_t n_expert_packed;  /* experts in the pack (ModelConfig::n_expert_packed, a subset
+                                  pack of the first experts, exec.rs:1545-1549): routed ids are
+                                  folded onto them (fold_ids, exec_batch.rs:214-225); 0 = n_expert */
 } trk_cfg;
 
 /* Replaces tr_model::exec::MoeStats counters rows/experts (exec.rs:558-605). */

@@ -610,3 +610,30 @@ def test_mass_profile(M):
     ctx.forward(W, dev(L.x(M, tid=690)), out)
     assert ctx.profile_report()[1] == rows  # off: nothing added
     ctx.close()
+
+
+@pytest.mark.parametrize("M", [1, 4, 40])
+def test_subset_pack_gguf(M):
+    """A subset pack on the GGUF kernels (n_expert_packed = 8 of 32): the decode gate/up routes,
+    folds (fold_ids, exec_batch.rs:214-225) and only then requests its slot's weights; the small and
+    the general dispatch group the folded ids.  Against the oracle with the same fold."""
+    say(f"subset pack gguf M={M}")
+    import torch
+    L, orc, W = layer("small", **SMALL)
+    orc.packed = 8
+    try:
+        x = L.x(M, tid=820 + M)
+        r = orc.moe_block(x[0], k=4) if M == 1 else orc.moe_batch(x, k=4)
+        want = r["out"][None] if M == 1 else r["out"]
+        ctx = trmoe.Context(L.H, L.E, L.F, 4, max(M, 16), n_expert_packed=8)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)[:, :4]
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)[:, :4]
+        rids = r["ids"][None] if M == 1 else r["ids"][:, :4]
+        rw = r["w"][None] if M == 1 else r["w"][:, :4]
+        assert np.array_equal(ids, rids) and ids.max() < 8
+        compare_out(host(out), want, np.array_equal(w, rw) and shared_gate_exact(L, x), f"subset gguf M={M}")
+        ctx.close()
+    finally:
+        orc.packed = 0

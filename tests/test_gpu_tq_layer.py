@@ -242,3 +242,91 @@ def test_tq_full_shape_m512_sampled(policy):
     say(f"tq full shape: {len(chosen)} tokens, {n_exact} bit-identical")
     ctx.close()
 
+
+
+# ---- packs written for T tiles, subset packs ---------------------------------------------------
+
+_tiled = {}
+
+
+def tiled_layer(key, **kw):
+    from layerdata import TiledTQLayer
+    if key not in _tiled:
+        L = TiledTQLayer(**kw)
+        W = trmoe.LayerWeights.from_tiled_tq(L.H, L.E, L.F, L.T, L.router, L.shexp_gate, L.gate, L.up, L.down,
+                                             L.sh_gate, L.sh_up, L.sh_down, L.gate_fmt, L.down_fmt)
+        _tiled[key] = (L, L.oracle(), W)
+    return _tiled[key]
+
+
+def run_tiled(L, orc, W, M, k, tid, policy=None):
+    """The layer on L at M rows against the oracle: every token's ids (and count) exact; returns
+    (out, oracle out, whether the routing weights and the shared gate agree bit for bit)."""
+    import torch
+    x = L.x(M, tid=tid)
+    r = orc.moe_block(x[0], k=k, policy=policy) if M == 1 else orc.moe_batch(x, k=k, policy=policy)
+    want = r["out"][None] if M == 1 else r["out"]
+    if M == 1:
+        rids, rws = [r["ids"]], [r["w"]]
+    else:
+        rids = [r["ids"][t, :r["n_sel"][t]] for t in range(M)]
+        rws = [r["w"][t, :r["n_sel"][t]] for t in range(M)]
+    ctx = trmoe.Context(L.H, L.E, L.F, k, max(M, 16), n_tiles=L.T, n_expert_packed=L.packed,
+                        k_cap=policy[1] if policy else 0)
+    if policy:
+        ctx.set_moe(policy)
+    out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+    ctx.forward(W, dev(x), out)
+    got = host(out).copy()
+    ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+    w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+    nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+    same_w = True
+    for t in range(M):
+        n = len(rids[t])
+        assert nsel[t] == n and np.array_equal(ids[t, :n], rids[t]), (t, ids[t, :nsel[t]], rids[t])
+        same_w = same_w and np.array_equal(w[t, :n], rws[t])
+    exact = same_w and shared_gate_exact_v(L.shexp_gate, x)
+    ctx.close()
+    return got, want, exact
+
+
+def shared_gate_exact_v(shexp_gate, x):
+    from test_gpu_layer import shared_gate_exact
+    return shared_gate_exact(SimpleNamespace(shexp_gate=shexp_gate), x)
+
+
+@pytest.mark.parametrize("T,M", [(2, 1), (2, 5), (2, 40), (8, 1), (8, 3), (8, 40)])
+def test_tiled_pack(T, M):
+    """A pack written for T tiles (python/trpack/plan.py:106-118,174-181), uploaded as it is: the
+    K-split router's partials and each tile's down partials summed in tile order (exec.rs:1003-1038,
+    exchange.rs:122-136, exec_batch.rs:821-849), against the oracle's T-tile restatement; bit-identical
+    where the routing weights and the shared gate agree."""
+    say(f"tiled pack T={T} M={M}")
+    L, orc, W = tiled_layer(f"t{T}", seed=60 + T, H=512, E=16, F=256, T=T)
+    got, want, exact = run_tiled(L, orc, W, M, 4, tid=10 + M)
+    compare_out(got, want, exact, f"tiled T={T} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 24])
+def test_tiled_pack_real_shape(M):
+    """The real expert shape packed for 8 tiles (H 2560, F 640: 80 rows / columns per tile, 320
+    router columns per tile), TQ4_32 / TQ5_16, top-8 of 32 experts, and dynamic k at M = 24."""
+    say(f"tiled pack real shape T=8 M={M}")
+    L, orc, W = tiled_layer("real8", seed=71, H=2560, E=32, F=640, T=8, gate_bits=4, down_bits=5)
+    got, want, exact = run_tiled(L, orc, W, M, 8, tid=20 + M)
+    compare_out(got, want, exact, f"tiled real M={M}")
+    if M > 1:
+        got, want, _ = run_tiled(L, orc, W, M, 8, tid=30 + M, policy=(1, 10, 0.9, O.BASIS_TOP))
+        compare_out(got, want, False, f"tiled real dynamic-k M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 40, 300])
+def test_subset_pack(M):
+    """A subset pack (n_expert_packed = 16 of 64 experts, exec.rs:1545-1549): every token's routed ids
+    folded onto the packed experts (fold_ids, exec_batch.rs:214-225) on the decode path, the small and
+    the general dispatch, against the oracle."""
+    say(f"subset pack M={M}")
+    L, orc, W = tiled_layer("sub", seed=81, H=512, E=64, F=128, T=1, packed=16)
+    got, want, exact = run_tiled(L, orc, W, M, 6, tid=40 + M)
+    compare_out(got, want, exact, f"subset M={M}")

@@ -115,8 +115,24 @@ static int check_cfg(const trk_cfg* cfg, uint32_t m_max, uint32_t& k_cap) {
     const geo::Caps caps{H, E, F, m_max, k_cap};
     if (geo::ent_cap(caps) > 0xffffffffull || geo::item_cap(caps) > 0xffffffffull)
         return fail(TRK_E_INVALID, "m_max * k_cap (%u * %u) too large", m_max, k_cap);
+    // a pack written for T tiles (plan.py:86-90): n_ff splits into 16-row strips per tile, the
+    // router's K into T slices (of a multiple of 16 columns: the dot and gemm orders step by 16)
+    const uint32_t T = cfg->n_tiles > 1 ? cfg->n_tiles : 1;
+    if (T > 64 || F % (16 * T) || H % (16 * T))
+        return fail(TRK_E_INVALID, "n_tiles (%u): n_ff (%u) must split into 16-row strips per tile and hidden (%u) "
+                    "into multiples of 16 per tile (at most 64 tiles)", T, F, H);
+    // fold_ids asserts at most `packed` routed ids per token (exec_batch.rs:217)
+    if (cfg->n_expert_packed && (cfg->n_expert_packed > E || cfg->n_expert_packed < k_cap))
+        return fail(TRK_E_INVALID, "n_expert_packed (%u) must be in k_cap (%u) .. n_expert (%u)", cfg->n_expert_packed,
+                    k_cap, E);
     return TRK_OK;
 }
+
+// The subset pack's expert count as the routing takes it (0: every expert is packed).
+static uint32_t packed_of(const trk_cfg& cfg) {
+    return cfg.n_expert_packed && cfg.n_expert_packed < cfg.n_expert ? cfg.n_expert_packed : 0u;
+}
+static uint32_t tiles_of(const trk_cfg& cfg) { return cfg.n_tiles > 1 ? cfg.n_tiles : 1u; }
 
 // The workspace of a layer configuration for m_max rows: sizes, then 256-byte aligned pieces cut
 // from base (nullptr: sizes only).  Returns the bytes the pieces take.
@@ -132,11 +148,14 @@ static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max
     ws.ent_cap = (uint32_t)geo::ent_cap(caps);
     ws.item_cap = (uint32_t)geo::item_cap(caps);  // items of <= 16 rows
     ws.act_rows = geo::act_rows(caps);
+    const uint32_t T = tiles_of(cfg);
+    ws.tiles = T;
     struct Piece {
         void** p;
         size_t bytes;
     };
     const size_t yrows = geo::yent_rows(caps);
+    ws.yent_tile = yrows * H;
     Piece pieces[] = {
         {(void**)&ws.xq, rows_x * H},
         {(void**)&ws.xs, rows_x * (H / 32) * 4},
@@ -163,7 +182,9 @@ static size_t layout_workspace(Workspace& ws, const trk_cfg& cfg, uint32_t m_max
         {(void**)&ws.acts, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.actsum, ws.act_rows * (F / 16) * 4},
         {(void**)&ws.actu, ws.act_rows * (F / 16) * 4},
-        {(void**)&ws.yent, yrows * H * 4},
+        {(void**)&ws.yent, T * yrows * H * 4},
+        {(void**)&ws.plog, T > 1 ? (size_t)T * M * E * 4 : 0},
+        {(void**)&ws.xt, T > 1 ? M * H * 4 : 0},
         {(void**)&ws.hgu, yrows * 2 * F * 4},
         {(void**)&ws.out_tmp, M * H * 4},
         {(void**)&ws.stats, 16},
@@ -199,7 +220,7 @@ extern "C" int trk_create(const trk_cfg* cfg, trk_ctx** out) {
     if (!c) return fail(TRK_E_NOMEM, "host allocation failed");
     c->cfg = *cfg;
     if (!c->cfg.router_dot_max_m) c->cfg.router_dot_max_m = 16;
-    c->pol = Policy{0, 0, 0, 0, 0.0f};
+    c->pol = Policy{0, 0, 0, 0, 0.0f, packed_of(c->cfg)};
     c->device = device;
     const size_t total = layout_workspace(c->ws, c->cfg, cfg->m_max, k_cap, nullptr);
     hipError_t e = hipMalloc(&c->block, total);
@@ -239,17 +260,18 @@ extern "C" int trk_destroy(trk_ctx* c) {
 extern "C" int trk_set_moe(trk_ctx* c, const trk_moe_policy* p) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     if (!p) {
-        c->pol = Policy{0, 0, 0, 0, 0.0f};
+        c->pol = Policy{0, 0, 0, 0, 0.0f, packed_of(c->cfg)};
         return TRK_OK;
     }
     int rc = check_policy(c, p);
     if (rc) return rc;
-    c->pol = Policy{1, p->min, p->max, p->basis, p->mass};
+    c->pol = Policy{1, p->min, p->max, p->basis, p->mass, packed_of(c->cfg)};
     return TRK_OK;
 }
 
+// tiles > 1: m describes one tile's stack (rows / k of one tile), the T stacks tile_stride apart
 static int make_mat(const trk_mat& m, uint32_t rows, uint32_t k, bool down_ok_q6, uint32_t min_count, const char* name,
-                    Mat& out) {
+                    Mat& out, uint32_t tiles = 1) {
     if (!m.ptr) return fail(TRK_E_INVALID, "%s: null weight pointer", name);
     if (m.rows != rows || m.k != k)
         return fail(TRK_E_INVALID, "%s: shape [%u][%u], expected [%u][%u]", name, m.rows, m.k, rows, k);
@@ -280,7 +302,17 @@ static int make_mat(const trk_mat& m, uint32_t rows, uint32_t k, bool down_ok_q6
                                                   (unsigned long long)m.stride, (unsigned long long)mb);
     if ((uintptr_t)m.ptr % align || (m.count > 1 && m.stride % align))
         return fail(TRK_E_INVALID, "%s: pointer/stride must be %llu-byte aligned", name, (unsigned long long)align);
-    out = Mat{(const uint8_t*)m.ptr, m.count > 1 ? m.stride : mb, rows, k, m.fmt, (uint32_t)pitch};
+    const uint64_t stride = m.count > 1 ? m.stride : mb;
+    out = Mat{(const uint8_t*)m.ptr, stride, rows, k, m.fmt, (uint32_t)pitch, 0, (rows + 15) / 16};
+    if (tiles > 1) {
+        if (!fmt_is_tq(m.fmt)) return fail(TRK_E_INVALID, "%s: a pack written for tiles holds TQ experts", name);
+        // the tiles' stacks follow one another without overlapping
+        const uint64_t stack = (uint64_t)(m.count - 1) * stride + mb;
+        if (m.tile_stride < stack || m.tile_stride % 16)
+            return fail(TRK_E_INVALID, "%s: tile_stride %llu below a tile's %llu bytes or not 16-byte aligned", name,
+                        (unsigned long long)m.tile_stride, (unsigned long long)stack);
+        out.tile_stride = m.tile_stride;
+    }
     return TRK_OK;
 }
 
@@ -290,14 +322,17 @@ struct Mats {
 
 static int check_weights(trk_ctx* c, const trk_moe_w* w, Mats& M) {
     const uint32_t H = c->cfg.hidden, F = c->cfg.n_ff, E = c->cfg.n_expert;
+    // a subset pack holds only its first n_expert_packed experts; with T tiles every stack is one
+    // tile's: gate/up [F / T][H] (rows split), down [H][F / T] (columns split)
+    const uint32_t T = tiles_of(c->cfg), Ep = packed_of(c->cfg) ? packed_of(c->cfg) : E, Ft = F / T;
     if (!w || !w->shexp_gate) return fail(TRK_E_INVALID, "weights: null pointer");
     int rc;
-    if ((rc = make_mat(w->gate, F, H, false, E, "gate", M.gate))) return rc;
-    if ((rc = make_mat(w->up, F, H, false, E, "up", M.up))) return rc;
-    if ((rc = make_mat(w->down, H, F, true, E, "down", M.down))) return rc;
-    if ((rc = make_mat(w->sh_gate, F, H, false, 1, "sh_gate", M.shg))) return rc;
-    if ((rc = make_mat(w->sh_up, F, H, false, 1, "sh_up", M.shu))) return rc;
-    if ((rc = make_mat(w->sh_down, H, F, true, 1, "sh_down", M.shd))) return rc;
+    if ((rc = make_mat(w->gate, Ft, H, false, Ep, "gate", M.gate, T))) return rc;
+    if ((rc = make_mat(w->up, Ft, H, false, Ep, "up", M.up, T))) return rc;
+    if ((rc = make_mat(w->down, H, Ft, true, Ep, "down", M.down, T))) return rc;
+    if ((rc = make_mat(w->sh_gate, Ft, H, false, 1, "sh_gate", M.shg, T))) return rc;
+    if ((rc = make_mat(w->sh_up, Ft, H, false, 1, "sh_up", M.shu, T))) return rc;
+    if ((rc = make_mat(w->sh_down, H, Ft, true, 1, "sh_down", M.shd, T))) return rc;
     if (M.shd.fmt != M.down.fmt) return fail(TRK_E_INVALID, "sh_down: format %u, down: %u (one down format per layer)",
                                              M.shd.fmt, M.down.fmt);
     // one gate/up format per layer; TQ and GGUF experts are not mixed within a layer
@@ -364,13 +399,27 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         // GEMVs, SwiGLU + quantisation + fold between them, and the combine
         const int pair = m == 1 && c->cfg.hiprec ? 1 : 0;
         const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, pair};
-        if (rlog)
+        const uint32_t T = ws.tiles;
+        if (rlog || T > 1)
             TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st,
                                                  &xq, norm));
         else
             TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H,
                                                  m == 1 ? 0 : gemm_order, ws.rlog, ws.shl, st, &xq, norm));
-        const bool mfma = c->tq_mfma && tqm_fits(H, ws.F);
+        if (!rlog && T > 1) {
+            // the K-split router of a pack written for T tiles (exec.rs:1003-1011, exec_batch.rs:
+            // 1008-1016): each tile's partial over its H / T columns of x, in the dot or gemm order,
+            // then the partials summed in tile order (exchange.rs:122-136) and the bias added
+            const uint32_t hl = H / T;
+            TIMED(K_LOGITS, launch_tile_split(x, m, H, T, ws.xt, st));
+            for (uint32_t t = 0; t < T; t++)
+                TIMED(K_LOGITS, launch_router_logits(w->router + (size_t)t * E * hl, nullptr, nullptr,
+                                                     ws.xt + (size_t)t * m * hl, m, E, hl, m == 1 ? 0 : gemm_order,
+                                                     ws.plog + (size_t)t * m * E, nullptr, st, nullptr, nullptr));
+            TIMED(K_LOGITS, launch_tile_reduce(ws.plog, m, E, T, w->router_bias, ws.rlog, st));
+        }
+        // tiles: the generic grouped TQ GEMV, which takes each tile's rows and columns
+        const bool mfma = c->tq_mfma && tqm_fits(H, ws.F) && T == 1;
         if (m == 1) {
             // the MFMA gate/up launch routes for itself
             if (!mfma) TIMED(K_ROUTE, launch_route(lg, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));
@@ -529,7 +578,7 @@ extern "C" int trk_moe_forward_noalloc(const trk_cfg* cfg, const trk_moe_policy*
     c.cfg = *cfg;
     c.cfg.m_max = m;
     if (!c.cfg.router_dot_max_m) c.cfg.router_dot_max_m = 16;
-    c.pol = Policy{0, 0, 0, 0, 0.0f};
+    c.pol = Policy{0, 0, 0, 0, 0.0f, packed_of(c.cfg)};
     c.block = nullptr;
     c.timing = 0;
     const size_t need = layout_workspace(c.ws, c.cfg, m, k_cap, nullptr);
@@ -538,7 +587,7 @@ extern "C" int trk_moe_forward_noalloc(const trk_cfg* cfg, const trk_moe_policy*
                     need, (size_t)TRK_NOALLOC_SCRATCH_BYTES);
     if (policy) {
         if ((rc = check_policy(&c, policy))) return rc;
-        c.pol = Policy{1, policy->min, policy->max, policy->basis, policy->mass};
+        c.pol = Policy{1, policy->min, policy->max, policy->basis, policy->mass, packed_of(c.cfg)};
     }
     void* base = nullptr;
     if ((rc = scratch_of_current_device(&base))) return rc;
@@ -566,7 +615,7 @@ extern "C" int trk_moe_residual(trk_ctx* c, const trk_moe_w* w, const float* rms
     const int only = -1;
     // Below the router GEMM threshold (and off the one-launch decode layer, which reads x itself)
     // the logits launch normalises h where it reads it: no rmsnorm launch, no normed copy
-    if (!c->fusion && m < c->cfg.router_dot_max_m && w->router) {
+    if (!c->fusion && m < c->cfg.router_dot_max_m && w->router && c->ws.tiles == 1) {
         const XNorm nrm{rms_w, eps};
         return forward(c, w, h, nullptr, m, h, 1, st, only, &nrm);
     }
@@ -726,7 +775,7 @@ extern "C" int trk_route(const float* logits, uint32_t m, uint32_t n_expert, uin
                         std::min<uint32_t>(TRK_MOE_K_MAX, n_expert));
         if (!(p->mass > 0.0f) || p->mass != p->mass)
             return fail(TRK_E_POLICY, "moe policy: target mass (%g) must be positive", (double)p->mass);
-        pol = Policy{1, p->min, p->max, p->basis, p->mass};
+        pol = Policy{1, p->min, p->max, p->basis, p->mass, 0};
     } else if (k < 1 || k > TRK_MOE_K_MAX || k > n_expert) {
         return fail(TRK_E_INVALID, "k (%u) must be in 1..min(32, n_expert)", k);
     }

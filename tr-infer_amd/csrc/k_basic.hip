@@ -264,4 +264,44 @@ hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, size_t n, double
     return hipGetLastError();
 }
 
+// ---- the K-split router of a pack written for T tiles -------------------------------------------
+
+// x [m][H] -> xt [T][m][H / T]: tile t's columns of every row, contiguous (the tile's router
+// launch then reads rows of H / T)
+__global__ __launch_bounds__(256) void tile_split_kernel(const float* __restrict__ x, uint32_t m, uint32_t H,
+                                                         uint32_t T, float* __restrict__ xt) {
+    const uint32_t hl = H / T, n4 = m * H / 4;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        const uint32_t row = 4 * i / H, col = 4 * i % H, t = col / hl, c = col % hl;  // hl % 16 == 0
+        *reinterpret_cast<float4*>(xt + ((size_t)t * m + row) * hl + c) = reinterpret_cast<const float4*>(x)[i];
+    }
+}
+
+// rlog[row][e] = the tiles' partials summed in tile order (Mailboxes::reduce, exchange.rs:122-136:
+// the first copied, the others added), then the bias
+__global__ __launch_bounds__(256) void tile_reduce_kernel(const float* __restrict__ plog, uint32_t m, uint32_t E,
+                                                          uint32_t T, const float* __restrict__ bias,
+                                                          float* __restrict__ rlog) {
+    const size_t n = (size_t)m * E;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float v = plog[i];
+        for (uint32_t t = 1; t < T; t++) v = v + plog[(size_t)t * n + i];
+        rlog[i] = bias ? v + bias[i % E] : v;
+    }
+}
+
+hipError_t launch_tile_split(const float* x, uint32_t m, uint32_t H, uint32_t T, float* xt, hipStream_t st) {
+    if (T == 0 || H % (16 * T)) return hipErrorInvalidValue;
+    const uint32_t n4 = m * H / 4, wgs = (n4 + 255) / 256;
+    tile_split_kernel<<<wgs < 2048 ? wgs : 2048, 256, 0, st>>>(x, m, H, T, xt);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_reduce(const float* plog, uint32_t m, uint32_t E, uint32_t T, const float* bias, float* rlog,
+                              hipStream_t st) {
+    const size_t n = (size_t)m * E, wgs = (n + 255) / 256;
+    tile_reduce_kernel<<<(uint32_t)(wgs < 2048 ? wgs : 2048), 256, 0, st>>>(plog, m, E, T, bias, rlog);
+    return hipGetLastError();
+}
+
 }  // namespace trk

@@ -1714,17 +1714,26 @@ __global__ __launch_bounds__(256) void batch_combine_kernel(Workspace ws, uint32
         if (tid < ns) pos[rank] = v;
     }
     __syncthreads();
-    const float4* y4 = reinterpret_cast<const float4*>(ws.yent);
     const uint32_t H4 = H / 4;
     for (uint32_t c = tid; c < H4; c += blockDim.x) {
-        float4 y = y4[(size_t)(n_ent + t) * H4 + c];
+        // a pack written for T tiles: each tile's sum is its partial, the partials summed in tile
+        // order (exec_batch.rs:821-849)
+        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t tl = 0; tl < ws.tiles; tl++) {
+            const float4* y4 = reinterpret_cast<const float4*>(ws.yent + (size_t)tl * ws.yent_tile);
+            float4 p = y4[(size_t)(n_ent + t) * H4 + c];
 #pragma unroll 4
-        for (uint32_t j = 0; j < ns; j++) {
-            const float4 v = y4[(size_t)pos[j] * H4 + c];
-            y.x = y.x + v.x;
-            y.y = y.y + v.y;
-            y.z = y.z + v.z;
-            y.w = y.w + v.w;
+            for (uint32_t j = 0; j < ns; j++) {
+                const float4 v = y4[(size_t)pos[j] * H4 + c];
+                p.x = p.x + v.x;
+                p.y = p.y + v.y;
+                p.z = p.z + v.z;
+                p.w = p.w + v.w;
+            }
+            if (tl == 0)
+                y = p;
+            else
+                y = make_float4(y.x + p.x, y.y + p.y, y.z + p.z, y.w + p.w);
         }
         float4* o = reinterpret_cast<float4*>(out + (size_t)t * H) + c;
         if (residual) {

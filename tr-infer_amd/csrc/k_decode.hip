@@ -104,7 +104,7 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
     // round trip through memory sits between the logits and the expert weights.  Without a mass
     // policy the selection alone fixes every slot's expert: the workgroup then requests its slot's
     // weights before wave 0 works out the routing weights
-    const bool early = route && !pol.enabled;  // workgroup-uniform
+    const bool early = route && !pol.enabled && !pol.packed;  // workgroup-uniform (a subset pack folds the ids after)
     uint32_t my_key = 0, my_idx = 0, ksel = 0;
     if (route && tid < 64) {
         ksel = route_select<NJ, COH>(lg, E, k, pol, tid, cand, my_key, my_idx);

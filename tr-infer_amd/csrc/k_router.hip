@@ -451,7 +451,9 @@ struct GemmCfg {
     uint32_t min_m, kc;
     int id;
 };
-static const GemmCfg kGemmCfg[] = {{256, 128, 1}, {64, 256, 5}, {0, 512, 2}, {0, 128, 3}};
+// (a chunk must divide H: the kernel walks H / KC whole chunks; 64- and 16-wide chunks take the
+// K-split slices of a tiled router, e.g. 2560 / 8 = 320 columns)
+static const GemmCfg kGemmCfg[] = {{256, 128, 1}, {64, 256, 5}, {0, 512, 2}, {0, 128, 3}, {0, 64, 6}, {0, 16, 7}};
 
 template <int RM, int RE, int QM, int KC, bool DB>
 static void launch_gemm_cfg(const float* router, const float* bias, const float* x, uint32_t m, uint32_t E,
@@ -481,6 +483,7 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
             router_dot_kernel<false><<<grid, 128, 0, st>>>(router, bias, shexp_gate, x, m, E, H, rlog, sh,
                                                            xquant ? *xquant : none, wgs, XNorm{});
     } else {
+        if (H % 16) return hipErrorInvalidValue;
         int id = 3;
         for (const GemmCfg& c : kGemmCfg)
             if (m >= c.min_m && H % c.kc == 0) {
@@ -510,6 +513,8 @@ hipError_t launch_router_logits(const float* router, const float* bias, const fl
             case 1: launch_gemm_cfg<4, 4, 4, 128, true>(GEMM_ARGS); break;
             case 2: launch_gemm_cfg<1, 2, 16, 512, false>(GEMM_ARGS); break;
             case 5: launch_gemm_cfg<4, 2, 4, 256, true>(GEMM_ARGS); break;
+            case 6: launch_gemm_cfg<1, 2, 16, 64, true>(GEMM_ARGS); break;
+            case 7: launch_gemm_cfg<1, 2, 16, 16, true>(GEMM_ARGS); break;
             default: launch_gemm_cfg<1, 2, 16, 128, true>(GEMM_ARGS); break;
 #undef GEMM_ARGS
         }

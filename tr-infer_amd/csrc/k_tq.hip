@@ -163,15 +163,19 @@ __global__ __launch_bounds__(256, 4) void tq_layer_kernel(TqArgs g, uint32_t S) 
         prow[tid] = pr;
         if (lv == 0) orow[i] = orr;
     }
-    // the strip: gate/up tiles 0 .. F/16 - 1 are gate strips, the next F/16 up strips
+    // the strip: gate/up tiles 0 .. F/16 - 1 are gate strips, the next F/16 up strips.  A pack
+    // written for T tiles: a gate/up strip lives in tile strip / (F / T / 16) (mat_strip); the down
+    // runs once per tile (grid.z) over the tile's columns [F / T z, F / T (z + 1)) of the activations,
+    // each into its own block of yent (the tiles' partials, exec.rs:1035-1038)
     const Mat& M = gu ? (t < F / 16 ? (shared ? g.sha : g.a) : (shared ? g.shb : g.b)) : (shared ? g.sha : g.a);
     const uint32_t strip = gu && t >= F / 16 ? t - F / 16 : t;
-    const uint8_t* sp = M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes;
-    const uint32_t K = gu ? H : F, nb = K / KB;
+    const uint32_t z = gu ? 0u : blockIdx.z, Kp = gu ? H : F, K = gu ? H : F / ws.tiles, nb = K / KB;
+    const uint32_t k0 = z * K, nbp = Kp / KB;  // first column of this tile; blocks per activation row
+    const uint8_t* sp = gu ? mat_strip(M, e, strip) : mat_tile(M, e, z) + (size_t)strip * M.row_bytes;
     const int8_t* q = gu ? ws.xq : ws.actq;
     const float* qs = gu ? ws.xs : ws.acts;
     const float* qu = gu ? ws.xu : ws.actu;
-    float* out = gu ? g.h : ws.yent;
+    float* out = gu ? g.h : ws.yent + (size_t)z * ws.yent_tile;
     const uint32_t opitch = gu ? 2 * F : H;
     const uint32_t np = nr * P, npass = (np + NA - 1) / NA;
 
@@ -196,7 +200,7 @@ __global__ __launch_bounds__(256, 4) void tq_layer_kernel(TqArgs g, uint32_t S) 
             for (uint32_t i = tid; i < NA * pr; i += 256) {
                 const uint32_t a = i / pr, o = (i % pr) * 16;
                 int4 v = make_int4(0, 0, 0, 0);
-                if (a < na) v = *reinterpret_cast<const int4*>(q + (size_t)prow[p0 + a] * K + (size_t)b0 * KB + o);
+                if (a < na) v = *reinterpret_cast<const int4*>(q + (size_t)prow[p0 + a] * Kp + k0 + (size_t)b0 * KB + o);
                 *reinterpret_cast<int4*>(XQ(a, o)) = v;
             }
             for (uint32_t i = tid; i < NA * S; i += 256) {
@@ -204,11 +208,11 @@ __global__ __launch_bounds__(256, 4) void tq_layer_kernel(TqArgs g, uint32_t S) 
                 float sx = 0.0f, u = 0.0f;
                 int xsum = 0;
                 if (a < na && j < sn) {
-                    const size_t bi = (size_t)prow[p0 + a] * nb + b0 + j;
+                    const size_t bi = (size_t)prow[p0 + a] * nbp + k0 / KB + b0 + j;
                     sx = qs[bi];
                     u = qu[bi];  // sx * (float)sum, formed where the row was quantised (gemv.rs:143)
                     if constexpr (XSUM) {
-                        const int4* xp = reinterpret_cast<const int4*>(q + (size_t)prow[p0 + a] * K + (size_t)(b0 + j) * KB);
+                        const int4* xp = reinterpret_cast<const int4*>(q + (size_t)prow[p0 + a] * Kp + k0 + (size_t)(b0 + j) * KB);
 #pragma unroll
                         for (int c = 0; c < KB / 16; c++) {
                             const int4 v = xp[c];
@@ -323,16 +327,21 @@ __global__ __launch_bounds__(256) void tq_act_kernel(Workspace ws, const float* 
     }
 }
 
-// decode: out (+)= the slots' down rows, summed in slot order (exec.rs:1610-1621)
+// decode: out (+)= the slots' down rows, summed in slot order (exec.rs:1610-1621); with T tiles each
+// tile's slot sum is its partial, and the partials are summed in tile order (exchange.rs:122-136)
 __global__ __launch_bounds__(256) void tq_combine_kernel(Workspace ws, float* __restrict__ out, int residual) {
     const uint32_t H4 = ws.H / 4, c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= H4) return;
     const uint32_t slots = ws.n_sel[0] + 1;
-    const float4* y4 = reinterpret_cast<const float4*>(ws.yent);
-    float4 y = y4[c];
-    for (uint32_t s = 1; s < slots; s++) {
-        const float4 v = y4[(size_t)s * H4 + c];
-        y = make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w);
+    float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t t = 0; t < ws.tiles; t++) {
+        const float4* y4 = reinterpret_cast<const float4*>(ws.yent + (size_t)t * ws.yent_tile);
+        float4 p = y4[c];
+        for (uint32_t s = 1; s < slots; s++) {
+            const float4 v = y4[(size_t)s * H4 + c];
+            p = make_float4(p.x + v.x, p.y + v.y, p.z + v.z, p.w + v.w);
+        }
+        y = t == 0 ? p : make_float4(y.x + p.x, y.y + p.y, y.z + p.z, y.w + p.w);
     }
     float4* o = reinterpret_cast<float4*>(out) + c;
     if (residual) {
@@ -532,8 +541,9 @@ hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& 
                           hipStream_t st) {
     if (tq_kb(down.fmt) != 16) return hipErrorInvalidValue;
     const TqArgs a{down, down, sh_down, sh_down, ws, nullptr, m == 1 ? TQ_DEC_DN : TQ_BAT_DN, pair};
-    const dim3 grid(ws.H / 16, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
-    return m == 1 ? tq_go<16, 2>(a, down.fmt, ws.F, grid, st) : tq_go<16, 4>(a, down.fmt, ws.F, grid, st);
+    const dim3 grid(ws.H / 16, m == 1 ? kcap + 1 : grouped_item_rows(ws, m), ws.tiles);  // z: the tiles
+    const uint32_t K = ws.F / ws.tiles;
+    return m == 1 ? tq_go<16, 2>(a, down.fmt, K, grid, st) : tq_go<16, 4>(a, down.fmt, K, grid, st);
 }
 
 hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st) {

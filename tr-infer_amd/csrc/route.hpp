@@ -174,6 +174,19 @@ __device__ uint32_t route_select(const float* __restrict__ lg, uint32_t E, uint3
     return ksel;
 }
 
+// fold_ids (exec_batch.rs:214-225) on one wave: lane i < n holds id i; in order, id i becomes the
+// first of id % packed, +1, +2, ... (mod packed) not taken by a lane below it.  The loops are
+// wave-uniform (id and the ballot are the same on every lane).
+__device__ __forceinline__ uint32_t fold_ids_wave(uint32_t id, uint32_t n, uint32_t packed, uint32_t lane) {
+    uint32_t f = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)id, (int)i) % packed;
+        while (__ballot(lane < i && f == v)) v = v + 1 == packed ? 0u : v + 1;
+        if (lane == i) f = v;
+    }
+    return lane < n ? f : id;
+}
+
 // Weights of a selection (route_select's per-lane winners): exp of (v - max), the mass loop of
 // route_mass, the renormalisation.  Lanes < count write ids_out / w_out; returns count.
 template <bool COH = false>
@@ -206,6 +219,9 @@ __device__ uint32_t route_weights(const float* __restrict__ lg, uint32_t E, uint
         }
     }
     if (count > ksel) count = ksel;
+    // a subset pack: the ids folded onto its experts (fold_ids, exec_batch.rs:214-225); the weights
+    // stay those of the routing
+    if (pol.packed) my_idx = fold_ids_wave(my_idx, count, pol.packed, lane);
     float sum = 0.0f;  // renorm (router.rs:93-104): the sequential f32 sum, four lane reads at a time
     for (uint32_t j0 = 0; j0 < count; j0 += 4) {
         float ev[4];

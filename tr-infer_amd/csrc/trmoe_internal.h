@@ -13,10 +13,12 @@ namespace trk {
 constexpr int K_MAX = TRK_MOE_K_MAX;
 constexpr int SH_SLOT = K_MAX;  // decode: the shared expert's activation slot (after 32 routed)
 
-// Routing policy as the kernels take it (enabled == 0: fixed top-k).
+// Routing policy as the kernels take it (enabled == 0: fixed top-k).  packed: n_expert_packed of a
+// subset pack, the routed ids are folded onto experts 0 .. packed - 1 (fold_ids); 0: no folding.
 struct Policy {
     uint32_t enabled, min, max, basis;
     float mass;
+    uint32_t packed;
 };
 
 // TQ codecs (codec.rs:1-46): fmt = bits << 8 | kb
@@ -32,13 +34,30 @@ __host__ __device__ inline uint32_t tq_block_bytes(uint32_t fmt) {
     return 64 + (b == 8 ? 16 * kb : 8 * kb) + (b == 5 ? 2 * kb : 0);
 }
 
-// A weight stack as the kernels take it.
+// A weight stack as the kernels take it.  With tiles (a pack written for T tiles), rows / k are one
+// tile's shape and tile t's stack starts at ptr + t * tile_stride; gate/up strip s of the full
+// F rows is strip s % tile_strips of tile s / tile_strips.
 struct Mat {
     const uint8_t* ptr;
     uint64_t stride;  // bytes between experts
     uint32_t rows, k, fmt;
-    uint32_t row_bytes;
+    uint32_t row_bytes;     // a GGUF row or a TQ strip (of one tile's matrix)
+    uint64_t tile_stride;   // 0: one tile
+    uint32_t tile_strips;   // strips of one tile's rows
 };
+
+// Strip `strip` (16 rows, counted over all tiles' rows) of expert e.
+__host__ __device__ inline const uint8_t* mat_strip(const Mat& M, uint32_t e, uint32_t strip) {
+    if (M.tile_stride) {
+        const uint32_t t = strip / M.tile_strips, s = strip % M.tile_strips;
+        return M.ptr + (size_t)t * M.tile_stride + (size_t)e * M.stride + (size_t)s * M.row_bytes;
+    }
+    return M.ptr + (size_t)e * M.stride + (size_t)strip * M.row_bytes;
+}
+// Expert e of tile t (a down stack split by columns: each tile a [rows][k] matrix of its own).
+__host__ __device__ inline const uint8_t* mat_tile(const Mat& M, uint32_t e, uint32_t t) {
+    return M.ptr + (size_t)t * M.tile_stride + (size_t)e * M.stride;
+}
 
 // Grouped-GEMM work item: `nrows` entry rows starting at `row0` of the sorted entries, all of
 // expert `expert` (expert == 0xffffffff: the shared expert, rows are tokens); `part` is the item's
@@ -57,6 +76,7 @@ constexpr uint32_t BAR_LINE = 64;
 
 struct Workspace {
     uint32_t H, E, F, m_max, k_cap, ent_cap, item_cap;
+    uint32_t tiles;       // T of a pack written for T tiles (1: one)
     int8_t* xq;           // [max(2, m_max)][H]
     float* xs;            // [max(2, m_max)][H/32]
     int32_t* xsum;
@@ -82,7 +102,10 @@ struct Workspace {
     float* acts;          // [act_rows][F/16]
     int32_t* actsum;
     float* actu;          // [act_rows][F/16]: folded scale * (float)sum
-    float* yent;          // [ent_cap + m_max][H] per-entry down outputs (batch)
+    float* yent;          // [tiles][ent_cap + m_max][H] per-entry down outputs (batch), per tile
+    size_t yent_tile;     // floats between two tiles' yent blocks
+    float* plog;          // [tiles][m_max][E] router partials of a tiled layer
+    float* xt;            // [tiles][m_max][H / tiles] x by tile (the router's K-split)
     float* hgu;           // [ent_cap + m_max][2F] gate / up outputs of the TQ layer
     float* out_tmp;       // [m_max][H]
     unsigned long long* stats;  // [2] rows, experts
@@ -156,6 +179,11 @@ hipError_t launch_tq_act(const Workspace& ws, const float* h, uint32_t m, uint32
 hipError_t launch_tq_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                           hipStream_t st);
 hipError_t launch_tq_combine(const Workspace& ws, float* out, int residual, hipStream_t st);
+// the K-split router of a tiled layer: x [m][H] -> xt [T][m][H / T]; then the tiles' partial logits
+// plog [T][m][E] -> rlog [m][E] summed in tile order, plus the bias (k_basic.hip)
+hipError_t launch_tile_split(const float* x, uint32_t m, uint32_t H, uint32_t T, float* xt, hipStream_t st);
+hipError_t launch_tile_reduce(const float* plog, uint32_t m, uint32_t E, uint32_t T, const float* bias, float* rlog,
+                              hipStream_t st);
 // the TQ layer's expert products on int8 MFMA (k_tqm.hip): gate/up + SwiGLU + quantisation + fold,
 // and down into yent; tqm_fits: the shapes whose staged activations fit a workgroup's LDS
 // lg != null at m = 1: the decode routing (top-k or mass policy) runs inside the launch

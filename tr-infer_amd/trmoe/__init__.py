@@ -31,7 +31,7 @@ class TrkError(RuntimeError):
 
 class Mat(C.Structure):
     _fields_ = [("ptr", C.c_void_p), ("rows", C.c_uint32), ("k", C.c_uint32), ("fmt", C.c_uint32),
-                ("count", C.c_uint32), ("stride", C.c_uint64)]
+                ("count", C.c_uint32), ("stride", C.c_uint64), ("tile_stride", C.c_uint64)]
 
 
 class HcW(C.Structure):
@@ -51,7 +51,8 @@ class Policy(C.Structure):
 class Cfg(C.Structure):
     _fields_ = [("hidden", C.c_uint32), ("n_expert", C.c_uint32), ("n_ff", C.c_uint32),
                 ("n_expert_used", C.c_uint32), ("m_max", C.c_uint32), ("k_cap", C.c_uint32),
-                ("router_dot_max_m", C.c_uint32), ("hiprec", C.c_int32)]
+                ("router_dot_max_m", C.c_uint32), ("hiprec", C.c_int32), ("n_tiles", C.c_uint32),
+                ("n_expert_packed", C.c_uint32)]
 
 
 class Stats(C.Structure):
@@ -145,8 +146,10 @@ def _stream(stream=None):
 class Context:
     """trk_create/trk_destroy around one layer shape (Model::load_with's workspace sizing)."""
 
-    def __init__(self, hidden, n_expert, n_ff, k, m_max, k_cap=0, router_dot_max_m=16, hiprec=True):
-        self.cfg = Cfg(hidden, n_expert, n_ff, k, m_max, k_cap, router_dot_max_m, int(hiprec))
+    def __init__(self, hidden, n_expert, n_ff, k, m_max, k_cap=0, router_dot_max_m=16, hiprec=True, n_tiles=1,
+                 n_expert_packed=0):
+        self.cfg = Cfg(hidden, n_expert, n_ff, k, m_max, k_cap, router_dot_max_m, int(hiprec), n_tiles,
+                       n_expert_packed)
         h = C.c_void_p()
         check(lib().trk_create(C.byref(self.cfg), C.byref(h)))
         self.h = h
@@ -253,7 +256,7 @@ class LayerWeights:
         gm, dmb = matrix_bytes(gate_fmt, F, H), matrix_bytes(down_fmt, H, F)
 
         def mat(t, rows, k, fmt, count, mb):
-            return Mat(t.data_ptr(), rows, k, fmt, count, mb)
+            return Mat(t.data_ptr(), rows, k, fmt, count, mb, 0)
 
         self.moew = MoeW(router.data_ptr() if router is not None else None,
                          router_bias.data_ptr() if router_bias is not None else None, shexp_gate.data_ptr(),
@@ -319,6 +322,41 @@ class LayerWeights:
         check(L.trk_gen_gguf(down_fmt, seed, sid(10), H, F, 1e-4, 2e-3, _ptr(sh_down), st))
         return cls(H, E, F, router, shg, gate, up, down, sh_gate, sh_up, sh_down, FMT_Q4_K, down_fmt, router_bias)
 
+
+    @classmethod
+    def from_tiled_tq(cls, H, E, F, T, router, shexp_gate, gate, up, down, sh_gate, sh_up, sh_down, gate_fmt,
+                      down_fmt, router_bias=None, device="cuda"):
+        """A layer as a pack written for T tiles holds it (python/trpack/plan.py:106-118,174-181),
+        uploaded unchanged: router [T][E][H/T]; gate / up [T][count][tile bytes] (tile t: rows
+        [F/T t, F/T (t+1)) as a [F/T][H] TQ matrix), down [T][count][tile bytes] (columns
+        [F/T t, F/T (t+1)), [H][F/T]); the shared expert's as [T][tile bytes].  count < E: a
+        subset pack of the first `count` experts."""
+        import numpy as np
+        import torch
+
+        def dev(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        self = cls.__new__(cls)
+        self.H, self.E, self.F = H, E, F
+        t = dict(router=dev(router), shexp_gate=dev(shexp_gate), gate=dev(gate), up=dev(up), down=dev(down),
+                 sh_gate=dev(sh_gate), sh_up=dev(sh_up), sh_down=dev(sh_down),
+                 router_bias=None if router_bias is None else dev(router_bias))
+        self.tensors = t
+        per = F // T
+
+        def mat(name, rows, k, fmt):
+            a = t[name]
+            if a.dim() == 2:  # [T][bytes]: one matrix per tile
+                return Mat(a.data_ptr(), rows, k, fmt, 1, a.shape[1], a.stride(0))
+            return Mat(a.data_ptr(), rows, k, fmt, a.shape[1], a.stride(1), a.stride(0))
+
+        self.moew = MoeW(t["router"].data_ptr(), None if router_bias is None else t["router_bias"].data_ptr(),
+                         t["shexp_gate"].data_ptr(), mat("gate", per, H, gate_fmt), mat("up", per, H, gate_fmt),
+                         mat("down", H, per, down_fmt), mat("sh_gate", per, H, gate_fmt),
+                         mat("sh_up", per, H, gate_fmt), mat("sh_down", H, per, down_fmt))
+        self.bytes_per_expert = T * (2 * matrix_bytes(gate_fmt, per, H) + matrix_bytes(down_fmt, H, per))
+        return self
 
     @classmethod
     def generate_tq(cls, gen, H, E, F, gate_fmt=None, down_fmt=None, router_bias=None, device="cuda"):
