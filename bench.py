@@ -53,11 +53,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--m", type=str, default="1,4,8,16,512")
-    ap.add_argument("--extra", type=str, default="c4,stack,tq",
+    ap.add_argument("--extra", type=str, default="c4,stack,tq,hc,gemv",
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
                          "48-layer RMSNorm + residual stack at M=1 and M=512); tq: the layer on packed TQ "
-                         "experts at the real shape (H=2560, F=640) at M=1 and M=512; q80 / q51 / q6k: the "
-                         "layer at M=1 and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
+                         "experts at the real shape (H=2560, F=640) at M=1 and M=512; hc: the same layer "
+                         "behind the hyper-connection mix (trk_moe_forward_hc, hc=4, low rank 320); gemv: "
+                         "trk_gemv on the real model's dense projections; q80 / q51 / q6k: the layer at M=1 "
+                         "and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
     ap.add_argument("--tq-layers", type=int, default=24,
                     help="layers in the rotation of the TQ extra (1.78 GB of experts each)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -201,6 +203,11 @@ def main():
     if "tq" in todo:
         for Mt, res in bench_tq(args, dev, stream, trmoe, torch, np).items():
             extras[f"TQ real shape M={Mt}"] = res
+    if "hc" in todo:
+        for Mh, res in bench_hc(args, dev, stream, trmoe, torch, np).items():
+            extras[f"hc mix + TQ layer M={Mh}"] = res
+    if "gemv" in todo:
+        extras["trk_gemv dense projections"] = bench_gemv(args, dev, stream, trmoe, torch, np)
     if "stack" in todo:
         for Ms in (1, 512):
             extras[f"C5 stack M={Ms}"] = bench_stack(args, layers, ctx if Ms <= m_max else None, Ms, dev, stream,
@@ -421,6 +428,109 @@ def bench_tq(args, dev, stream, trmoe, torch, np):
                   "steps": steps}
         log(f"TQ real shape M={M}: {per * 1e3:.1f} us/layer, {M / (per * 1e-3):.0f} tok/s, kernels {kern}")
     del lw
+    return res
+
+
+def bench_hc(args, dev, stream, trmoe, torch, np):
+    """8(f)1, the router input's producer: trk_moe_forward_hc (the hyper-connection mix part B,
+    exec.rs:1196-1234 / exec_batch.rs:929-968, as the layer's input stage) on the real model's
+    shapes: hc = 4 streams, low rank 320, H = 2560, then the TQ layer (E = 512, F = 640, TQ4_32 /
+    TQ5_16), over a rotation of 8 layers (14 GB of experts), at M = 1 and M = 512.  The mix's up
+    projection [hc H][lr] is TQ8_32.  Reports the layer with the mix, the layer alone on the same
+    rows, and the hc_mix kernel with its roofline (the up matrix, xn, lo and the mixed rows)."""
+    Ht, Et, Ft, hc, lr = 2560, 512, 640, 4, 320
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    ufmt = trmoe.FMT_TQ8_32
+    lw, ups = [], []
+    for _ in range(8):
+        lw.append(trmoe.LayerWeights.generate_tq(gen, Ht, Et, Ft, device=dev))
+        ups.append((trmoe.gen_tq_stack(gen, 1, hc * Ht, lr, ufmt, dev)[0], ufmt))
+    ub = trmoe.matrix_bytes(ufmt, hc * Ht, lr)
+    bias = torch.from_numpy(trmoe.zipf_bias(1, Et)).to(dev)
+    res = {}
+    for M in (1, 512):
+        for w in lw:
+            w.moew.router_bias = bias.data_ptr() if M >= 64 else None
+        ctx = trmoe.Context(Ht, Et, Ft, K, M)
+        xn = torch.randn((M, hc, Ht), device=dev, generator=gen)
+        lo = torch.randn((M, lr), device=dev, generator=gen)
+        xm = torch.randn((M, Ht), device=dev, generator=gen)
+        out = torch.empty((M, Ht), dtype=torch.float32, device=dev)
+        steps = min(args.steps, 2 * len(lw))
+        ctx.forward_hc(lw[0], ups[0], hc, lr, xn, lo, out)
+
+        def body_hc():
+            for i in range(steps):
+                ctx.forward_hc(lw[i % len(lw)], ups[i % len(ups)], hc, lr, xn, lo, out)
+
+        def body_plain():
+            for i in range(steps):
+                ctx.forward(lw[i % len(lw)], xm, out)
+
+        per_hc = timed_graph(torch, stream, body_hc, 1) / steps
+        per = timed_graph(torch, stream, body_plain, 1) / steps
+        ctx.set_timing(True)
+        for i in range(steps):
+            ctx.forward_hc(lw[i % len(lw)], ups[i % len(ups)], hc, lr, xn, lo, out)
+        mix_ms, n = ctx.timing()["hc_mix"]
+        ctx.set_timing(False)
+        ctx.close()
+        mix_us = mix_ms / n * 1e3
+        nbytes = ub + M * hc * Ht * 4 + M * lr * 4 + M * Ht * 4
+        ach = nbytes / (mix_us * 1e-6) / 1e9
+        res[M] = {"tokens_per_s": round(M / (per_hc * 1e-3), 1), "us_per_layer_with_mix": round(per_hc * 1e3, 2),
+                  "us_per_layer_without": round(per * 1e3, 2), "hc_mix_us": round(mix_us, 2),
+                  "roofline": {"bound": "hbm", "kernel": "hc_mix", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                               "alg_bytes_per_launch": int(nbytes), "avg_launch_us": round(mix_us, 2),
+                               "timing": "per-launch events around each hc_mix launch (eager)"},
+                  "layers": len(lw), "steps": steps, "hc": hc, "lr": lr, "up_fmt": "TQ8_32"}
+        log(f"hc mix M={M}: layer {per_hc * 1e3:.1f} us with the mix, {per * 1e3:.1f} without; "
+            f"hc_mix {mix_us:.2f} us ({ach:.0f} GB/s)")
+    del lw, ups
+    return res
+
+
+def bench_gemv(args, dev, stream, trmoe, torch, np):
+    """8(f)4: trk_gemv (gemv_tq_rows, gemv.rs:25-40) on the real model's dense projections at
+    decode (one token, two-level activations as TR_HIPREC quantises them), the matrices as a pack
+    holds them for one tile: the LM head (exec.rs:873, 1079) [248320][2560], attention q with its gate
+    (exec.rs:1376) [12288][2560], the GDN qkv (exec.rs:1252) [10240][2560], the hyper-connection low-
+    rank down (exec.rs:1181) [320][10240] and up (exec.rs:1214) [10240][320].  Each is timed over a
+    rotation of copies totalling at least 600 MB (the 256 MB MALL cannot hold it), with a roofline
+    (the matrix, the activations and the output per call)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+    shapes = [("lm_head", 248320, 2560, trmoe.FMT_TQ8_32), ("attn_q", 12288, 2560, trmoe.FMT_TQ5_32),
+              ("gdn_qkv", 10240, 2560, trmoe.FMT_TQ5_32), ("hc_down", 320, 10240, trmoe.FMT_TQ8_32),
+              ("hc_up", 10240, 320, trmoe.FMT_TQ8_32)]
+    res = {}
+    for name, rows, k, fmt in shapes:
+        mb = trmoe.matrix_bytes(fmt, rows, k)
+        copies = max(1, min(256, -(-600_000_000 // mb)))
+        wt = trmoe.gen_tq_stack(gen, copies, rows, k, fmt, dev)
+        x = torch.randn(k, device=dev, generator=gen)
+        q, s, su = trmoe.quantize(x, 32, pair=True)
+        y = torch.empty((1, (rows + 15) // 16 * 16), dtype=torch.float32, device=dev)
+        steps = max(copies, min(args.steps, 64))
+        trmoe.gemv(wt, rows, k, fmt, 0, copies, 32, q, s, su, pair=True, y=y)
+
+        def body():
+            for i in range(steps):
+                trmoe.gemv(wt, rows, k, fmt, i % copies, copies, 32, q, s, su, pair=True, y=y)
+
+        us = timed_graph(torch, stream, body, 1) / steps * 1e3
+        nbytes = mb + 2 * k + 2 * (k // 32) * 8 + rows * 4
+        ach = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"rows": rows, "k": k, "fmt": f"TQ{fmt >> 8}_{fmt & 0xff}", "MB": round(mb / 1e6, 2),
+                     "us": round(us, 2), "GBps": round(ach, 1),
+                     "roofline": {"bound": "hbm", "kernel": "gemv_rows_kernel", "achieved": round(ach, 1),
+                                  "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                                  "traffic": None, "alg_bytes_per_launch": int(nbytes), "avg_launch_us": round(us, 2)},
+                     "copies": copies, "steps": steps}
+        log(f"gemv {name} [{rows}][{k}] {res[name]['fmt']}: {us:.2f} us, {ach:.0f} GB/s")
+        del wt
     return res
 
 

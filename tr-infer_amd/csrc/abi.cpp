@@ -45,12 +45,12 @@ uint32_t row_bytes(uint32_t fmt, uint32_t k) {
 // Kernel ids for trk_get_timing.
 enum KernelId { K_LOGITS, K_ROUTE, K_QUANT, K_DEC_GATEUP, K_DEC_DOWN, K_DEC_LAYER, K_DISPATCH, K_B_GATEUP, K_B_DOWN,
                 K_S_GATEUP, K_S_DOWN, K_B_COMBINE, K_RMSNORM, K_PROFILE, K_TQ_GATEUP, K_TQ_ACT, K_TQ_DOWN,
-                K_TQ_COMBINE, K_COUNT };
+                K_TQ_COMBINE, K_HC_MIX, K_COUNT };
 static const char* const kKernelNames[K_COUNT] = {"router_logits", "route", "quantize", "decode_gateup",
                                                   "decode_down", "decode_layer", "dispatch", "batch_gateup",
                                                   "batch_down", "stream_gateup", "stream_down", "batch_combine",
                                                   "rmsnorm", "mass_profile", "tq_gateup", "tq_act", "tq_down",
-                                                  "tq_combine"};
+                                                  "tq_combine", "hc_mix"};
 
 // Which grouped items run on the streaming GEMV (the rest on the MFMA tiles), when the caller has
 // not chosen: all of them up to 16 tokens; the items of at most 4 rows while the selections
@@ -532,7 +532,8 @@ extern "C" int trk_moe_forward_hc(trk_ctx* c, const trk_moe_w* w, const trk_hc_w
     Mats M;
     if ((rc = check_weights(c, w, M))) return rc;
     hipStream_t st = (hipStream_t)stream;
-    HIP_TRY(launch_hc_mix(up, hc->hc, H, hc->lr, xn, lo, m, c->cfg.hiprec, c->ws.xn, st));
+    const int only = -1;
+    TIMED(K_HC_MIX, launch_hc_mix(up, hc->hc, H, hc->lr, xn, lo, m, c->cfg.hiprec, c->ws.xn, st));
     return forward(c, w, c->ws.xn, nullptr, m, out, 0, st);
 }
 
