@@ -200,7 +200,9 @@ int trk_router_logits(const float *router, const float *bias, const float *shexp
 
 /* The hyper-connection mix of the FFN input, part B (tr_model::exec::HcW {up}, exec.rs:49-55):
  * up = the low-rank up projection [hc * hidden][lr] in a kb-32 TQ codec, hc streams (1..8), low
- * rank lr (a multiple of 32, at most 1024). */
+ * rank lr (a multiple of 32, at most 1024).  A batch call keeps the quantised lo rows (1.375 lr
+ * bytes per row, rows rounded up to 16) in the context's per-entry output rows, which hold at least
+ * 4 (k + 1) m_max hidden bytes; a call beyond them returns TRK_E_CAPACITY. */
 typedef struct {
     trk_mat up;
     uint32_t hc, lr;
@@ -210,7 +212,8 @@ typedef struct {
  * normed streams xn[M][hc][H] (hc_mix_a's output) and the low-rank projection lo[M][lr] summed
  * over tiles: Model::hc_mix_b (exec.rs:1196-1234) + the S5 router + moe_block at M = 1 (two-level
  * lo with hiprec), hc_b_batch (exec_batch.rs:929-1019) + moe_batch at M >= 2, on one tile.  The
- * mix runs as the layer's input stage (one launch); the router then reads the mixed rows. */
+ * mix runs as the layer's input stage (one launch at M = 1; at M >= 2 a quantisation of lo, then
+ * the mix); the router then reads the mixed rows. */
 int trk_moe_forward_hc(trk_ctx *ctx, const trk_moe_w *w, const trk_hc_w *hc, const float *xn, const float *lo,
                        uint32_t m, float *out, void *stream);
 

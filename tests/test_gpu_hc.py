@@ -86,3 +86,81 @@ def test_moe_forward_hc_rejects_bad_shapes():
                                             C.c_void_p(lo.data_ptr()), 1, C.c_void_p(out.data_ptr()), None)
         assert rc == -1 and msg in trmoe.lib().trk_last_error(), (hc, lr, fmt)
     ctx.close()
+    # a batch's quantised lo rows (22 lr bytes per 16-row tile) beyond the per-entry output rows of
+    # a context made for two rows and top-1 (4 (k + 1) m_max H bytes): a status, nothing launched
+    ctx = trmoe.Context(L.H, L.E, L.F, 1, 2)
+    lr = 512
+    assert 22 * lr > 4 * 2 * 2 * L.H
+    lo2 = torch.zeros((2, lr), dtype=torch.float32, device="cuda")
+    x2 = torch.zeros((2, HC, L.H), dtype=torch.float32, device="cuda")
+    out2 = torch.empty((2, L.H), dtype=torch.float32, device="cuda")
+    hw = trmoe.HcW(trmoe.Mat(up.data_ptr(), HC * L.H, lr, trmoe.FMT_TQ4_32, 1, 0), HC, lr)
+    rc = trmoe.lib().trk_moe_forward_hc(ctx.h, C.byref(W.moew), C.byref(hw), C.c_void_p(x2.data_ptr()),
+                                        C.c_void_p(lo2.data_ptr()), 2, C.c_void_p(out2.data_ptr()), None)
+    assert rc == -3 and b"per-entry" in trmoe.lib().trk_last_error()
+    ctx.close()
+
+
+def _mixed(ctx, W, up, bits, hc, lr, xn, lo, H):
+    import torch
+    M = lo.shape[0]
+    out = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    ctx.forward_hc(W, (dev(up), (bits << 8) | 32), hc, lr, dev(xn), dev(lo), out)
+    torch.cuda.synchronize()
+    return ctx.read(trmoe.WS_MIXED, M * H * 4, np.float32).reshape(M, H)
+
+
+@pytest.mark.parametrize("hc,M,bits", [(1, 40, 8), (3, 40, 5), (8, 40, 4), (1, 1, 4), (3, 1, 8), (8, 1, 5)])
+def test_hc_streams(hc, M, bits):
+    """Stream counts other than the real model's 4 (a wave per stream: 64, 192 and 512 threads)."""
+    say(f"hc mix streams hc={hc} M={M} bits={bits}")
+    L, orc, W = layer("tq")
+    rng = np.random.default_rng(70 + hc + M)
+    up = random_tq(rng, hc * L.H, LR, bits, 32)
+    xn = rng.standard_normal((M, hc, L.H)).astype(np.float32)
+    lo = (rng.standard_normal((M, LR)) * 3).astype(np.float32)
+    ctx = trmoe.Context(L.H, L.E, L.F, 4, max(M, 8), hiprec=True)
+    mixed = _mixed(ctx, W, up, bits, hc, LR, xn, lo, L.H)
+    ctx.close()
+    want = O.hc_mix(up, bits, hc, LR, xn, lo, M == 1, True)
+    if M > 1:
+        assert np.array_equal(mixed.view(np.uint32), want.view(np.uint32)), np.abs(mixed - want).max()
+    else:
+        assert np.abs(mixed - want).max() <= 1e-6 * np.abs(want).max()
+        assert (mixed == want).mean() >= 0.99
+
+
+_real = {}
+
+
+@pytest.mark.parametrize("M", [1, 300, 512, 1000])
+def test_hc_mix_real_shape(M):
+    """The real model's mix shape (hc 4, lr 320, H 2560, up TQ8_32) at the token counts that take
+    one, two and four 16-token tiles per workgroup, ragged ends included.  A batch row's mix depends
+    on its own xn and lo rows only, so the oracle runs on a sample of rows (the first and last
+    tiles among them)."""
+    import torch
+    H, hc, lr, bits = 2560, 4, 320, 8
+    say(f"hc mix real shape M={M}")
+    if "w" not in _real:
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(5)
+        rng = np.random.default_rng(6)
+        _real["w"] = trmoe.LayerWeights.generate_tq(gen, H, 16, 128)
+        _real["up"] = random_tq(rng, hc * H, lr, bits, 32)
+    W, up = _real["w"], _real["up"]
+    rng = np.random.default_rng(80 + M)
+    xn = rng.standard_normal((M, hc, H)).astype(np.float32)
+    lo = (rng.standard_normal((M, lr)) * 3).astype(np.float32)
+    ctx = trmoe.Context(H, 16, 128, 4, M, hiprec=True)
+    mixed = _mixed(ctx, W, up, bits, hc, lr, xn, lo, H)
+    ctx.close()
+    if M == 1:
+        want = O.hc_mix(up, bits, hc, lr, xn, lo, True, True)
+        assert np.abs(mixed - want).max() <= 1e-6 * np.abs(want).max()
+        assert (mixed == want).mean() >= 0.99
+        return
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(M - 20, M), rng.choice(M, 16, replace=False)]))
+    want = O.hc_mix(up, bits, hc, lr, xn[rows], lo[rows], False)
+    got = mixed[rows]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.abs(got - want).max()

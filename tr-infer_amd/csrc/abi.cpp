@@ -525,6 +525,10 @@ extern "C" int trk_moe_forward_hc(trk_ctx* c, const trk_moe_w* w, const trk_hc_w
         return fail(TRK_E_INVALID, "up: a kb-32 TQ codec (the low-rank row is quantised per 32)");
     if (m == 0) return TRK_OK;
     if (m > c->cfg.m_max) return fail(TRK_E_CAPACITY, "M (%u) above m_max (%u)", m, c->cfg.m_max);
+    const size_t img = hc_image_bytes(m, hc->lr), yent = (size_t)c->ws.tiles * c->ws.yent_tile * 4;
+    if (m > 1 && img > yent)
+        return fail(TRK_E_CAPACITY, "the mix's quantised rows (%zu bytes) exceed the per-entry output rows (%zu bytes)",
+                    img, yent);
     const uint32_t H = c->cfg.hidden;
     Mat up;
     int rc = make_mat(hc->up, hc->hc * H, hc->lr, false, 1, "hc up", up);
@@ -533,7 +537,7 @@ extern "C" int trk_moe_forward_hc(trk_ctx* c, const trk_moe_w* w, const trk_hc_w
     if ((rc = check_weights(c, w, M))) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int only = -1;
-    TIMED(K_HC_MIX, launch_hc_mix(up, hc->hc, H, hc->lr, xn, lo, m, c->cfg.hiprec, c->ws.xn, st));
+    TIMED(K_HC_MIX, launch_hc_mix(up, hc->hc, H, hc->lr, xn, lo, m, c->cfg.hiprec, c->ws, c->ws.xn, st));
     return forward(c, w, c->ws.xn, nullptr, m, out, 0, st);
 }
 

@@ -351,162 +351,6 @@ __global__ __launch_bounds__(256) void tq_combine_kernel(Workspace ws, float* __
     *o = y;
 }
 
-// ---- hyper-connection mix, part B (the MoE layer's input stage) ----------------------------
-//
-// mixed [m][hh] from the normed streams xn [m][hc][hh] and the low-rank projection lo [m][lr]:
-//   decode (m = 1, exec.rs:1196-1234): l = silu(lo / hc) (scalar silu), quantised per 32, in
-//     pairs with hiprec; g = sigmoid(up . q) (scalar sigmoid); mixed[c] = (sum_s xn_s[c] g_s[c],
-//     from 0, multiply then add) * (1 / hc)
-//   batch (exec_batch.rs:929-968): l = silu(lo * (1 / hc)) (silu512 on 16-blocks), quantised per
-//     32; g = sigmoid512(up . q); mixed = xn_0 g_0, then fma(xn_s, g_s, .) for s >= 1, then * (1/hc)
-// Grid (hh / 16, ceil(m / HC_TOK)), 128 threads: a workgroup owns 16 columns c0 .. c0 + 15 and
-// computes the up rows s hh + c (one 16-row strip per stream) for HC_TOK tokens in turn: lane
-// (s, r) runs its row's chain over the lr / 32 blocks in order (gemv.rs:141-148).
-constexpr uint32_t HC_TOK = 16;    // tokens per workgroup
-constexpr uint32_t HC_MAXLR = 1024;  // most low-rank width (LDS for the quantised rows)
-
-struct HcArgs {
-    Mat up;  // TQ [hc * hh][lr], kb 32
-    const float* xn;
-    const float* lo;
-    float* mixed;
-    uint32_t hc, hh, lr, m;
-    int decode, pair;
-};
-
-template <int GK>
-__global__ __launch_bounds__(128) void hc_mix_kernel(HcArgs g) {
-    using T = GvTQ<GK, 32>;
-    constexpr uint32_t BITS = T::BITS;
-    __shared__ __align__(16) int8_t lq[2][HC_MAXLR];
-    __shared__ float4 ls[2][HC_MAXLR / 32];  // scale, u = scale * sum, byte sum (int bits), -
-    __shared__ float gate[8][16];
-    const uint32_t tid = threadIdx.x, s = tid / 16, r = tid % 16, c0 = blockIdx.x * 16;
-    const uint32_t nb = g.lr / 32, P = g.pair ? 2u : 1u;
-    const float inv = 1.0f / (float)g.hc;
-    const uint32_t R = s * g.hh + c0 + r;  // this lane's up row (when s < hc)
-    const uint8_t* strip = g.up.ptr + (size_t)(R / 16) * g.up.row_bytes;
-    for (uint32_t tk = 0; tk < HC_TOK; tk++) {
-        const uint32_t t = blockIdx.y * HC_TOK + tk;
-        if (t >= g.m) break;
-        // silu and quantisation of lo, a thread per 32-block
-        for (uint32_t b = tid; b < nb; b += blockDim.x) {
-            float v[32];
-            const float* src = g.lo + (size_t)t * g.lr + 32 * b;
-            const uint32_t body = g.lr / 16 * 16;
-#pragma unroll
-            for (int i = 0; i < 32; i++) {
-                const float x = src[i];
-                if (g.decode)
-                    v[i] = x / (float)g.hc * sigmoid_libm(x / (float)g.hc);
-                else {
-                    const float y = x * inv;
-                    v[i] = 32 * b + i < body ? silu512(y) : y * sigmoid_libm(y);
-                }
-            }
-            uint32_t qw[8];
-            float sc;
-            int32_t sum;
-            float res[32];
-            auto put = [&](uint32_t lv) {
-                int xs = 0;
-#pragma unroll
-                for (int w = 0; w < 8; w++) {
-                    *reinterpret_cast<uint32_t*>(&lq[lv][32 * b + 4 * w]) = qw[w];
-                    xs = sdot4((int)qw[w], 0x01010101, xs);
-                }
-                ls[lv][b] = make_float4(sc, sc * (float)sum, __int_as_float(xs), 0.0f);
-            };
-            if (g.pair) {
-                quant_block_regs<32, true>(v, qw, sc, sum, res);
-                put(0);
-                quant_block_regs<32>(res, qw, sc, sum);
-                put(1);
-            } else {
-                quant_block_regs<32>(v, qw, sc, sum);
-                put(0);
-            }
-        }
-        __syncthreads();
-        if (s < g.hc) {
-            float acc[2] = {0.0f, 0.0f};
-            for (uint32_t b = 0; b < nb; b++) {
-                const uint8_t* blk = strip + (size_t)b * T::BB;
-                const float d = h2f(*reinterpret_cast<const uint16_t*>(blk + 2 * r));
-                const float mn = h2f(*reinterpret_cast<const uint16_t*>(blk + 32 + 2 * r));
-                uint32_t lo4[8], hi4[4];
-                if constexpr (BITS == 8) {
-#pragma unroll
-                    for (int c = 0; c < 8; c++) lo4[c] = *reinterpret_cast<const uint32_t*>(blk + 64 + 64 * c + 4 * r) ^ 0x80808080u;
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const uint32_t w = *reinterpret_cast<const uint32_t*>(blk + 64 + 64 * c + 4 * r);
-                        lo4[c] = w & 0x0f0f0f0fu;
-                        hi4[c] = (w >> 4) & 0x0f0f0f0fu;
-                        if constexpr (BITS == 5) {
-                            const uint8_t* plane = blk + 64 + 256;
-                            const uint32_t pl = *reinterpret_cast<const uint32_t*>(plane + 16 * c + 4 * (r / 8));
-                            const uint32_t ph = *reinterpret_cast<const uint32_t*>(plane + 16 * c + 8 + 4 * (r / 8));
-                            lo4[c] |= q5_hi4((pl >> (4 * (r % 8))) & 0xfu);
-                            hi4[c] |= q5_hi4((ph >> (4 * (r % 8))) & 0xfu);
-                        }
-                    }
-                }
-                for (uint32_t lv = 0; lv < P; lv++) {
-                    const int* x = reinterpret_cast<const int*>(&lq[lv][32 * b]);
-                    int dot = 0;
-                    if constexpr (BITS == 8) {
-#pragma unroll
-                        for (int c = 0; c < 8; c++) dot = sdot4((int)lo4[c], x[c], dot);
-                        dot += 128 * __float_as_int(ls[lv][b].z);
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 4; c++) {
-                            dot = sdot4((int)lo4[c], x[c], dot);
-                            dot = sdot4((int)hi4[c], x[4 + c], dot);
-                        }
-                    }
-                    const float4 xs = ls[lv][b];
-                    acc[lv] = __builtin_fmaf(mn, xs.y, acc[lv]);
-                    acc[lv] = __builtin_fmaf((float)dot, d * xs.x, acc[lv]);
-                }
-            }
-            const float v = g.pair ? acc[0] + acc[1] : acc[0];
-            gate[s][r] = g.decode ? sigmoid_libm(v) : sigmoid512(v);
-        }
-        __syncthreads();
-        if (tid < 16) {
-            const float* x = g.xn + (size_t)t * g.hc * g.hh + c0 + tid;
-            float o;
-            if (g.decode) {
-                o = 0.0f;
-                for (uint32_t st = 0; st < g.hc; st++) o = o + x[(size_t)st * g.hh] * gate[st][tid];
-            } else {
-                o = x[0] * gate[0][tid];
-                for (uint32_t st = 1; st < g.hc; st++) o = __builtin_fmaf(x[(size_t)st * g.hh], gate[st][tid], o);
-            }
-            g.mixed[(size_t)t * g.hh + c0 + tid] = o * inv;
-        }
-        __syncthreads();
-    }
-}
-
-hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, const float* xn, const float* lo,
-                         uint32_t m, int pair, float* mixed, hipStream_t st) {
-    if (tq_kb(up.fmt) != 32 || hc == 0 || hc > 8 || lr == 0 || lr % 32 || lr > HC_MAXLR || hh % 16)
-        return hipErrorInvalidValue;
-    const HcArgs a{up, xn, lo, mixed, hc, hh, lr, m, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0};
-    const dim3 grid(hh / 16, (m + HC_TOK - 1) / HC_TOK);
-    switch (tq_bits(up.fmt)) {
-        case 4: hc_mix_kernel<GK_TQ4><<<grid, 128, 0, st>>>(a); break;
-        case 5: hc_mix_kernel<GK_TQ5><<<grid, 128, 0, st>>>(a); break;
-        case 8: hc_mix_kernel<GK_TQ8><<<grid, 128, 0, st>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 // the K slice: all of K up to 128 blocks (64 with four activation rows per pass), rounded up to 8
 template <int KB, int NA>
 static hipError_t tq_go(const TqArgs& a, uint32_t fmt, uint32_t K, dim3 grid, hipStream_t st) {

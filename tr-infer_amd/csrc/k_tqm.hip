@@ -578,4 +578,355 @@ hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace&
     return hipGetLastError();
 }
 
+
+// ---- hyper-connection mix, part B (the MoE layer's input stage) ----------------------------
+//
+// mixed [m][hh] from the normed streams xn [m][hc][hh] and the low-rank projection lo [m][lr]:
+//   decode (m = 1, exec.rs:1196-1234): l = silu(lo / hc) (scalar silu), quantised per 32, in
+//     pairs with hiprec; g = sigmoid(up . q) (scalar sigmoid); mixed[c] = (sum_s xn_s[c] g_s[c],
+//     from 0, multiply then add) * (1 / hc)
+//   batch (exec_batch.rs:929-968): l = silu(lo * (1 / hc)) (silu512 on 16-blocks), quantised per
+//     32; g = sigmoid512(up . q); mixed = xn_0 g_0, then fma(xn_s, g_s, .) for s >= 1, then * (1/hc)
+// The up rows s hh + c of the hc streams for a column c form one 16-row strip per stream, so a
+// workgroup owns 16 columns c0 .. c0 + 15 and runs a wave per stream: wave s chains strip
+// (s hh + c0) / 16 over the lr / 32 blocks in order (gemv.rs:141-148) with one MFMA per block and
+// token tile, the q rows as the A operand (the expert products' layout above).  The batch rows are
+// quantised once by hc_quant_kernel into the operand image below; decode quantises its one row
+// inside every workgroup while the strip's weights are in flight.
+constexpr uint32_t HC_MAXLR = 1024;  // most low-rank width
+
+// The operand image of a tile of nr <= 16 tokens (nr = 16 but for a ragged last tile), 44 nu nr
+// bytes for nu = lr / 32 blocks:
+//   As [nu][4][nr]  8 bytes: q of (block b, k group g, token row): the MFMA's A operand
+//   SU [nu][nr]     float2: the block's (scale, u = scale * sum) per token row
+//   XC [nu][nr]     int: 128 x the block's byte sum (the 8-bit codecs' accumulator input)
+// A full tile's image is the LDS image hc_mix_kernel chains from, so a workgroup stages its full
+// tiles with one contiguous copy; tiles are 704 nu bytes apart in the batch's image.
+__host__ __device__ constexpr uint32_t hc_img_as(uint32_t nu, uint32_t nr) { return 0; }
+__host__ __device__ constexpr uint32_t hc_img_su(uint32_t nu, uint32_t nr) { return 32 * nu * nr; }
+__host__ __device__ constexpr uint32_t hc_img_xc(uint32_t nu, uint32_t nr) { return 40 * nu * nr; }
+__host__ __device__ constexpr uint32_t hc_img_tile(uint32_t nu) { return 704 * nu; }
+
+struct HcArgs {
+    Mat up;  // TQ [hc * hh][lr], kb 32
+    const float* xn;
+    const float* lo;
+    const uint8_t* img;  // batch: the quantised rows' operand image (hc_quant_kernel)
+    float* mixed;
+    uint32_t hc, hh, lr, m;
+    int pair;
+};
+
+// batch: silu(lo * (1 / hc)) of every row quantised per 32, once, into the operand image.  A
+// thread per value and a half-wave per block (lr % 32 == 0: a block is 32 consecutive values of
+// one row): the lanes reduce the block's |max| and sums with xor shuffles (max and integer sums:
+// any order gives quant_block_regs' values for finite input), stage their q bytes in LDS, and
+// four lanes write the block's 8-byte operand pieces.
+__global__ __launch_bounds__(256) void hc_quant_kernel(const float* __restrict__ lo, uint32_t m, uint32_t lr,
+                                                       uint32_t hc, uint8_t* __restrict__ img) {
+    __shared__ __align__(16) int8_t qs[8][32];
+    const uint32_t tid = threadIdx.x, j = blockIdx.x * 256u + tid, n = m * lr, k = tid % 32, hb = tid / 32;
+    const bool live = j < n;  // a whole half-wave in or out
+    const float inv = 1.0f / (float)hc;
+    const uint32_t body = lr / 16 * 16;
+    float x = 0.0f;
+    if (live) {
+        const float y = lo[j] * inv;
+        x = j % lr < body ? silu512(y) : y * sigmoid_libm(y);
+    }
+    float amax = __builtin_fabsf(x);
+#pragma unroll
+    for (int o = 16; o >= 1; o /= 2) amax = mx_ps(amax, __shfl_xor(amax, o, 32));
+    const float sc = amax / 127.0f;
+    const float qinv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const int32_t qi = cvt_rne(x * qinv);
+    const int8_t qb = sat_i8(qi);
+    int sum = qi, bs = qb;
+#pragma unroll
+    for (int o = 16; o >= 1; o /= 2) {
+        sum += __shfl_xor(sum, o, 32);
+        bs += __shfl_xor(bs, o, 32);
+    }
+    qs[hb][k] = qb;
+    __syncthreads();
+    if (!live || k >= 6) return;
+    const uint32_t nu = lr / 32, bl = j / 32, tok = bl / nu, b = bl % nu, t = tok / 16, row = tok % 16;
+    const uint32_t nr = m - 16 * t < 16 ? m - 16 * t : 16;
+    uint8_t* ti = img + (size_t)t * hc_img_tile(nu);
+    if (k < 4)
+        reinterpret_cast<long*>(ti + hc_img_as(nu, nr))[(4 * b + k) * nr + row] =
+            *reinterpret_cast<const long*>(&qs[hb][8 * k]);
+    else if (k == 4)
+        reinterpret_cast<float2*>(ti + hc_img_su(nu, nr))[b * nr + row] = make_float2(sc, sc * (float)sum);
+    else
+        reinterpret_cast<int*>(ti + hc_img_xc(nu, nr))[b * nr + row] = 128 * bs;
+}
+
+// LDS of hc_mix_kernel: NT tile images (16 rows each), reused for the mix's xn values [TT][hc][16]
+// once the chains are done; the gates [hc][TT][16].
+struct HcLds {
+    size_t gate, total;
+};
+__host__ __device__ inline HcLds hc_lds(uint32_t nt, uint32_t nu, uint32_t hc) {
+    HcLds o;
+    const size_t ops = (size_t)nt * hc_img_tile(nu), xs = (size_t)16 * nt * hc * 16 * 4;
+    o.gate = ops > xs ? ops : xs;
+    o.total = o.gate + (size_t)hc * 16 * nt * 16 * 4;
+    return o;
+}
+
+constexpr uint32_t HC_PC = 8;  // batch staging: 16-byte pieces per thread per pass (real shape: one pass)
+
+// Grid (hh / 16, ceil(m / (16 NT))), 64 hc threads.  NT token tiles of 16 per workgroup share each
+// weight unit: a unit's B operand feeds NT MFMAs, one per tile.  The first loads issued are the
+// ones the first wait needs (batch: the tile images; decode: the lo row), then the strip's weights
+// and the mix's xn values, so their latency runs under the staging (or the quantisation).  The
+// block's f32 terms run as rank-1 MFMAs (rank1: fma(m, u, acc) and d * sx, the same bits), the
+// 8-bit codecs' + 128 x byte-sum correction as the integer MFMA's accumulator input, leaving the
+// VALU a conversion and one fma per output and block.
+template <int GK, int NT, bool DEC>
+__global__ __launch_bounds__(512) void hc_mix_kernel(HcArgs g) {
+    using B = TqmB<GK, 32>;
+    constexpr bool U8 = GvTQ<GK, 32>::BITS == 8;
+    constexpr uint32_t TT = 16 * NT;  // tokens per workgroup
+    constexpr uint32_t J = TT / 4;    // xn values per thread: TT hc 16 over 64 hc threads
+    // units in flight: about 64 VGPRs of raw words
+    constexpr uint32_t UB = 64 / B::REGS < 16 ? 64 / B::REGS : 16;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x, wv = tid / 64, l = tid % 64, gq = l / 16, r = l % 16;
+    const uint32_t nu = g.lr / 32, c0 = blockIdx.x * 16, t0 = blockIdx.y * TT;
+    const uint32_t nt = g.m - t0 < TT ? g.m - t0 : TT, ntl = (nt + 15) / 16;  // live tokens, tiles
+    const HcLds L = hc_lds(NT, nu, g.hc);
+    const uint32_t tile = hc_img_tile(nu), oSU = hc_img_su(nu, 16), oXC = hc_img_xc(nu, 16);
+    float* xs = reinterpret_cast<float*>(smem);  // over the tile images after the chains
+    float* gate = reinterpret_cast<float*>(smem + L.gate);
+    const uint8_t* strip = g.up.ptr + (size_t)((wv * g.hh + c0) / 16) * g.up.row_bytes;
+    B w[UB];
+    float xv[DEC ? 1 : J];
+    // the strip's first UB units; batch: xn (token tx + 4 j, stream sx / 16, column sx % 16) of the
+    // workgroup's [TT][hc][16], a 64-byte run per 16 threads; decode: lane r < 16 of wave s holds xn
+    // (s, c0 + r)
+    auto issue_rest = [&]() {
+#pragma unroll
+        for (uint32_t i = 0; i < UB; i++)
+            if (i < nu) tqm_load<GK, 32>(w[i], strip, i, l);
+        if constexpr (DEC) {
+            xv[0] = l < 16 ? g.xn[(size_t)wv * g.hh + c0 + l] : 0.0f;
+        } else {
+            const uint32_t tx = tid / (16 * g.hc), sx = tid % (16 * g.hc);
+            const float* xp = g.xn + ((size_t)(t0 + tx) * g.hc + sx / 16) * g.hh + c0 + sx % 16;
+            const size_t step = (size_t)4 * g.hc * g.hh;
+#pragma unroll
+            for (uint32_t j = 0; j < J; j++) xv[j] = tx + 4 * j < nt ? xp[step * j] : 0.0f;
+        }
+    };
+    if constexpr (DEC) {
+        // the one row's silu(lo / hc) and its per-32 quantisation (two levels with hiprec), a
+        // value per lane: block b = j / 32 of value j = tid + nthr c is a half-wave, whose lanes
+        // reduce the block's |max| and sums with xor shuffles (max and integer sums: any order
+        // gives quant_block_regs' values for finite input) and write their q bytes in the 16-row
+        // tile image, level lv as A row lv
+        long* As = reinterpret_cast<long*>(smem);
+        int8_t* Ab = reinterpret_cast<int8_t*>(smem);
+        float2* SU = reinterpret_cast<float2*>(smem + oSU);
+        int* XC = reinterpret_cast<int*>(smem + oXC);
+        const uint32_t P = g.pair ? 2u : 1u;
+        constexpr uint32_t NL = HC_MAXLR / 64;  // lo values per thread at most (64 threads)
+        float lv[NL];
+#pragma unroll
+        for (uint32_t c = 0; c < NL; c++) {
+            const uint32_t j = tid + nthr * c;
+            lv[c] = j < g.lr ? g.lo[j] : 0.0f;
+        }
+        issue_rest();
+        for (uint32_t i = tid; i < nu * 64; i += nthr)
+            if (i % 16 >= P) As[i] = 0;
+        for (uint32_t i = tid; i < nu * 16; i += nthr)
+            if (i % 16 >= P) {
+                SU[i] = make_float2(0.0f, 0.0f);
+                XC[i] = 0;
+            }
+        const uint32_t k = tid % 32;  // the value's index in its block
+#pragma unroll
+        for (uint32_t c = 0; c < NL; c++) {
+            const uint32_t j = tid + nthr * c, b = j / 32;
+            if (j < g.lr) {  // a whole half-wave in or out (lr % 32 == 0)
+                const float y = lv[c] / (float)g.hc;
+                float x = y * sigmoid_libm(y);
+                for (uint32_t lev = 0; lev < P; lev++) {
+                    float amax = __builtin_fabsf(x);
+#pragma unroll
+                    for (int o = 16; o >= 1; o /= 2) amax = mx_ps(amax, __shfl_xor(amax, o, 32));
+                    const float sc = amax / 127.0f;
+                    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+                    const int32_t qi = cvt_rne(x * inv);
+                    const int8_t qb = sat_i8(qi);
+                    int sum = qi, bs = qb;
+#pragma unroll
+                    for (int o = 16; o >= 1; o /= 2) {
+                        sum += __shfl_xor(sum, o, 32);
+                        bs += __shfl_xor(bs, o, 32);
+                    }
+                    Ab[((b * 4 + k / 8) * 16 + lev) * 8 + k % 8] = qb;
+                    if (k == 0) {
+                        SU[b * 16 + lev] = make_float2(sc, sc * (float)sum);
+                        XC[b * 16 + lev] = U8 ? 128 * bs : 0;
+                    }
+                    x = __builtin_fmaf(-(float)qi, sc, x);  // the residual, the second level's input
+                }
+            }
+        }
+    } else {
+        // the full tiles: one contiguous copy of their images; a ragged last tile (nr < 16 rows,
+        // compact in the batch image) spread to 16 rows with the rows past nr zero
+        const uint32_t full = nt / 16, nr = nt % 16, nch = full * tile / 16;
+        // (the loads unconditional at a clamped index, into a register vector: a conditional load
+        // into an array of structs went to scratch memory, each behind its own wait)
+        const v4i* src = reinterpret_cast<const v4i*>(g.img + (size_t)(t0 / 16) * tile);
+        v4i* dst = reinterpret_cast<v4i*>(smem);
+        const uint32_t last = nch ? nch - 1 : 0;
+        v4i v[HC_PC];
+#pragma unroll
+        for (uint32_t c = 0; c < HC_PC; c++) {
+            const uint32_t k = tid + nthr * c;
+            v[c] = src[k < nch ? k : last];
+        }
+        issue_rest();
+#pragma unroll
+        for (uint32_t c = 0; c < HC_PC; c++) {
+            const uint32_t k = tid + nthr * c;
+            if (k < nch) dst[k] = v[c];
+        }
+        for (uint32_t k0 = HC_PC * nthr; k0 < nch; k0 += HC_PC * nthr) {
+#pragma unroll
+            for (uint32_t c = 0; c < HC_PC; c++) {
+                const uint32_t k = k0 + tid + nthr * c;
+                v[c] = src[k < nch ? k : last];
+            }
+#pragma unroll
+            for (uint32_t c = 0; c < HC_PC; c++) {
+                const uint32_t k = k0 + tid + nthr * c;
+                if (k < nch) dst[k] = v[c];
+            }
+        }
+        if (nr) {
+            const uint8_t* ti = g.img + (size_t)(t0 / 16 + full) * tile;
+            const long* sA = reinterpret_cast<const long*>(ti + hc_img_as(nu, nr));
+            const float2* sS = reinterpret_cast<const float2*>(ti + hc_img_su(nu, nr));
+            const int* sX = reinterpret_cast<const int*>(ti + hc_img_xc(nu, nr));
+            uint8_t* di = smem + (size_t)full * tile;
+            long* As = reinterpret_cast<long*>(di);
+            float2* SU = reinterpret_cast<float2*>(di + oSU);
+            int* XC = reinterpret_cast<int*>(di + oXC);
+            for (uint32_t p = tid; p < nu * 64; p += nthr) As[p] = p % 16 < nr ? sA[(p / 16) * nr + p % 16] : 0;
+            for (uint32_t p = tid; p < nu * 16; p += nthr) {
+                const bool live = p % 16 < nr;
+                SU[p] = live ? sS[(p / 16) * nr + p % 16] : make_float2(0.0f, 0.0f);
+                XC[p] = live ? sX[(p / 16) * nr + p % 16] : 0;
+            }
+        }
+    }
+    __syncthreads();
+    // the chain: acc[t][v] for token 16 t + 4 gq + v of the tile and weight row r (column c0 + r);
+    // rank1's a operand is the (scale, u) of token 4 gq + l % 4
+    const uint32_t tl = 4 * gq + (l & 3);
+    v4f acc[NT];
+#pragma unroll
+    for (uint32_t t = 0; t < NT; t++) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t b0 = 0; b0 < nu; b0 += UB) {
+#pragma unroll
+        for (uint32_t i = 0; i < UB; i++) {
+            const uint32_t b = b0 + i;
+            if (b >= nu) break;
+            const B cw = w[i];
+            if (b + UB < nu) tqm_load<GK, 32>(w[i], strip, b + UB, l);  // the load UB units ahead
+            const long bq = tqm_operand<GK, 32>(cw, l);
+            const float dd = h2f((uint16_t)cw.d[0]), mm = h2f((uint16_t)cw.m[0]);
+#pragma unroll
+            for (uint32_t t = 0; t < NT; t++) {
+                if (t >= ntl) break;
+                const uint8_t* ti = smem + t * tile;
+                const v4i c4 = U8 ? *reinterpret_cast<const v4i*>(ti + oXC + 4 * (b * 16 + 4 * gq)) : v4i{0, 0, 0, 0};
+                const long a = *reinterpret_cast<const long*>(ti + 8 * (b * 64 + l));
+                const v4i d4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, c4, 0, 0, 0);
+                const float2 su = *reinterpret_cast<const float2*>(ti + oSU + 8 * (b * 16 + tl));
+                acc[t] = rank1(su.y, mm, acc[t]);
+                const v4f ds = rank1(su.x, dd, neg_zero4());
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[t][v] = __builtin_fmaf((float)d4[v], ds[v], acc[t][v]);
+            }
+        }
+    }
+    const float inv = 1.0f / (float)g.hc;
+    if constexpr (DEC) {
+        // lane r of wave s: the product xn_s[c] g_s[c] (rounded, as the reference's multiply then
+        // add); thread c then adds the hc products in stream order from 0
+        if (gq == 0) gate[wv * 16 + r] = xv[0] * sigmoid_libm(g.pair ? acc[0][0] + acc[0][1] : acc[0][0]);
+        __syncthreads();
+        if (tid < 16) {
+            float o = 0.0f;
+            for (uint32_t s = 0; s < g.hc; s++) o = o + gate[s * 16 + tid];
+            g.mixed[c0 + tid] = o * inv;
+        }
+    } else {
+#pragma unroll
+        for (uint32_t t = 0; t < NT; t++)
+            if (t < ntl)
+                for (int v = 0; v < 4; v++) gate[(wv * TT + 16 * t + 4 * gq + v) * 16 + r] = sigmoid512(acc[t][v]);
+        __syncthreads();  // the tile images free
+        {
+            const uint32_t tx = tid / (16 * g.hc), sx = tid % (16 * g.hc);
+#pragma unroll
+            for (uint32_t j = 0; j < J; j++) xs[((tx + 4 * j) * g.hc + sx / 16) * 16 + sx % 16] = xv[j];
+        }
+        __syncthreads();
+        for (uint32_t o = tid; o < TT * 16; o += nthr) {
+            const uint32_t tok = o / 16, c = o % 16;
+            if (tok >= nt) break;
+            const float* x = xs + (size_t)tok * g.hc * 16 + c;
+            float y = x[0] * gate[tok * 16 + c];
+            for (uint32_t s = 1; s < g.hc; s++) y = __builtin_fmaf(x[16 * s], gate[(s * TT + tok) * 16 + c], y);
+            g.mixed[(size_t)(t0 + tok) * g.hh + c0 + c] = y * inv;
+        }
+    }
+}
+
+hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, const float* xn, const float* lo,
+                         uint32_t m, int pair, const Workspace& ws, float* mixed, hipStream_t st) {
+    const uint32_t nu = lr / 32;
+    // the batch image (44 bytes per token and block: 1.375 m lr) lives in the per-entry output rows,
+    // free until the layer's down stage
+    const size_t img_bytes = hc_image_bytes(m, lr);
+    if (tq_kb(up.fmt) != 32 || hc == 0 || hc > 8 || lr == 0 || lr % 32 || lr > HC_MAXLR || hh % 16 ||
+        (m > 1 && img_bytes > (size_t)ws.tiles * ws.yent_tile * 4))
+        return hipErrorInvalidValue;
+    const bool dec = m == 1;
+    // batch: four (else two) token tiles per workgroup where the LDS allows and the grid keeps 1024
+    // workgroups (4 per CU)
+    uint32_t nt = 1;
+    if (!dec)
+        for (uint32_t c : {4u, 2u})
+            if (hc_lds(c, nu, hc).total <= 64 * 1024 && (size_t)(hh / 16) * ((m + 16 * c - 1) / (16 * c)) >= 1024) {
+                nt = c;
+                break;
+            }
+    uint8_t* img = reinterpret_cast<uint8_t*>(ws.yent);
+    const HcArgs a{up, xn, lo, img, mixed, hc, hh, lr, m, dec && pair ? 1 : 0};
+    if (!dec) hc_quant_kernel<<<(m * lr + 255) / 256, 256, 0, st>>>(lo, m, lr, hc, img);
+    const dim3 grid(hh / 16, (m + 16 * nt - 1) / (16 * nt));
+    const size_t lds = hc_lds(nt, nu, hc).total;
+    const uint32_t thr = 64 * hc;
+    switch (tq_bits(up.fmt) * 10 + (dec ? 0 : nt)) {
+#define HC_GO(bits, gk)                                                                \
+    case bits * 10: hc_mix_kernel<gk, 1, true><<<grid, thr, lds, st>>>(a); break;      \
+    case bits * 10 + 1: hc_mix_kernel<gk, 1, false><<<grid, thr, lds, st>>>(a); break; \
+    case bits * 10 + 2: hc_mix_kernel<gk, 2, false><<<grid, thr, lds, st>>>(a); break; \
+    case bits * 10 + 4: hc_mix_kernel<gk, 4, false><<<grid, thr, lds, st>>>(a); break;
+        HC_GO(4, GK_TQ4) HC_GO(5, GK_TQ5) HC_GO(8, GK_TQ8)
+#undef HC_GO
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace trk

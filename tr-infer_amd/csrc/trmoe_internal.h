@@ -197,9 +197,12 @@ inline bool tqm_fits(uint32_t H, uint32_t F) {
     const size_t dn = (size_t)(F / 32) * 64 * 8 + (size_t)(F / 16) * 16 * 16;
     return H % 64 == 0 && F % 32 == 0 && gu + 1024 * 4 <= 64 * 1024 && dn <= 64 * 1024;
 }
-// the hyper-connection mix part B (k_tq.hip): mixed [m][hh] from xn [m][hc][hh] and lo [m][lr]
+// the hyper-connection mix part B (k_tqm.hip): mixed [m][hh] from xn [m][hc][hh] and lo [m][lr]; a
+// batch quantises lo first into an operand image of hc_image_bytes in ws.yent (free until the down
+// stage): 704 bytes per 16-token tile and 32-wide block
+inline size_t hc_image_bytes(uint32_t m, uint32_t lr) { return (size_t)(m + 15) / 16 * 22 * lr; }
 hipError_t launch_hc_mix(const Mat& up, uint32_t hc, uint32_t hh, uint32_t lr, const float* xn, const float* lo,
-                         uint32_t m, int pair, float* mixed, hipStream_t st);
+                         uint32_t m, int pair, const Workspace& ws, float* mixed, hipStream_t st);
 hipError_t launch_swiglu(const float* g, const float* u, float* y, size_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t m, uint32_t n, float* y,
                           hipStream_t st);
