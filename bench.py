@@ -436,8 +436,9 @@ def bench_hc(args, dev, stream, trmoe, torch, np):
     exec.rs:1196-1234 / exec_batch.rs:929-968, as the layer's input stage) on the real model's
     shapes: hc = 4 streams, low rank 320, H = 2560, then the TQ layer (E = 512, F = 640, TQ4_32 /
     TQ5_16), over a rotation of 8 layers (14 GB of experts), at M = 1 and M = 512.  The mix's up
-    projection [hc H][lr] is TQ8_32.  Reports the layer with the mix, the layer alone on the same
-    rows, and the hc_mix kernel with its roofline (the up matrix, xn, lo and the mixed rows)."""
+    projection [hc H][lr] is TQ8_32.  Reports the layer with the mix, the layer alone on the first
+    layer's mixed rows, and the hc_mix stage (at M >= 2 the lo quantisation and the mix kernel) with
+    its roofline (the up matrix, xn, lo and the mixed rows)."""
     Ht, Et, Ft, hc, lr = 2560, 512, 640, 4, 320
     gen = torch.Generator(device=dev)
     gen.manual_seed(11)
@@ -455,10 +456,12 @@ def bench_hc(args, dev, stream, trmoe, torch, np):
         ctx = trmoe.Context(Ht, Et, Ft, K, M)
         xn = torch.randn((M, hc, Ht), device=dev, generator=gen)
         lo = torch.randn((M, lr), device=dev, generator=gen)
-        xm = torch.randn((M, Ht), device=dev, generator=gen)
         out = torch.empty((M, Ht), dtype=torch.float32, device=dev)
         steps = min(args.steps, 2 * len(lw))
         ctx.forward_hc(lw[0], ups[0], hc, lr, xn, lo, out)
+        # the layer alone runs on the mixed rows themselves, so both legs route the same tokens
+        torch.cuda.synchronize()
+        xm = torch.from_numpy(ctx.read(trmoe.WS_MIXED, M * Ht * 4, np.float32).reshape(M, Ht).copy()).to(dev)
 
         def body_hc():
             for i in range(steps):

@@ -234,7 +234,7 @@ template <int GK, int KB, bool R1>
 __device__ __forceinline__ void tqm_strip(const uint8_t* __restrict__ strip, uint32_t K, const long* As,
                                           const float* Sc, uint32_t l, float (&acc)[4]) {
     // the walk over K is sequential per wave (the chain), so the loads run UB units ahead (about
-    // 64 VGPRs of raw words)
+    // 64 VGPRs of raw words: with about 4 loads per unit, near the 63 a wave's load counter tracks)
     constexpr uint32_t UB0 = 64 / TqmB<GK, KB>::REGS < 16 ? 64 / TqmB<GK, KB>::REGS : 16;
     constexpr uint32_t UB = R1 ? (UB0 / 4 > 0 ? UB0 / 4 : 1u) : UB0;
     constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
@@ -401,7 +401,7 @@ __device__ __forceinline__ void tqm_swiglu_store(const Workspace& ws, int decode
 
 // Grid (ceil(F / 16 / 2), units), 256 threads: waves 2i, 2i + 1 = gate and up of strip
 // 2 blockIdx.x + i.
-template <int GK, int NJ>
+template <int GK, int NJ, bool DEC>
 __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t prow[2 * BR], orow[BR];
@@ -442,19 +442,19 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
                 }
             }
         }
-    } else if (g.decode) {
+    } else if (DEC) {
         ns = ws.n_sel[0];
     }
     bool shared;
     uint32_t e, nr, P;
-    if (!tqm_unit(ws, true, g.decode, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid, ns, ids)) return;
+    if (!tqm_unit(ws, true, DEC, g.pair, blockIdx.y, shared, e, nr, P, prow, orow, tid, ns, ids)) return;
     __syncthreads();
     tqm_stage<32, GK == GK_TQ8>(ws.xq, ws.xs, ws.xu, prow, nr * P, H, As, Sc, tid, 256);
     __syncthreads();
     const uint32_t gq = l / 16, r = l % 16, n_ent = ws.n_groups[1];
     const Mat& Ga = shared ? g.sha : g.a;
     const Mat& Ub = shared ? g.shb : g.b;
-    if (NJ == 0 && !g.decode) {
+    if constexpr (!DEC) {
         // Batch: four strips per pass (strip pairs blockIdx.x and blockIdx.x + gridDim.x, then every
         // 2 gridDim.x further); a wave takes one strip, its gate and up rows as two chains over the
         // staged activations (tqm_strip2), and finishes it with SwiGLU itself, so no accumulators
@@ -468,8 +468,7 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
                                Ub.ptr + (size_t)e * Ub.stride + (size_t)strip * Ub.row_bytes, H, As, Sc, l, acc, accu);
             tqm_swiglu_store(ws, 0, 0, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc, accu, ns, wsel);
         }
-        return;
-    }
+    } else {
     // decode: waves 2i, 2i + 1 = gate and up of strip 2 blockIdx.x + i; the up wave hands its
     // accumulators over in LDS
     float (*hu)[64][4] = reinterpret_cast<float (*)[64][4]>(tail);  // [2 strips][64][4]
@@ -485,9 +484,10 @@ __global__ __launch_bounds__(256) void tqm_gateup_kernel(TqmArgs g) {
         if (up)
             for (int v = 0; v < 4; v++) hu[wv / 2][l][v] = acc[v];
         __syncthreads();
-        if (!up && live) tqm_swiglu_store(ws, g.decode, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
+        if (!up && live) tqm_swiglu_store(ws, 1, g.pair, P, nr, orow, n_ent, F, nbf, strip, gq, r, acc,
                                           hu[wv / 2][l], ns, wsel);
         __syncthreads();  // hu read before the next pass writes it
+    }
     }
 }
 
@@ -526,6 +526,316 @@ __global__ __launch_bounds__(256) void tqm_down_kernel(TqmArgs g) {
     }
 }
 
+// ---- decode from LDS copies of the strips ----------------------------------------------------
+//
+// A decode wave chains one strip over its whole K.  Reading the strip unit by unit from global
+// memory keeps at most ~60 loads (about 15 units) in flight per wave, so a real-shape gate/up strip
+// (80 units, 25.6 KB) arrives in several memory round trips.  These kernels instead copy each
+// strip into LDS with 16-byte loads (25 per lane for that strip, all in flight), then run the same
+// operands and chain (tqm_load / tqm_operand from the LDS copy).  Only the P <= 2 live activation
+// rows are staged: As_c [unit][k group g][2] (8 bytes), Sc_c [block][2] (scale, u, byte sum); the
+// A operand's other rows are zero.
+
+constexpr uint32_t TQD_NLD = 32;  // 16-byte loads per lane in flight per copy pass (a real-shape strip: one)
+constexpr uint32_t TQD_LDS_MAX = 160 * 1024;  // gfx950's LDS; above 64 KB the launch opts in
+constexpr uint32_t TQD_GU_SPW = 1;             // gate/up strips per workgroup (two waves each)
+
+// The wave's copy of n16 16-byte pieces from src to the LDS at dst, in passes of TQD_NLD loads per
+// lane; the loads of a pass are unconditional at a clamped index, so they stay in registers and in
+// flight together.  issue() requests the first pass, finish() stores it and runs the rest, so the
+// caller can request other data in between.
+template <uint32_t NLD = TQD_NLD>
+struct TqdCopy {
+    v4i v[NLD];
+    __device__ __forceinline__ void issue(const uint8_t* __restrict__ src, uint32_t n16, uint32_t l) {
+        const v4i* s4 = reinterpret_cast<const v4i*>(src);
+#pragma unroll
+        for (uint32_t c = 0; c < NLD; c++) {
+            const uint32_t i = l + 64 * c;
+            if (64 * c < n16) v[c] = s4[i < n16 ? i : n16 - 1];  // wave-uniform: only the pass's live loads
+        }
+    }
+    __device__ __forceinline__ void finish(const uint8_t* __restrict__ src, uint8_t* dst, uint32_t n16, uint32_t l) {
+        const v4i* s4 = reinterpret_cast<const v4i*>(src);
+        v4i* d4 = reinterpret_cast<v4i*>(dst);
+        const uint32_t last = n16 ? n16 - 1 : 0;
+        for (uint32_t i0 = 0;; i0 += NLD * 64) {
+#pragma unroll
+            for (uint32_t c = 0; c < NLD; c++) {
+                const uint32_t i = i0 + l + 64 * c;
+                if (i < n16) d4[i] = v[c];
+            }
+            if (i0 + NLD * 64 >= n16) break;
+#pragma unroll
+            for (uint32_t c = 0; c < NLD; c++) {
+                const uint32_t i = i0 + NLD * 64 + l + 64 * c;
+                if (i0 + NLD * 64 + 64 * c < n16) v[c] = s4[i < n16 ? i : last];
+            }
+        }
+    }
+};
+
+// Stage P <= 2 activation rows (q rows r0, r0 + 1, K bytes each; scales and u per KBS-block) as
+// As_c / Sc_c (byte sums for the 8-bit codecs), rows past P zero.  Every load of a pass is issued
+// before the first store (row r0 + 1 exists in every caller's buffer; its values are dropped when
+// P = 1).
+template <int KBS, bool XSUM>
+__device__ __forceinline__ void tqd_stage(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                          const float* __restrict__ u, uint32_t r0, uint32_t P, uint32_t K,
+                                          long* As_c, float* Sc_c, uint32_t tid, uint32_t nthr) {
+    constexpr uint32_t SC = XSUM ? 4 : 2, PA = 12, PE = 4, NX = XSUM ? KBS / 16 : 1;
+    const uint32_t npc = K / 8, nbs = K / KBS, nA = 2 * npc, nE = 2 * nbs;
+    for (uint32_t pa = 0, pe = 0; pa < nA || pe < nE; pa += PA * nthr, pe += PE * nthr) {
+        long va[PA];
+        float vs[PE], vu[PE];
+        int4 vq[PE][NX];
+#pragma unroll
+        for (uint32_t c = 0; c < PA; c++) {  // piece i: row i % 2, 8-byte piece i / 2 (= 4 unit + g)
+            const uint32_t i = pa + tid + nthr * c, ic = i < nA ? i : nA - 1;
+            va[c] = *reinterpret_cast<const long*>(q + (size_t)(r0 + ic % 2) * K + 8 * (ic / 2));
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < PE; c++) {  // entry i: row i % 2, block i / 2
+            const uint32_t i = pe + tid + nthr * c, ic = i < nE ? i : nE - 1;
+            const size_t bi = (size_t)(r0 + ic % 2) * nbs + ic / 2;
+            vs[c] = s[bi];
+            vu[c] = u[bi];
+            if constexpr (XSUM) {
+                const int4* xp = reinterpret_cast<const int4*>(q + (size_t)(r0 + ic % 2) * K + (size_t)KBS * (ic / 2));
+#pragma unroll
+                for (uint32_t t = 0; t < NX; t++) vq[c][t] = xp[t];
+            }
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < PA; c++) {
+            const uint32_t i = pa + tid + nthr * c;
+            if (i < nA) As_c[i] = i % 2 < P ? va[c] : 0;
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < PE; c++) {
+            const uint32_t i = pe + tid + nthr * c;
+            if (i >= nE) continue;
+            const bool live = i % 2 < P;
+            float* e = Sc_c + i * SC;
+            e[0] = live ? vs[c] : 0.0f;
+            e[1] = live ? vu[c] : 0.0f;
+            if constexpr (XSUM) {
+                int xs = 0;
+#pragma unroll
+                for (uint32_t t = 0; t < NX; t++) {
+                    xs = sdot4(vq[c][t].x, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].y, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].z, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].w, 0x01010101, xs);
+                }
+                e[2] = live ? __int_as_float(xs) : 0.0f;
+            }
+        }
+    }
+}
+
+// The chain of one strip (an LDS copy) over K for the live rows v < P (lanes of group 0 hold
+// them: D[row v][weight row r]).  Units go in groups of G: their LDS reads, then their MFMAs back
+// to back, then their epilogues in unit order.
+// FULL: nu a multiple of G (no partial group).  Every lane reads A row r % 2 (rows past P are
+// zero in As_c; the output rows past 1 are not used).
+template <int GK, int KB, bool FULL>
+__device__ __forceinline__ void tqd_chain(const uint8_t* strip, uint32_t K, const long* As_c, const float* Sc_c,
+                                          uint32_t l, float (&acc)[4]) {
+    constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
+    constexpr uint32_t SC = U8 ? 4 : 2, NBL = TqmB<GK, KB>::NBL, G = 8;
+    const uint32_t nu = K / 32, g = l / 16, r = l % 16;
+    for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    constexpr uint32_t UBB = NBL * GvTQ<GK, KB>::BB;  // bytes of a unit
+    for (uint32_t b0 = 0; b0 < nu; b0 += G) {
+        TqmB<GK, KB> w[G];
+        long a[G];
+        // the group's bases, so a unit's reads take immediate offsets
+        const uint8_t* sg = strip + (size_t)b0 * UBB;
+        const long* ag = As_c + 8 * b0 + 2 * g + (r & 1);
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++) {
+            const uint32_t bi = FULL || b0 + i < nu ? i : nu - 1 - b0;
+            tqm_load<GK, KB>(w[i], sg, bi, l);
+            a[i] = ag[8 * bi];
+        }
+        v4i d[G][NBL];
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++) {
+            const long bq = tqm_operand<GK, KB>(w[i], l);
+#pragma unroll
+            for (uint32_t hb = 0; hb < NBL; hb++)
+                d[i][hb] = tqm_mfma(KB == 16 ? ((g / 2 == hb) ? a[i] : 0) : a[i], bq);
+        }
+        const float* scg = Sc_c + (size_t)b0 * NBL * 2 * SC;
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++) {
+            const uint32_t b = b0 + i;
+            if (!FULL && b >= nu) break;
+#pragma unroll
+            for (uint32_t hb = 0; hb < NBL; hb++) {
+                const float dd = h2f((uint16_t)w[i].d[hb]), mm = h2f((uint16_t)w[i].m[hb]);
+#pragma unroll
+                for (uint32_t v = 0; v < 2; v++) {
+                    const float* sx = scg + ((NBL * i + hb) * 2 + v) * SC;
+                    const int dot = U8 ? d[i][hb][v] + 128 * __float_as_int(sx[2]) : d[i][hb][v];
+                    acc[v] = __builtin_fmaf(mm, sx[1], acc[v]);
+                    acc[v] = __builtin_fmaf((float)dot, dd * sx[0], acc[v]);
+                }
+            }
+        }
+    }
+}
+
+template <int GK, int KB>
+__device__ __forceinline__ void tqd_chain_any(const uint8_t* strip, uint32_t K, const long* As_c, const float* Sc_c,
+                                              uint32_t l, float (&acc)[4]) {
+    if ((K / 32) % 8 == 0)
+        tqd_chain<GK, KB, true>(strip, K, As_c, Sc_c, l, acc);
+    else
+        tqd_chain<GK, KB, false>(strip, K, As_c, Sc_c, l, acc);
+}
+
+struct TqdLds {
+    uint32_t strips, as, sc, hu, route, total;
+};
+// gate/up (spw strips per workgroup): [2 spw strips][row_bytes], As_c, Sc_c, hu [spw][64][2], the
+// routing scratch (+ E floats for MassBasis::All); down: [4 strips][row_bytes], As_c, Sc_c
+__host__ __device__ inline TqdLds tqd_lds(bool gu, uint32_t row_bytes, uint32_t K, uint32_t kbs, bool u8, uint32_t ex,
+                                          uint32_t spw = 1) {
+    TqdLds o;
+    o.strips = 0;
+    o.as = (gu ? 2 * spw : 4) * row_bytes;
+    o.sc = o.as + K / 8 * 2 * 8;
+    o.hu = o.sc + K / kbs * 2 * (u8 ? 16 : 8);
+    o.route = o.hu + (gu ? spw * 64 * 2 * 4 : 0);
+    o.total = o.route + (gu ? ROUTE_CAND * 8 + K_MAX * 8 + 16 + ex : 0);
+    o.total = (o.total + 15) / 16 * 16;
+    return o;
+}
+
+// Decode gate/up: grid (F / 16, kcap + 1), 128 threads; wave 0 the gate strip, wave 1 the up strip
+// of strip blockIdx.x for slot blockIdx.y.  Wave 0 routes (route_row, router.rs:106-148) while
+// wave 1 stages x; the shared expert's row (slot ns) copies its strips before routing.  Row
+// blockIdx.y = kcap is the shared expert's when ns = kcap (fixed top-k); with fewer selected, the
+// shared expert is row ns and the rows between are idle, as in the generic decode.
+template <int GK, int NJ, int SPW>
+__global__ __launch_bounds__(128 * SPW) void tqd_gateup_kernel(TqmArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool U8 = GK == GK_TQ8;
+    const Workspace& ws = g.ws;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
+    const uint32_t strip = SPW * blockIdx.x + wv / 2, y = blockIdx.y, P = g.pair ? 2u : 1u;
+    const TqdLds L = tqd_lds(true, g.a.row_bytes, H, 32, U8,
+                             g.pol.enabled && g.pol.basis == TRK_BASIS_ALL ? ws.E * 4 : 0, SPW);
+    uint8_t* my = smem + wv * g.a.row_bytes;
+    long* As_c = reinterpret_cast<long*>(smem + L.as);
+    float* Sc_c = reinterpret_cast<float*>(smem + L.sc);
+    float* hu = reinterpret_cast<float*>(smem + L.hu);
+    uint2* cand = reinterpret_cast<uint2*>(smem + L.route);
+    uint32_t* r_ids = reinterpret_cast<uint32_t*>(cand + ROUTE_CAND);
+    float* r_w = reinterpret_cast<float*>(r_ids + K_MAX);
+    uint32_t* r_n = reinterpret_cast<uint32_t*>(r_w + K_MAX);
+    float* ex = reinterpret_cast<float*>(r_n + 4);
+    const bool last = y == gridDim.y - 1;  // the shared expert's row when ns = kcap
+    // this wave's stacks by value (a reference chosen at run time would put the arguments in
+    // scratch memory): routed (gate or up) and shared
+    const bool isup = wv % 2 == 1;
+    const uint8_t* rptr = isup ? g.b.ptr : g.a.ptr;
+    const uint64_t rstride = isup ? g.b.stride : g.a.stride;
+    const uint8_t* sptr = (isup ? g.shb.ptr : g.sha.ptr) + (size_t)strip * g.a.row_bytes;
+    const uint32_t n16 = g.a.row_bytes / 16;
+    if (last) {  // the shared expert's strips need no routing: copied first
+        TqdCopy<> cp;
+        cp.issue(sptr, n16, l);
+        cp.finish(sptr, my, n16, l);
+    }
+    if (wv == 0) {
+        const uint32_t n = route_row<NJ>(g.lg, ws.E, g.k, g.pol, l, cand, ex, r_ids, r_w);
+        if (l == 0) r_n[0] = n;
+    } else {
+        tqd_stage<32, U8>(ws.xq, ws.xs, ws.xu, 0, P, H, As_c, Sc_c, tid - 64, 128 * SPW - 64);
+    }
+    __syncthreads();
+    const uint32_t ns = r_n[0];
+    if (blockIdx.x == 0 && y == 0) {  // for the down and combine launches, MoeStats
+        if (tid < ns) {
+            ws.ids[tid] = r_ids[tid];
+            ws.w[tid] = r_w[tid];
+        }
+        if (tid == 0) {
+            ws.n_sel[0] = ns;
+            if (ws.stats) {
+                atomicAdd(&ws.stats[0], 1ull);
+                atomicAdd(&ws.stats[1], (unsigned long long)ns);
+            }
+        }
+    }
+    // the unit: routed slot y < ns; the shared expert at row ns (the last row when ns = kcap)
+    const bool shared = last ? ns == gridDim.y - 1 : y == ns;
+    if (!shared && y >= ns) return;
+    if (last && !shared) return;  // ns < kcap: the last row is idle; row ns runs the shared expert
+    if (!last) {
+        const uint8_t* src = shared ? sptr : rptr + (size_t)r_ids[y] * rstride + (size_t)strip * g.a.row_bytes;
+        TqdCopy<> cp;
+        cp.issue(src, n16, l);
+        cp.finish(src, my, n16, l);
+    }
+    __syncthreads();
+    float acc[4];
+    if ((H / 32) % 8 == 0)
+        tqd_chain<GK, 32, true>(my, H, As_c, Sc_c, l, acc);
+    else
+        tqd_chain<GK, 32, false>(my, H, As_c, Sc_c, l, acc);
+    float* hs = hu + (wv / 2) * 128;  // this strip's up accumulators
+    if (wv % 2 == 1) {
+        hs[2 * l] = acc[0];
+        hs[2 * l + 1] = acc[1];
+    }
+    __syncthreads();
+    if (wv % 2 == 0) {
+        const uint32_t orow[1] = {shared ? ns : y};
+        const float hv[4] = {hs[2 * l], hs[2 * l + 1], 0.0f, 0.0f};
+        tqm_swiglu_store(ws, 1, g.pair, P, 1, orow, 0, F, nbf, strip, l / 16, l % 16, acc, hv, ns, r_w);
+    }
+}
+
+// Decode down: grid (H / 64, kcap + 1), 256 threads; wave w the strip 4 blockIdx.x + w of H for
+// slot blockIdx.y (the routing from the gate/up launch: ids, n_sel; the shared expert at row ns).
+template <int GK>
+__global__ __launch_bounds__(256) void tqd_down_kernel(TqmArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool U8 = GK == GK_TQ8;
+    const Workspace& ws = g.ws;
+    const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F;
+    const uint32_t y = blockIdx.y, strip = 4 * blockIdx.x + wv, P = g.pair ? 2u : 1u;
+    const uint32_t ns = ws.n_sel[0], id = ws.ids[y < K_MAX ? y : 0];  // both requested at once
+    if (y > ns) return;
+    const bool shared = y == ns;
+    const TqdLds L = tqd_lds(false, g.a.row_bytes, F, 16, U8, 0);
+    uint8_t* my = smem + wv * g.a.row_bytes;
+    long* As_c = reinterpret_cast<long*>(smem + L.as);
+    float* Sc_c = reinterpret_cast<float*>(smem + L.sc);
+    const uint8_t* src = (shared ? g.sha.ptr : g.a.ptr + (size_t)id * g.a.stride) + (size_t)strip * g.a.row_bytes;
+    const uint32_t n16 = g.a.row_bytes / 16;
+    TqdCopy<16> cp;  // a strip of up to 16 KB per pass
+    cp.issue(src, n16, l);  // the weights first, then the activations (one round trip for both)
+    tqd_stage<16, U8>(ws.actq, ws.acts, ws.actu, 2 * y, P, F, As_c, Sc_c, tid, 256);
+    cp.finish(src, my, n16, l);
+    __syncthreads();
+    float acc[4];
+    tqd_chain_any<GK, 16>(my, F, As_c, Sc_c, l, acc);
+    if (l < 16) ws.yent[(size_t)y * H + strip * 16 + l] = P == 2 ? acc[0] + acc[1] : acc[0];
+}
+
+// The LDS decode kernels' shape conditions: 16-byte aligned strips and LDS within the limit.
+static bool tqd_ok(const Mat& a, const Mat& b, const Mat& sa, const Mat& sb, size_t lds) {
+    auto al = [](const Mat& m) {
+        return ((uintptr_t)m.ptr % 16 == 0) && m.stride % 16 == 0 && m.row_bytes % 16 == 0 && m.tile_stride == 0;
+    };
+    return al(a) && al(b) && al(sa) && al(sb) && lds <= TQD_LDS_MAX;
+}
+
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
                              uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
                              hipStream_t st) {
@@ -535,6 +845,33 @@ hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate,
     // decode: a workgroup per strip pair; batch: a workgroup per TQM_PAIRS strip pairs of an item,
     // looping over them with the item's activations staged once (5 or 2 pairs per workgroup at the
     // real shape: 478 / 484 us against 460 for 4)
+    if (m == 1 && nj) {  // decode from LDS copies of the strips where they fit
+        const uint32_t ex = pol.enabled && pol.basis == TRK_BASIS_ALL ? ws.E * 4 : 0;
+        constexpr uint32_t SPW = TQD_GU_SPW;
+        const size_t lds = tqd_lds(true, gate.row_bytes, ws.H, 32, tq_bits(gate.fmt) == 8, ex, SPW).total;
+        if (tqd_ok(gate, up, sh_gate, sh_up, lds) && gate.row_bytes == up.row_bytes &&
+            gate.row_bytes == sh_gate.row_bytes && gate.row_bytes == sh_up.row_bytes && (ws.F / 16) % SPW == 0) {
+            const dim3 grid(ws.F / 16 / SPW, kcap + 1);
+            auto go = [&](auto kern) {
+                if (lds > 64 * 1024) {
+                    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                    if (e != hipSuccess) return e;
+                }
+                kern<<<grid, 128 * SPW, lds, st>>>(a);
+                return hipGetLastError();
+            };
+            switch (tq_bits(gate.fmt) * 100 + nj) {
+                case 408: return go(tqd_gateup_kernel<GK_TQ4, 8, SPW>);
+                case 416: return go(tqd_gateup_kernel<GK_TQ4, 16, SPW>);
+                case 508: return go(tqd_gateup_kernel<GK_TQ5, 8, SPW>);
+                case 516: return go(tqd_gateup_kernel<GK_TQ5, 16, SPW>);
+                case 808: return go(tqd_gateup_kernel<GK_TQ8, 8, SPW>);
+                case 816: return go(tqd_gateup_kernel<GK_TQ8, 16, SPW>);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     const uint32_t pairs = (ws.F / 16 + 1) / 2;
     const dim3 grid(m == 1 ? pairs : (pairs + TQM_PAIRS - 1) / TQM_PAIRS, m == 1 ? kcap + 1 : grouped_item_rows(ws, m));
     const size_t sc = tq_bits(gate.fmt) == 8 ? 16 : 8;  // bytes per Sc entry
@@ -543,11 +880,12 @@ hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate,
         const size_t ex = nj && pol.enabled && pol.basis == TRK_BASIS_ALL ? (size_t)ws.E * 4 : 0;
         lds += ex > 2 * 64 * 4 * 4 ? ex : 2 * 64 * 4 * 4;
     }
-    switch (tq_bits(gate.fmt) * 100 + nj) {
-#define TQM_GU(b, gk)                                                                 \
-    case b * 100: tqm_gateup_kernel<gk, 0><<<grid, 256, lds, st>>>(a); break;         \
-    case b * 100 + 8: tqm_gateup_kernel<gk, 8><<<grid, 256, lds, st>>>(a); break;     \
-    case b * 100 + 16: tqm_gateup_kernel<gk, 16><<<grid, 256, lds, st>>>(a); break;
+    switch (tq_bits(gate.fmt) * 100 + nj + (m == 1 ? 1 : 0)) {
+#define TQM_GU(b, gk)                                                                       \
+    case b * 100: tqm_gateup_kernel<gk, 0, false><<<grid, 256, lds, st>>>(a); break;        \
+    case b * 100 + 1: tqm_gateup_kernel<gk, 0, true><<<grid, 256, lds, st>>>(a); break;     \
+    case b * 100 + 8 + 1: tqm_gateup_kernel<gk, 8, true><<<grid, 256, lds, st>>>(a); break; \
+    case b * 100 + 16 + 1: tqm_gateup_kernel<gk, 16, true><<<grid, 256, lds, st>>>(a); break;
         TQM_GU(4, GK_TQ4) TQM_GU(5, GK_TQ5) TQM_GU(8, GK_TQ8)
 #undef TQM_GU
         default: return hipErrorInvalidValue;
@@ -559,6 +897,19 @@ hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace&
                            hipStream_t st) {
     if (tq_kb(down.fmt) != 16 || ws.F % 32 || ws.H % 64) return hipErrorInvalidValue;
     const TqmArgs a{down, down, sh_down, sh_down, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0, nullptr, 0, Policy{}};
+    if (m == 1) {  // decode from LDS copies of the strips where they fit
+        const size_t lds = tqd_lds(false, down.row_bytes, ws.F, 16, tq_bits(down.fmt) == 8, 0).total;
+        if (tqd_ok(down, down, sh_down, sh_down, lds) && down.row_bytes == sh_down.row_bytes) {
+            const dim3 grid(ws.H / 64, kcap + 1);
+            switch (tq_bits(down.fmt)) {
+                case 4: tqd_down_kernel<GK_TQ4><<<grid, 256, lds, st>>>(a); break;
+                case 5: tqd_down_kernel<GK_TQ5><<<grid, 256, lds, st>>>(a); break;
+                case 8: tqd_down_kernel<GK_TQ8><<<grid, 256, lds, st>>>(a); break;
+                default: return hipErrorInvalidValue;
+            }
+            return hipGetLastError();
+        }
+    }
     // decode: a workgroup per strip group; batch: per four strip groups of an item (each wave walks
     // four strips), so an item's activations are staged once per 256 output rows rather than per
     // 64 (real shape M = 512: 343 -> 301 us; per 128 rows 315, per 512 320)
