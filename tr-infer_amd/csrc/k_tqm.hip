@@ -640,14 +640,13 @@ __device__ __forceinline__ void tqd_stage(const int8_t* __restrict__ q, const fl
 // FULL: nu a multiple of G (no partial group).  Every lane reads A row r % 2 (rows past P are
 // zero in As_c; the output rows past 1 are not used).
 template <int GK, int KB, bool FULL>
-__device__ __forceinline__ void tqd_chain(const uint8_t* strip, uint32_t K, const long* As_c, const float* Sc_c,
-                                          uint32_t l, float (&acc)[4]) {
+__device__ __forceinline__ void tqd_chain(const uint8_t* strip, uint32_t u0, uint32_t nu, const long* As_c,
+                                          const float* Sc_c, uint32_t l, float (&acc)[4]) {
     constexpr bool U8 = GvTQ<GK, KB>::BITS == 8;
     constexpr uint32_t SC = U8 ? 4 : 2, NBL = TqmB<GK, KB>::NBL, G = 8;
-    const uint32_t nu = K / 32, g = l / 16, r = l % 16;
-    for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    const uint32_t g = l / 16, r = l % 16;
     constexpr uint32_t UBB = NBL * GvTQ<GK, KB>::BB;  // bytes of a unit
-    for (uint32_t b0 = 0; b0 < nu; b0 += G) {
+    for (uint32_t b0 = u0; b0 < nu; b0 += G) {
         TqmB<GK, KB> w[G];
         long a[G];
         // the group's bases, so a unit's reads take immediate offsets
@@ -687,14 +686,93 @@ __device__ __forceinline__ void tqd_chain(const uint8_t* strip, uint32_t K, cons
     }
 }
 
+// Units [u0, u1) of the chain (acc carried in).
 template <int GK, int KB>
-__device__ __forceinline__ void tqd_chain_any(const uint8_t* strip, uint32_t K, const long* As_c, const float* Sc_c,
-                                              uint32_t l, float (&acc)[4]) {
-    if ((K / 32) % 8 == 0)
-        tqd_chain<GK, KB, true>(strip, K, As_c, Sc_c, l, acc);
+__device__ __forceinline__ void tqd_chain_any(const uint8_t* strip, uint32_t u0, uint32_t u1, const long* As_c,
+                                              const float* Sc_c, uint32_t l, float (&acc)[4]) {
+    if ((u1 - u0) % 8 == 0)
+        tqd_chain<GK, KB, true>(strip, u0, u1, As_c, Sc_c, l, acc);
     else
-        tqd_chain<GK, KB, false>(strip, K, As_c, Sc_c, l, acc);
+        tqd_chain<GK, KB, false>(strip, u0, u1, As_c, Sc_c, l, acc);
 }
+
+// Copy a strip of n16 16-byte pieces (NLD = ceil(n16 / 64): every lane's loads unconditional, so
+// each store waits for its own load only) and chain it from LDS, the first half of the passes'
+// units while the second half is still arriving.  issue() requests the pieces; run() stores and
+// chains.
+template <int GK, int KB, uint32_t NLD>
+struct TqdStream {
+    v4i v[NLD];
+    __device__ __forceinline__ void issue(const uint8_t* __restrict__ src, uint32_t n16, uint32_t l) {
+        const v4i* s4 = reinterpret_cast<const v4i*>(src);
+#pragma unroll
+        for (uint32_t c = 0; c < NLD; c++) v[c] = s4[l + 64 * c < n16 ? l + 64 * c : n16 - 1];
+    }
+    __device__ __forceinline__ void run(uint8_t* my, uint32_t n16, uint32_t K, const long* As_c, const float* Sc_c,
+                                        uint32_t l, float (&acc)[4]) {
+        constexpr uint32_t UBB = TqmB<GK, KB>::NBL * GvTQ<GK, KB>::BB, H1 = (NLD + 1) / 2;
+        v4i* d4 = reinterpret_cast<v4i*>(my);
+#pragma unroll
+        for (uint32_t c = 0; c < H1; c++)
+            if (l + 64 * c < n16) d4[l + 64 * c] = v[c];
+        const uint32_t nu = K / 32, done = 64 * H1 < n16 ? 64 * H1 : n16;
+        uint32_t um = done * 16 / UBB;  // units wholly copied, then whole groups of 8
+        um = (um < nu ? um : nu) / 8 * 8;
+        for (int q = 0; q < 4; q++) acc[q] = 0.0f;
+        tqd_chain_any<GK, KB>(my, 0, um, As_c, Sc_c, l, acc);
+#pragma unroll
+        for (uint32_t c = H1; c < NLD; c++)
+            if (l + 64 * c < n16) d4[l + 64 * c] = v[c];
+        tqd_chain_any<GK, KB>(my, um, nu, As_c, Sc_c, l, acc);
+    }
+};
+
+// Single-pass staging (every thread at most one piece and one entry of each kind), split so the
+// caller can issue other loads between the staging loads and stores.
+template <int KBS, bool XSUM>
+struct TqdStage1 {
+    static constexpr uint32_t NX = XSUM ? KBS / 16 : 1;
+    long va;
+    float vs, vu;
+    int4 vq[NX];
+    __device__ __forceinline__ static bool fits(uint32_t K, uint32_t nthr) { return 2 * (K / 8) <= nthr; }
+    __device__ __forceinline__ void load(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                         const float* __restrict__ u, uint32_t r0, uint32_t K, uint32_t tid) {
+        const uint32_t nA = 2 * (K / 8), nbs = K / KBS, nE = 2 * nbs;
+        const uint32_t ia = tid < nA ? tid : nA - 1, ie = tid < nE ? tid : nE - 1;
+        va = *reinterpret_cast<const long*>(q + (size_t)(r0 + ia % 2) * K + 8 * (ia / 2));
+        const size_t bi = (size_t)(r0 + ie % 2) * nbs + ie / 2;
+        vs = s[bi];
+        vu = u[bi];
+        if constexpr (XSUM) {
+            const int4* xp = reinterpret_cast<const int4*>(q + (size_t)(r0 + ie % 2) * K + (size_t)KBS * (ie / 2));
+#pragma unroll
+            for (uint32_t t = 0; t < NX; t++) vq[t] = xp[t];
+        }
+    }
+    __device__ __forceinline__ void store(uint32_t P, uint32_t K, long* As_c, float* Sc_c, uint32_t tid) {
+        constexpr uint32_t SC = XSUM ? 4 : 2;
+        const uint32_t nA = 2 * (K / 8), nE = 2 * (K / KBS);
+        if (tid < nA) As_c[tid] = tid % 2 < P ? va : 0;
+        if (tid < nE) {
+            const bool live = tid % 2 < P;
+            float* e = Sc_c + tid * SC;
+            e[0] = live ? vs : 0.0f;
+            e[1] = live ? vu : 0.0f;
+            if constexpr (XSUM) {
+                int xs = 0;
+#pragma unroll
+                for (uint32_t t = 0; t < NX; t++) {
+                    xs = sdot4(vq[t].x, 0x01010101, xs);
+                    xs = sdot4(vq[t].y, 0x01010101, xs);
+                    xs = sdot4(vq[t].z, 0x01010101, xs);
+                    xs = sdot4(vq[t].w, 0x01010101, xs);
+                }
+                e[2] = live ? __int_as_float(xs) : 0.0f;
+            }
+        }
+    }
+};
 
 struct TqdLds {
     uint32_t strips, as, sc, hu, route, total;
@@ -775,18 +853,22 @@ __global__ __launch_bounds__(128 * SPW) void tqd_gateup_kernel(TqmArgs g) {
     const bool shared = last ? ns == gridDim.y - 1 : y == ns;
     if (!shared && y >= ns) return;
     if (last && !shared) return;  // ns < kcap: the last row is idle; row ns runs the shared expert
-    if (!last) {
-        const uint8_t* src = shared ? sptr : rptr + (size_t)r_ids[y] * rstride + (size_t)strip * g.a.row_bytes;
-        TqdCopy<> cp;
-        cp.issue(src, n16, l);
-        cp.finish(src, my, n16, l);
-    }
-    __syncthreads();
     float acc[4];
-    if ((H / 32) % 8 == 0)
-        tqd_chain<GK, 32, true>(my, H, As_c, Sc_c, l, acc);
-    else
-        tqd_chain<GK, 32, false>(my, H, As_c, Sc_c, l, acc);
+    const uint8_t* src = shared ? sptr : rptr + (size_t)r_ids[y] * rstride + (size_t)strip * g.a.row_bytes;
+    if (!last && (n16 + 63) / 64 == 25) {
+        // the real shape's strip (25 passes): the chain starts on the first half while the rest arrives
+        TqdStream<GK, 32, 25> sm;
+        sm.issue(src, n16, l);
+        sm.run(my, n16, H, As_c, Sc_c, l, acc);
+    } else {
+        if (!last) {
+            TqdCopy<> cp;
+            cp.issue(src, n16, l);
+            cp.finish(src, my, n16, l);
+        }
+        for (int q = 0; q < 4; q++) acc[q] = 0.0f;
+        tqd_chain_any<GK, 32>(my, 0, H / 32, As_c, Sc_c, l, acc);
+    }
     float* hs = hu + (wv / 2) * 128;  // this strip's up accumulators
     if (wv % 2 == 1) {
         hs[2 * l] = acc[0];
@@ -818,13 +900,26 @@ __global__ __launch_bounds__(256) void tqd_down_kernel(TqmArgs g) {
     float* Sc_c = reinterpret_cast<float*>(smem + L.sc);
     const uint8_t* src = (shared ? g.sha.ptr : g.a.ptr + (size_t)id * g.a.stride) + (size_t)strip * g.a.row_bytes;
     const uint32_t n16 = g.a.row_bytes / 16;
-    TqdCopy<16> cp;  // a strip of up to 16 KB per pass
-    cp.issue(src, n16, l);  // the weights first, then the activations (one round trip for both)
-    tqd_stage<16, U8>(ws.actq, ws.acts, ws.actu, 2 * y, P, F, As_c, Sc_c, tid, 256);
-    cp.finish(src, my, n16, l);
-    __syncthreads();
     float acc[4];
-    tqd_chain_any<GK, 16>(my, F, As_c, Sc_c, l, acc);
+    if ((n16 + 63) / 64 == 9 && TqdStage1<16, U8>::fits(F, 256)) {
+        // the real shape's strip (9 passes): the activations' loads, the strip's, the activations
+        // stored (a wait for their own loads only), then the streamed copy and chain
+        TqdStage1<16, U8> sg;
+        sg.load(ws.actq, ws.acts, ws.actu, 2 * y, F, tid);
+        TqdStream<GK, 16, 9> sm;
+        sm.issue(src, n16, l);
+        sg.store(P, F, As_c, Sc_c, tid);
+        __syncthreads();
+        sm.run(my, n16, F, As_c, Sc_c, l, acc);
+    } else {
+        TqdCopy<16> cp;  // a strip of up to 16 KB per pass
+        cp.issue(src, n16, l);  // the weights first, then the activations (one round trip for both)
+        tqd_stage<16, U8>(ws.actq, ws.acts, ws.actu, 2 * y, P, F, As_c, Sc_c, tid, 256);
+        cp.finish(src, my, n16, l);
+        __syncthreads();
+        for (int q = 0; q < 4; q++) acc[q] = 0.0f;
+        tqd_chain_any<GK, 16>(my, 0, F / 32, As_c, Sc_c, l, acc);
+    }
     if (l < 16) ws.yent[(size_t)y * H + strip * 16 + l] = P == 2 ? acc[0] + acc[1] : acc[0];
 }
 
