@@ -436,6 +436,12 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
             // int8 MFMA per TQ block, SwiGLU + quantisation + fold in the gate/up launch
             TIMED(K_TQ_GATEUP, launch_tqm_gateup(M.gate, M.up, M.shg, M.shu, ws, m, kcap, pair, m == 1 ? lg : nullptr, k,
                                                  c->pol, st));
+            if (m == 1 && tqd_dc_ok(M.down, M.shd, ws, kcap)) {
+                // decode: the down adds the slots' rows in order itself (no combine launch)
+                TIMED(K_TQ_DOWN, launch_tqd_down_combine(M.down, M.shd, ws, kcap, pair, out, residual, st));
+                if (c->profile) TIMED(K_PROFILE, launch_mass_profile(lg, m, E, ws.prof, st));
+                return TRK_OK;
+            }
             TIMED(K_TQ_DOWN, launch_tqm_down(M.down, M.shd, ws, m, kcap, pair, st));
         } else {
             TIMED(K_TQ_GATEUP, launch_tq_gateup(M.gate, M.up, M.shg, M.shu, ws, ws.hgu, m, kcap, pair, st));

@@ -923,6 +923,146 @@ __global__ __launch_bounds__(256) void tqd_down_kernel(TqmArgs g) {
     if (l < 16) ws.yent[(size_t)y * H + strip * 16 + l] = P == 2 ? acc[0] + acc[1] : acc[0];
 }
 
+// Staging of P <= 2 activation rows by one wave in a single pass (PA pieces and PE entries per
+// lane at most), split so the caller can issue other loads between the loads and the stores.
+template <int KBS, bool XSUM, uint32_t PA, uint32_t PE>
+struct TqdStageW {
+    static constexpr uint32_t NX = XSUM ? KBS / 16 : 1;
+    long va[PA];
+    float vs[PE], vu[PE];
+    int4 vq[PE][NX];
+    __host__ __device__ static bool fits(uint32_t K) { return 2 * (K / 8) <= PA * 64 && 2 * (K / KBS) <= PE * 64; }
+    __device__ __forceinline__ void load(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                         const float* __restrict__ u, uint32_t r0, uint32_t K, uint32_t l) {
+        const uint32_t nA = 2 * (K / 8), nbs = K / KBS, nE = 2 * nbs;
+#pragma unroll
+        for (uint32_t c = 0; c < PA; c++) {
+            const uint32_t i = l + 64 * c, ic = i < nA ? i : nA - 1;
+            va[c] = *reinterpret_cast<const long*>(q + (size_t)(r0 + ic % 2) * K + 8 * (ic / 2));
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < PE; c++) {
+            const uint32_t i = l + 64 * c, ic = i < nE ? i : nE - 1;
+            const size_t bi = (size_t)(r0 + ic % 2) * nbs + ic / 2;
+            vs[c] = s[bi];
+            vu[c] = u[bi];
+            if constexpr (XSUM) {
+                const int4* xp = reinterpret_cast<const int4*>(q + (size_t)(r0 + ic % 2) * K + (size_t)KBS * (ic / 2));
+#pragma unroll
+                for (uint32_t t = 0; t < NX; t++) vq[c][t] = xp[t];
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint32_t P, uint32_t K, long* As_c, float* Sc_c, uint32_t l) {
+        constexpr uint32_t SC = XSUM ? 4 : 2;
+        const uint32_t nA = 2 * (K / 8), nE = 2 * (K / KBS);
+#pragma unroll
+        for (uint32_t c = 0; c < PA; c++) {
+            const uint32_t i = l + 64 * c;
+            if (i < nA) As_c[i] = i % 2 < P ? va[c] : 0;
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < PE; c++) {
+            const uint32_t i = l + 64 * c;
+            if (i >= nE) continue;
+            const bool live = i % 2 < P;
+            float* e = Sc_c + i * SC;
+            e[0] = live ? vs[c] : 0.0f;
+            e[1] = live ? vu[c] : 0.0f;
+            if constexpr (XSUM) {
+                int xs = 0;
+#pragma unroll
+                for (uint32_t t = 0; t < NX; t++) {
+                    xs = sdot4(vq[c][t].x, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].y, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].z, 0x01010101, xs);
+                    xs = sdot4(vq[c][t].w, 0x01010101, xs);
+                }
+                e[2] = live ? __int_as_float(xs) : 0.0f;
+            }
+        }
+    }
+};
+
+// LDS of the fused decode down: nw strips, per wave its activations (As_c, Sc_c), the slots' rows
+__host__ __device__ inline size_t tqd_dc_lds(uint32_t nw, uint32_t row_bytes, uint32_t F, bool u8) {
+    return (size_t)nw * row_bytes + (size_t)nw * (F / 8 * 2 * 8 + F / 16 * 2 * (u8 ? 16 : 8)) + (size_t)nw * 16 * 4;
+}
+
+// Decode down and combine in one launch: grid H / 16, 64 (kcap + 1) threads.  Wave y chains strip
+// blockIdx.x of H for slot y (the routed expert y < ns, the shared expert at y = ns: the routing of
+// the gate/up launch), from a streamed LDS copy; then the strip's 16 outputs are the slots' rows
+// added in slot order from slot 0, shared last (exec.rs:1610-1621), plus out when residual.  This
+// replaces the per-slot rows in yent and the combine launch.
+template <int GK>
+__global__ __launch_bounds__(1024) void tqd_down_combine_kernel(TqmArgs g, float* __restrict__ out, int residual) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool U8 = GK == GK_TQ8;
+    constexpr uint32_t SC = U8 ? 4 : 2;
+    const Workspace& ws = g.ws;
+    const uint32_t tid = threadIdx.x, y = tid / 64, l = tid % 64, nw = blockDim.x / 64, F = ws.F;
+    const uint32_t strip = blockIdx.x, P = g.pair ? 2u : 1u, rb = g.a.row_bytes;
+    const uint32_t ns = ws.n_sel[0], id = ws.ids[y < K_MAX ? y : 0];  // both requested at once
+    uint8_t* my = smem + (size_t)y * rb;
+    const size_t act = (size_t)F / 8 * 2 * 8 + (size_t)F / 16 * 2 * SC * 4;
+    long* As_c = reinterpret_cast<long*>(smem + (size_t)nw * rb + y * act);
+    float* Sc_c = reinterpret_cast<float*>(smem + (size_t)nw * rb + y * act + (size_t)F / 8 * 2 * 8);
+    float* res = reinterpret_cast<float*>(smem + (size_t)nw * (rb + act));
+    if (y <= ns) {  // wave-uniform
+        const uint8_t* src = (y == ns ? g.sha.ptr : g.a.ptr + (size_t)id * g.a.stride) + (size_t)strip * rb;
+        const uint32_t n16 = rb / 16;
+        float acc[4];
+        // the activations' loads, the strip's, the activations stored, then the streamed chain
+        TqdStageW<16, U8, 4, 2> sg;
+        sg.load(ws.actq, ws.acts, ws.actu, 2 * y, F, l);
+        TqdStream<GK, 16, 9> sm;
+        sm.issue(src, n16, l);
+        sg.store(P, F, As_c, Sc_c, l);
+        sm.run(my, n16, F, As_c, Sc_c, l, acc);
+        if (l < 16) res[y * 16 + l] = P == 2 ? acc[0] + acc[1] : acc[0];
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float p = res[tid];
+        for (uint32_t s = 1; s <= ns; s++) p = p + res[s * 16 + tid];
+        float* o = out + (size_t)strip * 16 + tid;
+        *o = residual ? *o + p : p;
+    }
+}
+
+bool tqd_dc_ok(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap) {
+    const uint32_t F = ws.F, rb = down.row_bytes;
+    auto al = [](const Mat& m) {
+        return ((uintptr_t)m.ptr % 16 == 0) && m.stride % 16 == 0 && m.row_bytes % 16 == 0 && m.tile_stride == 0;
+    };
+    return tq_kb(down.fmt) == 16 && ws.tiles == 1 && al(down) && al(sh_down) && rb == sh_down.row_bytes &&
+           (rb / 16 + 63) / 64 == 9 && TqdStageW<16, false, 4, 2>::fits(F) && kcap + 1 <= 16 && ws.H % 16 == 0 &&
+           tqd_dc_lds(kcap + 1, rb, F, tq_bits(down.fmt) == 8) <= TQD_LDS_MAX;
+}
+
+hipError_t launch_tqd_down_combine(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap, int pair,
+                                   float* out, int residual, hipStream_t st) {
+    if (!tqd_dc_ok(down, sh_down, ws, kcap)) return hipErrorInvalidValue;
+    const TqmArgs a{down, down, sh_down, sh_down, ws, 1, pair, nullptr, 0, Policy{}};
+    const uint32_t nw = kcap + 1;
+    const size_t lds = tqd_dc_lds(nw, down.row_bytes, ws.F, tq_bits(down.fmt) == 8);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        kern<<<ws.H / 16, 64 * nw, lds, st>>>(a, out, residual);
+        return hipGetLastError();
+    };
+    switch (tq_bits(down.fmt)) {
+        case 4: return go(tqd_down_combine_kernel<GK_TQ4>);
+        case 5: return go(tqd_down_combine_kernel<GK_TQ5>);
+        case 8: return go(tqd_down_combine_kernel<GK_TQ8>);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 // The LDS decode kernels' shape conditions: 16-byte aligned strips and LDS within the limit.
 static bool tqd_ok(const Mat& a, const Mat& b, const Mat& sa, const Mat& sb, size_t lds) {
     auto al = [](const Mat& m) {

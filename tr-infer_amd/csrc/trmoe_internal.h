@@ -190,6 +190,11 @@ hipError_t launch_tile_reduce(const float* plog, uint32_t m, uint32_t E, uint32_
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
                              uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
                              hipStream_t st);
+// decode down and combine in one launch (k_tqm.hip) where the shape allows (tqd_dc_ok): out (+)= the
+// slots' down rows in slot order, no per-slot rows in yent
+bool tqd_dc_ok(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap);
+hipError_t launch_tqd_down_combine(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap, int pair,
+                                   float* out, int residual, hipStream_t st);
 hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                            hipStream_t st);
 inline bool tqm_fits(uint32_t H, uint32_t F) {
