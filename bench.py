@@ -70,6 +70,9 @@ def main():
     ap.add_argument("--stream-rows", type=int, default=None, metavar="ROWS",
                     help="batch items of at most ROWS rows on the streaming GEMV (-1 the library's choice, "
                          "0 all on the MFMA tiles)")
+    ap.add_argument("--decode-rows", type=int, default=None, metavar="ROWS",
+                    help="batches of 2..ROWS tokens as per-token decode units (0 never; default: the "
+                         "library's, 8)")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
                     help="finish with three device copies of MIB MiB (a known-size kernel for calibrating "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -102,6 +105,8 @@ def main():
         ctx.set_fusion(args.fusion)
     if args.stream_rows is not None:
         ctx.set_stream_rows(args.stream_rows)
+    if args.decode_rows is not None:
+        ctx.set_decode_rows(args.decode_rows)
     xs = {M: trmoe.gen_normal(1, (9 << 32) | M, M * H, 1.0, device=dev).view(M, H) for M in ms_list}
     out = torch.empty((m_max, H), dtype=torch.float32, device=dev)
 

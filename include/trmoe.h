@@ -279,6 +279,13 @@ int trk_set_fusion(trk_ctx *ctx, int on);
  * counterpart in the reference, which runs one grouped kernel per expert matrix. */
 int trk_set_stream_rows(trk_ctx *ctx, int rows);
 
+/* 2 <= M <= rows (default 8, 0..16) on GGUF layers: every token runs as a decode (its routing inside
+ * its gate/up workgroups, its rows added by the down launch in the batch combine's order: shared
+ * expert first, then ascending expert), three launches with no dispatch, grouped items or
+ * combine.  The same bits as the grouped path (exec_batch.rs:1404-1580); the dispatch arrays
+ * (TRK_WS_ENT_*, items) are then not written.  No counterpart in the reference. */
+int trk_set_decode_rows(trk_ctx *ctx, int rows);
+
 /* Layers on TQ experts: the int8 MFMA kernels (on, the default, where H / 32 units of staged
  * activations fit a workgroup's LDS) or the generic grouped TQ GEMV (off).  Both give the same
  * bits; no counterpart in the reference. */

@@ -158,6 +158,7 @@ def test_batch_layer_and_dispatch(shape, M, k):
     say(f"batch layer {shape} M={M} k={k}")
     L, orc, W = layer(shape, **{"small": SMALL, "full": FULL, "odd": ODD}[shape])
     ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))
+    ctx.set_decode_rows(0)  # the grouped path, which writes the dispatch arrays
     import torch
     x = L.x(M, tid=200 + M)
     r = orc.moe_batch(x, k=k, router_dot_max_m=16)
@@ -207,6 +208,7 @@ def test_stream_items_match_mfma_tiles(shape, M, k):
     for rows in (0, 1, 4, 16, -1):
         ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M))
         ctx.set_stream_rows(rows)
+        ctx.set_decode_rows(0)
         out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
         ctx.forward(W, dev(x), out)
         outs[rows] = host(out).copy()
@@ -216,6 +218,40 @@ def test_stream_items_match_mfma_tiles(shape, M, k):
         ctx.close()
     for rows, o in outs.items():
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"rows={rows}"
+
+
+@pytest.mark.parametrize("shape,M,k,policy", [("small", 2, 4, None), ("small", 3, 4, (1, 4, 0.9, O.BASIS_TOP)),
+                                              ("full", 4, 10, None), ("full", 4, 10, (2, 10, 0.8, O.BASIS_ALL)),
+                                              ("full", 16, 10, None), ("odd", 9, 5, None), ("wide", 5, 6, None)])
+def test_decode_rows_match_grouped(shape, M, k, policy):
+    """Batches run as per-token decode units (trk_set_decode_rows) give the grouped path's bits
+    (the batch combine's order: shared expert first, then ascending expert), match the oracle's
+    moe_batch, publish the same routing and count the same MoeStats."""
+    say(f"decode rows {shape} M={M} k={k} policy={policy}")
+    L, orc, W = layer(shape, **{"small": SMALL, "full": FULL, "odd": ODD, "wide": WIDE}[shape])
+    import torch
+    x = L.x(M, tid=270 + M)
+    kcap = policy[1] if policy else k
+    r = orc.moe_batch(x, k=k, router_dot_max_m=16, policy=policy)
+    outs, routing = [], []
+    for rows in (0, 16):
+        ctx = trmoe.Context(L.H, L.E, L.F, k, max(64, M), k_cap=kcap)
+        if policy:
+            ctx.set_moe(policy)
+        ctx.set_decode_rows(rows)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        outs.append(host(out).copy())
+        nsel = ctx.read(trmoe.WS_NSEL, 4 * M, np.uint32)
+        ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+        routing.append([(ids[t, :nsel[t]].copy(), w[t, :nsel[t]].copy()) for t in range(M)])
+        assert ctx.stats() == (M, int(nsel.sum()))
+        ctx.close()
+    assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), f"{shape} M={M}: bits differ"
+    for (i0, w0), (i1, w1) in zip(routing[0], routing[1]):
+        assert np.array_equal(i0, i1) and np.array_equal(w0.view(np.uint32), w1.view(np.uint32))
+    compare_out(outs[1], r["out"], False, f"decode rows {shape} M={M}")
 
 
 def test_decode_odd_superblocks():

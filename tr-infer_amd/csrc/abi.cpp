@@ -82,6 +82,7 @@ struct trk_ctx {
     int stream_rows = -1;  // batch: items of at most this many rows on the streaming GEMV (-1: automatic)
     int tq_mfma = 1;       // TQ layers: the MFMA kernels where the shape fits (0: the generic TQ GEMV)
     int profile = 0;       // MoeStats::profile: add every routed row's mass profile to ws.prof
+    int decode_rows = 8;   // batch: up to this many tokens run as per-token decode units (0: never)
 };
 
 extern "C" const char* trk_last_error(void) { return g_err; }
@@ -481,6 +482,19 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
                                                  ws.shl, st, &xq, norm));
         TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, pair, kcap, st));
         TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, pair, kcap, out, residual, st));
+    } else if (m <= (uint32_t)c->decode_rows && ws.tiles == 1) {
+        // a few tokens: each one a decode (routing inside its gate/up units, its rows added by the
+        // down in the batch combine's order), so no routing, dispatch or combine launch and no
+        // grouped items; the logits and quantised x exactly as for a batch
+        const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, 0};
+        if (rlog)
+            TIMED(K_LOGITS, launch_router_logits(nullptr, nullptr, w->shexp_gate, x, m, 0, H, 0, nullptr, ws.shl, st,
+                                                 &xq, norm));
+        else
+            TIMED(K_LOGITS, launch_router_logits(w->router, w->router_bias, w->shexp_gate, x, m, E, H, gemm_order,
+                                                 ws.rlog, ws.shl, st, &xq, norm));
+        TIMED(K_DEC_GATEUP, launch_decode_gateup(M.gate, M.up, M.shg, M.shu, x, lg, ws, k, c->pol, 0, kcap, st, m));
+        TIMED(K_DEC_DOWN, launch_decode_down(M.down, M.shd, ws, 0, kcap, out, residual, st, m));
     } else {
         // the logits launch also quantises x (single level, per 32) for the grouped kernels
         const XQuant xq{ws.xq, ws.xs, ws.xsum, ws.xu, 0};
@@ -692,6 +706,13 @@ extern "C" int trk_set_stream_rows(trk_ctx* c, int rows) {
     if (!c) return fail(TRK_E_INVALID, "null context");
     if (rows < -1 || rows > (int)BR) return fail(TRK_E_INVALID, "stream rows (%d) must be in -1..%u", rows, BR);
     c->stream_rows = rows;
+    return TRK_OK;
+}
+
+extern "C" int trk_set_decode_rows(trk_ctx* c, int rows) {
+    if (!c) return fail(TRK_E_INVALID, "null context");
+    if (rows < 0 || rows > 16) return fail(TRK_E_INVALID, "decode rows (%d) must be in 0..16", rows);
+    c->decode_rows = rows;
     return TRK_OK;
 }
 

@@ -13,6 +13,11 @@
 //            row's superblocks, forms the per-16 block dots against the staged activations and
 //            runs the chain in registers; slot 0 is stored and later slots (routing order,
 //            shared last) are added — tasks C with the combine fused.
+//   a few tokens (2 <= M <= 16): both launches take a token dimension (each token its own
+//            routing, x row and activation slots, exactly a decode's), and the down adds a token's
+//            rows in the batch combine's order (shared first, then ascending expert:
+//            exec_batch.rs:1539-1578), so the grouped path's bits come out with no dispatch,
+//            grouped items or combine launch.
 #include "gemv.hpp"
 #include "route.hpp"
 #include "router.hpp"
@@ -291,7 +296,7 @@ __device__ __forceinline__ void gateup_unit(const Mat& gate, const Mat& up, cons
         const float u = P == 2 ? hres[(16 + tid) * P] + hres[(16 + tid) * P + 1] : hres[(16 + tid) * P];
         const float av = silu512(g) * u;
         if (shared) wgt = sigmoid_libm(shl);  // exec.rs:1606
-        const uint32_t aslot = shared ? (uint32_t)SH_SLOT : slot;
+        const uint32_t aslot = shared ? kcap : slot;
         const uint32_t nbf = F / 16;
         int8_t* dq = ws.actq + (size_t)aslot * P * F + strip * 16;
         float* ds = ws.acts + (size_t)aslot * P * nbf + strip;
@@ -342,23 +347,49 @@ struct NoPre {
     __device__ void operator()() const {}
 };
 
+// Token t's view of the workspace for a batch run as per-token decode units (P = 1): its x row,
+// shared-gate logit, routing row and (kcap + 1) activation slots.  t = 0 is the decode layout.
+__device__ __forceinline__ Workspace ws_token(const Workspace& ws, uint32_t t, uint32_t kcap, uint32_t P) {
+    Workspace w = ws;
+    const uint32_t nb = ws.H / 32, nbf = ws.F / 16;
+    const size_t ar = (size_t)t * (kcap + 1) * P;
+    w.xq += (size_t)t * ws.H;
+    w.xs += (size_t)t * nb;
+    w.xsum += (size_t)t * nb;
+    w.xu += (size_t)t * nb;
+    w.shl += t;
+    w.ids += (size_t)t * K_MAX;
+    w.w += (size_t)t * K_MAX;
+    w.n_sel += t;
+    w.actq += ar * ws.F;
+    w.acts += ar * nbf;
+    w.actsum += ar * nbf;
+    w.actu += ar * nbf;
+    return w;
+}
+
+// Grid (F / 16 strips, kcap + 1 slots, tokens): token blockIdx.z's unit (slot, strip).
 template <int P, int NSB, int NJ>
 __global__ __launch_bounds__(GU_THREADS(NSB)) void decode_gateup_kernel(
         Mat gate, Mat up, Mat shg, Mat shu, const float* __restrict__ x, const float* __restrict__ lg, Workspace ws,
         uint32_t k, Policy pol, uint32_t kcap) {
     extern __shared__ __align__(16) uint8_t smem[];
-    gateup_unit<P, NSB, NJ, false, true>(gate, up, shg, shu, x, lg, ws, k, pol, kcap, blockIdx.y, blockIdx.x, true, false,
-                            blockIdx.x == 0 && blockIdx.y == 0, smem, smem + gu_lds_x<P, NSB>(), NoPre{}, NoHook{});
+    const uint32_t t = blockIdx.z;
+    const Workspace wt = ws_token(ws, t, kcap, P);
+    gateup_unit<P, NSB, NJ, false, true>(gate, up, shg, shu, x + (size_t)t * ws.H, lg + (size_t)t * ws.E, wt, k, pol,
+                                         kcap, blockIdx.y, blockIdx.x, true, false, blockIdx.x == 0 && blockIdx.y == 0,
+                                         smem, smem + gu_lds_x<P, NSB>(), NoPre{}, NoHook{});
 }
 
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
                                 const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
-                                hipStream_t st) {
+                                hipStream_t st, uint32_t m) {
+    if (m > 1 && pair) return hipErrorInvalidValue;  // a batch's activations are single-level
     const uint32_t H = gate.k, F = gate.rows, nb = H / 32, nsb = H / 256;
     const int P = pair ? 2 : 1;
     size_t lds = (size_t)P * nsb * 272 + (size_t)P * nb * 8 + 32 * P * 4 + ROUTE_LDS;
     if (pol.enabled && pol.basis == TRK_BASIS_ALL) lds += (size_t)ws.E * 4;
-    const dim3 g(F / 16, kcap + 1);
+    const dim3 g(F / 16, kcap + 1, m);
     const uint32_t threads = GU_THREADS(nsb);
     const bool nj16 = route_nj(ws.E) == 16;
     switch ((nsb * 2 + (pair ? 1 : 0)) * 2 + (nj16 ? 1 : 0)) {
@@ -458,7 +489,7 @@ __device__ __forceinline__ void down_stage_load(const Workspace& ws, uint32_t kc
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const uint32_t i = i0 + tid + 256 * c, ic = i < nq ? i : nq - 1;
-        const uint32_t s = ic / QP, a = s < kcap ? s : (uint32_t)SH_SLOT;
+        const uint32_t a = ic / QP;  // slot (the shared expert's at kcap)
         const int4* src = reinterpret_cast<const int4*>(ws.actq + (size_t)a * P * F) + ic % QP;
         const size_t o = (size_t)a * QP + ic % QP;
         if constexpr (COH) {
@@ -496,7 +527,10 @@ __device__ __forceinline__ void down_stage_store(uint8_t* smem, uint32_t kcap, u
 
 // PRE: st holds the first staging round, already requested (the standalone kernel requests it ahead
 // of the weights, so the activations' round trip overlaps the weights'); otherwise requested here
-template <int P, int NSB, bool COH, bool PRE>
+// BORDER: the batch combine's order (exec_batch.rs:1539-1578: the shared expert's row first, then
+// the token's entries by ascending expert) instead of the decode's (slots in routing order, the
+// shared expert last).
+template <int P, int NSB, bool COH, bool PRE, bool BORDER = false>
 __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const Workspace& ws, uint32_t kcap,
                                           uint32_t n, const uint32_t* ids, float* __restrict__ out, int residual,
                                           uint32_t row0, uint8_t* smem, const DownFirst& first, DownStage& st) {
@@ -575,32 +609,51 @@ __device__ __forceinline__ void down_unit(const Mat& down, const Mat& shd, const
         if (live && q == (uint32_t)DL::L - 1)
             vres[s * DN_R + u % DN_R] = P == 2 ? acc[0] + acc[1] : acc[0];  // gemv.rs:154
     }
+    uint32_t* perm = reinterpret_cast<uint32_t*>(vres + slots * DN_R);  // [32] BORDER: slots by expert
+    if constexpr (BORDER) {
+        if (tid < n) {  // the token's experts are distinct: rank = how many are smaller
+            const uint32_t e = ids[tid];
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < n; j++) rank += ids[j] < e ? 1u : 0u;
+            perm[rank] = tid;
+        }
+    }
     __syncthreads();
     if (tid < DN_R) {
-        // slot 0 stores, later slots accumulate, the shared expert last (gemv.rs:150-160 with
-        // accumulate = slot > 0; exec.rs:1607-1620)
-        float y = n > 0 ? vres[tid] : vres[kcap * DN_R + tid];
-        for (uint32_t s = 1; s < n; s++) y = y + vres[s * DN_R + tid];
-        if (n > 0) y = y + vres[kcap * DN_R + tid];
+        float y;
+        if constexpr (BORDER) {
+            y = vres[kcap * DN_R + tid];
+            for (uint32_t j = 0; j < n; j++) y = y + vres[perm[j] * DN_R + tid];
+        } else {
+            // slot 0 stores, later slots accumulate, the shared expert last (gemv.rs:150-160 with
+            // accumulate = slot > 0; exec.rs:1607-1620)
+            y = n > 0 ? vres[tid] : vres[kcap * DN_R + tid];
+            for (uint32_t s = 1; s < n; s++) y = y + vres[s * DN_R + tid];
+            if (n > 0) y = y + vres[kcap * DN_R + tid];
+        }
         float* o = out + row0 + tid;
         *o = residual ? *o + y : y;
     }
 }
 
-template <int P, int NSB, int Q4>
+// Grid (H / DN_R, tokens): token blockIdx.y's output rows; BORDER for a batch (the batch combine's
+// order), the decode's order otherwise.
+template <int P, int NSB, int Q4, bool BORDER>
 __global__ __launch_bounds__(256) void decode_down_kernel(Mat down, Mat shd, Workspace ws, uint32_t kcap,
                                                          float* __restrict__ out, int residual) {
     extern __shared__ __align__(16) uint8_t smem[];
+    const Workspace wt = ws_token(ws, blockIdx.y, kcap, P);
+    out += (size_t)blockIdx.y * ws.H;
     // the count and the first unit's expert id are requested together (slots below kcap are inside
     // the id row; a slot past the count is never used), then the activations, whose round trip runs
     // beside the weights' once the id is in
-    const uint32_t row0 = blockIdx.x * DN_R, n = ws.n_sel[0], eid0 = down_first_id<NSB>(ws.ids, kcap);
+    const uint32_t row0 = blockIdx.x * DN_R, n = wt.n_sel[0], eid0 = down_first_id<NSB>(wt.ids, kcap);
     DownStage st;
-    down_stage_load<P, NSB, false>(ws, kcap, 0, st);
+    down_stage_load<P, NSB, false>(wt, kcap, 0, st);
     __builtin_amdgcn_sched_barrier(0);  // keep those requests ahead of the weights'
     DownFirst first;
     down_first<NSB, Q4>(down, shd, kcap, n, eid0, row0, first);
-    down_unit<P, NSB, false, true>(down, shd, ws, kcap, n, ws.ids, out, residual, row0, smem, first, st);
+    down_unit<P, NSB, false, true, BORDER>(down, shd, wt, kcap, n, wt.ids, out, residual, row0, smem, first, st);
 }
 
 // ---- the whole decode layer in one launch ----------------------------------------------------
@@ -785,16 +838,22 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
 }
 
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair, uint32_t kcap,
-                              float* out, int residual, hipStream_t st) {
+                              float* out, int residual, hipStream_t st, uint32_t m) {
     const uint32_t H = down.rows, F = down.k, nbf = F / 16;
     const int P = pair ? 2 : 1;
+    if (m > 1 && pair) return hipErrorInvalidValue;  // a batch's activations are single-level
     const size_t slots = kcap + 1;
-    const size_t lds = slots * ((size_t)P * F + 16) + slots * P * nbf * 8 + slots * DN_R * 4 + 64;
+    const size_t lds = slots * ((size_t)P * F + 16) + slots * P * nbf * 8 + slots * DN_R * 4 + K_MAX * 4 + 64;
     const bool q4 = down.fmt == TRK_FMT_Q4_K;
+    const dim3 grid(H / DN_R, m);
     switch ((F / 256 * 2 + (pair ? 1 : 0)) * 2 + (q4 ? 1 : 0)) {
 #define DN_CASE2(ns, p, q)                                                                                          \
     case (ns * 2 + p - 1) * 2 + q:                                                                                  \
-        decode_down_kernel<p, ns, q><<<H / DN_R, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual); break;
+        if (m > 1)                                                                                                  \
+            decode_down_kernel<p, ns, q, true><<<grid, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual);     \
+        else                                                                                                        \
+            decode_down_kernel<p, ns, q, false><<<grid, 256, lds, st>>>(down, sh_down, ws, kcap, out, residual);    \
+        break;
 #define DN_CASE(ns) DN_CASE2(ns, 1, 0) DN_CASE2(ns, 1, 1) DN_CASE2(ns, 2, 0) DN_CASE2(ns, 2, 1)
         DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7) DN_CASE(8)
 #undef DN_CASE

@@ -11,7 +11,6 @@
 namespace trk {
 
 constexpr int K_MAX = TRK_MOE_K_MAX;
-constexpr int SH_SLOT = K_MAX;  // decode: the shared expert's activation slot (after 32 routed)
 
 // Routing policy as the kernels take it (enabled == 0: fixed top-k).  packed: n_expert_packed of a
 // subset pack, the routed ids are folded onto experts 0 .. packed - 1 (fold_ids); 0: no folding.
@@ -98,7 +97,7 @@ struct Workspace {
     Item* items;          // [item_cap]
     uint32_t* pairs;      // [item_cap / 2 + 1]: first item of each pair (parts 2j, 2j + 1 of one expert)
     uint32_t* single;     // [item_cap]: the items in no pair (an expert's last when its count is odd)
-    int8_t* actq;         // [act_rows][F] (decode: [33][2][F])
+    int8_t* actq;         // [act_rows][F] (decode: [kcap + 1][P][F], the shared expert's slot last)
     float* acts;          // [act_rows][F/16]
     int32_t* actsum;
     float* actu;          // [act_rows][F/16]: folded scale * (float)sum
@@ -140,7 +139,7 @@ hipError_t launch_route(const float* logits, uint32_t m, uint32_t E, uint32_t k,
                         float* w, uint32_t* n_sel, unsigned long long* stats, hipStream_t st);
 hipError_t launch_decode_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const float* x,
                                 const float* lg, const Workspace& ws, uint32_t k, Policy pol, int pair, uint32_t kcap,
-                                hipStream_t st);
+                                hipStream_t st, uint32_t m = 1);
 hipError_t launch_decode_layer(const float* router, const float* bias, const float* shexp_gate, const Mat& gate,
                                const Mat& up, const Mat& down, const Mat& sh_gate, const Mat& sh_up,
                                const Mat& sh_down, const float* x, const float* rlog, const Workspace& ws, uint32_t k,
@@ -148,8 +147,10 @@ hipError_t launch_decode_layer(const float* router, const float* bias, const flo
                                hipStream_t st);
 bool decode_layer_supported(const Mat& gate, const Mat& down, const Mat& sh_down, uint32_t E, int pair,
                             uint32_t kcap);
+// m >= 2 (pair = 0): m tokens as per-token decode units, each token's rows added in the batch
+// combine's order; the routing, x rows and activation slots of token t at t times the decode's
 hipError_t launch_decode_down(const Mat& down, const Mat& sh_down, const Workspace& ws, int pair,
-                              uint32_t kcap, float* out, int residual, hipStream_t st);
+                              uint32_t kcap, float* out, int residual, hipStream_t st, uint32_t m = 1);
 hipError_t launch_dispatch(const Workspace& ws, uint32_t m, uint32_t kcap, hipStream_t st);
 // m <= 16 (m * kcap <= 1024): the same dispatch in one launch with the routing (lg != null) or
 // from ws.ids / w / n_sel (lg == null)

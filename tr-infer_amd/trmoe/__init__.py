@@ -98,6 +98,7 @@ def lib() -> C.CDLL:
         L.trk_set_timing.argtypes = [vp, i]
         L.trk_set_fusion.argtypes = [vp, i]
         L.trk_set_stream_rows.argtypes = [vp, i]
+        L.trk_set_decode_rows.argtypes = [vp, i]
         L.trk_set_tq_mfma.argtypes = [vp, i]
         L.trk_get_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_uint64), i]
         _lib = L
@@ -223,6 +224,10 @@ class Context:
     def set_stream_rows(self, rows: int):
         """Batch items of at most `rows` rows on the streaming GEMV (-1 automatic, 0 none)."""
         check(lib().trk_set_stream_rows(self.h, int(rows)))
+
+    def set_decode_rows(self, rows: int):
+        """GGUF batches of 2..rows tokens as per-token decode units (0 never, default 8)."""
+        check(lib().trk_set_decode_rows(self.h, int(rows)))
 
     def set_timing(self, on: bool):
         check(lib().trk_set_timing(self.h, int(on)))
