@@ -215,8 +215,10 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs g) {
     // phase-1 units: GGUF: (row, unit column), the columns of a row on consecutive lanes (NCOL
     // columns, NRG rows at a time); TQ: (strip, block), one per 16-lane group (NSTR strips)
     constexpr uint32_t NCOL = TQ ? 16 : (R == 16 ? 16 : 4), NRG = 256 / NCOL, NSTR = R / 16;
-    // units whose loads a thread issues together: about 48 registers of weights
-    constexpr uint32_t UW = sizeof(GvW<GK, KB>) / 4, UB = UW * 8 <= 48 ? 8 : (48 / UW > 2 ? 48 / UW : 2);
+    // units whose loads a thread issues together: about 48 registers of weights, 24 for TQ strips
+    // (two units: more waves per SIMD beat more loads per wave, e.g. the LM head 165 -> 148 us)
+    constexpr uint32_t UW = sizeof(GvW<GK, KB>) / 4, UREG = TQ ? 24 : 48;
+    constexpr uint32_t UB = UW * 8 <= UREG ? 8 : (UREG / UW > 2 ? UREG / UW : 2);
     constexpr bool XSUM = GK == GK_Q80 || GK == GK_TQ8;
     __shared__ __align__(16) int8_t xq[NA][S * KB];
     __shared__ __align__(16) float4 xs[NA][S];  // sx, u = sx * sum, byte sum (int bits), -
