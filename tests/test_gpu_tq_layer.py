@@ -15,7 +15,7 @@ import pytest
 import oracle as O
 import trmoe
 from layerdata import TQLayer
-from test_gpu_layer import compare_out, dev, host, routing_exact, say
+from test_gpu_layer import compare_out, dev, host, routing_exact, say, shared_gate_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -47,10 +47,14 @@ def reference(orc, x, k, policy=None, hiprec=True):
         cpu.close()
         lg = orc.logits(x, False)
         w = np.zeros((M, 32), np.float32)
+        ids = np.zeros((M, 32), np.uint32)
+        n_sel = np.zeros(M, np.uint32)
         for t in range(M):
-            _, wt = O.route_mass(lg[t], *policy) if policy else O.route_topk(lg[t], k)
+            it, wt = O.route_mass(lg[t], *policy) if policy else O.route_topk(lg[t], k)
             w[t, :len(wt)] = wt
-        return {"w": w}, got["out"]
+            ids[t, :len(it)] = it
+            n_sel[t] = len(wt)
+        return {"w": w, "ids": ids, "n_sel": n_sel}, got["out"]
     r = orc.moe_batch(x, k=k, policy=policy)
     return r, r["out"]
 
@@ -74,12 +78,31 @@ def run_case(L, orc, W, M, k, hiprec=True, policy=None, tid=0, mfma=None):
         ctx.set_timing(False)
         assert "tq_gateup" in launched and ("tq_act" not in launched) == mfma, launched
     got = host(out).copy()
-    exact = routing_exact(ctx, r, M, policy[1] if policy else k, L, x) if not policy else False
+    exact = routing_exact(ctx, r, M, k, L, x) if not policy else policy_exact(ctx, r, M, L, x)
     # MoeStats: rows and selected experts, counted by whichever launch routed
     nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
     assert ctx.stats() == (M, int(nsel.sum()))
     ctx.close()
     return got, want, exact
+
+
+def policy_exact(ctx, r, M, L, x):
+    """Cumulative-mass routing: every token's count and ids equal the oracle's (asserted); True
+    when the weights and the shared gate also agree bit for bit, so the outputs must too."""
+    nsel = ctx.read(trmoe.WS_NSEL, M * 4, np.uint32)
+    ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+    w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+    if M == 1:
+        want_n, want_ids, want_w = [r["k"]], [np.asarray(r["ids"])], [np.asarray(r["w"])]
+    else:
+        want_n, want_ids, want_w = r["n_sel"], r["ids"], r["w"]
+    same = True
+    for t in range(M):
+        n = int(want_n[t])
+        assert nsel[t] == n, (t, nsel[t], n)
+        assert np.array_equal(ids[t, :n], np.asarray(want_ids[t])[:n]), t
+        same = same and np.array_equal(w[t, :n], np.asarray(want_w[t])[:n])
+    return same and shared_gate_exact(L, x)
 
 
 @pytest.mark.parametrize("M,hiprec", [(1, True), (1, False), (3, True), (16, True), (64, True)])
@@ -110,8 +133,9 @@ def test_tq_layer_dynamic_k(M):
     say(f"tq layer dynamic k M={M}")
     L, orc, W = tq_layer("real", **REAL)
     pol = (1, 10, 0.9, O.BASIS_TOP)
-    got, want, _ = run_case(L, orc, W, M, 8, policy=pol, tid=200 + M)
-    compare_out(got, want, False, f"tq dynamic-k M={M}")
+    got, want, exact = run_case(L, orc, W, M, 8, policy=pol, tid=200 + M)
+    say(f"tq dynamic-k M={M}: routing weights and shared gate bit-identical: {exact}")
+    compare_out(got, want, exact, f"tq dynamic-k M={M}")
 
 
 def test_tq_weights_rejected_when_mixed():
