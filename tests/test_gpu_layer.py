@@ -318,7 +318,8 @@ def routing_exact(ctx, r, M, k, L, x):
 def test_q6k_down(M, F):
     """Q6_K downs (unsigned 6-bit q, dd = f16(d sc), mm = f16(-32 dd)) on every down kernel: the
     decode path (M = 1), and for batches every split between the streaming GEMV and the MFMA tiles
-    gives the same bits, identical to the oracle's TQ8_16 path where the routing weights agree."""
+    and the per-token path (M = 6) give the same bits, identical to the oracle's TQ8_16 path where
+    the routing weights agree."""
     say(f"q6k down M={M} F={F}")
     L, orc, W = layer(f"q6F{F}", seed=4, H=512, E=16, F=F, down_fmt=O.FMT_Q6_K)
     import torch
@@ -326,9 +327,13 @@ def test_q6k_down(M, F):
     r = orc.moe_block(x[0], k=3) if M == 1 else orc.moe_batch(x, k=3)
     want = r["out"][None] if M == 1 else r["out"]
     outs = []
-    for rows in ((-1,) if M == 1 else (0, 1, 4, 16, -1)):
+    # batches: every stream / MFMA split of the grouped path, then (None) the default, which runs
+    # each token as a decode up to 8 tokens
+    for rows in ((-1,) if M == 1 else (0, 1, 4, 16, -1, None)):
         ctx = trmoe.Context(L.H, L.E, L.F, 3, max(64, M))
-        ctx.set_stream_rows(rows)
+        if rows is not None:
+            ctx.set_stream_rows(rows)
+            ctx.set_decode_rows(0)
         out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
         ctx.forward(W, dev(x), out)
         outs.append(host(out).copy())
@@ -344,8 +349,8 @@ def test_q6k_down(M, F):
 def test_q80_q51_down(fmt, M, F):
     """Q8_0 and Q5_1 downs (the reference's q8_0_rows / q5_1_rows forms: q = int8 + 128 with
     m = f16(-128 d); 5-bit q with d, m as stored) on every down kernel: the decode path (M = 1),
-    and for batches every split between the streaming GEMV and the MFMA tiles gives the same
-    bits, within tolerance of the oracle's TQ8_16 / TQ5_16 GEMV."""
+    and for batches every split between the streaming GEMV and the MFMA tiles and the per-token
+    path (M = 6) give the same bits, within tolerance of the oracle's TQ8_16 / TQ5_16 GEMV."""
     say(f"down fmt={fmt} M={M} F={F}")
     L, orc, W = layer(f"dfmt{fmt}F{F}", seed=6, H=512, E=16, F=F, down_fmt=fmt)
     import torch
@@ -353,9 +358,11 @@ def test_q80_q51_down(fmt, M, F):
     r = orc.moe_block(x[0], k=3) if M == 1 else orc.moe_batch(x, k=3)
     want = r["out"][None] if M == 1 else r["out"]
     outs = []
-    for rows in ((-1,) if M == 1 else (0, 16, -1)):
+    for rows in ((-1,) if M == 1 else (0, 16, -1, None)):
         ctx = trmoe.Context(L.H, L.E, L.F, 3, max(64, M))
-        ctx.set_stream_rows(rows)
+        if rows is not None:
+            ctx.set_stream_rows(rows)
+            ctx.set_decode_rows(0)
         out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
         ctx.forward(W, dev(x), out)
         outs.append(host(out).copy())
