@@ -138,6 +138,46 @@ def test_tq_layer_dynamic_k(M):
     compare_out(got, want, exact, f"tq dynamic-k M={M}")
 
 
+@pytest.mark.parametrize("M,policy", [(2, None), (3, (1, 8, 0.9, O.BASIS_TOP)), (8, None),
+                                      (5, (2, 8, 0.8, O.BASIS_ALL))])
+def test_tq_decode_rows_match_grouped(M, policy):
+    """A batch of a few tokens run as per-token decodes (trk_set_decode_rows: each token's routing
+    inside the gate/up launch, its rows added by the down + combine launch in the batch combine's
+    order) gives the grouped path's bits, publishes the same routing and counts the same MoeStats;
+    both against the oracle's moe_batch."""
+    say(f"tq decode rows M={M} policy={policy}")
+    L, orc, W = tq_layer("real", **REAL)
+    import torch
+    x = L.x(M, tid=260 + M)
+    k = 8
+    r, want = reference(orc, x, k, policy)
+    outs, routing, launched = [], [], []
+    for rows in (0, 8):
+        ctx = trmoe.Context(L.H, L.E, L.F, k, M, k_cap=policy[1] if policy else 0)
+        if policy:
+            ctx.set_moe(policy)
+        ctx.set_decode_rows(rows)
+        ctx.set_timing(True)
+        out = torch.empty((M, L.H), dtype=torch.float32, device="cuda")
+        ctx.forward(W, dev(x), out)
+        launched.append(set(ctx.timing()))
+        ctx.set_timing(False)
+        outs.append(host(out).copy())
+        nsel = ctx.read(trmoe.WS_NSEL, 4 * M, np.uint32)
+        ids = ctx.read(trmoe.WS_IDS, M * 32 * 4, np.uint32).reshape(M, 32)
+        w = ctx.read(trmoe.WS_W, M * 32 * 4, np.float32).reshape(M, 32)
+        routing.append([(ids[t, :nsel[t]].copy(), w[t, :nsel[t]].copy()) for t in range(M)])
+        assert ctx.stats() == (M, int(nsel.sum()))
+        exact = policy_exact(ctx, r, M, L, x) if policy else routing_exact(ctx, r, M, k, L, x)
+        ctx.close()
+    assert "dispatch" in launched[0] and "dispatch" not in launched[1], launched  # the path asked for ran
+    assert np.array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32)), f"M={M}: bits differ"
+    for (i0, w0), (i1, w1) in zip(routing[0], routing[1]):
+        assert np.array_equal(i0, i1) and np.array_equal(w0.view(np.uint32), w1.view(np.uint32))
+    say(f"tq decode rows M={M}: routing weights and shared gate bit-identical: {exact}")
+    compare_out(outs[1], want, exact, f"tq decode rows M={M}")
+
+
 def test_tq_weights_rejected_when_mixed():
     """One gate/up codec and one down codec per layer, TQ and GGUF not mixed; gate/up must be
     kb 32 and down kb 16 (the activations' block sizes)."""

@@ -421,6 +421,15 @@ static int forward(trk_ctx* c, const trk_moe_w* w, const float* x, const float* 
         }
         // tiles: the generic grouped TQ GEMV, which takes each tile's rows and columns
         const bool mfma = c->tq_mfma && tqm_fits(H, ws.F) && T == 1;
+        // a few tokens: each one a decode (routing inside the gate/up launch, its rows added by the
+        // down in the batch combine's order), no routing, dispatch or combine launch
+        if (m >= 2 && m <= (uint32_t)c->decode_rows && mfma && tqd_tokens_fit(ws, m, kcap) &&
+            tqd_gateup_ok(M.gate, M.up, M.shg, M.shu, ws, c->pol) && tqd_dc_ok(M.down, M.shd, ws, kcap)) {
+            TIMED(K_TQ_GATEUP, launch_tqm_gateup(M.gate, M.up, M.shg, M.shu, ws, m, kcap, 0, lg, k, c->pol, st));
+            TIMED(K_TQ_DOWN, launch_tqd_down_combine(M.down, M.shd, ws, kcap, 0, out, residual, st, m));
+            if (c->profile) TIMED(K_PROFILE, launch_mass_profile(lg, m, E, ws.prof, st));
+            return TRK_OK;
+        }
         if (m == 1) {
             // the MFMA gate/up launch routes for itself
             if (!mfma) TIMED(K_ROUTE, launch_route(lg, 1, E, k, c->pol, ws.ids, ws.w, ws.n_sel, ws.stats, st));

@@ -30,11 +30,14 @@ inline uint64_t items_max(uint32_t E, uint32_t m, uint32_t kcap) {
     const uint64_t nonempty = ent < E ? ent : E;
     return nonempty + ent / ITEM_ROWS + (m + ITEM_ROWS - 1) / ITEM_ROWS;
 }
-// activation rows of the down input: one per entry and one per token (shared), and the decode
-// slots (K_MAX routed + the shared one, two levels each)
+// activation rows of the down input: one per entry and one per token (shared), the decode slots
+// (K_MAX routed + the shared one, two levels each), and a TQ batch of up to 16 tokens run as
+// per-token decodes (k_cap + 1 slots of two rows per token)
 inline uint64_t act_rows(const Caps& c) {
     const uint64_t a = ent_cap(c) + c.m_max, d = (uint64_t)(KMAX + 1) * 2;
-    return a > d ? a : d;
+    const uint64_t t = 2ull * (c.m_max < 16 ? c.m_max : 16) * (c.k_cap + 1);
+    const uint64_t ad = a > d ? a : d;
+    return ad > t ? ad : t;
 }
 inline uint64_t yent_rows(const Caps& c) { return ent_cap(c) + c.m_max; }
 // dispatch chunks of 64 tokens, and the per-(chunk, expert) offsets the split dispatch writes

@@ -792,7 +792,29 @@ __host__ __device__ inline TqdLds tqd_lds(bool gu, uint32_t row_bytes, uint32_t 
     return o;
 }
 
-// Decode gate/up: grid (F / 16, kcap + 1), 128 threads; wave 0 the gate strip, wave 1 the up strip
+// Token t's view of the workspace for a batch run as per-token decode units: its x row (single
+// level), shared-gate logit, routing row and kcap + 1 activation slots of two rows each (the
+// decode layout, the second row unused).  t = 0 is the decode layout itself.
+__device__ __forceinline__ Workspace tqd_token(const Workspace& ws, uint32_t t, uint32_t kcap) {
+    Workspace w = ws;
+    const uint32_t nb = ws.H / 32, nbf = ws.F / 16;
+    const size_t ar = (size_t)t * (kcap + 1) * 2;
+    w.xq += (size_t)t * ws.H;
+    w.xs += (size_t)t * nb;
+    w.xsum += (size_t)t * nb;
+    w.xu += (size_t)t * nb;
+    w.shl += t;
+    w.ids += (size_t)t * K_MAX;
+    w.w += (size_t)t * K_MAX;
+    w.n_sel += t;
+    w.actq += ar * ws.F;
+    w.acts += ar * nbf;
+    w.actsum += ar * nbf;
+    w.actu += ar * nbf;
+    return w;
+}
+
+// Decode gate/up: grid (F / 16, kcap + 1, tokens), 128 threads; wave 0 the gate strip, wave 1 the up strip
 // of strip blockIdx.x for slot blockIdx.y.  Wave 0 routes (route_row, router.rs:106-148) while
 // wave 1 stages x; the shared expert's row (slot ns) copies its strips before routing.  Row
 // blockIdx.y = kcap is the shared expert's when ns = kcap (fixed top-k); with fewer selected, the
@@ -801,7 +823,8 @@ template <int GK, int NJ, int SPW>
 __global__ __launch_bounds__(128 * SPW) void tqd_gateup_kernel(TqmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr bool U8 = GK == GK_TQ8;
-    const Workspace& ws = g.ws;
+    const Workspace ws = tqd_token(g.ws, blockIdx.z, gridDim.y - 1);  // token blockIdx.z's
+    const float* lg = g.lg + (size_t)blockIdx.z * ws.E;
     const uint32_t tid = threadIdx.x, wv = tid / 64, l = tid % 64, H = ws.H, F = ws.F, nbf = F / 16;
     const uint32_t strip = SPW * blockIdx.x + wv / 2, y = blockIdx.y, P = g.pair ? 2u : 1u;
     const TqdLds L = tqd_lds(true, g.a.row_bytes, H, 32, U8,
@@ -829,7 +852,7 @@ __global__ __launch_bounds__(128 * SPW) void tqd_gateup_kernel(TqmArgs g) {
         cp.finish(sptr, my, n16, l);
     }
     if (wv == 0) {
-        const uint32_t n = route_row<NJ>(g.lg, ws.E, g.k, g.pol, l, cand, ex, r_ids, r_w);
+        const uint32_t n = route_row<NJ>(lg, ws.E, g.k, g.pol, l, cand, ex, r_ids, r_w);
         if (l == 0) r_n[0] = n;
     } else {
         tqd_stage<32, U8>(ws.xq, ws.xs, ws.xu, 0, P, H, As_c, Sc_c, tid - 64, 128 * SPW - 64);
@@ -984,30 +1007,42 @@ struct TqdStageW {
     }
 };
 
-// LDS of the fused decode down: nw strips, per wave its activations (As_c, Sc_c), the slots' rows
+// LDS of the fused decode down: nw strips, per wave its activations (As_c, Sc_c), the slots' rows,
+// the slots in expert order (batch order)
 __host__ __device__ inline size_t tqd_dc_lds(uint32_t nw, uint32_t row_bytes, uint32_t F, bool u8) {
-    return (size_t)nw * row_bytes + (size_t)nw * (F / 8 * 2 * 8 + F / 16 * 2 * (u8 ? 16 : 8)) + (size_t)nw * 16 * 4;
+    return (size_t)nw * row_bytes + (size_t)nw * (F / 8 * 2 * 8 + F / 16 * 2 * (u8 ? 16 : 8)) + (size_t)nw * 16 * 4 +
+           K_MAX * 4;
 }
 
-// Decode down and combine in one launch: grid H / 16, 64 (kcap + 1) threads.  Wave y chains strip
-// blockIdx.x of H for slot y (the routed expert y < ns, the shared expert at y = ns: the routing of
-// the gate/up launch), from a streamed LDS copy; then the strip's 16 outputs are the slots' rows
-// added in slot order from slot 0, shared last (exec.rs:1610-1621), plus out when residual.  This
+// Decode down and combine in one launch: grid (H / 16, tokens), 64 (kcap + 1) threads.  Wave y
+// chains strip blockIdx.x of H for slot y (the routed expert y < ns, the shared expert at y = ns:
+// the routing of the gate/up launch), from a streamed LDS copy; then the strip's 16 outputs are the
+// slots' rows added in slot order from slot 0, shared last (exec.rs:1610-1621), or for a batch run
+// as per-token decodes (border) in the batch combine's order, the shared row first, then the
+// token's entries by ascending expert (exec_batch.rs:1539-1578); plus out when residual.  This
 // replaces the per-slot rows in yent and the combine launch.
 template <int GK>
-__global__ __launch_bounds__(1024) void tqd_down_combine_kernel(TqmArgs g, float* __restrict__ out, int residual) {
+__global__ __launch_bounds__(1024) void tqd_down_combine_kernel(TqmArgs g, float* __restrict__ out, int residual,
+                                                               int border) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr bool U8 = GK == GK_TQ8;
     constexpr uint32_t SC = U8 ? 4 : 2;
-    const Workspace& ws = g.ws;
-    const uint32_t tid = threadIdx.x, y = tid / 64, l = tid % 64, nw = blockDim.x / 64, F = ws.F;
-    const uint32_t strip = blockIdx.x, P = g.pair ? 2u : 1u, rb = g.a.row_bytes;
+    const uint32_t tid = threadIdx.x, y = tid / 64, l = tid % 64, nw = blockDim.x / 64;
+    const Workspace ws = tqd_token(g.ws, blockIdx.y, nw - 1);  // token blockIdx.y's
+    out += (size_t)blockIdx.y * ws.H;
+    const uint32_t F = ws.F, strip = blockIdx.x, P = g.pair ? 2u : 1u, rb = g.a.row_bytes;
     const uint32_t ns = ws.n_sel[0], id = ws.ids[y < K_MAX ? y : 0];  // both requested at once
     uint8_t* my = smem + (size_t)y * rb;
     const size_t act = (size_t)F / 8 * 2 * 8 + (size_t)F / 16 * 2 * SC * 4;
     long* As_c = reinterpret_cast<long*>(smem + (size_t)nw * rb + y * act);
     float* Sc_c = reinterpret_cast<float*>(smem + (size_t)nw * rb + y * act + (size_t)F / 8 * 2 * 8);
     float* res = reinterpret_cast<float*>(smem + (size_t)nw * (rb + act));
+    uint32_t* perm = reinterpret_cast<uint32_t*>(res + nw * 16);  // [K_MAX] border: slots by expert
+    if (border && y < ns && l == 0) {  // the token's experts are distinct: rank = how many are smaller
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ns; j++) rank += ws.ids[j] < id ? 1u : 0u;
+        perm[rank] = y;
+    }
     if (y <= ns) {  // wave-uniform
         const uint8_t* src = (y == ns ? g.sha.ptr : g.a.ptr + (size_t)id * g.a.stride) + (size_t)strip * rb;
         const uint32_t n16 = rb / 16;
@@ -1023,8 +1058,14 @@ __global__ __launch_bounds__(1024) void tqd_down_combine_kernel(TqmArgs g, float
     }
     __syncthreads();
     if (tid < 16) {
-        float p = res[tid];
-        for (uint32_t s = 1; s <= ns; s++) p = p + res[s * 16 + tid];
+        float p;
+        if (border) {
+            p = res[ns * 16 + tid];
+            for (uint32_t j = 0; j < ns; j++) p = p + res[perm[j] * 16 + tid];
+        } else {
+            p = res[tid];
+            for (uint32_t s = 1; s <= ns; s++) p = p + res[s * 16 + tid];
+        }
         float* o = out + (size_t)strip * 16 + tid;
         *o = residual ? *o + p : p;
     }
@@ -1041,8 +1082,9 @@ bool tqd_dc_ok(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_
 }
 
 hipError_t launch_tqd_down_combine(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap, int pair,
-                                   float* out, int residual, hipStream_t st) {
-    if (!tqd_dc_ok(down, sh_down, ws, kcap)) return hipErrorInvalidValue;
+                                   float* out, int residual, hipStream_t st, uint32_t m) {
+    if (!tqd_dc_ok(down, sh_down, ws, kcap) || (m > 1 && (pair || !tqd_tokens_fit(ws, m, kcap))))
+        return hipErrorInvalidValue;
     const TqmArgs a{down, down, sh_down, sh_down, ws, 1, pair, nullptr, 0, Policy{}};
     const uint32_t nw = kcap + 1;
     const size_t lds = tqd_dc_lds(nw, down.row_bytes, ws.F, tq_bits(down.fmt) == 8);
@@ -1052,7 +1094,7 @@ hipError_t launch_tqd_down_combine(const Mat& down, const Mat& sh_down, const Wo
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
-        kern<<<ws.H / 16, 64 * nw, lds, st>>>(a, out, residual);
+        kern<<<dim3(ws.H / 16, m), 64 * nw, lds, st>>>(a, out, residual, m > 1 ? 1 : 0);
         return hipGetLastError();
     };
     switch (tq_bits(down.fmt)) {
@@ -1071,22 +1113,40 @@ static bool tqd_ok(const Mat& a, const Mat& b, const Mat& sa, const Mat& sb, siz
     return al(a) && al(b) && al(sa) && al(sb) && lds <= TQD_LDS_MAX;
 }
 
+bool tqd_gateup_ok(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
+                   const Policy& pol) {
+    const uint32_t ex = pol.enabled && pol.basis == TRK_BASIS_ALL ? ws.E * 4 : 0;
+    constexpr uint32_t SPW = TQD_GU_SPW;
+    const size_t lds = tqd_lds(true, gate.row_bytes, ws.H, 32, tq_bits(gate.fmt) == 8, ex, SPW).total;
+    return tq_kb(gate.fmt) == 32 && ws.H % 32 == 0 && tqd_ok(gate, up, sh_gate, sh_up, lds) &&
+           gate.row_bytes == up.row_bytes && gate.row_bytes == sh_gate.row_bytes &&
+           gate.row_bytes == sh_up.row_bytes && (ws.F / 16) % SPW == 0;
+}
+
+bool tqd_tokens_fit(const Workspace& ws, uint32_t m, uint32_t kcap) {
+    return m <= ws.m_max && (uint64_t)m * (kcap + 1) * 2 <= ws.act_rows && ws.tiles == 1;
+}
+
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
                              uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
                              hipStream_t st) {
     if (tq_kb(gate.fmt) != 32 || ws.H % 32) return hipErrorInvalidValue;
-    const TqmArgs a{gate, up, sh_gate, sh_up, ws, m == 1 ? 1 : 0, m == 1 && pair ? 1 : 0, lg, k, pol};
-    const int nj = m == 1 && lg ? (int)route_nj(ws.E) : 0;  // decode: routing inside
+    // tokens: a batch of m rows as per-token decodes (grid z), routing inside, single-level
+    const bool tokens = m > 1 && lg;
+    if (tokens && (pair || !tqd_gateup_ok(gate, up, sh_gate, sh_up, ws, pol) || !tqd_tokens_fit(ws, m, kcap)))
+        return hipErrorInvalidValue;
+    const bool dec = m == 1 || tokens;
+    const TqmArgs a{gate, up, sh_gate, sh_up, ws, dec ? 1 : 0, m == 1 && pair ? 1 : 0, lg, k, pol};
+    const int nj = dec && lg ? (int)route_nj(ws.E) : 0;  // decode: routing inside
     // decode: a workgroup per strip pair; batch: a workgroup per TQM_PAIRS strip pairs of an item,
     // looping over them with the item's activations staged once (5 or 2 pairs per workgroup at the
     // real shape: 478 / 484 us against 460 for 4)
-    if (m == 1 && nj) {  // decode from LDS copies of the strips where they fit
+    if (dec && nj) {  // decode from LDS copies of the strips where they fit
         const uint32_t ex = pol.enabled && pol.basis == TRK_BASIS_ALL ? ws.E * 4 : 0;
         constexpr uint32_t SPW = TQD_GU_SPW;
         const size_t lds = tqd_lds(true, gate.row_bytes, ws.H, 32, tq_bits(gate.fmt) == 8, ex, SPW).total;
-        if (tqd_ok(gate, up, sh_gate, sh_up, lds) && gate.row_bytes == up.row_bytes &&
-            gate.row_bytes == sh_gate.row_bytes && gate.row_bytes == sh_up.row_bytes && (ws.F / 16) % SPW == 0) {
-            const dim3 grid(ws.F / 16 / SPW, kcap + 1);
+        if (tqd_gateup_ok(gate, up, sh_gate, sh_up, ws, pol)) {
+            const dim3 grid(ws.F / 16 / SPW, kcap + 1, m);
             auto go = [&](auto kern) {
                 if (lds > 64 * 1024) {
                     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

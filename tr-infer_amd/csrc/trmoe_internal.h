@@ -187,15 +187,22 @@ hipError_t launch_tile_reduce(const float* plog, uint32_t m, uint32_t E, uint32_
                               hipStream_t st);
 // the TQ layer's expert products on int8 MFMA (k_tqm.hip): gate/up + SwiGLU + quantisation + fold,
 // and down into yent; tqm_fits: the shapes whose staged activations fit a workgroup's LDS
-// lg != null at m = 1: the decode routing (top-k or mass policy) runs inside the launch
+// lg != null at m = 1: the decode routing (top-k or mass policy) runs inside the launch; at m >= 2
+// (pair = 0, tqd_gateup_ok, tqd_tokens_fit): every token runs as such a decode (lg [m][E])
 hipError_t launch_tqm_gateup(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
                              uint32_t m, uint32_t kcap, int pair, const float* lg, uint32_t k, Policy pol,
                              hipStream_t st);
 // decode down and combine in one launch (k_tqm.hip) where the shape allows (tqd_dc_ok): out (+)= the
-// slots' down rows in slot order, no per-slot rows in yent
+// slots' down rows in slot order, no per-slot rows in yent.  m >= 2 (pair = 0, tqd_tokens_fit): m
+// tokens as per-token decodes, each token's rows in the batch combine's order
 bool tqd_dc_ok(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap);
 hipError_t launch_tqd_down_combine(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t kcap, int pair,
-                                   float* out, int residual, hipStream_t st);
+                                   float* out, int residual, hipStream_t st, uint32_t m = 1);
+// the decode gate/up from LDS copies of the strips takes this layer's shape; m tokens' decode
+// slots (two activation rows each) fit the workspace
+bool tqd_gateup_ok(const Mat& gate, const Mat& up, const Mat& sh_gate, const Mat& sh_up, const Workspace& ws,
+                   const Policy& pol);
+bool tqd_tokens_fit(const Workspace& ws, uint32_t m, uint32_t kcap);
 hipError_t launch_tqm_down(const Mat& down, const Mat& sh_down, const Workspace& ws, uint32_t m, uint32_t kcap, int pair,
                            hipStream_t st);
 inline bool tqm_fits(uint32_t H, uint32_t F) {
