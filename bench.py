@@ -56,7 +56,7 @@ def main():
     ap.add_argument("--extra", type=str, default="c4,stack,tq,hc,gemv",
                     help="also time config 4 (c4: M=3072, Q6_K down, dynamic-k) and config 5 (stack: the "
                          "48-layer RMSNorm + residual stack at M=1 and M=512); tq: the layer on packed TQ "
-                         "experts at the real shape (H=2560, F=640) at M=1 and M=512; hc: the same layer "
+                         "experts at the real shape (H=2560, F=640) at M=1, 4 and 512; hc: the same layer "
                          "behind the hyper-connection mix (trk_moe_forward_hc, hc=4, low rank 320); gemv: "
                          "trk_gemv on the real model's dense projections; q80 / q51 / q6k: the layer at M=1 "
                          "and M=512 with Q8_0 / Q5_1 / Q6_K downs; '' for none")
@@ -377,8 +377,8 @@ def bench_down_format(args, layers, fmt, name, dev, stream, trmoe, torch):
 def bench_tq(args, dev, stream, trmoe, torch, np):
     """The layer on the reference's own packed TQ experts at the real expert shape: H = 2560,
     F = 640, E = 512, top-10, gate/up TQ4_32 and down TQ5_16 (python/tests/test_blocks_real.py:
-    23-26), over a rotation of args.tq_layers layers (synthetic packs generated on the GPU), at M = 1
-    and M = 512 (Zipf-biased router)."""
+    23-26), over a rotation of args.tq_layers layers (synthetic packs generated on the GPU), at M = 1,
+    M = 4 (each token as a decode) and M = 512 (Zipf-biased router)."""
     Ht, Et, Ft = 2560, 512, 640
     gf, df = trmoe.FMT_TQ4_32, trmoe.FMT_TQ5_16
     gen = torch.Generator(device=dev)
@@ -392,7 +392,7 @@ def bench_tq(args, dev, stream, trmoe, torch, np):
     log(f"TQ layers: {len(lw)} x {Et} experts ({len(lw) * Et * per_expert / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
     bias = torch.from_numpy(trmoe.zipf_bias(1, Et)).to(dev)
     res = {}
-    for M in (1, 512):
+    for M in (1, 4, 512):
         for w in lw:
             w.moew.router_bias = bias.data_ptr() if M >= 64 else None
         ctx = trmoe.Context(Ht, Et, Ft, K, M)

@@ -279,11 +279,13 @@ int trk_set_fusion(trk_ctx *ctx, int on);
  * counterpart in the reference, which runs one grouped kernel per expert matrix. */
 int trk_set_stream_rows(trk_ctx *ctx, int rows);
 
-/* 2 <= M <= rows (default 8, 0..16) on GGUF layers: every token runs as a decode (its routing inside
- * its gate/up workgroups, its rows added by the down launch in the batch combine's order: shared
- * expert first, then ascending expert), three launches with no dispatch, grouped items or
- * combine.  The same bits as the grouped path (exec_batch.rs:1404-1580); the dispatch arrays
- * (TRK_WS_ENT_*, items) are then not written.  No counterpart in the reference. */
+/* 2 <= M <= rows (default 8, 0..16): every token runs as a decode (its routing inside its gate/up
+ * workgroups, its rows added by the down launch in the batch combine's order: shared expert
+ * first, then ascending expert), three launches with no dispatch, grouped items or combine.  GGUF
+ * layers with one tile; TQ layers where the decode kernels take the shape (the real one: kb-32
+ * gate/up, kb-16 down, one tile, k_cap <= 15).  The same bits as the grouped path
+ * (exec_batch.rs:1404-1580); the dispatch arrays (TRK_WS_ENT_*, items) are then not written.
+ * No counterpart in the reference. */
 int trk_set_decode_rows(trk_ctx *ctx, int rows);
 
 /* Layers on TQ experts: the int8 MFMA kernels (on, the default, where H / 32 units of staged
