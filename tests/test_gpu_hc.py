@@ -38,7 +38,8 @@ def layer(kind):
 
 
 @pytest.mark.parametrize("kind,M,hiprec,bits", [("tq", 1, True, 8), ("tq", 1, False, 4), ("gguf", 1, True, 5),
-                                                ("tq", 5, True, 4), ("gguf", 40, True, 8), ("tq", 33, True, 5)])
+                                                ("tq", 5, True, 4), ("gguf", 3, True, 8), ("gguf", 40, True, 8),
+                                                ("tq", 33, True, 5)])
 def test_moe_forward_hc(kind, M, hiprec, bits):
     say(f"moe forward hc {kind} M={M} hiprec={hiprec} up bits={bits}")
     import torch
