@@ -313,21 +313,29 @@ __device__ __forceinline__ void tqm_strip2(const uint8_t* __restrict__ s0, const
         for (uint32_t i = 0; i < UB; i++) {
             const uint32_t b = b0 + i;
             if (b >= nu) break;
-            const TqmB<GK, KB> c0 = w0[i], c1 = w1[i];
-            if (b + UB < nu) {  // the loads UB units ahead
-                tqm_load<GK, KB>(w0[i], s0, b + UB, l);
-                tqm_load<GK, KB>(w1[i], s1, b + UB, l);
-            }
-            const long a = As[b * 64 + l];
-            const long bq0 = tqm_operand<GK, KB>(c0, l), bq1 = tqm_operand<GK, KB>(c1, l);
+            // the unit's operands and scales out of its registers first, then the loads UB units
+            // ahead into the same registers, unconditionally (the strip's last unit again past its
+            // end): no branch, so no copies of the window
             constexpr uint32_t NBL = TqmB<GK, KB>::NBL;  // blocks of the unit
+            const long bq0 = tqm_operand<GK, KB>(w0[i], l), bq1 = tqm_operand<GK, KB>(w1[i], l);
+            float dd0v[NBL], mm0v[NBL], dd1v[NBL], mm1v[NBL];
+#pragma unroll
+            for (uint32_t hb = 0; hb < NBL; hb++) {
+                dd0v[hb] = h2f((uint16_t)w0[i].d[hb]);
+                mm0v[hb] = h2f((uint16_t)w0[i].m[hb]);
+                dd1v[hb] = h2f((uint16_t)w1[i].d[hb]);
+                mm1v[hb] = h2f((uint16_t)w1[i].m[hb]);
+            }
+            const uint32_t bn = b + UB < nu ? b + UB : nu - 1;
+            tqm_load<GK, KB>(w0[i], s0, bn, l);
+            tqm_load<GK, KB>(w1[i], s1, bn, l);
+            const long a = As[b * 64 + l];
 #pragma unroll
             for (uint32_t hb = 0; hb < NBL; hb++) {
                 const long am = KB == 16 ? ((g / 2 == hb) ? a : 0) : a;
                 const v4i d40 = tqm_mfma(am, bq0), d41 = tqm_mfma(am, bq1);
                 const uint32_t blk = NBL * b + hb;
-                const float dd0 = h2f((uint16_t)c0.d[hb]), mm0 = h2f((uint16_t)c0.m[hb]);
-                const float dd1 = h2f((uint16_t)c1.d[hb]), mm1 = h2f((uint16_t)c1.m[hb]);
+                const float dd0 = dd0v[hb], mm0 = mm0v[hb], dd1 = dd1v[hb], mm1 = mm1v[hb];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const float* sx = Sc + (blk * 16 + 4 * g + v) * SC;
